@@ -1,0 +1,278 @@
+"""Benchmark of the Strata hot path on one MI355X (driver contract: one JSON line).
+
+Headline (``value``): NA3D forward TFLOP/s at BASELINE configs[2] — 6 halo-
+padded cube-face tiles (16,144,144), outputs for the interior (16,128,128),
+16 heads x 64, window (3,13,13), bf16, q/k/v ~ N(0,1) * per-head U(0.5,2).
+One step = one NA3D launch over the whole batch; inputs are resident in HBM.
+FLOPs = 4 * N_q(interior) * |W| * D per head.
+
+Also reported: the full Strata block tokens/s with a per-kernel
+breakdown and the RoPE+QKV-pack prologue's HBM GB/s, the roofline of the
+dominant kernel, and the CPU oracle timed on a bounded sample on this host.
+
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-block] [--no-cpu]
+"""
+
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import statistics
+import sys
+import time
+from pathlib import Path
+
+ROOT = Path(__file__).resolve().parent
+sys.path.insert(0, str(ROOT))
+
+PEAK_BF16_TFLOPS = 2516.6  # 256 CU x 4096 bf16 FLOP/clk/CU x 2.4 GHz (vendor "2.5 PF" dense)
+PEAK_HBM_GBPS = 8000.0
+METRIC = "NA3D fwd TFLOP/s & % bf16 MFMA peak; Strata-block tokens/s, 1 MI355X"
+
+
+def log(msg: str) -> None:
+    print(msg, file=sys.stderr, flush=True)
+
+
+def cfg2_inputs(device):
+    import torch
+
+    g = torch.Generator(device=device).manual_seed(0)
+    s_h = torch.rand(16, generator=g, device=device) * 1.5 + 0.5
+    shape = (6, 16, 144, 144, 16, 64)
+    return [
+        (torch.randn(shape, generator=g, device=device) * s_h.view(1, 1, 1, 1, 16, 1)).bfloat16() for _ in range(3)
+    ]
+
+
+def time_na3d(q, k, v, steps, warmup):
+    """Per-launch time of the NA3D kernel (HIP events on torch's current
+    stream, which is the stream the op launches on)."""
+    import torch
+
+    op = torch.ops.strata_hip.na3d_fwd
+    args = ([3, 13, 13], [1, 1, 1], None, [0, 8, 8], [16, 128, 128])
+    for _ in range(warmup):
+        out = op(q, k, v, *args)
+    torch.cuda.synchronize()
+    start, stop = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    t0 = time.perf_counter()
+    start.record()
+    for _ in range(steps):
+        out = op(q, k, v, *args)
+    stop.record()
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t0
+    return start.elapsed_time(stop) / steps, wall / steps * 1e3, out
+
+
+def bench_block(device, steps, warmup):
+    """one Strata block forward on [4, 8, 64, 64, 1024] bf16."""
+    import torch
+
+    from strata_amd import ops
+    from strata_amd import rope as P
+    from strata_amd.modules import StrataBlock, init_xavier_
+
+    B, Z, Y, X, C, H = 4, 8, 64, 64, 1024, 16
+    blk = StrataBlock(C, H, (3, 7, 7))
+    init_xavier_(blk, torch.Generator().manual_seed(1))
+    blk = blk.to(device).bfloat16().eval()
+    gx = torch.Generator(device=device).manual_seed(0)
+    x = torch.randn(B, Z, Y, X, C, generator=gx, device=device).bfloat16()
+    lat, lon = P.synthetic_tile_latlon(B, Y, X, torch.Generator().manual_seed(0))
+    cos, sin = P.stereographic_rope_tables(lat.to(device), lon.to(device), C // H, 10000.0, P.default_rope_length_scale(1))
+    rope = (cos, sin)
+    with torch.no_grad():
+        for _ in range(warmup):
+            y = blk(x, rope)
+        torch.cuda.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        for _ in range(steps):
+            y = blk(x, rope)
+        e1.record()
+        torch.cuda.synchronize()
+    ms = e0.elapsed_time(e1) / steps
+    M = B * Z * Y * X
+
+    # per-kernel breakdown: the block's launches one by one, each bracketed by events
+    def timed(fn, reps=5):
+        fn()
+        torch.cuda.synchronize()
+        a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        a.record()
+        for _ in range(reps):
+            r = fn()
+        b.record()
+        torch.cuda.synchronize()
+        return a.elapsed_time(b) / reps, r
+
+    attn, mlp = blk.attn, blk.mlp
+    with torch.no_grad():
+        t_ln, h = timed(lambda: ops.layer_norm(x, 1e-6))
+        t_qkv, qkv = timed(lambda: ops.gemm_bias_act(h, attn.qkv.weight, attn.qkv.bias, None, 0))
+        t_rope, (q, k, v) = timed(lambda: ops.rope_qkv_pack(qkv, cos, sin, H, 0))
+        t_na, a = timed(lambda: ops.na3d_fwd(q, k, v, [3, 7, 7], [1, 1, 1], None, [0, 0, 0], [Z, Y, X]))
+        a = a.view(B, Z, Y, X, C)
+        t_proj, x1 = timed(lambda: ops.gemm_bias_act(a, attn.proj.weight, attn.proj.bias, x, 0))
+        t_fc1, f = timed(lambda: ops.gemm_bias_act(h, mlp.layers[0].weight, mlp.layers[0].bias, None, 1))
+        t_fc2, _ = timed(lambda: ops.gemm_bias_act(f, mlp.layers[2].weight, mlp.layers[2].bias, x1, 0))
+    gemm_flops = {"qkv": 2 * M * C * 3 * C, "proj": 2 * M * C * C, "fc1": 2 * M * C * 4 * C, "fc2": 2 * M * 4 * C * C}
+    na_flops = 4.0 * M * H * 147 * (C // H)
+    rope_bytes = M * 3 * C * 2 * 2 + B * Y * X * (C // H // 2) * 4 * 2  # qkv read + q/k/v write + tables
+    kernels = {
+        "layer_norm_ms": t_ln,
+        "qkv_gemm_ms": t_qkv,
+        "rope_pack_ms": t_rope,
+        "na3d_ms": t_na,
+        "proj_gemm_ms": t_proj,
+        "fc1_gelu_gemm_ms": t_fc1,
+        "fc2_gemm_ms": t_fc2,
+    }
+    tflops = {
+        "qkv_gemm": gemm_flops["qkv"] / t_qkv / 1e9,
+        "proj_gemm": gemm_flops["proj"] / t_proj / 1e9,
+        "fc1_gelu_gemm": gemm_flops["fc1"] / t_fc1 / 1e9,
+        "fc2_gemm": gemm_flops["fc2"] / t_fc2 / 1e9,
+        "na3d": na_flops / t_na / 1e9,
+    }
+    total_flops = sum(gemm_flops.values()) + na_flops
+    return {
+        "workload": "configs[3] Strata block fwd: x [4,8,64,64,1024] bf16, 16x64 heads, W=(3,7,7), "
+        "stereographic RoPE, MLP 4096 GELU(tanh), Xavier seed 1",
+        "tokens_per_s": M / (ms * 1e-3),
+        "ms_per_step": ms,
+        "block_tflops": total_flops / (ms * 1e-3) / 1e12,
+        "pct_bf16_peak": 100.0 * total_flops / (ms * 1e-3) / 1e12 / PEAK_BF16_TFLOPS,
+        "kernel_ms": {k: round(v, 4) for k, v in kernels.items()},
+        "kernel_tflops": {k: round(v, 1) for k, v in tflops.items()},
+        "prologue_GBps": rope_bytes / (t_rope * 1e-3) / 1e9,
+        "prologue_pct_hbm": 100.0 * rope_bytes / (t_rope * 1e-3) / 1e9 / PEAK_HBM_GBPS,
+    }
+
+
+def cpu_baseline():
+    """The CPU oracle on a bounded sample of configs[2]: tile 0, head 0, 4 z-slices."""
+    import torch
+
+    from oracle import na3d as O
+
+    threads = min(16, os.cpu_count() or 1)
+    torch.set_num_threads(threads)
+    g = torch.Generator().manual_seed(0)
+    shape = (1, 16, 144, 144, 1, 64)
+    q, k, v = (torch.randn(shape, generator=g) for _ in range(3))
+    box_o, box_e = (0, 8, 8), (4, 128, 128)
+    nq = box_e[0] * box_e[1] * box_e[2]
+    flops = O.na3d_flops(1, 1, 64, nq, (3, 13, 13))
+    O.na3d(q, k, v, (3, 13, 13), q_origin=box_o, q_extent=(1, 16, 128))  # warm-up
+    times = []
+    for _ in range(3):
+        t0 = time.perf_counter()
+        O.na3d(q, k, v, (3, 13, 13), q_origin=box_o, q_extent=box_e)
+        times.append(time.perf_counter() - t0)
+    t = statistics.median(times)
+    return {
+        "value": flops / t / 1e12,
+        "unit": "TFLOP/s",
+        "cores": threads,
+        "kind": "port",
+        "sample": "configs[2] NA3D, tile 0, head 0, query box z 0-3 x interior 128x128 (4.25 GFLOP), "
+        f"fp32 torch-CPU oracle, median of 3 = {t:.2f} s",
+    }
+
+
+def load_traffic():
+    """HBM bytes per NA3D launch from the committed rocprofv3 --pmc summary, if any."""
+    p = ROOT / "profiles" / "na3d_cfg2_traffic.json"
+    if p.exists():
+        try:
+            return json.loads(p.read_text()).get("traffic_bytes")
+        except (ValueError, OSError):
+            return None
+    return None
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=3)
+    ap.add_argument("--no-block", action="store_true")
+    ap.add_argument("--no-cpu", action="store_true")
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(
+            f"bench.py: this build measures one GPU only (asked for --gpus {args.gpus}); the tiles are "
+            "independent per GPU, so run it per GPU.",
+            file=sys.stderr,
+        )
+        sys.exit(2)
+
+    import torch
+
+    import strata_amd  # noqa: F401
+    from strata_amd import _lib
+
+    _lib.load()
+    dev = torch.device("cuda:0")
+    log("bench: generating configs[2] inputs")
+    q, k, v = cfg2_inputs(dev)
+    torch.cuda.synchronize()
+    log("bench: timing NA3D configs[2]")
+    ms, wall_ms, _ = time_na3d(q, k, v, args.steps, args.warmup)
+    flops = 4.0 * 6 * 16 * (16 * 128 * 128) * 507 * 64
+    tflops = flops / (ms * 1e-3) / 1e12
+    alg_bytes = (6 * 16 * 128 * 128 * 16 * 64 * 2) * 2 + (6 * 16 * 144 * 144 * 16 * 64 * 2) * 2
+    del q, k, v
+    torch.cuda.empty_cache()
+
+    result = {
+        "metric": METRIC,
+        "value": round(tflops, 2),
+        "unit": "TFLOP/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic",
+        "config": {
+            "workload": "configs[2] NA3D fwd: 6 halo-padded tiles (16,144,144) -> interior (16,128,128), "
+            "16 heads x 64, W=(3,13,13), bf16, q/k/v ~ N(0,1)*U(0.5,2) per head, seed 0",
+            "batch": 6,
+            "grid": [16, 144, 144],
+            "interior": [16, 128, 128],
+            "heads": 16,
+            "head_dim": 64,
+            "kernel": [3, 13, 13],
+        },
+        "pct_bf16_peak": round(100.0 * tflops / PEAK_BF16_TFLOPS, 2),
+        "wall_ms_per_step": round(wall_ms, 4),
+        "roofline": {
+            "bound": "mfma",
+            "achieved": round(tflops, 2),
+            "peak": PEAK_BF16_TFLOPS,
+            "unit": "TFLOP/s",
+            "frac": round(tflops / PEAK_BF16_TFLOPS, 4),
+            "traffic": load_traffic(),
+            "algorithmic_bytes": alg_bytes,
+            "algorithmic_GBps": round(alg_bytes / (ms * 1e-3) / 1e9, 1),
+        },
+    }
+    if not args.no_block:
+        log("bench: timing the configs[3] block")
+        result["block"] = bench_block(dev, max(3, args.steps // 2), 2)
+    if not args.no_cpu:
+        log("bench: timing the CPU oracle sample")
+        result["cpu_baseline"] = cpu_baseline()
+    print(json.dumps(result), flush=True)
+
+
+if __name__ == "__main__":
+    main()

@@ -1,0 +1,178 @@
+/*
+ * strata_hip.h — C ABI of the MI355X (gfx950) kernels for the Strata
+ * transformer block's hot path: 3D neighbourhood attention (NA3D), the
+ * stereographic-RoPE + QKV-pack prologue, the bias/GELU/residual GEMM and the
+ * non-affine LayerNorm.
+ *
+ * Conventions shared by every entry point
+ *   - All pointers are device pointers owned by the caller.  The library never
+ *     allocates or frees device memory and keeps no state between calls.
+ *   - `stream` is a hipStream_t (passed as void* so that the header needs no
+ *     HIP include).  Work is enqueued asynchronously on that stream; there is
+ *     no device synchronisation inside the library.
+ *   - Return value: STRATA_HIP_OK (0) or a negative STRATA_HIP_E* code.  The
+ *     message of the last failure on the calling thread is returned by
+ *     strata_hip_last_error().
+ *   - Token tensors use the heads-last layout [B, Z, Y, X, H, D] (NATTEN >= 0.20
+ *     layout).  Strides are in ELEMENTS over (b, z, y, x, h); the d stride is 1.
+ */
+#ifndef STRATA_HIP_H
+#define STRATA_HIP_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define STRATA_HIP_ABI_VERSION 1
+
+enum strata_hip_status {
+  STRATA_HIP_OK = 0,
+  STRATA_HIP_EINVAL = -1,      /* bad shape, stride, kernel size or pointer */
+  STRATA_HIP_EUNSUPPORTED = -2, /* valid request this build has no kernel for */
+  STRATA_HIP_ELAUNCH = -3       /* hipLaunchKernel / hipGetLastError failure */
+};
+
+enum strata_hip_dtype { STRATA_HIP_F32 = 0, STRATA_HIP_BF16 = 1 };
+
+enum strata_hip_act { STRATA_HIP_ACT_NONE = 0, STRATA_HIP_ACT_GELU_TANH = 1, STRATA_HIP_ACT_GELU_ERF = 2 };
+
+enum strata_hip_rope_layout {
+  STRATA_HIP_ROPE_HALF = 0,       /* pair p = (d=p, d=p+D/2)   ("rotate_half") */
+  STRATA_HIP_ROPE_INTERLEAVED = 1 /* pair p = (d=2p, d=2p+1) */
+};
+
+/* ---------------------------------------------------------------------------
+ * NA3D forward.
+ * Replaces natten.na3d(query, key, value, kernel_size, stride=1, dilation,
+ * is_causal=False, scale) of NATTEN 0.21.5 (pinned at
+ * docker/build_natten.sh:21 and Makefile:11; reached through the backend
+ * string of screamcast/config.py:99 -> train.py:143 ->
+ * screamcast/strata_wrappers.py:331,490,582).
+ *
+ * q, k, v share the token grid `grid` = (Z, Y, X).  Only the queries inside
+ * the box [q_origin, q_origin + q_extent) are computed; `out` has the box's
+ * shape [B, Ez, Ey, Ex, H, D].  Windows are NATTEN's clamped windows on the
+ * full grid, so out == natten.na3d(q, k, v)[:, box].  Per axis: odd kernel
+ * k, dilation d with d*k <= L; a query i with g = i mod d attends keys
+ * g + d*(s + [0, k)), s = clamp(i/d - k/2, 0, ceil((L-g)/d) - k).
+ * bf16 inputs: fp32 accumulation and softmax, bf16 output.  f32 inputs: f32.
+ * ------------------------------------------------------------------------- */
+typedef struct strata_hip_na3d_args {
+  const void* q;
+  const void* k;
+  const void* v;
+  void* out;
+  int32_t dtype;       /* strata_hip_dtype, same for q, k, v, out */
+  int32_t batch;
+  int32_t heads;
+  int32_t head_dim;
+  int32_t grid[3];     /* Z, Y, X of the q/k/v token grid */
+  int32_t q_origin[3]; /* first query (z, y, x) of the output box */
+  int32_t q_extent[3]; /* output box size (Ez, Ey, Ex) */
+  int32_t kernel[3];   /* window (kz, ky, kx), odd */
+  int32_t dilation[3];
+  int32_t reserved;
+  float scale;         /* softmax scale, usually head_dim^-1/2 */
+  float reserved_f;
+  int64_t q_stride[5]; /* element strides over (b, z, y, x, h) */
+  int64_t k_stride[5];
+  int64_t v_stride[5];
+  int64_t o_stride[5]; /* strides of `out` over (b, z', y', x', h) */
+} strata_hip_na3d_args;
+
+int strata_hip_na3d_fwd(const strata_hip_na3d_args* args, void* stream);
+
+/* ---------------------------------------------------------------------------
+ * Stereographic-RoPE + QKV pack.
+ * Replaces the attention's qkv split + RoPE of the physicsnemo Strata block
+ * (attn.qkv keys at tests/regression_data/sweep1_...param_order.txt:3-4;
+ * RoPE helpers imported at screamcast/strata_wrappers.py:52, base and length
+ * scale set at :333-338).
+ *
+ * qkv: [M, 3*H*D] bf16, row stride `qkv_row_stride` elements, column order
+ * (3, H, D) (nn.Linear output of attn.qkv).  M = B*Z*Y*X tokens.
+ * cos/sin: f32 tables [B, Zt, Y, X, D/2] contiguous, Zt in {1, Z} (Zt = 1
+ * broadcasts one table over all levels).
+ * q, k, v: [M, H, D] bf16 contiguous (heads-last token layout).  RoPE rotates
+ * the pairs of q and k; v is copied.  Any of q/k/v may alias nothing else.
+ * ------------------------------------------------------------------------- */
+typedef struct strata_hip_rope_pack_args {
+  const void* qkv;
+  const float* cos;
+  const float* sin;
+  void* q;
+  void* k;
+  void* v;
+  int32_t batch;
+  int32_t grid[3];    /* Z, Y, X */
+  int32_t table_z;    /* Zt: 1 or Z */
+  int32_t heads;
+  int32_t head_dim;
+  int32_t layout;     /* strata_hip_rope_layout */
+  int64_t qkv_row_stride;
+} strata_hip_rope_pack_args;
+
+int strata_hip_rope_qkv_pack(const strata_hip_rope_pack_args* args, void* stream);
+
+/* ---------------------------------------------------------------------------
+ * GEMM with fused epilogue:  out = act(x @ w^T + bias) + residual
+ * Replaces nn.Linear (+ GELU) of the block: attn.qkv, attn.proj and the Mlp
+ * fc1 -> GELU(tanh) -> fc2 chain (Mlp layers.0 / layers.2 at
+ * screamcast/checkpoint_compat.py:243-249; tanh GELU forced by
+ * screamcast/strata_wrappers.py:76-100).
+ *
+ * x: [M, K] bf16 (row stride ldx), w: [N, K] bf16 (nn.Linear layout, row
+ * stride ldw), bias: [N] bf16 or NULL, residual: [M, N] bf16 (row stride ldr)
+ * or NULL, out: [M, N] bf16 (row stride ldo).  fp32 accumulation.  The
+ * residual is added after the activation.  K must be a multiple of 8 and
+ * every row stride a multiple of 8 elements.  `out` may alias `residual`.
+ * ------------------------------------------------------------------------- */
+typedef struct strata_hip_gemm_args {
+  const void* x;
+  const void* w;
+  const void* bias;
+  const void* residual;
+  void* out;
+  int64_t m;
+  int64_t n;
+  int64_t k;
+  int64_t ldx;
+  int64_t ldw;
+  int64_t ldr;
+  int64_t ldo;
+  int32_t act; /* strata_hip_act */
+  int32_t reserved;
+} strata_hip_gemm_args;
+
+int strata_hip_gemm_bias_act(const strata_hip_gemm_args* args, void* stream);
+
+/* ---------------------------------------------------------------------------
+ * Non-affine LayerNorm over the last dimension (the block's two pre-norms,
+ * which carry no parameters in the state-dict manifests
+ * tests/regression_data/sweep1_...param_order.txt:3-12).
+ * x, out: [M, C] bf16, row strides ldx / ldo elements; fp32 statistics.
+ * ------------------------------------------------------------------------- */
+typedef struct strata_hip_layer_norm_args {
+  const void* x;
+  void* out;
+  int64_t m;
+  int64_t c;
+  int64_t ldx;
+  int64_t ldo;
+  float eps;
+  int32_t reserved;
+} strata_hip_layer_norm_args;
+
+int strata_hip_layer_norm(const strata_hip_layer_norm_args* args, void* stream);
+
+/* Library bookkeeping (no counterpart in the reference). */
+const char* strata_hip_last_error(void);
+int strata_hip_abi_version(void);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* STRATA_HIP_H */

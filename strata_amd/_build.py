@@ -1,0 +1,89 @@
+"""Build ``libstrata_hip.so`` in-tree with hipcc for gfx950.
+
+The library is a plain C-ABI shared object (see ``include/strata_hip.h``); it is
+compiled directly with ``hipcc`` (no torch headers, no JIT cache), so the
+built file travels with the source tree to a GPU host.
+
+Flags:
+  * ``--offload-arch=gfx950`` only: the kernels are written for CDNA4.
+  * ``-Xclang -target-feature -Xclang -packed-fp32-ops``: keep the compiler from
+    forming packed-fp32 VALU ops (v_pk_fma_f32 and friends).
+  * ``-mcode-object-version=5``: loadable by the HIP 7.0 runtime that the
+    installed torch wheel bundles (the library binds to that runtime when torch
+    is imported first; both carry the SONAME libamdhip64.so.7).
+"""
+
+from __future__ import annotations
+
+import os
+import shutil
+import subprocess
+from concurrent.futures import ThreadPoolExecutor
+from pathlib import Path
+
+PKG_DIR = Path(__file__).resolve().parent
+CSRC = PKG_DIR / "csrc"
+BUILD_DIR = PKG_DIR / "_build"
+LIB_NAME = "libstrata_hip.so"
+LIB_PATH = PKG_DIR / LIB_NAME
+INCLUDE_DIR = PKG_DIR.parent / "include"
+
+ARCH = "gfx950"
+DEVICE_FLAGS = [
+    f"--offload-arch={ARCH}",
+    "-O3",
+    "-fPIC",
+    "-std=c++17",
+    "-mcode-object-version=5",
+    "-Xclang",
+    "-target-feature",
+    "-Xclang",
+    "-packed-fp32-ops",
+    "-Wno-unused-command-line-argument",
+]
+
+
+def hipcc() -> str:
+    rocm = os.environ.get("ROCM_PATH", "/opt/rocm")
+    cand = Path(rocm) / "bin" / "hipcc"
+    if cand.exists():
+        return str(cand)
+    found = shutil.which("hipcc")
+    if not found:
+        raise RuntimeError("hipcc not found: set ROCM_PATH or put hipcc on PATH")
+    return found
+
+
+def sources() -> list[Path]:
+    return sorted(CSRC.glob("*.hip")) + sorted(CSRC.glob("*.cpp"))
+
+
+def _compile(src: Path) -> Path:
+    obj = BUILD_DIR / (src.stem + ".o")
+    cmd = [hipcc(), *DEVICE_FLAGS, f"-I{INCLUDE_DIR}", "-c", str(src), "-o", str(obj)]
+    res = subprocess.run(cmd, capture_output=True, text=True)
+    if res.returncode != 0:
+        raise RuntimeError(f"hipcc failed for {src.name}:\n{' '.join(cmd)}\n{res.stdout}\n{res.stderr}")
+    return obj
+
+
+def build(verbose: bool = False, jobs: int | None = None) -> Path:
+    """Compile every source under csrc/ and link ``strata_amd/libstrata_hip.so``."""
+    BUILD_DIR.mkdir(exist_ok=True)
+    srcs = sources()
+    jobs = jobs or min(len(srcs), max(1, (os.cpu_count() or 2)))
+    with ThreadPoolExecutor(max_workers=jobs) as ex:
+        objs = list(ex.map(_compile, srcs))
+    tmp = LIB_PATH.with_suffix(".so.tmp")
+    cmd = [hipcc(), f"--offload-arch={ARCH}", "-shared", "-fPIC", *map(str, objs), "-o", str(tmp)]
+    res = subprocess.run(cmd, capture_output=True, text=True)
+    if res.returncode != 0:
+        raise RuntimeError(f"link failed:\n{' '.join(cmd)}\n{res.stdout}\n{res.stderr}")
+    os.replace(tmp, LIB_PATH)
+    if verbose:
+        print(f"built {LIB_PATH}")
+    return LIB_PATH
+
+
+if __name__ == "__main__":
+    build(verbose=True)

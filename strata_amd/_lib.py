@@ -1,0 +1,169 @@
+"""ctypes binding of ``libstrata_hip.so`` (C ABI declared in ``include/strata_hip.h``).
+
+The structures below mirror the header field for field.  The library is
+loaded lazily, after ``torch`` so that it binds to the HIP runtime torch
+already loaded (both carry the SONAME ``libamdhip64.so.7``).  There is no
+fallback: if the library is missing every op raises.
+"""
+
+from __future__ import annotations
+
+import ctypes
+import threading
+from pathlib import Path
+
+LIB_PATH = Path(__file__).resolve().parent / "libstrata_hip.so"
+
+ABI_VERSION = 1
+
+OK = 0
+EINVAL = -1
+EUNSUPPORTED = -2
+ELAUNCH = -3
+
+F32 = 0
+BF16 = 1
+
+ACT_NONE = 0
+ACT_GELU_TANH = 1
+ACT_GELU_ERF = 2
+
+ROPE_HALF = 0
+ROPE_INTERLEAVED = 1
+
+_i32x3 = ctypes.c_int32 * 3
+_i64x5 = ctypes.c_int64 * 5
+
+
+class Na3dArgs(ctypes.Structure):
+    _fields_ = [
+        ("q", ctypes.c_void_p),
+        ("k", ctypes.c_void_p),
+        ("v", ctypes.c_void_p),
+        ("out", ctypes.c_void_p),
+        ("dtype", ctypes.c_int32),
+        ("batch", ctypes.c_int32),
+        ("heads", ctypes.c_int32),
+        ("head_dim", ctypes.c_int32),
+        ("grid", _i32x3),
+        ("q_origin", _i32x3),
+        ("q_extent", _i32x3),
+        ("kernel", _i32x3),
+        ("dilation", _i32x3),
+        ("reserved", ctypes.c_int32),
+        ("scale", ctypes.c_float),
+        ("reserved_f", ctypes.c_float),
+        ("q_stride", _i64x5),
+        ("k_stride", _i64x5),
+        ("v_stride", _i64x5),
+        ("o_stride", _i64x5),
+    ]
+
+
+class RopePackArgs(ctypes.Structure):
+    _fields_ = [
+        ("qkv", ctypes.c_void_p),
+        ("cos", ctypes.c_void_p),
+        ("sin", ctypes.c_void_p),
+        ("q", ctypes.c_void_p),
+        ("k", ctypes.c_void_p),
+        ("v", ctypes.c_void_p),
+        ("batch", ctypes.c_int32),
+        ("grid", _i32x3),
+        ("table_z", ctypes.c_int32),
+        ("heads", ctypes.c_int32),
+        ("head_dim", ctypes.c_int32),
+        ("layout", ctypes.c_int32),
+        ("qkv_row_stride", ctypes.c_int64),
+    ]
+
+
+class GemmArgs(ctypes.Structure):
+    _fields_ = [
+        ("x", ctypes.c_void_p),
+        ("w", ctypes.c_void_p),
+        ("bias", ctypes.c_void_p),
+        ("residual", ctypes.c_void_p),
+        ("out", ctypes.c_void_p),
+        ("m", ctypes.c_int64),
+        ("n", ctypes.c_int64),
+        ("k", ctypes.c_int64),
+        ("ldx", ctypes.c_int64),
+        ("ldw", ctypes.c_int64),
+        ("ldr", ctypes.c_int64),
+        ("ldo", ctypes.c_int64),
+        ("act", ctypes.c_int32),
+        ("reserved", ctypes.c_int32),
+    ]
+
+
+class LayerNormArgs(ctypes.Structure):
+    _fields_ = [
+        ("x", ctypes.c_void_p),
+        ("out", ctypes.c_void_p),
+        ("m", ctypes.c_int64),
+        ("c", ctypes.c_int64),
+        ("ldx", ctypes.c_int64),
+        ("ldo", ctypes.c_int64),
+        ("eps", ctypes.c_float),
+        ("reserved", ctypes.c_int32),
+    ]
+
+
+# Every function the header declares, with its ctypes signature.
+EXPORTS = {
+    "strata_hip_na3d_fwd": ([ctypes.POINTER(Na3dArgs), ctypes.c_void_p], ctypes.c_int),
+    "strata_hip_rope_qkv_pack": ([ctypes.POINTER(RopePackArgs), ctypes.c_void_p], ctypes.c_int),
+    "strata_hip_gemm_bias_act": ([ctypes.POINTER(GemmArgs), ctypes.c_void_p], ctypes.c_int),
+    "strata_hip_layer_norm": ([ctypes.POINTER(LayerNormArgs), ctypes.c_void_p], ctypes.c_int),
+    "strata_hip_last_error": ([], ctypes.c_char_p),
+    "strata_hip_abi_version": ([], ctypes.c_int),
+}
+
+_lock = threading.Lock()
+_lib: ctypes.CDLL | None = None
+
+
+class StrataHipError(RuntimeError):
+    """Raised when the HIP library rejects a call or a launch fails."""
+
+    def __init__(self, fn: str, code: int, msg: str):
+        super().__init__(f"{fn} failed ({code}): {msg}")
+        self.code = code
+
+
+def load() -> ctypes.CDLL:
+    """Load the library (once).  Raises if it has not been built."""
+    global _lib
+    if _lib is not None:
+        return _lib
+    with _lock:
+        if _lib is not None:
+            return _lib
+        import torch  # noqa: F401  (bind to torch's HIP runtime first)
+
+        if not LIB_PATH.exists():
+            raise RuntimeError(
+                f"{LIB_PATH} is not built; run `python -c 'import __graft_entry__ as g; g.build()'` "
+                "or `python -m strata_amd._build`"
+            )
+        lib = ctypes.CDLL(str(LIB_PATH))
+        for name, (argtypes, restype) in EXPORTS.items():
+            fn = getattr(lib, name)
+            fn.argtypes = argtypes
+            fn.restype = restype
+        ver = lib.strata_hip_abi_version()
+        if ver != ABI_VERSION:
+            raise RuntimeError(f"{LIB_PATH}: ABI version {ver}, expected {ABI_VERSION}; rebuild it")
+        _lib = lib
+        return lib
+
+
+def call(name: str, args: ctypes.Structure, stream: int) -> None:
+    lib = load()
+    rc = getattr(lib, name)(ctypes.byref(args), ctypes.c_void_p(stream))
+    if rc != OK:
+        msg = lib.strata_hip_last_error().decode(errors="replace")
+        if rc == EINVAL:
+            raise ValueError(f"{name}: {msg}")
+        raise StrataHipError(name, rc, msg)

@@ -1,0 +1,82 @@
+// Non-affine LayerNorm over the channel dimension, bf16 in/out, fp32 stats.
+// One wave per row; each lane keeps its 16-byte runs of the row in registers
+// (rows up to 4096 channels) so the row is read from HBM once.
+#include "common.h"
+
+namespace strata {
+
+constexpr int LN_MAX_RUNS = 8;  // 8 runs x 8 elements x 64 lanes = 4096 channels
+
+__device__ __forceinline__ float wave_sum(float v) {
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o);
+  return v;
+}
+
+__global__ __launch_bounds__(256) void layer_norm_kernel(const bf16* __restrict__ x, bf16* __restrict__ out, int64_t M,
+                                                         int C, int64_t ldx, int64_t ldo, float eps) {
+  const int64_t row = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (row >= M) return;
+  const int lane = threadIdx.x & 63;
+  const int runs = C / 8;
+  const bf16* xr = x + row * ldx;
+  u32x4 v[LN_MAX_RUNS];
+  float s = 0.f;
+#pragma unroll
+  for (int r = 0; r < LN_MAX_RUNS; ++r) {
+    const int run = lane + 64 * r;
+    v[r] = (u32x4){0u, 0u, 0u, 0u};
+    if (run < runs) {
+      v[r] = *(const u32x4*)(xr + 8 * run);
+#pragma unroll
+      for (int w = 0; w < 4; ++w) s += bf16_lo(v[r][w]) + bf16_hi(v[r][w]);
+    }
+  }
+  const float mean = wave_sum(s) / C;
+  float q = 0.f;
+#pragma unroll
+  for (int r = 0; r < LN_MAX_RUNS; ++r) {
+    if (lane + 64 * r < runs) {
+#pragma unroll
+      for (int w = 0; w < 4; ++w) {
+        const float a = bf16_lo(v[r][w]) - mean, b = bf16_hi(v[r][w]) - mean;
+        q = fmaf(a, a, q);
+        q = fmaf(b, b, q);
+      }
+    }
+  }
+  const float rstd = rsqrtf(wave_sum(q) / C + eps);
+  bf16* orow = out + row * ldo;
+#pragma unroll
+  for (int r = 0; r < LN_MAX_RUNS; ++r) {
+    const int run = lane + 64 * r;
+    if (run < runs) {
+      u32x4 o;
+#pragma unroll
+      for (int w = 0; w < 4; ++w)
+        o[w] = pack_bf16x2((bf16_lo(v[r][w]) - mean) * rstd, (bf16_hi(v[r][w]) - mean) * rstd);
+      *(u32x4*)(orow + 8 * run) = o;
+    }
+  }
+}
+
+}  // namespace strata
+
+using namespace strata;
+
+extern "C" int strata_hip_layer_norm(const strata_hip_layer_norm_args* a, void* stream) {
+  if (!a) return fail(STRATA_HIP_EINVAL, "layer_norm: null args");
+  if (a->m < 0 || a->c <= 0) return fail(STRATA_HIP_EINVAL, "layer_norm: bad m/c");
+  if (a->m == 0) return STRATA_HIP_OK;
+  if (!a->x || !a->out) return fail(STRATA_HIP_EINVAL, "layer_norm: null pointer");
+  if (a->c % 8 || a->c > 8 * 64 * LN_MAX_RUNS)
+    return fail(STRATA_HIP_EUNSUPPORTED, "layer_norm: channels must be a multiple of 8 and at most 4096");
+  if (a->ldx < a->c || a->ldo < a->c || a->ldx % 8 || a->ldo % 8 || ((uintptr_t)a->x & 15) || ((uintptr_t)a->out & 15))
+    return fail(STRATA_HIP_EINVAL, "layer_norm: rows must be 16-byte aligned with strides >= c");
+  if (!(a->eps >= 0.f)) return fail(STRATA_HIP_EINVAL, "layer_norm: eps must be non-negative");
+  const int64_t blocks = (a->m + 3) / 4;
+  if (blocks > 0x7fffffff) return fail(STRATA_HIP_EUNSUPPORTED, "layer_norm: too many rows");
+  hipLaunchKernelGGL(layer_norm_kernel, dim3((unsigned)blocks), dim3(256), 0, (hipStream_t)stream, (const bf16*)a->x,
+                     (bf16*)a->out, a->m, (int)a->c, a->ldx, a->ldo, a->eps);
+  return check_launch("layer_norm_kernel");
+}

@@ -1,0 +1,167 @@
+// Stereographic-RoPE + QKV pack for gfx950 (bandwidth-bound).
+//
+// Reads the attn.qkv GEMM output [M, (3, H, D)] and the per-token cos/sin
+// tables, rotates the channel pairs of q and k, copies v, and writes three
+// heads-last [M, H, D] tensors.  Each thread handles one 16-byte run of
+// pairs of one (token, head): 8 pairs for the half layout (two 16-byte runs
+// D/2 apart), 4 pairs for the interleaved layout (one 16-byte run).
+#include "common.h"
+
+namespace strata {
+
+struct RopeParams {
+  const bf16* qkv;
+  const float* cos;
+  const float* sin;
+  bf16* q;
+  bf16* k;
+  bf16* v;
+  int64_t M;
+  int Z, Y, X, Zt, H, D;
+  int64_t ld;
+};
+
+__device__ __forceinline__ int64_t table_row(const RopeParams& p, int64_t tok) {
+  const int64_t x = tok % p.X;
+  int64_t r = tok / p.X;
+  const int64_t y = r % p.Y;
+  r /= p.Y;
+  const int64_t z = r % p.Z;
+  const int64_t b = r / p.Z;
+  const int64_t zt = p.Zt == 1 ? 0 : z;
+  return ((b * p.Zt + zt) * p.Y + y) * p.X + x;
+}
+
+__device__ __forceinline__ void rot8(const u32x4& a, const u32x4& b, const float* c, const float* s, u32x4& oa,
+                                     u32x4& ob) {
+#pragma unroll
+  for (int w = 0; w < 4; ++w) {
+    const float a0 = bf16_lo(a[w]), a1 = bf16_hi(a[w]);
+    const float b0 = bf16_lo(b[w]), b1 = bf16_hi(b[w]);
+    const float c0 = c[2 * w], c1 = c[2 * w + 1], s0 = s[2 * w], s1 = s[2 * w + 1];
+    oa[w] = pack_bf16x2(a0 * c0 - b0 * s0, a1 * c1 - b1 * s1);
+    ob[w] = pack_bf16x2(a0 * s0 + b0 * c0, a1 * s1 + b1 * c1);
+  }
+}
+
+// Half layout: pair p = (d = p, d = p + D/2).
+__global__ __launch_bounds__(256) void rope_pack_half_kernel(RopeParams p, int64_t total) {
+  const int64_t idx = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (idx >= total) return;
+  const int cph = p.D / 16;
+  const int c = (int)(idx % cph);
+  const int64_t th = idx / cph;
+  const int h = (int)(th % p.H);
+  const int64_t tok = th / p.H;
+  const int half = p.D / 2;
+  const int64_t C = (int64_t)p.H * p.D;
+
+  const bf16* src = p.qkv + tok * p.ld + (int64_t)h * p.D + 8 * c;
+  const int64_t trow = table_row(p, tok) * half + 8 * c;
+  float cs[8], sn[8];
+  *(f32x4*)&cs[0] = *(const f32x4*)(p.cos + trow);
+  *(f32x4*)&cs[4] = *(const f32x4*)(p.cos + trow + 4);
+  *(f32x4*)&sn[0] = *(const f32x4*)(p.sin + trow);
+  *(f32x4*)&sn[4] = *(const f32x4*)(p.sin + trow + 4);
+
+  const int64_t dst = tok * C + (int64_t)h * p.D + 8 * c;
+  {
+    const u32x4 a = *(const u32x4*)(src), b = *(const u32x4*)(src + half);
+    u32x4 oa, ob;
+    rot8(a, b, cs, sn, oa, ob);
+    *(u32x4*)(p.q + dst) = oa;
+    *(u32x4*)(p.q + dst + half) = ob;
+  }
+  {
+    const u32x4 a = *(const u32x4*)(src + C), b = *(const u32x4*)(src + C + half);
+    u32x4 oa, ob;
+    rot8(a, b, cs, sn, oa, ob);
+    *(u32x4*)(p.k + dst) = oa;
+    *(u32x4*)(p.k + dst + half) = ob;
+  }
+  *(u32x4*)(p.v + dst) = *(const u32x4*)(src + 2 * C);
+  *(u32x4*)(p.v + dst + half) = *(const u32x4*)(src + 2 * C + half);
+}
+
+// Interleaved layout: pair p = (d = 2p, d = 2p + 1).
+__device__ __forceinline__ u32x4 rot_inter(const u32x4& a, const float* c, const float* s) {
+  u32x4 o;
+#pragma unroll
+  for (int w = 0; w < 4; ++w) {
+    const float x0 = bf16_lo(a[w]), x1 = bf16_hi(a[w]);
+    o[w] = pack_bf16x2(x0 * c[w] - x1 * s[w], x0 * s[w] + x1 * c[w]);
+  }
+  return o;
+}
+
+__global__ __launch_bounds__(256) void rope_pack_inter_kernel(RopeParams p, int64_t total) {
+  const int64_t idx = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (idx >= total) return;
+  const int cph = p.D / 8;
+  const int c = (int)(idx % cph);
+  const int64_t th = idx / cph;
+  const int h = (int)(th % p.H);
+  const int64_t tok = th / p.H;
+  const int half = p.D / 2;
+  const int64_t C = (int64_t)p.H * p.D;
+
+  const bf16* src = p.qkv + tok * p.ld + (int64_t)h * p.D + 8 * c;
+  const int64_t trow = table_row(p, tok) * half + 4 * c;
+  float cs[4], sn[4];
+  *(f32x4*)&cs[0] = *(const f32x4*)(p.cos + trow);
+  *(f32x4*)&sn[0] = *(const f32x4*)(p.sin + trow);
+  const int64_t dst = tok * C + (int64_t)h * p.D + 8 * c;
+  *(u32x4*)(p.q + dst) = rot_inter(*(const u32x4*)(src), cs, sn);
+  *(u32x4*)(p.k + dst) = rot_inter(*(const u32x4*)(src + C), cs, sn);
+  *(u32x4*)(p.v + dst) = *(const u32x4*)(src + 2 * C);
+}
+
+}  // namespace strata
+
+using namespace strata;
+
+extern "C" int strata_hip_rope_qkv_pack(const strata_hip_rope_pack_args* a, void* stream) {
+  if (!a) return fail(STRATA_HIP_EINVAL, "rope_qkv_pack: null args");
+  if (!a->qkv || !a->cos || !a->sin || !a->q || !a->k || !a->v)
+    return fail(STRATA_HIP_EINVAL, "rope_qkv_pack: null pointer");
+  if (a->batch < 0 || a->grid[0] <= 0 || a->grid[1] <= 0 || a->grid[2] <= 0 || a->heads <= 0)
+    return fail(STRATA_HIP_EINVAL, "rope_qkv_pack: bad batch/grid/heads");
+  if (a->table_z != 1 && a->table_z != a->grid[0])
+    return fail(STRATA_HIP_EINVAL, "rope_qkv_pack: table_z must be 1 or Z");
+  if (a->layout != STRATA_HIP_ROPE_HALF && a->layout != STRATA_HIP_ROPE_INTERLEAVED)
+    return fail(STRATA_HIP_EINVAL, "rope_qkv_pack: bad layout");
+  if (a->layout == STRATA_HIP_ROPE_HALF ? (a->head_dim % 16) : (a->head_dim % 8))
+    return fail(STRATA_HIP_EINVAL, "rope_qkv_pack: head_dim must be a multiple of 16 (half) or 8 (interleaved)");
+  const int64_t C = (int64_t)a->heads * a->head_dim;
+  if (a->qkv_row_stride < 3 * C || a->qkv_row_stride % 8)
+    return fail(STRATA_HIP_EINVAL, "rope_qkv_pack: qkv row stride must be >= 3*H*D and a multiple of 8");
+  const void* ptrs[6] = {a->qkv, a->cos, a->sin, a->q, a->k, a->v};
+  for (int i = 0; i < 6; ++i)
+    if ((uintptr_t)ptrs[i] & 15) return fail(STRATA_HIP_EINVAL, "rope_qkv_pack: pointers must be 16-byte aligned");
+  RopeParams p;
+  p.qkv = (const bf16*)a->qkv;
+  p.cos = a->cos;
+  p.sin = a->sin;
+  p.q = (bf16*)a->q;
+  p.k = (bf16*)a->k;
+  p.v = (bf16*)a->v;
+  p.Z = a->grid[0];
+  p.Y = a->grid[1];
+  p.X = a->grid[2];
+  p.Zt = a->table_z;
+  p.H = a->heads;
+  p.D = a->head_dim;
+  p.ld = a->qkv_row_stride;
+  p.M = (int64_t)a->batch * p.Z * p.Y * p.X;
+  const int cph = a->layout == STRATA_HIP_ROPE_HALF ? p.D / 16 : p.D / 8;
+  const int64_t total = p.M * p.H * cph;
+  if (total == 0) return STRATA_HIP_OK;
+  const int threads = 256;
+  const int64_t blocks = (total + threads - 1) / threads;
+  if (blocks > 0x7fffffff) return fail(STRATA_HIP_EUNSUPPORTED, "rope_qkv_pack: too many tokens");
+  if (a->layout == STRATA_HIP_ROPE_HALF)
+    hipLaunchKernelGGL(rope_pack_half_kernel, dim3((unsigned)blocks), dim3(threads), 0, (hipStream_t)stream, p, total);
+  else
+    hipLaunchKernelGGL(rope_pack_inter_kernel, dim3((unsigned)blocks), dim3(threads), 0, (hipStream_t)stream, p, total);
+  return check_launch("rope_pack_kernel");
+}

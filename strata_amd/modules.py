@@ -1,0 +1,180 @@
+"""Drop-in modules for the Strata transformer block, backed by ``torch.ops.strata_hip``.
+
+State-dict keys and parameter registration order match the reference's
+manifests (tests/regression_data/sweep1_...param_order.txt:3-12, pinned by
+tests/test_param_order.py:87-119): per block ``attn.qkv.{weight,bias}``,
+``attn.proj.{weight,bias}``, optional ``attn.gate_proj.{weight,bias}``,
+``mlp.layers.0.{weight,bias}``, ``mlp.layers.2.{weight,bias}``; the two
+LayerNorms are non-affine and carry no parameters.
+
+The modules run bf16 weights and activations on one GPU (fp32 accumulation
+inside the kernels).  They never fall back to eager PyTorch math: CPU tensors
+or a missing HIP library raise.
+"""
+
+from __future__ import annotations
+
+from typing import Optional, Sequence
+
+import torch
+import torch.nn as nn
+from torch import Tensor
+
+from . import _lib, ops  # noqa: F401  (ops registers torch.ops.strata_hip)
+
+_ACT = {"tanh": _lib.ACT_GELU_TANH, "none": _lib.ACT_GELU_ERF}
+
+
+def _triple(v) -> list[int]:
+    return [v, v, v] if isinstance(v, int) else [int(x) for x in v]
+
+
+class GemmGeluMlp(nn.Module):
+    """``layers = Sequential(fc1, GELU, fc2)`` computed as two fused GEMM launches.
+
+    Drop-in for physicsnemo's ``Mlp`` (layer indices 0/2 per
+    screamcast/checkpoint_compat.py:243-249; GELU(tanh) per
+    screamcast/strata_wrappers.py:76-100): fc1 + bias + GELU is one launch,
+    fc2 + bias (+ the block's residual) another.
+    """
+
+    def __init__(self, in_features: int, hidden_features: int, out_features: Optional[int] = None,
+                 bias: bool = True, approximate: str = "tanh"):
+        super().__init__()
+        out_features = out_features or in_features
+        self.layers = nn.Sequential(
+            nn.Linear(in_features, hidden_features, bias=bias),
+            nn.GELU(approximate=approximate),
+            nn.Linear(hidden_features, out_features, bias=bias),
+        )
+
+    @classmethod
+    def from_mlp(cls, mlp: nn.Module) -> "GemmGeluMlp":
+        """Wrap an existing ``Mlp``-shaped module, sharing its Linear layers."""
+        fc1, act, fc2 = mlp.layers
+        if not (isinstance(fc1, nn.Linear) and isinstance(act, nn.GELU) and isinstance(fc2, nn.Linear)):
+            raise TypeError("expected layers = Sequential(Linear, GELU, Linear)")
+        new = cls.__new__(cls)
+        nn.Module.__init__(new)
+        new.layers = mlp.layers
+        return new
+
+    def forward(self, x: Tensor, residual: Optional[Tensor] = None) -> Tensor:
+        fc1, act, fc2 = self.layers
+        h = ops.gemm_bias_act(x, fc1.weight, fc1.bias, None, _ACT[act.approximate])
+        return ops.gemm_bias_act(h, fc2.weight, fc2.bias, residual, _lib.ACT_NONE)
+
+
+class FusedNA3DAttention(nn.Module):
+    """qkv GEMM -> RoPE + QKV pack -> NA3D -> (gate) -> proj GEMM (+ residual).
+
+    Drop-in for the physicsnemo Strata attention's ``qkv -> split -> RoPE ->
+    natten.na3d -> proj`` chain (keys attn.qkv / attn.proj / attn.gate_proj;
+    gate applied as ``a * sigmoid(gate_proj(x))`` before proj).
+    """
+
+    def __init__(self, dim: int, num_heads: int, kernel_size, dilation=1, qkv_bias: bool = True,
+                 gated: bool = False, rope_layout: int = _lib.ROPE_HALF, scale: Optional[float] = None):
+        super().__init__()
+        if dim % num_heads:
+            raise ValueError("dim must be divisible by num_heads")
+        self.dim, self.num_heads = dim, num_heads
+        self.head_dim = dim // num_heads
+        self.kernel_size = _triple(kernel_size)
+        self.dilation = _triple(dilation)
+        self.rope_layout = rope_layout
+        self.scale = scale
+        self.qkv = nn.Linear(dim, 3 * dim, bias=qkv_bias)
+        self.proj = nn.Linear(dim, dim)
+        if gated:
+            self.gate_proj = nn.Linear(dim, dim)
+        else:
+            self.gate_proj = None
+
+    def attention(self, x: Tensor, rope: Optional[tuple[Tensor, Tensor]] = None) -> Tensor:
+        """Attention output before the projection, ``[B, Z, Y, X, C]``."""
+        B, Z, Y, X, C = x.shape
+        H, D = self.num_heads, self.head_dim
+        qkv = ops.gemm_bias_act(x, self.qkv.weight, self.qkv.bias, None, _lib.ACT_NONE)
+        if rope is not None:
+            q, k, v = ops.rope_qkv_pack(qkv, rope[0], rope[1], H, self.rope_layout)
+        else:
+            qkv6 = qkv.view(B, Z, Y, X, 3, H, D)
+            q, k, v = qkv6[..., 0, :, :], qkv6[..., 1, :, :], qkv6[..., 2, :, :]
+        a = ops.na3d_fwd(q, k, v, self.kernel_size, self.dilation, self.scale, [0, 0, 0], [Z, Y, X])
+        a = a.view(B, Z, Y, X, C)
+        if self.gate_proj is not None:
+            gate = ops.gemm_bias_act(x, self.gate_proj.weight, self.gate_proj.bias, None, _lib.ACT_NONE)
+            a = a * torch.sigmoid(gate)
+        return a
+
+    def forward(self, x: Tensor, rope: Optional[tuple[Tensor, Tensor]] = None,
+                residual: Optional[Tensor] = None) -> Tensor:
+        a = self.attention(x, rope)
+        return ops.gemm_bias_act(a, self.proj.weight, self.proj.bias, residual, _lib.ACT_NONE)
+
+
+class StrataBlock(nn.Module):
+    """Pre-norm Strata transformer block (the configs[3] block).
+
+    ``x = x + proj(na3d(rope(qkv(LN(x)))))``; ``x = x + fc2(GELU(fc1(LN(x))))``
+    with non-affine LayerNorms (eps 1e-6).  Stand-in for physicsnemo's
+    ``StrataTransformer3DBlock`` (tests/test_dit_3d_pixel.py:109-111) with the
+    same parameter names and order.
+    """
+
+    def __init__(self, dim: int, num_heads: int, kernel_size, mlp_ratio: float = 4.0, dilation=1,
+                 qkv_bias: bool = True, gated: bool = False, eps: float = 1e-6):
+        super().__init__()
+        self.eps = eps
+        self.attn = FusedNA3DAttention(dim, num_heads, kernel_size, dilation, qkv_bias, gated)
+        self.mlp = GemmGeluMlp(dim, int(dim * mlp_ratio))
+
+    def forward(self, x: Tensor, rope: Optional[tuple[Tensor, Tensor]] = None) -> Tensor:
+        h = ops.layer_norm(x, self.eps)
+        x = self.attn(h, rope, residual=x)
+        h = ops.layer_norm(x, self.eps)
+        return self.mlp(h, residual=x)
+
+
+def swap_mlps(model: nn.Module) -> int:
+    """Replace every ``Mlp``-shaped child (``layers = Sequential(Linear, GELU, Linear)``)
+    by a :class:`GemmGeluMlp` sharing its parameters, in the pattern of the
+    reference's ``_use_tanh_gelu`` (screamcast/strata_wrappers.py:76-100).
+    Keys and parameter order are unchanged.  Returns the number swapped."""
+    n = 0
+    for parent in list(model.modules()):
+        for name, child in list(parent.named_children()):
+            if isinstance(child, GemmGeluMlp):
+                continue
+            layers = getattr(child, "layers", None)
+            if (
+                isinstance(layers, nn.Sequential)
+                and len(layers) == 3
+                and isinstance(layers[0], nn.Linear)
+                and isinstance(layers[1], nn.GELU)
+                and isinstance(layers[2], nn.Linear)
+            ):
+                setattr(parent, name, GemmGeluMlp.from_mlp(child))
+                n += 1
+    return n
+
+
+def init_xavier_(module: nn.Module, generator: torch.Generator) -> None:
+    """Xavier-uniform weights, zero biases (DiT-style init), from one CPU generator."""
+    for m in module.modules():
+        if isinstance(m, nn.Linear):
+            fan_out, fan_in = m.weight.shape
+            bound = (6.0 / (fan_in + fan_out)) ** 0.5
+            with torch.no_grad():
+                w = torch.rand(m.weight.shape, generator=generator, dtype=torch.float32) * (2 * bound) - bound
+                m.weight.copy_(w)
+                if m.bias is not None:
+                    m.bias.zero_()
+
+
+def block_param_names(gated: bool = False) -> Sequence[str]:
+    names = ["attn.qkv.weight", "attn.qkv.bias", "attn.proj.weight", "attn.proj.bias"]
+    if gated:
+        names += ["attn.gate_proj.weight", "attn.gate_proj.bias"]
+    return names + ["mlp.layers.0.weight", "mlp.layers.0.bias", "mlp.layers.2.weight", "mlp.layers.2.bias"]

@@ -1,0 +1,303 @@
+"""PyTorch-ROCm custom ops ``torch.ops.strata_hip.*`` over the C-ABI HIP library.
+
+Each op validates its tensors, allocates the output through torch's caching
+allocator, and enqueues the kernel on torch's current stream of the input's
+device.  There is no CPU or eager fallback: CPU tensors are rejected and a
+missing library raises.  Every op has a fake (meta) implementation so that
+``torch.compile`` traces through it, and an autograd formula that raises,
+because the kernels are forward-only (inference).
+"""
+
+from __future__ import annotations
+
+import math
+from typing import Optional, Sequence
+
+import torch
+from torch import Tensor
+
+from . import _lib
+
+__all__ = ["na3d_fwd", "rope_qkv_pack", "gemm_bias_act", "layer_norm"]
+
+
+def _stream(t: Tensor) -> int:
+    return torch.cuda.current_stream(t.device).cuda_stream
+
+
+def _require_gpu(name: str, *ts: Optional[Tensor]) -> torch.device:
+    dev = None
+    for t in ts:
+        if t is None:
+            continue
+        if not t.is_cuda:
+            raise ValueError(f"{name}: expected GPU tensors, got a tensor on {t.device}")
+        if dev is None:
+            dev = t.device
+        elif t.device != dev:
+            raise ValueError(f"{name}: tensors on different devices ({dev} and {t.device})")
+    return dev
+
+
+def _dtype_code(name: str, t: Tensor) -> int:
+    if t.dtype == torch.bfloat16:
+        return _lib.BF16
+    if t.dtype == torch.float32:
+        return _lib.F32
+    raise ValueError(f"{name}: dtype must be bfloat16 or float32, got {t.dtype}")
+
+
+def _triple(name: str, v: Sequence[int] | int) -> list[int]:
+    if isinstance(v, int):
+        return [v, v, v]
+    v = [int(x) for x in v]
+    if len(v) != 3:
+        raise ValueError(f"{name} must have 3 entries, got {v}")
+    return v
+
+
+def _token_strides(name: str, t: Tensor) -> list[int]:
+    if t.dim() != 6:
+        raise ValueError(f"{name}: expected a heads-last [B, Z, Y, X, H, D] tensor, got shape {tuple(t.shape)}")
+    if t.stride(-1) != 1:
+        raise ValueError(f"{name}: the head_dim axis must be contiguous (stride 1)")
+    return [t.stride(i) for i in range(5)]
+
+
+def _no_backward(op_name: str):
+    def backward(ctx, *grads):
+        raise RuntimeError(f"{op_name} is forward-only (inference kernels); no backward is implemented")
+
+    return backward
+
+
+# ---------------------------------------------------------------------------
+# NA3D
+# ---------------------------------------------------------------------------
+@torch.library.custom_op("strata_hip::na3d_fwd", mutates_args=())
+def na3d_fwd(
+    q: Tensor,
+    k: Tensor,
+    v: Tensor,
+    kernel: Sequence[int],
+    dilation: Sequence[int],
+    scale: Optional[float],
+    q_origin: Sequence[int],
+    q_extent: Sequence[int],
+) -> Tensor:
+    """Neighbourhood attention over a clamped 3D window (NATTEN ``na3d`` semantics).
+
+    q, k, v: heads-last ``[B, Z, Y, X, H, D]`` on one GPU, bf16 or fp32.
+    Only queries in the box ``[q_origin, q_origin + q_extent)`` are computed;
+    the result has shape ``[B, *q_extent, H, D]`` and equals
+    ``natten.na3d(q, k, v, kernel, dilation=dilation, scale=scale)`` cropped to
+    the box.  Replaces NATTEN 0.21.5 ``na3d`` (pins docker/build_natten.sh:21,
+    Makefile:11; call routed by screamcast/config.py:99 -> train.py:143 ->
+    screamcast/strata_wrappers.py:331,490,582).
+    """
+    name = "na3d_fwd"
+    _require_gpu(name, q, k, v)
+    if not (q.shape == k.shape == v.shape):
+        raise ValueError(f"{name}: q, k, v must share one shape, got {tuple(q.shape)}, {tuple(k.shape)}, {tuple(v.shape)}")
+    if not (q.dtype == k.dtype == v.dtype):
+        raise ValueError(f"{name}: q, k, v must share one dtype")
+    dt = _dtype_code(name, q)
+    qs, ks, vs = _token_strides(name, q), _token_strides(name, k), _token_strides(name, v)
+    B, Z, Y, X, H, D = q.shape
+    kernel, dilation = _triple("kernel", kernel), _triple("dilation", dilation)
+    q_origin, q_extent = _triple("q_origin", q_origin), _triple("q_extent", q_extent)
+    out = torch.empty((B, *q_extent, H, D), dtype=q.dtype, device=q.device)
+    if out.numel() == 0:
+        return out
+    a = _lib.Na3dArgs()
+    a.q, a.k, a.v, a.out = q.data_ptr(), k.data_ptr(), v.data_ptr(), out.data_ptr()
+    a.dtype = dt
+    a.batch, a.heads, a.head_dim = B, H, D
+    a.grid[:] = [Z, Y, X]
+    a.q_origin[:] = q_origin
+    a.q_extent[:] = q_extent
+    a.kernel[:] = kernel
+    a.dilation[:] = dilation
+    a.scale = float(D**-0.5 if scale is None else scale)
+    a.q_stride[:] = qs
+    a.k_stride[:] = ks
+    a.v_stride[:] = vs
+    a.o_stride[:] = [out.stride(i) for i in range(5)]
+    with torch.cuda.device(q.device):
+        _lib.call("strata_hip_na3d_fwd", a, _stream(q))
+    return out
+
+
+@na3d_fwd.register_fake
+def _(q, k, v, kernel, dilation, scale, q_origin, q_extent):
+    B, H, D = q.shape[0], q.shape[4], q.shape[5]
+    return q.new_empty((B, *[int(e) for e in q_extent], H, D))
+
+
+na3d_fwd.register_autograd(_no_backward("strata_hip::na3d_fwd"))
+
+
+# ---------------------------------------------------------------------------
+# RoPE + QKV pack
+# ---------------------------------------------------------------------------
+@torch.library.custom_op("strata_hip::rope_qkv_pack", mutates_args=())
+def rope_qkv_pack(qkv: Tensor, cos: Tensor, sin: Tensor, heads: int, rope_layout: int) -> tuple[Tensor, Tensor, Tensor]:
+    """Split ``attn.qkv``'s output into heads-last q, k, v and rotate q, k.
+
+    qkv: ``[B, Z, Y, X, 3*H*D]`` bf16 (column order (3, H, D), last dim
+    contiguous, rows possibly strided).  cos, sin: fp32 ``[B, Zt, Y, X, D/2]``
+    with Zt in {1, Z}.  rope_layout: 0 = half split (pair p = (p, p + D/2)),
+    1 = interleaved (pair p = (2p, 2p+1)).  Returns q, k, v ``[B, Z, Y, X, H, D]``.
+    """
+    name = "rope_qkv_pack"
+    _require_gpu(name, qkv, cos, sin)
+    if qkv.dtype != torch.bfloat16:
+        raise ValueError(f"{name}: qkv must be bfloat16")
+    if cos.dtype != torch.float32 or sin.dtype != torch.float32:
+        raise ValueError(f"{name}: cos/sin tables must be float32")
+    if qkv.dim() != 5:
+        raise ValueError(f"{name}: qkv must be [B, Z, Y, X, 3C], got {tuple(qkv.shape)}")
+    B, Z, Y, X, C3 = qkv.shape
+    if C3 % (3 * heads):
+        raise ValueError(f"{name}: last dim {C3} is not divisible by 3*heads")
+    D = C3 // (3 * heads)
+    if cos.shape != sin.shape or cos.dim() != 5 or tuple(cos.shape[2:]) != (Y, X, D // 2) or cos.shape[0] != B:
+        raise ValueError(f"{name}: cos/sin must be [B, Zt, Y, X, D/2] = [{B}, 1|{Z}, {Y}, {X}, {D // 2}], got {tuple(cos.shape)}")
+    # rows of qkv must be evenly strided over the flattened token index
+    flat = qkv.reshape(B * Z * Y * X, C3) if not qkv.is_contiguous() else qkv.view(-1, C3)
+    if flat.stride(1) != 1:
+        raise ValueError(f"{name}: the last dim of qkv must be contiguous")
+    cos_c, sin_c = cos.contiguous(), sin.contiguous()
+    shape = (B, Z, Y, X, heads, D)
+    q = torch.empty(shape, dtype=qkv.dtype, device=qkv.device)
+    k = torch.empty_like(q)
+    v = torch.empty_like(q)
+    if q.numel() == 0:
+        return q, k, v
+    a = _lib.RopePackArgs()
+    a.qkv, a.cos, a.sin = flat.data_ptr(), cos_c.data_ptr(), sin_c.data_ptr()
+    a.q, a.k, a.v = q.data_ptr(), k.data_ptr(), v.data_ptr()
+    a.batch = B
+    a.grid[:] = [Z, Y, X]
+    a.table_z = cos.shape[1]
+    a.heads, a.head_dim, a.layout = heads, D, int(rope_layout)
+    a.qkv_row_stride = flat.stride(0)
+    with torch.cuda.device(qkv.device):
+        _lib.call("strata_hip_rope_qkv_pack", a, _stream(qkv))
+    return q, k, v
+
+
+@rope_qkv_pack.register_fake
+def _(qkv, cos, sin, heads, rope_layout):
+    B, Z, Y, X, C3 = qkv.shape
+    D = C3 // (3 * heads)
+    shape = (B, Z, Y, X, heads, D)
+    return qkv.new_empty(shape), qkv.new_empty(shape), qkv.new_empty(shape)
+
+
+rope_qkv_pack.register_autograd(_no_backward("strata_hip::rope_qkv_pack"))
+
+
+# ---------------------------------------------------------------------------
+# GEMM + bias + activation + residual
+# ---------------------------------------------------------------------------
+ACTS = {"none": _lib.ACT_NONE, "gelu_tanh": _lib.ACT_GELU_TANH, "gelu": _lib.ACT_GELU_ERF}
+
+
+def _rows(name: str, t: Tensor, what: str) -> Tensor:
+    """View t as a 2D [rows, cols] matrix with a contiguous last dim (copy if needed)."""
+    t2 = t.reshape(-1, t.shape[-1])
+    if t2.stride(-1) != 1 or (t2.shape[0] > 1 and t2.stride(0) % 8) or t2.data_ptr() % 16:
+        t2 = t2.contiguous()
+    return t2
+
+
+@torch.library.custom_op("strata_hip::gemm_bias_act", mutates_args=())
+def gemm_bias_act(x: Tensor, w: Tensor, bias: Optional[Tensor], residual: Optional[Tensor], act: int) -> Tensor:
+    """``act(x @ w.T + bias) + residual`` with fp32 accumulation, bf16 in/out.
+
+    x ``[..., K]``, w ``[N, K]`` (nn.Linear layout), bias ``[N]``, residual
+    ``[..., N]``.  act: 0 none, 1 GELU(tanh), 2 GELU(erf).  Replaces
+    nn.Linear (+ nn.GELU) in the block's attn.qkv / attn.proj / Mlp
+    (screamcast/checkpoint_compat.py:243-249, screamcast/strata_wrappers.py:76-100).
+    """
+    name = "gemm_bias_act"
+    _require_gpu(name, x, w, bias, residual)
+    for t, nm in ((x, "x"), (w, "w"), (bias, "bias"), (residual, "residual")):
+        if t is not None and t.dtype != torch.bfloat16:
+            raise ValueError(f"{name}: {nm} must be bfloat16, got {t.dtype}")
+    K = x.shape[-1]
+    if w.dim() != 2 or w.shape[1] != K:
+        raise ValueError(f"{name}: w must be [N, {K}], got {tuple(w.shape)}")
+    N = w.shape[0]
+    if bias is not None and tuple(bias.shape) != (N,):
+        raise ValueError(f"{name}: bias must be [{N}]")
+    out_shape = (*x.shape[:-1], N)
+    if residual is not None and tuple(residual.shape) != out_shape:
+        raise ValueError(f"{name}: residual must have shape {out_shape}, got {tuple(residual.shape)}")
+    x2 = _rows(name, x, "x")
+    w2 = _rows(name, w, "w")
+    b2 = bias.contiguous() if bias is not None else None
+    r2 = _rows(name, residual, "residual") if residual is not None else None
+    out = torch.empty(out_shape, dtype=torch.bfloat16, device=x.device)
+    M = x2.shape[0]
+    if M == 0 or N == 0:
+        return out
+    a = _lib.GemmArgs()
+    a.x, a.w = x2.data_ptr(), w2.data_ptr()
+    a.bias = b2.data_ptr() if b2 is not None else None
+    a.residual = r2.data_ptr() if r2 is not None else None
+    a.out = out.data_ptr()
+    a.m, a.n, a.k = M, N, K
+    a.ldx, a.ldw = x2.stride(0) if M > 1 else K, w2.stride(0) if N > 1 else K
+    a.ldr = (r2.stride(0) if M > 1 else N) if r2 is not None else 0
+    a.ldo = N
+    a.act = int(act)
+    with torch.cuda.device(x.device):
+        _lib.call("strata_hip_gemm_bias_act", a, _stream(x))
+    return out
+
+
+@gemm_bias_act.register_fake
+def _(x, w, bias, residual, act):
+    return x.new_empty((*x.shape[:-1], w.shape[0]))
+
+
+gemm_bias_act.register_autograd(_no_backward("strata_hip::gemm_bias_act"))
+
+
+# ---------------------------------------------------------------------------
+# LayerNorm (non-affine)
+# ---------------------------------------------------------------------------
+@torch.library.custom_op("strata_hip::layer_norm", mutates_args=())
+def layer_norm(x: Tensor, eps: float) -> Tensor:
+    """Non-affine LayerNorm over the last dim, bf16 in/out, fp32 statistics."""
+    name = "layer_norm"
+    _require_gpu(name, x)
+    if x.dtype != torch.bfloat16:
+        raise ValueError(f"{name}: x must be bfloat16")
+    x2 = _rows(name, x, "x")
+    out = torch.empty(x.shape, dtype=x.dtype, device=x.device)
+    if x2.shape[0] == 0:
+        return out
+    a = _lib.LayerNormArgs()
+    a.x, a.out = x2.data_ptr(), out.data_ptr()
+    a.m, a.c = x2.shape[0], x2.shape[1]
+    a.ldx = x2.stride(0) if x2.shape[0] > 1 else x2.shape[1]
+    a.ldo = x2.shape[1]
+    a.eps = float(eps)
+    with torch.cuda.device(x.device):
+        _lib.call("strata_hip_layer_norm", a, _stream(x))
+    return out
+
+
+@layer_norm.register_fake
+def _(x, eps):
+    return torch.empty_like(x)
+
+
+layer_norm.register_autograd(_no_backward("strata_hip::layer_norm"))
+
+
+def default_scale(head_dim: int) -> float:
+    return 1.0 / math.sqrt(head_dim)

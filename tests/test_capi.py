@@ -1,0 +1,130 @@
+"""The C-ABI library: loads, exports what include/strata_hip.h declares, its
+structs match the ctypes mirrors byte for byte, and argument validation
+rejects bad calls before touching the GPU (no GPU needed)."""
+
+import ctypes
+import re
+import shutil
+import subprocess
+
+import pytest
+
+from strata_amd import _lib
+
+from .conftest import ROOT
+
+HEADER = ROOT / "include" / "strata_hip.h"
+STRUCTS = {
+    "strata_hip_na3d_args": _lib.Na3dArgs,
+    "strata_hip_rope_pack_args": _lib.RopePackArgs,
+    "strata_hip_gemm_args": _lib.GemmArgs,
+    "strata_hip_layer_norm_args": _lib.LayerNormArgs,
+}
+
+
+@pytest.fixture(scope="module")
+def lib():
+    if not _lib.LIB_PATH.exists():
+        pytest.fail(f"{_lib.LIB_PATH} not built; run __graft_entry__.build()")
+    return _lib.load()
+
+
+def declared_functions() -> set[str]:
+    text = HEADER.read_text()
+    return set(re.findall(r"^\s*(?:const\s+)?\w+\s*\*?\s*(strata_hip_\w+)\s*\(", text, flags=re.M))
+
+
+def test_exports_every_declared_symbol(lib):
+    names = declared_functions()
+    assert names == set(_lib.EXPORTS), names ^ set(_lib.EXPORTS)
+    for n in names:
+        assert hasattr(lib, n), n
+    assert lib.strata_hip_abi_version() == _lib.ABI_VERSION
+
+
+@pytest.mark.skipif(shutil.which("gcc") is None, reason="gcc not available")
+def test_struct_layout_matches_header(tmp_path):
+    lines = ['#include <stdio.h>', '#include <stddef.h>', f'#include "{HEADER}"', "int main(void) {"]
+    for cname, cls in STRUCTS.items():
+        lines.append(f'printf("{cname} size %zu\\n", sizeof({cname}));')
+        for fname, _ in cls._fields_:
+            lines.append(f'printf("{cname} {fname} %zu\\n", offsetof({cname}, {fname}));')
+    lines.append("return 0; }")
+    src = tmp_path / "layout.c"
+    src.write_text("\n".join(lines))
+    exe = tmp_path / "layout"
+    subprocess.run(["gcc", "-std=c99", str(src), "-o", str(exe)], check=True)
+    out = subprocess.run([str(exe)], check=True, capture_output=True, text=True).stdout.split("\n")
+    got = {}
+    for line in out:
+        if line:
+            s, f, v = line.split()
+            got[(s, f)] = int(v)
+    for cname, cls in STRUCTS.items():
+        assert got[(cname, "size")] == ctypes.sizeof(cls), cname
+        for fname, _ in cls._fields_:
+            assert got[(cname, fname)] == getattr(cls, fname).offset, (cname, fname)
+
+
+def _na3d_args(**over):
+    a = _lib.Na3dArgs()
+    a.q = a.k = a.v = a.out = 0x1000
+    a.dtype = _lib.BF16
+    a.batch, a.heads, a.head_dim = 1, 2, 64
+    a.grid[:] = [4, 8, 8]
+    a.q_origin[:] = [0, 0, 0]
+    a.q_extent[:] = [4, 8, 8]
+    a.kernel[:] = [3, 3, 3]
+    a.dilation[:] = [1, 1, 1]
+    a.scale = 0.125
+    for k, v in over.items():
+        if isinstance(v, list):
+            getattr(a, k)[:] = v
+        else:
+            setattr(a, k, v)
+    return a
+
+
+@pytest.mark.parametrize(
+    "over, msg",
+    [
+        (dict(kernel=[2, 3, 3]), "odd"),
+        (dict(kernel=[5, 3, 3]), "exceeds"),
+        (dict(dilation=[1, 3, 3]), "exceeds"),
+        (dict(dilation=[0, 1, 1]), "dilation"),
+        (dict(q_extent=[4, 9, 8]), "box"),
+        (dict(dtype=7), "dtype"),
+        (dict(q=0), "null"),
+    ],
+)
+def test_na3d_validation_rejects_before_launch(lib, over, msg):
+    a = _na3d_args(**over)
+    rc = lib.strata_hip_na3d_fwd(ctypes.byref(a), None)
+    assert rc == _lib.EINVAL
+    assert msg in lib.strata_hip_last_error().decode()
+
+
+def test_gemm_and_layernorm_validation(lib):
+    g = _lib.GemmArgs()
+    g.x = g.w = g.out = 0x1000
+    g.m, g.n, g.k = 16, 16, 12  # k not a multiple of 8
+    g.ldx = g.ldw = 12
+    g.ldo = 16
+    assert lib.strata_hip_gemm_bias_act(ctypes.byref(g), None) == _lib.EINVAL
+    assert "multiple of 8" in lib.strata_hip_last_error().decode()
+    ln = _lib.LayerNormArgs()
+    ln.x = ln.out = 0x1000
+    ln.m, ln.c, ln.ldx, ln.ldo, ln.eps = 4, 8192, 8192, 8192, 1e-6
+    assert lib.strata_hip_layer_norm(ctypes.byref(ln), None) == _lib.EUNSUPPORTED
+    r = _lib.RopePackArgs()
+    r.qkv = r.cos = r.sin = r.q = r.k = r.v = 0x1000
+    r.batch, r.heads, r.head_dim, r.layout, r.table_z = 1, 2, 64, 0, 3
+    r.grid[:] = [4, 8, 8]
+    r.qkv_row_stride = 384
+    assert lib.strata_hip_rope_qkv_pack(ctypes.byref(r), None) == _lib.EINVAL
+    assert "table_z" in lib.strata_hip_last_error().decode()
+
+
+def test_empty_problem_is_a_no_op(lib):
+    a = _na3d_args(batch=0)
+    assert lib.strata_hip_na3d_fwd(ctypes.byref(a), None) == _lib.OK

@@ -1,0 +1,112 @@
+"""GEMM (+bias/GELU/residual), RoPE+QKV pack and LayerNorm on the GPU vs CPU references."""
+
+import pytest
+import torch
+import torch.nn.functional as F
+
+from oracle import rope as R
+from strata_amd import _lib, ops  # noqa: F401
+from strata_amd import rope as P
+
+from .conftest import rel_l2
+
+pytestmark = pytest.mark.gpu
+
+
+def _randn(shape, g, scale=1.0):
+    return (torch.randn(shape, generator=g) * scale).bfloat16()
+
+
+GEMM_CASES = [
+    # M, N, K, act, bias, residual
+    (256, 256, 64, _lib.ACT_NONE, False, False),
+    (300, 200, 72, _lib.ACT_NONE, True, False),
+    (1000, 384, 1024, _lib.ACT_GELU_TANH, True, False),
+    (513, 1024, 256, _lib.ACT_GELU_ERF, True, True),
+    (128, 96, 80, _lib.ACT_NONE, True, True),
+    (4096, 3072, 1024, _lib.ACT_NONE, True, False),
+]
+
+
+@pytest.mark.parametrize("case", GEMM_CASES, ids=[str(c[:4]) for c in GEMM_CASES])
+def test_gemm_vs_fp64(gpu, case):
+    M, N, K, act, has_b, has_r = case
+    print(f"gemm {case}", flush=True)
+    g = torch.Generator().manual_seed(M + N + K)
+    x = _randn((M, K), g)
+    w = _randn((N, K), g, K**-0.5)
+    b = _randn((N,), g) if has_b else None
+    r = _randn((M, N), g) if has_r else None
+    out = torch.ops.strata_hip.gemm_bias_act(
+        x.to(gpu), w.to(gpu), None if b is None else b.to(gpu), None if r is None else r.to(gpu), act
+    )
+    ref = x.double() @ w.double().T
+    if b is not None:
+        ref = ref + b.double()
+    if act == _lib.ACT_GELU_TANH:
+        ref = F.gelu(ref, approximate="tanh")
+    elif act == _lib.ACT_GELU_ERF:
+        ref = F.gelu(ref)
+    if r is not None:
+        ref = ref + r.double()
+    assert out.shape == (M, N)
+    assert rel_l2(out.float(), ref) <= 1e-2
+
+
+def test_gemm_batched_shape_and_aliasing(gpu):
+    g = torch.Generator().manual_seed(1)
+    x = _randn((2, 3, 5, 64), g).to(gpu)
+    w = _randn((128, 64), g, 0.125).to(gpu)
+    r = _randn((2, 3, 5, 128), g).to(gpu)
+    out = torch.ops.strata_hip.gemm_bias_act(x, w, None, r, 0)
+    ref = x.double() @ w.double().T + r.double()
+    assert out.shape == (2, 3, 5, 128)
+    assert rel_l2(out.float(), ref) <= 1e-2
+
+
+@pytest.mark.parametrize("layout", [_lib.ROPE_HALF, _lib.ROPE_INTERLEAVED])
+@pytest.mark.parametrize("zt", [1, 4])
+def test_rope_pack_vs_oracle(gpu, layout, zt):
+    B, Z, Y, X, H, D = 2, 4, 8, 12, 3, 64
+    g = torch.Generator().manual_seed(7 + layout + zt)
+    qkv = _randn((B, Z, Y, X, 3 * H * D), g)
+    ang = torch.rand(B, zt, Y, X, D // 2, generator=g, dtype=torch.float64) * 20 - 10
+    cos, sin = torch.cos(ang), torch.sin(ang)
+    q, k, v = torch.ops.strata_hip.rope_qkv_pack(qkv.to(gpu), cos.float().to(gpu), sin.float().to(gpu), H, layout)
+    t = qkv.double().view(B, Z, Y, X, 3, H, D)
+    name = "half" if layout == _lib.ROPE_HALF else "interleaved"
+    rq = R.apply_rope(t[..., 0, :, :], cos, sin, name)
+    rk = R.apply_rope(t[..., 1, :, :], cos, sin, name)
+    # bf16 output of an fp32 rotation: within one bf16 rounding of the exact value
+    for got, ref in ((q, rq), (k, rk)):
+        d = (got.double().cpu() - ref).abs()
+        assert (d <= ref.abs() * 2**-8 + 1e-6).all(), d.max()
+    assert torch.equal(v.cpu(), qkv.view(B, Z, Y, X, 3, H, D)[..., 2, :, :])
+
+
+def test_rope_pack_stereographic_tables(gpu):
+    """configs[1]-style tables (64x64 tile, 32 pairs, base 1e4) built by the
+    product helper agree with the float64 oracle and drive the pack kernel."""
+    g = torch.Generator().manual_seed(0)
+    lat, lon = P.synthetic_tile_latlon(2, 64, 64, g)
+    ls = P.default_rope_length_scale(1)
+    cos, sin = P.stereographic_rope_tables(lat.to(gpu), lon.to(gpu), 64, 10000.0, ls)
+    c2, s2 = R.tables(lat, lon, 64, 10000.0, ls)
+    assert (cos.double().cpu() - c2).abs().max() < 1e-5
+    assert (sin.double().cpu() - s2).abs().max() < 1e-5
+
+
+@pytest.mark.parametrize("C", [64, 768, 1024, 4096])
+def test_layer_norm(gpu, C):
+    g = torch.Generator().manual_seed(C)
+    x = (_randn((257, C), g) * 3 + 1).bfloat16()
+    out = torch.ops.strata_hip.layer_norm(x.to(gpu), 1e-6)
+    ref = F.layer_norm(x.double(), (C,), eps=1e-6)
+    assert rel_l2(out.float(), ref) <= 1e-2
+    assert (out.double().cpu() - ref).abs().max() < 0.05
+
+
+def test_ops_reject_cpu_tensors(gpu):
+    x = torch.zeros(4, 64, dtype=torch.bfloat16)
+    with pytest.raises(ValueError, match="GPU"):
+        torch.ops.strata_hip.layer_norm(x, 1e-6)

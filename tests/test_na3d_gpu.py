@@ -1,0 +1,158 @@
+"""NA3D on the GPU through the C-ABI library vs the CPU oracle.
+
+Bars: fp32 max-abs <= 1e-5; bf16 relative L2
+<= 1e-2 against an fp32 oracle evaluated on the same (bf16-rounded) inputs.
+"""
+
+import pytest
+import torch
+
+from oracle import na3d as O
+from strata_amd import ops  # noqa: F401
+from strata_amd.natten import na3d as natten_na3d
+
+from .conftest import rel_l2
+
+pytestmark = pytest.mark.gpu
+
+BF16_TOL = 1e-2
+F32_TOL = 1e-5
+
+
+def _run(q, k, v, kernel, dilation=(1, 1, 1), origin=(0, 0, 0), extent=None, scale=None):
+    extent = list(q.shape[1:4]) if extent is None else list(extent)
+    return torch.ops.strata_hip.na3d_fwd(q, k, v, list(kernel), list(dilation), scale, list(origin), extent)
+
+
+def _rand(shape, seed, dtype, device, scale=None):
+    g = torch.Generator().manual_seed(seed)
+    t = [torch.randn(shape, generator=g) for _ in range(3)]
+    if scale is not None:
+        t = [x * scale for x in t]
+    return [x.to(dtype).to(device) for x in t]
+
+
+def test_goldens_fp32(gpu, na3d_golden):
+    for name, c in na3d_golden.items():
+        q, k, v = (torch.from_numpy(c[t]).to(gpu) for t in "qkv")
+        print(f"golden fp32 {name} {c['shape']} kernel {c['kernel']} dil {c['dilation']}", flush=True)
+        out = _run(q, k, v, c["kernel"], c["dilation"])
+        torch.cuda.synchronize()
+        err = (out.cpu() - torch.from_numpy(c["out"])).abs().max().item()
+        assert err <= F32_TOL, (name, err)
+
+
+def test_goldens_bf16(gpu, na3d_golden):
+    for name, c in na3d_golden.items():
+        q, k, v = (torch.from_numpy(c[t]).bfloat16() for t in "qkv")
+        print(f"golden bf16 {name} {c['shape']} kernel {c['kernel']} dil {c['dilation']}", flush=True)
+        out = _run(q.to(gpu), k.to(gpu), v.to(gpu), c["kernel"], c["dilation"])
+        ref = O.na3d(q, k, v, c["kernel"], c["dilation"], compute_dtype=torch.float64)
+        assert rel_l2(out.float(), ref) <= BF16_TOL, name
+
+
+def test_cfg0_fp32_vs_unfold(gpu):
+    """fp32 [1,4,16,16,4,32], W=(3,5,5), seed 0, vs naive unfold."""
+    g = torch.Generator().manual_seed(0)
+    shape = (1, 4, 16, 16, 4, 32)
+    q, k, v = (torch.randn(shape, generator=g) for _ in range(3))
+    print("cfg0 fp32", flush=True)
+    out = _run(q.to(gpu), k.to(gpu), v.to(gpu), (3, 5, 5)).cpu()
+    ref = O.na3d_unfold(q, k, v, (3, 5, 5), compute_dtype=torch.float64)
+    assert (out.double() - ref).abs().max().item() <= F32_TOL
+
+
+MFMA_CASES = [
+    # shape (B, Z, Y, X, H, D), kernel, dilation, origin, extent
+    ((1, 4, 16, 16, 2, 64), (3, 5, 5), (1, 1, 1), None, None),
+    ((2, 5, 12, 20, 2, 64), (3, 7, 7), (1, 1, 1), None, None),
+    ((1, 4, 20, 24, 2, 64), (3, 13, 13), (1, 1, 1), None, None),
+    ((1, 3, 17, 19, 3, 64), (3, 9, 9), (1, 1, 1), None, None),
+    ((1, 3, 16, 30, 1, 64), (1, 5, 15), (1, 1, 1), None, None),
+    ((1, 2, 8, 16, 1, 64), (1, 1, 1), (1, 1, 1), None, None),
+    ((1, 4, 12, 12, 2, 32), (3, 5, 5), (1, 1, 1), None, None),
+    ((1, 4, 12, 12, 2, 128), (3, 5, 5), (1, 1, 1), None, None),
+    ((1, 6, 14, 18, 2, 64), (3, 3, 5), (2, 2, 3), None, None),
+    ((1, 4, 20, 20, 2, 64), (3, 7, 7), (1, 1, 1), (1, 3, 2), (2, 14, 15)),
+    ((2, 4, 24, 24, 2, 64), (3, 13, 13), (1, 1, 1), (0, 4, 4), (4, 16, 16)),
+    ((1, 3, 7, 9, 2, 64), (3, 7, 9), (1, 1, 1), None, None),  # window spans the y/x grid
+]
+
+
+@pytest.mark.parametrize("case", MFMA_CASES, ids=[f"{c[0]}-k{c[1]}-d{c[2]}-box{c[3]}" for c in MFMA_CASES])
+def test_mfma_vs_oracle(gpu, case):
+    shape, kernel, dil, origin, extent = case
+    origin = (0, 0, 0) if origin is None else origin
+    extent = shape[1:4] if extent is None else extent
+    print(f"mfma case {shape} k{kernel} d{dil} o{origin} e{extent}", flush=True)
+    q, k, v = _rand(shape, 11, torch.bfloat16, gpu)
+    out = _run(q, k, v, kernel, dil, origin, extent)
+    ref = O.na3d(q.cpu(), k.cpu(), v.cpu(), kernel, dil, q_origin=origin, q_extent=extent)
+    err = rel_l2(out.float(), ref)
+    assert err <= BF16_TOL, err
+    assert torch.isfinite(out.float()).all()
+
+
+def test_strided_views_of_packed_qkv(gpu):
+    """q/k/v as views into one [B,Z,Y,X,3,H,D] buffer equal the contiguous result."""
+    B, Z, Y, X, H, D = 1, 4, 12, 16, 4, 64
+    g = torch.Generator().manual_seed(3)
+    qkv = torch.randn(B, Z, Y, X, 3, H, D, generator=g).bfloat16().to(gpu)
+    q, k, v = qkv[..., 0, :, :], qkv[..., 1, :, :], qkv[..., 2, :, :]
+    out_view = _run(q, k, v, (3, 5, 5))
+    out_cont = _run(q.contiguous(), k.contiguous(), v.contiguous(), (3, 5, 5))
+    assert torch.equal(out_view, out_cont)
+
+
+def test_natten_shim(gpu):
+    q, k, v = _rand((1, 4, 10, 12, 2, 64), 5, torch.bfloat16, gpu)
+    out = natten_na3d(q, k, v, kernel_size=(3, 5, 7))
+    ref = O.na3d(q.cpu(), k.cpu(), v.cpu(), (3, 5, 7))
+    assert rel_l2(out.float(), ref) <= BF16_TOL
+    with pytest.raises(NotImplementedError):
+        natten_na3d(q, k, v, kernel_size=3, is_causal=True)
+    with pytest.raises(ValueError):
+        natten_na3d(q, k, v, kernel_size=(5, 3, 3))
+
+
+def test_cfg1_shape_subboxes(gpu):
+    """configs[1] shape [2,8,64,64,8,64], W=(3,7,7): full launch, oracle on boxes
+    at the grid corners and the middle (a few seconds of CPU)."""
+    shape = (2, 8, 64, 64, 8, 64)
+    g = torch.Generator(device=gpu).manual_seed(0)
+    q, k, v = (torch.randn(shape, generator=g, device=gpu).bfloat16() for _ in range(3))
+    print("cfg1 full launch", flush=True)
+    out = _run(q, k, v, (3, 7, 7))
+    torch.cuda.synchronize()
+    qc, kc, vc = q.cpu(), k.cpu(), v.cpu()
+    for b, h in ((0, 0), (1, 7)):
+        for org in ((0, 0, 0), (6, 56, 56), (3, 28, 30)):
+            ext = (2, 8, 8)
+            sl = (slice(b, b + 1), slice(None), slice(None), slice(None), slice(h, h + 1))
+            ref = O.na3d(qc[sl], kc[sl], vc[sl], (3, 7, 7), q_origin=org, q_extent=ext)
+            got = out[b : b + 1, org[0] : org[0] + 2, org[1] : org[1] + 8, org[2] : org[2] + 8, h : h + 1]
+            assert rel_l2(got.float(), ref) <= BF16_TOL, (b, h, org)
+
+
+def test_cfg2_halo_interior_subboxes(gpu):
+    """6 x padded (16,144,144) x 16 heads x 64, W=(3,13,13), per-head
+    scale U(0.5,2), outputs for the interior y, x in [8,136)."""
+    g = torch.Generator(device=gpu).manual_seed(0)
+    s_h = torch.rand(16, generator=g, device=gpu) * 1.5 + 0.5
+    shape = (6, 16, 144, 144, 16, 64)
+    q, k, v = (
+        (torch.randn(shape, generator=g, device=gpu) * s_h.view(1, 1, 1, 1, 16, 1)).bfloat16() for _ in range(3)
+    )
+    print("cfg2 full launch", flush=True)
+    out = _run(q, k, v, (3, 13, 13), origin=(0, 8, 8), extent=(16, 128, 128))
+    torch.cuda.synchronize()
+    assert out.shape == (6, 16, 128, 128, 16, 64)
+    for b, h in ((0, 0), (5, 15), (2, 9)):
+        sl = (slice(b, b + 1), slice(None), slice(None), slice(None), slice(h, h + 1))
+        qc, kc, vc = q[sl].cpu(), k[sl].cpu(), v[sl].cpu()
+        for org in ((0, 8, 8), (14, 120, 120), (7, 60, 70)):
+            ext = (2, 16, 16)
+            ref = O.na3d(qc, kc, vc, (3, 13, 13), q_origin=org, q_extent=ext)
+            o = (org[0], org[1] - 8, org[2] - 8)
+            got = out[b : b + 1, o[0] : o[0] + 2, o[1] : o[1] + 16, o[2] : o[2] + 16, h : h + 1]
+            assert rel_l2(got.float(), ref) <= BF16_TOL, (b, h, org)
