@@ -202,6 +202,11 @@ def main():
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--no-block", action="store_true")
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument(
+        "--copy-calibration",
+        action="store_true",
+        help="only run a plain 1 GiB device-to-device copy (steps times); for scaling rocprofv3 byte counters",
+    )
     args = ap.parse_args()
     if args.gpus != 1:
         print(
@@ -218,6 +223,14 @@ def main():
 
     _lib.load()
     dev = torch.device("cuda:0")
+    if args.copy_calibration:
+        src = torch.ones(1 << 29, dtype=torch.bfloat16, device=dev)  # 1 GiB
+        dst = torch.empty_like(src)
+        for _ in range(args.steps):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        print(json.dumps({"copy_calibration_bytes_read": src.numel() * 2, "copies": args.steps}), flush=True)
+        return
     log("bench: generating configs[2] inputs")
     q, k, v = cfg2_inputs(dev)
     torch.cuda.synchronize()

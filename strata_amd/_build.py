@@ -58,9 +58,15 @@ def sources() -> list[Path]:
     return sorted(CSRC.glob("*.hip")) + sorted(CSRC.glob("*.cpp"))
 
 
+# Per-file extras.  na3d: the softmax max-reductions need no NaN quieting
+# (inputs are finite scores or -inf), so drop the IEEE-mode canonicalisation
+# that doubles every v_max_f32.
+FILE_FLAGS = {"na3d.hip": ["-fno-honor-nans", "-mno-amdgpu-ieee"]}
+
+
 def _compile(src: Path) -> Path:
     obj = BUILD_DIR / (src.stem + ".o")
-    cmd = [hipcc(), *DEVICE_FLAGS, f"-I{INCLUDE_DIR}", "-c", str(src), "-o", str(obj)]
+    cmd = [hipcc(), *DEVICE_FLAGS, *FILE_FLAGS.get(src.name, []), f"-I{INCLUDE_DIR}", "-c", str(src), "-o", str(obj)]
     res = subprocess.run(cmd, capture_output=True, text=True)
     if res.returncode != 0:
         raise RuntimeError(f"hipcc failed for {src.name}:\n{' '.join(cmd)}\n{res.stdout}\n{res.stderr}")

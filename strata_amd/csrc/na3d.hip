@@ -6,13 +6,16 @@
 //  * na3d_scalar_kernel: one thread per (batch, query, head), fp32 math, used
 //    for fp32 inputs and for shapes the MFMA kernel does not cover.
 //  * na3d_mfma_kernel:   bf16 inputs, fp32 accumulation.  A workgroup owns a
-//    (1, TY, NWX*TX) box of queries of one (batch, head, dilation residue);
-//    each wave owns a (TY, TX) = 16-query tile.  The workgroup streams the
-//    union of its queries' windows through LDS one pair of key rows (two
-//    (z, y) rows of 16+ keys along x) at a time, double buffered.  Per pair a
-//    wave computes S^T = K Q^T on v_mfma_f32_16x16x32_bf16 (keys on M,
-//    queries on N), applies the window mask and an online softmax, and
-//    accumulates O^T += V^T P^T with V^T read from LDS by ds_read_b64_tr_b16.
+//    (1, NTY*TY, 4*TX) box of queries of one (batch, head, dilation residue);
+//    each of its 4 waves owns NTY tiles of (TY, TX) = 16 queries stacked in y.
+//    The union of the box's windows streams from HBM straight into an LDS ring
+//    (buffer_load ... lds), two (z, y) key rows per stage.  Per stage a wave
+//    reads its 16-key K block and the V^T operands once and, for every tile
+//    whose windows reach those rows, computes S^T = K Q^T on
+//    v_mfma_f32_16x16x32_bf16 (keys on M, queries on N), masks the window,
+//    runs an online softmax with lazy rescaling, and accumulates
+//    O^T += V^T P^T (V^T via ds_read_b64_tr_b16) and the row sums (ones x P^T)
+//    on the same MFMA.
 #include "common.h"
 
 namespace strata {
@@ -107,10 +110,22 @@ __global__ __launch_bounds__(256) void na3d_scalar_kernel(Na3dParams p, int64_t 
 // ---------------------------------------------------------------------------
 // Tile bookkeeping shared by host and device.
 struct Na3dTiles {
-  int nxt, nyt, nzt;  // tiles per axis (max over residue classes)
+  int nxt, nyt, nzt;  // workgroup tiles per axis (max over residue classes)
   int nres;           // dil_z * dil_y * dil_x
-  int total;          // total workgroups
+  int total;          // workgroups in the launch
 };
+
+// Linear workgroup id remapped so that consecutive tiles run on one XCD:
+// the dispatcher deals workgroups round-robin over the 8 XCDs, so XCD k gets
+// ids k, k+8, ...; map those to the k-th contiguous block of tiles.
+// (__builtin_amdgcn_workgroup_id_x keeps the id visibly uniform to the
+// compiler, unlike blockIdx.x's out-of-line library call.)
+__device__ __forceinline__ int xcd_tile_order(int n) {
+  const int id = (int)__builtin_amdgcn_workgroup_id_x();
+  const int xcd = id & 7, local = id >> 3;
+  const int q = n >> 3, rem = n & 7;
+  return xcd < rem ? xcd * (q + 1) + local : rem * (q + 1) + (xcd - rem) * q + local;
+}
 
 // Swizzle of the 16-byte chunks of one key row in LDS.  f(key) permutes
 // 0..7 so that (a) any 8 consecutive keys read at one chunk hit 8 distinct
@@ -121,39 +136,97 @@ __device__ __forceinline__ int swz(int chunk, int key, int cmask) {
   return chunk ^ (f & cmask);
 }
 
-__device__ __forceinline__ float xor16_max(float x) {
-  return fmaxf(x, __shfl_xor(x, 16));
-}
-__device__ __forceinline__ float xor32_max(float x) {
-  return fmaxf(x, __shfl_xor(x, 32));
+// Cross-lane max over lanes l, l^16 and l^32 (the four lanes of one MFMA
+// output column) with the gfx950 permlane swaps.
+__device__ __forceinline__ float colmax(float x) {
+  const uint32_t u = __float_as_uint(x);
+  auto a = __builtin_amdgcn_permlane16_swap(u, u, false, false);
+  x = fmaxf(__uint_as_float(a[0]), __uint_as_float(a[1]));
+  const uint32_t v = __float_as_uint(x);
+  auto b = __builtin_amdgcn_permlane32_swap(v, v, false, false);
+  return fmaxf(__uint_as_float(b[0]), __uint_as_float(b[1]));
 }
 
-template <int D, int TX, int NWX>
-__global__ __launch_bounds__(64 * NWX) void na3d_mfma_kernel(Na3dParams p, Na3dTiles tg) {
+__device__ __forceinline__ void wait_vmcnt(int n) {
+  // gfx9 s_waitcnt immediate: vmcnt[3:0] | expcnt[6:4] | lgkmcnt[11:8] | vmcnt[5:4] at [15:14]
+  switch (n) {
+#define STRATA_VMCNT(N) \
+  case N:               \
+    __builtin_amdgcn_s_waitcnt(((N) & 15) | (7 << 4) | (15 << 8) | (((N) >> 4) << 14)); \
+    break;
+    STRATA_VMCNT(0) STRATA_VMCNT(1) STRATA_VMCNT(2) STRATA_VMCNT(3) STRATA_VMCNT(4) STRATA_VMCNT(5)
+    STRATA_VMCNT(6) STRATA_VMCNT(7) STRATA_VMCNT(8) STRATA_VMCNT(9) STRATA_VMCNT(10) STRATA_VMCNT(11)
+    STRATA_VMCNT(12) STRATA_VMCNT(13) STRATA_VMCNT(14) STRATA_VMCNT(15) STRATA_VMCNT(16)
+#undef STRATA_VMCNT
+    default:
+      __builtin_amdgcn_s_waitcnt((7 << 4) | (15 << 8));  // vmcnt(0)
+  }
+}
+
+// One 1-KiB global->LDS copy: lane i's 16 bytes at `voff` within the buffer
+// described by `rsrc` land at LDS byte address `lds_addr + 16*i`; offsets
+// beyond the descriptor's record count read as zero.  Issued as inline asm so
+// that the compiler does not add its own conservative vmcnt(0) before every
+// later LDS read (it cannot tell the ring slots apart); completion is tracked
+// explicitly with wait_vmcnt() before the barrier that publishes a stage.
+__device__ __forceinline__ void dma_row16(u32x4 rsrc, uint32_t lds_addr, uint32_t voff) {
+  asm volatile(
+      "s_mov_b32 m0, %0\n\t"
+      "s_nop 0\n\t"
+      "buffer_load_dwordx4 %1, %2, 0 offen lds" ::"s"(lds_addr),
+      "v"(voff), "s"(rsrc)
+      : "memory", "m0");
+}
+
+__device__ __forceinline__ u32x4 make_rsrc(const void* base, uint32_t num_records) {
+  const uint64_t a = (uint64_t)base;
+  // dword1 holds base[47:32] with stride 0; dword3 = gfx9 data/num format for raw buffers.
+  // Every operand is workgroup-uniform; readfirstlane pins the descriptor in SGPRs.
+  const uint32_t lo = (uint32_t)__builtin_amdgcn_readfirstlane((int)(uint32_t)a);
+  const uint32_t hi = (uint32_t)__builtin_amdgcn_readfirstlane((int)((uint32_t)(a >> 32) & 0xffffu));
+  const uint32_t nr = (uint32_t)__builtin_amdgcn_readfirstlane((int)num_records);
+  return (u32x4){lo, hi, nr, 0x00020000u};
+}
+
+// Workgroup barrier without the release/acquire fences of __syncthreads():
+// those would also wait for the in-flight global->LDS loads of later stages.
+// LDS visibility is established by each wave's own vmcnt wait before it.
+__device__ __forceinline__ void lds_barrier() { asm volatile("s_barrier" ::: "memory"); }
+
+constexpr int NA3D_NWX = 4;          // waves per workgroup, side by side along x
+constexpr uint32_t OOB = 0x7ffffff0u;  // buffer offset / record count that reads as zero
+
+// Workgroup = 4 waves along x; each wave owns NTY query tiles of (TY, TX) =
+// 16 queries stacked along y, so a workgroup covers (1, NTY*TY, 4*TX) queries
+// of one (batch, head, dilation residue, z).  K and V rows of the union of
+// the workgroup's windows stream through an NBUF-deep LDS ring, two (z, y)
+// rows per stage, loaded straight from HBM into LDS (buffer_load ... lds).
+// Each stage's K block (16 keys per row) and V^T operands are read from LDS
+// once per wave and shared by every tile whose window union covers the rows.
+template <int D, int TX, int NTY, int NBUF>
+__device__ __forceinline__ void na3d_mfma_body(const Na3dParams p, const Na3dTiles tg) {
+#if defined(__HIP_DEVICE_COMPILE__)  // the body is device code only; the host pass needs just the signature
+  constexpr int NWX = NA3D_NWX;
   constexpr int TY = 16 / TX;
-  constexpr int WQX = NWX * TX;          // workgroup query width along x
-  constexpr int LW = (NWX - 1) * TX + 16; // keys per LDS row
+  constexpr int WY = NTY * TY;            // workgroup query rows
+  constexpr int WQX = NWX * TX;           // workgroup query columns
+  constexpr int LW = (NWX - 1) * TX + 16; // keys per LDS row that are read
+  constexpr int KPK = 512 / D;            // keys per KiB
+  constexpr int LWP = (LW + KPK - 1) / KPK * KPK;
+  constexpr int RB = LWP * D * 2;         // bytes per (tensor, row) region
+  constexpr int RKB = RB / 1024;
+  constexpr int STAGE_B = 4 * RB;         // K row 0, K row 1, V row 0, V row 1
+  constexpr int LPT = 4 * RKB / NWX;      // 1-KiB DMA loads per wave per stage
   constexpr int CPK = D / 8;              // 16-byte chunks per key
   constexpr int KS = D / 32;              // k-steps of the QK MFMA
   constexpr int DB = D / 16;              // d-blocks of the PV MFMA
-  constexpr int ROW = LW * D;             // elements per LDS key row
-  constexpr int TENSOR = 2 * ROW;         // two rows per stage
-  constexpr int STAGE = 2 * TENSOR;       // K and V
-  constexpr int NCHUNK = STAGE / 8;
-  constexpr int NT = 64 * NWX;
-  constexpr int CPT = (NCHUNK + NT - 1) / NT;  // chunks per thread per stage
   constexpr int CMASK = CPK >= 8 ? 7 : CPK - 1;
+  constexpr float TAU = 8.f;              // lazy-rescale slack (log2 units)
+  static_assert(RB % 1024 == 0 && (4 * RKB) % NWX == 0, "stage layout");
 
-  __shared__ __attribute__((aligned(16))) bf16 lds[2 * STAGE];
+  __shared__ __attribute__((aligned(1024))) char lds[NBUF * STAGE_B];
 
-  // ---- XCD-aware workgroup order: consecutive tiles stay on one XCD ----
-  int wg;
-  {
-    const int id = blockIdx.x, n = gridDim.x;
-    const int xcd = id & 7, local = id >> 3;
-    const int q = n >> 3, rem = n & 7;
-    wg = xcd < rem ? xcd * (q + 1) + local : rem * (q + 1) + (xcd - rem) * q + local;
-  }
+  const int wg = xcd_tile_order(tg.total);
   const int xt = wg % tg.nxt;
   int t = wg / tg.nxt;
   const int yt = t % tg.nyt;
@@ -164,216 +237,259 @@ __global__ __launch_bounds__(64 * NWX) void na3d_mfma_kernel(Na3dParams p, Na3dT
   t /= tg.nres;
   const int h = t % p.H;
   const int b = t / p.H;
-
   const int gx = res % p.dil[2];
   const int gy = (res / p.dil[2]) % p.dil[1];
   const int gz = res / (p.dil[2] * p.dil[1]);
+  const int dz = p.dil[0], dy = p.dil[1], dx = p.dil[2];
 
-  // Sub-grid (one residue class) lengths and query ranges.
-  const int Lz = sub_len(p.L[0], gz, p.dil[0]);
-  const int Ly = sub_len(p.L[1], gy, p.dil[1]);
-  const int Lx = sub_len(p.L[2], gx, p.dil[2]);
-  const int qz0 = sub_first(p.org[0], gz, p.dil[0]), qz1 = sub_end(p.org[0], p.ext[0], gz, p.dil[0]);
-  const int qy0 = sub_first(p.org[1], gy, p.dil[1]), qy1 = sub_end(p.org[1], p.ext[1], gy, p.dil[1]);
-  const int qx0 = sub_first(p.org[2], gx, p.dil[2]), qx1 = sub_end(p.org[2], p.ext[2], gx, p.dil[2]);
-
+  const int Lz = sub_len(p.L[0], gz, dz);
+  const int Ly = sub_len(p.L[1], gy, dy);
+  const int Lx = sub_len(p.L[2], gx, dx);
+  const int qz0 = sub_first(p.org[0], gz, dz), qz1 = sub_end(p.org[0], p.ext[0], gz, dz);
+  const int qy0 = sub_first(p.org[1], gy, dy), qy1 = sub_end(p.org[1], p.ext[1], gy, dy);
+  const int qx0 = sub_first(p.org[2], gx, dx), qx1 = sub_end(p.org[2], p.ext[2], gx, dx);
   const int iz = qz0 + zt;
-  const int y0 = qy0 + yt * TY;
+  const int y0 = qy0 + yt * WY;
   const int x0 = qx0 + xt * WQX;
   if (iz >= qz1 || y0 >= qy1 || x0 >= qx1) return;  // uniform over the workgroup
 
   const int kz = p.ker[0], ky = p.ker[1], kx = p.ker[2];
   const int sz = win_start(iz, Lz, kz);
-  const int ylast = min(y0 + TY - 1, qy1 - 1);
   const int Y0 = win_start(y0, Ly, ky);
-  const int NR = win_start(ylast, Ly, ky) + ky - Y0;  // rows of the y-union
-  const int NP = (NR + 1) >> 1;                      // row pairs per z-slice
+  const int NR = win_start(min(y0 + WY - 1, qy1 - 1), Ly, ky) + ky - Y0;
+  const int NP = (NR + 1) >> 1;
   const int X0 = win_start(x0, Lx, kx);
   const int nstage = kz * NP;
 
-  const int tid = threadIdx.x;
-  const int wave = tid >> 6;
+  const int tid = (int)__builtin_amdgcn_workitem_id_x();
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // uniform: keeps DMA descriptors in SGPRs
   const int lane = tid & 63;
   const int n16 = lane & 15;
   const int g = lane >> 4;
+  const uint32_t lds_base = (uint32_t)(uintptr_t)(__attribute__((address_space(3))) char*)lds;
 
-  // ---- this lane's query ----
+  // ---- per-lane x geometry (shared by the wave's tiles) ----
   const int xw0 = x0 + wave * TX;
-  const int off_w = win_start(min(xw0, qx1 - 1), Lx, kx) - X0;  // wave's key block inside the LDS row
-  const int qy = y0 + n16 / TX;
+  const int off_w = win_start(min(xw0, qx1 - 1), Lx, kx) - X0;
   const int qx = xw0 + n16 % TX;
-  const bool qvalid = qy < qy1 && qx < qx1;
-  const int qyc = min(qy, qy1 - 1);
-  const int qxc = min(qx, qx1 - 1);
-  const int sy = win_start(qyc, Ly, ky);
-  const int sx = win_start(qxc, Lx, kx);
-  uint32_t xbits = 0;
+  const int sx = win_start(min(qx, qx1 - 1), Lx, kx);
+  float xbias[4];
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
     const int kxs = X0 + off_w + 4 * g + i;
-    xbits |= (kxs >= sx && kxs < sx + kx) ? (1u << i) : 0u;
+    xbias[i] = (kxs >= sx && kxs < sx + kx) ? 0.f : -INFINITY;
   }
 
-  const int rz = gz + p.dil[0] * iz;
-  bf16x8 qreg[KS];
-  {
-    const bf16* qp = (const bf16*)p.q + (int64_t)b * p.qs[0] + (int64_t)rz * p.qs[1] +
-                     (int64_t)(gy + p.dil[1] * qyc) * p.qs[2] + (int64_t)(gx + p.dil[2] * qxc) * p.qs[3] +
-                     (int64_t)h * p.qs[4];
+  // ---- per-tile y geometry (tile rows relative to Y0) ----
+  int U0[NTY], U1[NTY], F0[NTY], F1[NTY], syl[NTY], qyl[NTY];
 #pragma unroll
-    for (int ks = 0; ks < KS; ++ks) qreg[ks] = *(const bf16x8*)(qp + 32 * ks + 8 * g);
+  for (int tt = 0; tt < NTY; ++tt) {
+    const int yt0 = y0 + tt * TY;
+    if (yt0 < qy1) {
+      const int ytl = min(yt0 + TY - 1, qy1 - 1);
+      U0[tt] = win_start(yt0, Ly, ky) - Y0;
+      U1[tt] = win_start(ytl, Ly, ky) + ky - Y0;
+      F0[tt] = win_start(ytl, Ly, ky) - Y0;
+      F1[tt] = win_start(yt0, Ly, ky) + ky - Y0;
+    } else {
+      U0[tt] = 1 << 20;
+      U1[tt] = 0;
+      F0[tt] = F1[tt] = 0;
+    }
+    qyl[tt] = yt0 + n16 / TX;
+    syl[tt] = win_start(min(qyl[tt], qy1 - 1), Ly, ky) - Y0;
   }
 
-  const bf16* kbase = (const bf16*)p.k + (int64_t)b * p.ks[0] + (int64_t)h * p.ks[4];
-  const bf16* vbase = (const bf16*)p.v + (int64_t)b * p.vs[0] + (int64_t)h * p.vs[4];
+  // ---- Q operands ----
+  const int rz = gz + dz * iz;
+  const int rqx = gx + dx * min(qx, qx1 - 1);
+  bf16x8 qreg[NTY][KS];
+#pragma unroll
+  for (int tt = 0; tt < NTY; ++tt) {
+    const int rqy = gy + dy * min(qyl[tt], qy1 - 1);
+    const bf16* qp = (const bf16*)p.q + (int64_t)b * p.qs[0] + (int64_t)rz * p.qs[1] + (int64_t)rqy * p.qs[2] +
+                     (int64_t)rqx * p.qs[3] + (int64_t)h * p.qs[4];
+#pragma unroll
+    for (int ks = 0; ks < KS; ++ks) qreg[tt][ks] = *(const bf16x8*)(qp + 32 * ks + 8 * g);
+  }
+  // Q must land before the DMA ring starts: the compiler does not see the
+  // ring's loads, so a deferred wait for Q inside the loop would drain them.
+  wait_vmcnt(0);
 
-  // ---- stage loader: global -> registers -> LDS ----
-  u32x4 stage_regs[CPT];
-  auto load_stage = [&](int s) {
+  // ---- DMA descriptors: lane offsets are fixed, row bases change per stage ----
+  uint32_t voff[LPT];
+#pragma unroll
+  for (int j = 0; j < LPT; ++j) {
+    const int gc = j * NWX + wave;          // 1-KiB chunk of the stage
+    const int tensor = (gc / RKB) >> 1;
+    const int key = (gc % RKB) * KPK + lane / CPK;
+    const int pc = lane % CPK;
+    const int c = swz(pc, key, CMASK);      // logical chunk stored at slot pc
+    const int64_t sx3 = tensor ? p.vs[3] : p.ks[3];
+    voff[j] = (key < LW && X0 + key < Lx) ? (uint32_t)((int64_t)(gx + dx * (X0 + key)) * sx3 * 2 + 16 * c) : OOB;
+  }
+  const char* kbase = (const char*)p.k + 2 * ((int64_t)b * p.ks[0] + (int64_t)h * p.ks[4]);
+  const char* vbase = (const char*)p.v + 2 * ((int64_t)b * p.vs[0] + (int64_t)h * p.vs[4]);
+
+  auto issue = [&](int s) {
     const int dzi = s / NP;
     const int pr = s - dzi * NP;
-    const int zk = sz + dzi;
-    const int rzk = gz + p.dil[0] * zk;
+    const int64_t zr = gz + dz * (sz + dzi);
+    char* dst = lds + (s % NBUF) * STAGE_B;
 #pragma unroll
-    for (int c = 0; c < CPT; ++c) {
-      const int ci = tid + c * NT;
-      u32x4 val = {0u, 0u, 0u, 0u};
-      if (ci < NCHUNK) {
-        const int chunk = ci % CPK;
-        int tt = ci / CPK;
-        const int key = tt % LW;
-        tt /= LW;
-        const int row = tt & 1;
-        const int tensor = tt >> 1;
-        const int yr = 2 * pr + row;
-        const int xs = X0 + key;
-        if (yr < NR && xs < Lx) {
-          const int ry = gy + p.dil[1] * (Y0 + yr);
-          const int rx = gx + p.dil[2] * xs;
-          const int64_t* st = tensor ? p.vs : p.ks;
-          const bf16* src = (tensor ? vbase : kbase) + (int64_t)rzk * st[1] + (int64_t)ry * st[2] +
-                            (int64_t)rx * st[3] + 8 * chunk;
-          val = *(const u32x4*)src;
-        }
-      }
-      stage_regs[c] = val;
-    }
-  };
-  auto store_stage = [&](int buf) {
-    bf16* dst = lds + buf * STAGE;
-#pragma unroll
-    for (int c = 0; c < CPT; ++c) {
-      const int ci = tid + c * NT;
-      if (ci < NCHUNK) {
-        const int chunk = ci % CPK;
-        const int kr = ci / CPK;  // (tensor, row, key) flattened
-        const int key = kr % LW;
-        *(u32x4*)(dst + kr * D + 8 * swz(chunk, key, CMASK)) = stage_regs[c];
-      }
+    for (int j = 0; j < LPT; ++j) {
+      const int gc = j * NWX + wave;
+      const int reg = gc / RKB;
+      const int tensor = reg >> 1, row = reg & 1;
+      const int yrel = 2 * pr + row;
+      const bool ok = yrel < NR;
+      const int64_t st1 = tensor ? p.vs[1] : p.ks[1];
+      const int64_t st2 = tensor ? p.vs[2] : p.ks[2];
+      const char* base = (tensor ? vbase : kbase) +
+                         (ok ? 2 * (zr * st1 + (int64_t)(gy + dy * (Y0 + yrel)) * st2) : 0);
+      dma_row16(make_rsrc(base, ok ? OOB : 0u), lds_base + (uint32_t)(dst - lds) + gc * 1024, voff[j]);
     }
   };
 
-  const float c2 = p.scale * 1.4426950408889634f;  // scores in log2 units
-  f32x4 oacc[DB];
+  // ---- LDS read offsets (bytes within a stage) ----
+  uint32_t koff[2][KS];
 #pragma unroll
-  for (int db = 0; db < DB; ++db) oacc[db] = (f32x4){0.f, 0.f, 0.f, 0.f};
-  float mrun = -INFINITY, lrun = 0.f;
-
-  load_stage(0);
-  store_stage(0);
-  for (int s = 0; s < nstage; ++s) {
-    __syncthreads();
-    if (s + 1 < nstage) load_stage(s + 1);
-
-    const int buf = s & 1;
-    const bf16* Kb = lds + buf * STAGE;
-    const bf16* Vb = Kb + TENSOR;
-    const int pr = s % NP;
-
-    // S^T = K Q^T for the two rows of the pair.
-    f32x4 sacc[2];
+  for (int r = 0; r < 2; ++r)
 #pragma unroll
-    for (int r = 0; r < 2; ++r) {
-      sacc[r] = (f32x4){0.f, 0.f, 0.f, 0.f};
+    for (int ks = 0; ks < KS; ++ks) {
       const int key = off_w + n16;
-      const bf16* krow = Kb + (r * LW + key) * D;
-#pragma unroll
-      for (int ks = 0; ks < KS; ++ks) {
-        const bf16x8 a = *(const bf16x8*)(krow + 8 * swz(4 * ks + g, key, CMASK));
-        sacc[r] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, qreg[ks], sacc[r], 0, 0, 0);
-      }
+      koff[r][ks] = r * RB + (key * D + 8 * swz(4 * ks + g, key, CMASK)) * 2;
     }
-
-    // Window mask + online softmax (4 lanes of a column share one query).
-    float tv[8];
-    float mloc = -INFINITY;
+  uint32_t voffs[DB];
+  {
+    const int keyv = off_w + 4 * g + (n16 >> 2);
+    const int dq = n16 & 3;
 #pragma unroll
-    for (int r = 0; r < 2; ++r) {
-      const int yk = Y0 + 2 * pr + r;
-      const bool yok = yk >= sy && yk < sy + ky;
-#pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const bool ok = yok && ((xbits >> i) & 1u);
-        const float v = ok ? sacc[r][i] * c2 : -INFINITY;
-        tv[4 * r + i] = v;
-        mloc = fmaxf(mloc, v);
-      }
-    }
-    mloc = xor16_max(mloc);
-    mloc = xor32_max(mloc);
-    const float mnew = fmaxf(mrun, mloc);
-    const float muse = mnew == -INFINITY ? 0.f : mnew;
-    const float alpha = __builtin_amdgcn_exp2f(mrun - muse);
-    lrun *= alpha;
-#pragma unroll
-    for (int db = 0; db < DB; ++db) oacc[db] *= alpha;
-    float pv[8];
-#pragma unroll
-    for (int j = 0; j < 8; ++j) {
-      pv[j] = __builtin_amdgcn_exp2f(tv[j] - muse);
-      lrun += pv[j];
-    }
-    mrun = mnew;
-    const u32x4 pw = {pack_bf16x2(pv[0], pv[1]), pack_bf16x2(pv[2], pv[3]), pack_bf16x2(pv[4], pv[5]),
-                      pack_bf16x2(pv[6], pv[7])};
-    const bf16x8 pb = __builtin_bit_cast(bf16x8, pw);
-
-    // O^T += V^T P^T.  Lane m of group g reads 4 d-values of key (4g + m/4)
-    // of each row; the transpose read hands lane m the 4 keys at d = m.
-    {
-      const int keyv = off_w + 4 * g + (n16 >> 2);
-      const int dq = n16 & 3;
-#pragma unroll
-      for (int db = 0; db < DB; ++db) {
-        const int chunk = 2 * db + (dq >> 1);
-        const int eoff = 8 * swz(chunk, keyv, CMASK) + 4 * (dq & 1);
-        const bf16x4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4bf16(LDS_PTR(bf16x4, Vb + keyv * D + eoff));
-        const bf16x4 hi = __builtin_amdgcn_ds_read_tr16_b64_v4bf16(LDS_PTR(bf16x4, Vb + (LW + keyv) * D + eoff));
-        const bf16x8 a = __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7);
-        oacc[db] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, pb, oacc[db], 0, 0, 0);
-      }
-    }
-
-    if (s + 1 < nstage) store_stage(buf ^ 1);
+    for (int db = 0; db < DB; ++db)
+      voffs[db] = 2 * RB + (keyv * D + 8 * swz(2 * db + (dq >> 1), keyv, CMASK) + 4 * (dq & 1)) * 2;
   }
 
+  const float c2 = p.scale * 1.4426950408889634f;  // scores in log2 units
+  f32x4 oacc[NTY][DB];
+  f32x4 lacc[NTY];
+  float mrun[NTY];
+#pragma unroll
+  for (int tt = 0; tt < NTY; ++tt) {
+#pragma unroll
+    for (int db = 0; db < DB; ++db) oacc[tt][db] = (f32x4){0.f, 0.f, 0.f, 0.f};
+    lacc[tt] = (f32x4){0.f, 0.f, 0.f, 0.f};
+    mrun[tt] = -INFINITY;
+  }
+  typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
+  const bf16x8_t ones = {(bf16)1.f, (bf16)1.f, (bf16)1.f, (bf16)1.f, (bf16)1.f, (bf16)1.f, (bf16)1.f, (bf16)1.f};
+
+#pragma unroll
+  for (int s = 0; s < NBUF - 1; ++s)
+    if (s < nstage) issue(s);
+
+  for (int s = 0; s < nstage; ++s) {
+    wait_vmcnt(min(NBUF - 2, nstage - 1 - s) * LPT);
+    lds_barrier();
+    if (s + NBUF - 1 < nstage) issue(s + NBUF - 1);
+
+    const char* st = lds + (s % NBUF) * STAGE_B;
+    const int pr = s % NP;
+    const int r0 = 2 * pr;
+
+    bf16x8 ak[2][KS];
+#pragma unroll
+    for (int r = 0; r < 2; ++r)
+#pragma unroll
+      for (int ks = 0; ks < KS; ++ks) ak[r][ks] = *(const bf16x8*)(st + koff[r][ks]);
+    bf16x8 av[DB];
+#pragma unroll
+    for (int db = 0; db < DB; ++db) {
+      const bf16x4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4bf16(LDS_PTR(bf16x4, st + voffs[db]));
+      const bf16x4 hi = __builtin_amdgcn_ds_read_tr16_b64_v4bf16(LDS_PTR(bf16x4, st + voffs[db] + RB));
+      av[db] = __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7);
+    }
+
+#pragma unroll
+    for (int tt = 0; tt < NTY; ++tt) {
+      if (r0 + 1 < U0[tt] || r0 >= U1[tt]) continue;  // rows outside this tile's window union
+      f32x4 sacc[2];
+#pragma unroll
+      for (int r = 0; r < 2; ++r) {
+        sacc[r] = (f32x4){0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int ks = 0; ks < KS; ++ks)
+          sacc[r] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ak[r][ks], qreg[tt][ks], sacc[r], 0, 0, 0);
+      }
+      float tv[8];
+      if (r0 >= F0[tt] && r0 + 1 < F1[tt]) {
+        // both rows inside every window of the tile: only the x mask applies
+#pragma unroll
+        for (int r = 0; r < 2; ++r)
+#pragma unroll
+          for (int i = 0; i < 4; ++i) tv[4 * r + i] = fmaf(sacc[r][i], c2, xbias[i]);
+      } else {
+#pragma unroll
+        for (int r = 0; r < 2; ++r) {
+          const int yr = r0 + r;
+          const bool yok = yr >= syl[tt] && yr < syl[tt] + ky;
+#pragma unroll
+          for (int i = 0; i < 4; ++i) tv[4 * r + i] = fmaf(sacc[r][i], c2, yok ? xbias[i] : -INFINITY);
+        }
+      }
+      float mx = fmaxf(fmaxf(fmaxf(tv[0], tv[1]), fmaxf(tv[2], tv[3])), fmaxf(fmaxf(tv[4], tv[5]), fmaxf(tv[6], tv[7])));
+      mx = colmax(mx);
+      if (__builtin_amdgcn_ballot_w64(mx > mrun[tt] + TAU) != 0) {
+        const float mnew = fmaxf(mrun[tt], mx);
+        const float alpha = mnew == -INFINITY ? 1.f : __builtin_amdgcn_exp2f(mrun[tt] - mnew);
+#pragma unroll
+        for (int db = 0; db < DB; ++db) oacc[tt][db] *= alpha;
+        lacc[tt] *= alpha;
+        mrun[tt] = mnew;
+      }
+      const float muse = mrun[tt] == -INFINITY ? 0.f : mrun[tt];
+      float pv[8];
+#pragma unroll
+      for (int j = 0; j < 8; ++j) pv[j] = __builtin_amdgcn_exp2f(tv[j] - muse);
+      const u32x4 pw = {pack_bf16x2(pv[0], pv[1]), pack_bf16x2(pv[2], pv[3]), pack_bf16x2(pv[4], pv[5]),
+                        pack_bf16x2(pv[6], pv[7])};
+      const bf16x8 pb = __builtin_bit_cast(bf16x8, pw);
+      lacc[tt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ones, pb, lacc[tt], 0, 0, 0);
+#pragma unroll
+      for (int db = 0; db < DB; ++db)
+        oacc[tt][db] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(av[db], pb, oacc[tt][db], 0, 0, 0);
+    }
+  }
+  wait_vmcnt(0);
+
   // ---- normalise and store ----
-  float ltot = lrun + __shfl_xor(lrun, 16);
-  ltot += __shfl_xor(ltot, 32);
-  const float inv = 1.f / ltot;
-  if (qvalid) {
+#pragma unroll
+  for (int tt = 0; tt < NTY; ++tt) {
+    const int qy = qyl[tt];
+    if (qy >= qy1 || qx >= qx1) continue;
+    const float inv = 1.f / lacc[tt][0];
     const int oz = rz - p.org[0];
-    const int oy = gy + p.dil[1] * qy - p.org[1];
-    const int ox = gx + p.dil[2] * qx - p.org[2];
+    const int oy = gy + dy * qy - p.org[1];
+    const int ox = gx + dx * qx - p.org[2];
     bf16* op = (bf16*)p.o + (int64_t)b * p.os[0] + (int64_t)oz * p.os[1] + (int64_t)oy * p.os[2] +
                (int64_t)ox * p.os[3] + (int64_t)h * p.os[4];
 #pragma unroll
     for (int db = 0; db < DB; ++db) {
-      const u32x2 w = {pack_bf16x2(oacc[db][0] * inv, oacc[db][1] * inv),
-                       pack_bf16x2(oacc[db][2] * inv, oacc[db][3] * inv)};
+      const u32x2 w = {pack_bf16x2(oacc[tt][db][0] * inv, oacc[tt][db][1] * inv),
+                       pack_bf16x2(oacc[tt][db][2] * inv, oacc[tt][db][3] * inv)};
       *(u32x2*)(op + 16 * db + 4 * g) = w;
     }
   }
+#endif
+}
+
+// Two workgroups per CU for head_dim <= 64; head_dim 128 needs the full register file.
+template <int D, int TX, int NTY, int NBUF>
+__global__ __launch_bounds__(256, 2) void na3d_mfma_kernel(Na3dParams p, Na3dTiles tg) {
+  na3d_mfma_body<D, TX, NTY, NBUF>(p, tg);
+}
+template <int D, int TX, int NTY, int NBUF>
+__global__ __launch_bounds__(256, 1) void na3d_mfma_wide_kernel(Na3dParams p, Na3dTiles tg) {
+  na3d_mfma_body<D, TX, NTY, NBUF>(p, tg);
 }
 
 // ---------------------------------------------------------------------------
@@ -402,7 +518,7 @@ static int launch_scalar(const Na3dParams& p, hipStream_t st) {
   return check_launch("na3d_scalar_kernel");
 }
 
-template <int D, int TX, int NWX>
+template <int D, int TX, int NTY, int NBUF>
 static int launch_mfma_cfg(const Na3dParams& p, hipStream_t st) {
   Na3dTiles tg;
   int nq[3] = {0, 0, 0};
@@ -413,24 +529,38 @@ static int launch_mfma_cfg(const Na3dParams& p, hipStream_t st) {
     }
   constexpr int TY = 16 / TX;
   tg.nzt = nq[0];
-  tg.nyt = (nq[1] + TY - 1) / TY;
-  tg.nxt = (nq[2] + NWX * TX - 1) / (NWX * TX);
+  tg.nyt = (nq[1] + NTY * TY - 1) / (NTY * TY);
+  tg.nxt = (nq[2] + NA3D_NWX * TX - 1) / (NA3D_NWX * TX);
   tg.nres = p.dil[0] * p.dil[1] * p.dil[2];
   const int64_t total = (int64_t)tg.nxt * tg.nyt * tg.nzt * tg.nres * p.H * p.B;
   if (total == 0) return STRATA_HIP_OK;
   if (total > 0x7fffffff) return fail(STRATA_HIP_EUNSUPPORTED, "na3d: problem too large for one launch");
   tg.total = (int)total;
-  hipLaunchKernelGGL((na3d_mfma_kernel<D, TX, NWX>), dim3(tg.total), dim3(64 * NWX), 0, st, p, tg);
+  if (D >= 128)
+    hipLaunchKernelGGL((na3d_mfma_wide_kernel<D, TX, NTY, NBUF>), dim3((unsigned)total), dim3(64 * NA3D_NWX), 0, st, p, tg);
+  else
+    hipLaunchKernelGGL((na3d_mfma_kernel<D, TX, NTY, NBUF>), dim3((unsigned)total), dim3(64 * NA3D_NWX), 0, st, p, tg);
   return check_launch("na3d_mfma_kernel");
+}
+
+// LDS ring depth for a stage of `stage_bytes`: as deep as fits in ~80 KiB
+// (two workgroups per CU), at least double buffered.
+constexpr int ring_depth(int stage_bytes) {
+  return 81920 / stage_bytes >= 4 ? 4 : (81920 / stage_bytes >= 3 ? 3 : 2);
+}
+template <int D, int TX>
+constexpr int stage_bytes() {
+  return 4 * (((NA3D_NWX - 1) * TX + 16 + 512 / D - 1) / (512 / D) * (512 / D)) * D * 2;
 }
 
 template <int D>
 static int launch_mfma_d(const Na3dParams& p, hipStream_t st) {
+  constexpr int NTY = D >= 128 ? 2 : 4;
   const int kx = p.ker[2];
-  if (kx == 1) return launch_mfma_cfg<D, 16, 4>(p, st);
-  if (kx <= 9) return launch_mfma_cfg<D, 8, 4>(p, st);
-  if (kx <= 13) return launch_mfma_cfg<D, 4, 4>(p, st);
-  return launch_mfma_cfg<D, 2, 4>(p, st);  // kx <= 15
+  if (kx == 1) return launch_mfma_cfg<D, 16, NTY, ring_depth(stage_bytes<D, 16>())>(p, st);
+  if (kx <= 9) return launch_mfma_cfg<D, 8, NTY, ring_depth(stage_bytes<D, 8>())>(p, st);
+  if (kx <= 13) return launch_mfma_cfg<D, 4, NTY, ring_depth(stage_bytes<D, 4>())>(p, st);
+  return launch_mfma_cfg<D, 2, (NTY > 2 ? 2 : NTY), ring_depth(stage_bytes<D, 2>())>(p, st);  // kx <= 15
 }
 
 static bool aligned16(const void* ptr) { return ((uintptr_t)ptr & 15u) == 0; }
@@ -494,6 +624,11 @@ extern "C" int strata_hip_na3d_fwd(const strata_hip_na3d_args* a, void* stream) 
       for (int i = 0; i < 5; ++i)
         if (strides[t][i] % 8 != 0) mfma_ok = false;
     }
+  }
+  if (mfma_ok) {
+    // the buffer loads address one (z, y) row per descriptor with 32-bit byte offsets along x
+    const int64_t xspan_k = (int64_t)p.L[2] * p.ks[3] * 2 + 256, xspan_v = (int64_t)p.L[2] * p.vs[3] * 2 + 256;
+    if (xspan_k >= (int64_t)OOB || xspan_v >= (int64_t)OOB) mfma_ok = false;
   }
   if (!mfma_ok) return launch_scalar<bf16>(p, st);
   switch (p.D) {
