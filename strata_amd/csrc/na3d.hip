@@ -194,15 +194,40 @@ __device__ __forceinline__ u32x4 make_rsrc(const void* base, uint32_t num_record
 __device__ __forceinline__ void lds_barrier() { asm volatile("s_barrier" ::: "memory"); }
 
 constexpr int NA3D_NWX = 4;          // waves per workgroup, side by side along x
-constexpr uint32_t OOB = 0x7ffffff0u;  // buffer offset / record count that reads as zero
+constexpr uint32_t OOB = 0x7ffffff0u;  // lane offset that reads as zero (beyond any record count)
+
+// Sum over lanes l, l^16, l^32 (the four lanes of one MFMA output column).
+__device__ __forceinline__ float colsum(float x) {
+  const uint32_t u = __float_as_uint(x);
+  auto a = __builtin_amdgcn_permlane16_swap(u, u, false, false);
+  x = __uint_as_float(a[0]) + __uint_as_float(a[1]);
+  const uint32_t v = __float_as_uint(x);
+  auto b = __builtin_amdgcn_permlane32_swap(v, v, false, false);
+  return __uint_as_float(b[0]) + __uint_as_float(b[1]);
+}
+
+// Bits [lo, hi) of a 32-bit mask (empty if hi <= lo).
+__device__ __forceinline__ uint32_t bit_range(int lo, int hi) {
+  lo = lo < 0 ? 0 : lo;
+  hi = hi > 32 ? 32 : hi;
+  if (hi <= lo) return 0;
+  const uint32_t top = hi == 32 ? ~0u : ((1u << hi) - 1);
+  return top & ~((1u << lo) - 1);
+}
 
 // Workgroup = 4 waves along x; each wave owns NTY query tiles of (TY, TX) =
 // 16 queries stacked along y, so a workgroup covers (1, NTY*TY, 4*TX) queries
 // of one (batch, head, dilation residue, z).  K and V rows of the union of
 // the workgroup's windows stream through an NBUF-deep LDS ring, two (z, y)
-// rows per stage, loaded straight from HBM into LDS (buffer_load ... lds).
-// Each stage's K block (16 keys per row) and V^T operands are read from LDS
-// once per wave and shared by every tile whose window union covers the rows.
+// rows ("a pair") per stage, loaded straight from HBM into LDS.  Each stage's
+// K block (16 keys per row) and V^T operands are read from LDS once per wave
+// and shared by every tile whose window union covers the pair.
+//
+// Softmax: scores live in log2 units, u = s*scale*log2(e) - m, where m is a
+// per-query reference that starts at the query's score against its own key
+// (always inside its window) and only moves up, lazily, when a stage's
+// maximum exceeds it by more than TAU.  The subtraction and the window mask
+// fold into one FMA per score: u = fma(s, c2, bias - m), bias in {0, -inf}.
 template <int D, int TX, int NTY, int NBUF>
 __device__ __forceinline__ void na3d_mfma_body(const Na3dParams p, const Na3dTiles tg) {
 #if defined(__HIP_DEVICE_COMPILE__)  // the body is device code only; the host pass needs just the signature
@@ -237,10 +262,10 @@ __device__ __forceinline__ void na3d_mfma_body(const Na3dParams p, const Na3dTil
   t /= tg.nres;
   const int h = t % p.H;
   const int b = t / p.H;
-  const int gx = res % p.dil[2];
-  const int gy = (res / p.dil[2]) % p.dil[1];
-  const int gz = res / (p.dil[2] * p.dil[1]);
   const int dz = p.dil[0], dy = p.dil[1], dx = p.dil[2];
+  const int gx = res % dx;
+  const int gy = (res / dx) % dy;
+  const int gz = res / (dx * dy);
 
   const int Lz = sub_len(p.L[0], gz, dz);
   const int Ly = sub_len(p.L[1], gy, dy);
@@ -256,8 +281,8 @@ __device__ __forceinline__ void na3d_mfma_body(const Na3dParams p, const Na3dTil
   const int kz = p.ker[0], ky = p.ker[1], kx = p.ker[2];
   const int sz = win_start(iz, Lz, kz);
   const int Y0 = win_start(y0, Ly, ky);
-  const int NR = win_start(min(y0 + WY - 1, qy1 - 1), Ly, ky) + ky - Y0;
-  const int NP = (NR + 1) >> 1;
+  const int NR = win_start(min(y0 + WY - 1, qy1 - 1), Ly, ky) + ky - Y0;  // rows of the y-union (<= 64)
+  const int NP = (NR + 1) >> 1;                                          // pairs per z-slice (<= 32)
   const int X0 = win_start(x0, Lx, kx);
   const int nstage = kz * NP;
 
@@ -272,7 +297,8 @@ __device__ __forceinline__ void na3d_mfma_body(const Na3dParams p, const Na3dTil
   const int xw0 = x0 + wave * TX;
   const int off_w = win_start(min(xw0, qx1 - 1), Lx, kx) - X0;
   const int qx = xw0 + n16 % TX;
-  const int sx = win_start(min(qx, qx1 - 1), Lx, kx);
+  const int qxc = min(qx, qx1 - 1);
+  const int sx = win_start(qxc, Lx, kx);
   float xbias[4];
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
@@ -280,86 +306,125 @@ __device__ __forceinline__ void na3d_mfma_body(const Na3dParams p, const Na3dTil
     xbias[i] = (kxs >= sx && kxs < sx + kx) ? 0.f : -INFINITY;
   }
 
-  // ---- per-tile y geometry (tile rows relative to Y0) ----
-  int U0[NTY], U1[NTY], F0[NTY], F1[NTY], syl[NTY], qyl[NTY];
+  // ---- per-tile y geometry: which pairs each tile touches / needs a y mask for ----
+  uint32_t act_mask[NTY], ym_mask[NTY];
+  int syl[NTY], qyl[NTY];
 #pragma unroll
   for (int tt = 0; tt < NTY; ++tt) {
     const int yt0 = y0 + tt * TY;
     if (yt0 < qy1) {
       const int ytl = min(yt0 + TY - 1, qy1 - 1);
-      U0[tt] = win_start(yt0, Ly, ky) - Y0;
-      U1[tt] = win_start(ytl, Ly, ky) + ky - Y0;
-      F0[tt] = win_start(ytl, Ly, ky) - Y0;
-      F1[tt] = win_start(yt0, Ly, ky) + ky - Y0;
+      const int U0 = win_start(yt0, Ly, ky) - Y0, U1 = win_start(ytl, Ly, ky) + ky - Y0;  // union rows
+      const int F0 = win_start(ytl, Ly, ky) - Y0, F1 = win_start(yt0, Ly, ky) + ky - Y0;  // rows in every window
+      act_mask[tt] = bit_range(U0 >> 1, (U1 + 1) >> 1);
+      ym_mask[tt] = act_mask[tt] & ~bit_range((F0 + 1) >> 1, F1 >> 1);
     } else {
-      U0[tt] = 1 << 20;
-      U1[tt] = 0;
-      F0[tt] = F1[tt] = 0;
+      act_mask[tt] = ym_mask[tt] = 0;
     }
     qyl[tt] = yt0 + n16 / TX;
     syl[tt] = win_start(min(qyl[tt], qy1 - 1), Ly, ky) - Y0;
   }
 
-  // ---- Q operands ----
+  // ---- Q operands and each query's score against its own key ----
   const int rz = gz + dz * iz;
-  const int rqx = gx + dx * min(qx, qx1 - 1);
+  const int rqx = gx + dx * qxc;
+  const float c2 = p.scale * 1.4426950408889634f;  // scores in log2 units
   bf16x8 qreg[NTY][KS];
+  float mref[NTY];
+  {
+    bf16x8 kself[NTY][KS];
 #pragma unroll
-  for (int tt = 0; tt < NTY; ++tt) {
-    const int rqy = gy + dy * min(qyl[tt], qy1 - 1);
-    const bf16* qp = (const bf16*)p.q + (int64_t)b * p.qs[0] + (int64_t)rz * p.qs[1] + (int64_t)rqy * p.qs[2] +
-                     (int64_t)rqx * p.qs[3] + (int64_t)h * p.qs[4];
+    for (int tt = 0; tt < NTY; ++tt) {
+      const int rqy = gy + dy * min(qyl[tt], qy1 - 1);
+      const bf16* qp = (const bf16*)p.q + (int64_t)b * p.qs[0] + (int64_t)rz * p.qs[1] + (int64_t)rqy * p.qs[2] +
+                       (int64_t)rqx * p.qs[3] + (int64_t)h * p.qs[4];
+      const bf16* kp = (const bf16*)p.k + (int64_t)b * p.ks[0] + (int64_t)rz * p.ks[1] + (int64_t)rqy * p.ks[2] +
+                       (int64_t)rqx * p.ks[3] + (int64_t)h * p.ks[4];
 #pragma unroll
-    for (int ks = 0; ks < KS; ++ks) qreg[tt][ks] = *(const bf16x8*)(qp + 32 * ks + 8 * g);
+      for (int ks = 0; ks < KS; ++ks) {
+        qreg[tt][ks] = *(const bf16x8*)(qp + 32 * ks + 8 * g);
+        kself[tt][ks] = *(const bf16x8*)(kp + 32 * ks + 8 * g);
+      }
+    }
+    // Q must land before the DMA ring starts: the compiler does not see the
+    // ring's loads, so a deferred wait for Q inside the loop would drain them.
+    wait_vmcnt(0);
+#pragma unroll
+    for (int tt = 0; tt < NTY; ++tt) {
+      float d = 0.f;
+#pragma unroll
+      for (int ks = 0; ks < KS; ++ks)
+#pragma unroll
+        for (int e = 0; e < 8; ++e) d = fmaf((float)qreg[tt][ks][e], (float)kself[tt][ks][e], d);
+      mref[tt] = colsum(d) * c2;
+    }
   }
-  // Q must land before the DMA ring starts: the compiler does not see the
-  // ring's loads, so a deferred wait for Q inside the loop would drain them.
-  wait_vmcnt(0);
 
-  // ---- DMA descriptors: lane offsets are fixed, row bases change per stage ----
+  // ---- DMA descriptors ----
+  // A stage is 4 regions (K row 0, K row 1, V row 0, V row 1), each LWP keys of
+  // D bf16 in swizzled 16-byte chunks; wave w loads 1-KiB chunks w, w+4, ...
+  // One buffer descriptor per tensor covers both rows of the pair (the row
+  // offset is part of the lane offset; the record count stops at the last
+  // valid row, so rows past the window union read as zero).
+  const int64_t rowk = 2 * (int64_t)dy * p.ks[2], rowv = 2 * (int64_t)dy * p.vs[2];  // bytes per sub-grid row
   uint32_t voff[LPT];
+  bool vten[LPT];
 #pragma unroll
   for (int j = 0; j < LPT; ++j) {
-    const int gc = j * NWX + wave;          // 1-KiB chunk of the stage
-    const int tensor = (gc / RKB) >> 1;
+    const int gc = j * NWX + wave;  // 1-KiB chunk of the stage
+    const int reg = gc / RKB;
+    const int tensor = reg >> 1, row = reg & 1;
     const int key = (gc % RKB) * KPK + lane / CPK;
-    const int pc = lane % CPK;
-    const int c = swz(pc, key, CMASK);      // logical chunk stored at slot pc
+    const int c = swz(lane % CPK, key, CMASK);  // logical chunk stored at this slot
     const int64_t sx3 = tensor ? p.vs[3] : p.ks[3];
-    voff[j] = (key < LW && X0 + key < Lx) ? (uint32_t)((int64_t)(gx + dx * (X0 + key)) * sx3 * 2 + 16 * c) : OOB;
+    const int64_t rowb = tensor ? rowv : rowk;
+    voff[j] = (key < LW && X0 + key < Lx)
+                  ? (uint32_t)(row * rowb + (int64_t)(gx + dx * (X0 + key)) * sx3 * 2 + 16 * c)
+                  : OOB;
+    vten[j] = tensor;
   }
-  const char* kbase = (const char*)p.k + 2 * ((int64_t)b * p.ks[0] + (int64_t)h * p.ks[4]);
-  const char* vbase = (const char*)p.v + 2 * ((int64_t)b * p.vs[0] + (int64_t)h * p.vs[4]);
+  // Issue cursor: z-slice `cz`, pair `cp`; row pointers at the cursor.
+  const char* kz0p = (const char*)p.k + 2 * ((int64_t)b * p.ks[0] + (int64_t)h * p.ks[4] +
+                                             (int64_t)(gz + dz * sz) * p.ks[1] + (int64_t)(gy + dy * Y0) * p.ks[2]);
+  const char* vz0p = (const char*)p.v + 2 * ((int64_t)b * p.vs[0] + (int64_t)h * p.vs[4] +
+                                             (int64_t)(gz + dz * sz) * p.vs[1] + (int64_t)(gy + dy * Y0) * p.vs[2]);
+  const int64_t zstepk = 2 * (int64_t)dz * p.ks[1], zstepv = 2 * (int64_t)dz * p.vs[1];
+  int cz = 0, cp = 0;
+  const char* kcur = kz0p;
+  const char* vcur = vz0p;
+  uint32_t issue_off = 0;  // LDS byte offset of the ring slot the cursor fills
 
-  auto issue = [&](int s) {
-    const int dzi = s / NP;
-    const int pr = s - dzi * NP;
-    const int64_t zr = gz + dz * (sz + dzi);
-    char* dst = lds + (s % NBUF) * STAGE_B;
+  auto issue = [&]() {
+    const bool zok = cz < kz;
+    const uint32_t nk = !zok ? 0u : (2 * cp + 1 < NR ? (uint32_t)(2 * rowk) : (2 * cp < NR ? (uint32_t)rowk : 0u));
+    const uint32_t nv = !zok ? 0u : (2 * cp + 1 < NR ? (uint32_t)(2 * rowv) : (2 * cp < NR ? (uint32_t)rowv : 0u));
+    const u32x4 rk = make_rsrc(kcur, nk);
+    const u32x4 rv = make_rsrc(vcur, nv);
+    const uint32_t m0 = lds_base + issue_off + (uint32_t)wave * 1024;
 #pragma unroll
-    for (int j = 0; j < LPT; ++j) {
-      const int gc = j * NWX + wave;
-      const int reg = gc / RKB;
-      const int tensor = reg >> 1, row = reg & 1;
-      const int yrel = 2 * pr + row;
-      const bool ok = yrel < NR;
-      const int64_t st1 = tensor ? p.vs[1] : p.ks[1];
-      const int64_t st2 = tensor ? p.vs[2] : p.ks[2];
-      const char* base = (tensor ? vbase : kbase) +
-                         (ok ? 2 * (zr * st1 + (int64_t)(gy + dy * (Y0 + yrel)) * st2) : 0);
-      dma_row16(make_rsrc(base, ok ? OOB : 0u), lds_base + (uint32_t)(dst - lds) + gc * 1024, voff[j]);
+    for (int j = 0; j < LPT; ++j) dma_row16(vten[j] ? rv : rk, m0 + j * NWX * 1024, voff[j]);
+    // advance the cursor
+    issue_off = issue_off + STAGE_B == NBUF * STAGE_B ? 0 : issue_off + STAGE_B;
+    if (++cp == NP) {
+      cp = 0;
+      ++cz;
+      kz0p += zstepk;
+      vz0p += zstepv;
+      kcur = kz0p;
+      vcur = vz0p;
+    } else {
+      kcur += 2 * rowk;
+      vcur += 2 * rowv;
     }
   };
 
   // ---- LDS read offsets (bytes within a stage) ----
-  uint32_t koff[2][KS];
+  uint32_t koff[KS];
 #pragma unroll
-  for (int r = 0; r < 2; ++r)
-#pragma unroll
-    for (int ks = 0; ks < KS; ++ks) {
-      const int key = off_w + n16;
-      koff[r][ks] = r * RB + (key * D + 8 * swz(4 * ks + g, key, CMASK)) * 2;
-    }
+  for (int ks = 0; ks < KS; ++ks) {
+    const int key = off_w + n16;
+    koff[ks] = (key * D + 8 * swz(4 * ks + g, key, CMASK)) * 2;
+  }
   uint32_t voffs[DB];
   {
     const int keyv = off_w + 4 * g + (n16 >> 2);
@@ -369,38 +434,36 @@ __device__ __forceinline__ void na3d_mfma_body(const Na3dParams p, const Na3dTil
       voffs[db] = 2 * RB + (keyv * D + 8 * swz(2 * db + (dq >> 1), keyv, CMASK) + 4 * (dq & 1)) * 2;
   }
 
-  const float c2 = p.scale * 1.4426950408889634f;  // scores in log2 units
   f32x4 oacc[NTY][DB];
   f32x4 lacc[NTY];
-  float mrun[NTY];
+  float nb[NTY][4];  // xbias - mref
 #pragma unroll
   for (int tt = 0; tt < NTY; ++tt) {
 #pragma unroll
     for (int db = 0; db < DB; ++db) oacc[tt][db] = (f32x4){0.f, 0.f, 0.f, 0.f};
     lacc[tt] = (f32x4){0.f, 0.f, 0.f, 0.f};
-    mrun[tt] = -INFINITY;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) nb[tt][i] = xbias[i] - mref[tt];
   }
   typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
   const bf16x8_t ones = {(bf16)1.f, (bf16)1.f, (bf16)1.f, (bf16)1.f, (bf16)1.f, (bf16)1.f, (bf16)1.f, (bf16)1.f};
 
 #pragma unroll
-  for (int s = 0; s < NBUF - 1; ++s)
-    if (s < nstage) issue(s);
+  for (int s = 0; s < NBUF - 1; ++s) issue();
 
+  uint32_t cur_off = 0;  // ring slot of the stage being computed
+  int pr = 0;
   for (int s = 0; s < nstage; ++s) {
-    wait_vmcnt(min(NBUF - 2, nstage - 1 - s) * LPT);
+    wait_vmcnt((NBUF - 2) * LPT);  // constant: the tail issues empty (zero-record) stages
     lds_barrier();
-    if (s + NBUF - 1 < nstage) issue(s + NBUF - 1);
+    issue();
 
-    const char* st = lds + (s % NBUF) * STAGE_B;
-    const int pr = s % NP;
-    const int r0 = 2 * pr;
-
+    const char* st = lds + cur_off;
     bf16x8 ak[2][KS];
 #pragma unroll
     for (int r = 0; r < 2; ++r)
 #pragma unroll
-      for (int ks = 0; ks < KS; ++ks) ak[r][ks] = *(const bf16x8*)(st + koff[r][ks]);
+      for (int ks = 0; ks < KS; ++ks) ak[r][ks] = *(const bf16x8*)(st + r * RB + koff[ks]);
     bf16x8 av[DB];
 #pragma unroll
     for (int db = 0; db < DB; ++db) {
@@ -408,10 +471,11 @@ __device__ __forceinline__ void na3d_mfma_body(const Na3dParams p, const Na3dTil
       const bf16x4 hi = __builtin_amdgcn_ds_read_tr16_b64_v4bf16(LDS_PTR(bf16x4, st + voffs[db] + RB));
       av[db] = __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7);
     }
+    const int r0 = 2 * pr;
 
 #pragma unroll
     for (int tt = 0; tt < NTY; ++tt) {
-      if (r0 + 1 < U0[tt] || r0 >= U1[tt]) continue;  // rows outside this tile's window union
+      if (!((act_mask[tt] >> pr) & 1)) continue;  // rows outside this tile's window union
       f32x4 sacc[2];
 #pragma unroll
       for (int r = 0; r < 2; ++r) {
@@ -420,36 +484,39 @@ __device__ __forceinline__ void na3d_mfma_body(const Na3dParams p, const Na3dTil
         for (int ks = 0; ks < KS; ++ks)
           sacc[r] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ak[r][ks], qreg[tt][ks], sacc[r], 0, 0, 0);
       }
-      float tv[8];
-      if (r0 >= F0[tt] && r0 + 1 < F1[tt]) {
+      float u[8];
+      if (!((ym_mask[tt] >> pr) & 1)) {
         // both rows inside every window of the tile: only the x mask applies
 #pragma unroll
         for (int r = 0; r < 2; ++r)
 #pragma unroll
-          for (int i = 0; i < 4; ++i) tv[4 * r + i] = fmaf(sacc[r][i], c2, xbias[i]);
+          for (int i = 0; i < 4; ++i) u[4 * r + i] = fmaf(sacc[r][i], c2, nb[tt][i]);
       } else {
 #pragma unroll
         for (int r = 0; r < 2; ++r) {
           const int yr = r0 + r;
           const bool yok = yr >= syl[tt] && yr < syl[tt] + ky;
 #pragma unroll
-          for (int i = 0; i < 4; ++i) tv[4 * r + i] = fmaf(sacc[r][i], c2, yok ? xbias[i] : -INFINITY);
+          for (int i = 0; i < 4; ++i) u[4 * r + i] = fmaf(sacc[r][i], c2, yok ? nb[tt][i] : -INFINITY);
         }
       }
-      float mx = fmaxf(fmaxf(fmaxf(tv[0], tv[1]), fmaxf(tv[2], tv[3])), fmaxf(fmaxf(tv[4], tv[5]), fmaxf(tv[6], tv[7])));
+      float mx = fmaxf(fmaxf(fmaxf(u[0], u[1]), fmaxf(u[2], u[3])), fmaxf(fmaxf(u[4], u[5]), fmaxf(u[6], u[7])));
       mx = colmax(mx);
-      if (__builtin_amdgcn_ballot_w64(mx > mrun[tt] + TAU) != 0) {
-        const float mnew = fmaxf(mrun[tt], mx);
-        const float alpha = mnew == -INFINITY ? 1.f : __builtin_amdgcn_exp2f(mrun[tt] - mnew);
+      if (__builtin_amdgcn_ballot_w64(mx > TAU) != 0) {
+        // move the reference up by the excess (only where it exceeds TAU)
+        const float d = mx > TAU ? mx : 0.f;
+        const float alpha = __builtin_amdgcn_exp2f(-d);
 #pragma unroll
         for (int db = 0; db < DB; ++db) oacc[tt][db] *= alpha;
         lacc[tt] *= alpha;
-        mrun[tt] = mnew;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) nb[tt][i] -= d;
+#pragma unroll
+        for (int j = 0; j < 8; ++j) u[j] -= d;
       }
-      const float muse = mrun[tt] == -INFINITY ? 0.f : mrun[tt];
       float pv[8];
 #pragma unroll
-      for (int j = 0; j < 8; ++j) pv[j] = __builtin_amdgcn_exp2f(tv[j] - muse);
+      for (int j = 0; j < 8; ++j) pv[j] = __builtin_amdgcn_exp2f(u[j]);
       const u32x4 pw = {pack_bf16x2(pv[0], pv[1]), pack_bf16x2(pv[2], pv[3]), pack_bf16x2(pv[4], pv[5]),
                         pack_bf16x2(pv[6], pv[7])};
       const bf16x8 pb = __builtin_bit_cast(bf16x8, pw);
@@ -458,6 +525,8 @@ __device__ __forceinline__ void na3d_mfma_body(const Na3dParams p, const Na3dTil
       for (int db = 0; db < DB; ++db)
         oacc[tt][db] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(av[db], pb, oacc[tt][db], 0, 0, 0);
     }
+    cur_off = cur_off + STAGE_B == NBUF * STAGE_B ? 0 : cur_off + STAGE_B;
+    pr = pr + 1 == NP ? 0 : pr + 1;
   }
   wait_vmcnt(0);
 
@@ -626,9 +695,20 @@ extern "C" int strata_hip_na3d_fwd(const strata_hip_na3d_args* a, void* stream) 
     }
   }
   if (mfma_ok) {
-    // the buffer loads address one (z, y) row per descriptor with 32-bit byte offsets along x
-    const int64_t xspan_k = (int64_t)p.L[2] * p.ks[3] * 2 + 256, xspan_v = (int64_t)p.L[2] * p.vs[3] * 2 + 256;
-    if (xspan_k >= (int64_t)OOB || xspan_v >= (int64_t)OOB) mfma_ok = false;
+    // One buffer descriptor covers a pair of (z, y) key rows with 31-bit byte
+    // offsets: the x extent of a row must fit inside the row stride, two row
+    // strides must stay below the out-of-range offset, strides must be
+    // positive, and a workgroup's y-union (<= 16 + ky - 1 rows) must fit the
+    // 32-bit per-pair masks.
+    const int64_t* kv[2] = {p.ks, p.vs};
+    for (int t = 0; t < 2; ++t) {
+      const int64_t* sd = kv[t];
+      for (int i = 0; i < 5; ++i)
+        if (sd[i] <= 0 && !(i == 0 && p.B == 1) && !(i == 4 && p.H == 1)) mfma_ok = false;
+      if ((int64_t)(p.L[2] - 1) * sd[3] + p.D > sd[2]) mfma_ok = false;
+      if (4 * (int64_t)p.dil[1] * sd[2] * 2 >= (int64_t)OOB) mfma_ok = false;
+    }
+    if (16 + p.ker[1] - 1 > 64) mfma_ok = false;
   }
   if (!mfma_ok) return launch_scalar<bf16>(p, st);
   switch (p.D) {
