@@ -246,7 +246,10 @@ __device__ __forceinline__ void na3d_mfma_body(const Na3dParams p, const Na3dTil
   constexpr int KS = D / 32;              // k-steps of the QK MFMA
   constexpr int DB = D / 16;              // d-blocks of the PV MFMA
   constexpr int CMASK = CPK >= 8 ? 7 : CPK - 1;
-  constexpr float TAU = 8.f;              // lazy-rescale slack (log2 units)
+  // Lazy-rescale slack (log2 units): probabilities reach at most 2^TAU and the
+  // fp32 sums at most |W| * 2^TAU * max|v|, far inside fp32/bf16 range; terms
+  // more than 126 below the reference underflow, i.e. are < 2^-126 of the max.
+  constexpr float TAU = 64.f;
   static_assert(RB % 1024 == 0 && (4 * RKB) % NWX == 0, "stage layout");
 
   __shared__ __attribute__((aligned(1024))) char lds[NBUF * STAGE_B];
@@ -500,10 +503,11 @@ __device__ __forceinline__ void na3d_mfma_body(const Na3dParams p, const Na3dTil
           for (int i = 0; i < 4; ++i) u[4 * r + i] = fmaf(sacc[r][i], c2, yok ? nb[tt][i] : -INFINITY);
         }
       }
-      float mx = fmaxf(fmaxf(fmaxf(u[0], u[1]), fmaxf(u[2], u[3])), fmaxf(fmaxf(u[4], u[5]), fmaxf(u[6], u[7])));
-      mx = colmax(mx);
-      if (__builtin_amdgcn_ballot_w64(mx > TAU) != 0) {
-        // move the reference up by the excess (only where it exceeds TAU)
+      // The reference only has to move when some score exceeds it by TAU; the
+      // in-lane max decides that, the column max is needed only to move it.
+      const float ml = fmaxf(fmaxf(fmaxf(u[0], u[1]), fmaxf(u[2], u[3])), fmaxf(fmaxf(u[4], u[5]), fmaxf(u[6], u[7])));
+      if (__builtin_amdgcn_ballot_w64(ml > TAU) != 0) {
+        const float mx = colmax(ml);
         const float d = mx > TAU ? mx : 0.f;
         const float alpha = __builtin_amdgcn_exp2f(-d);
 #pragma unroll
