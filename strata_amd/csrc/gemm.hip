@@ -8,8 +8,9 @@
 // output columns of one row per accumulator quad, which the epilogue stores
 // as one 8-byte write after bias, GELU and residual.
 //
-// Workgroup tile BM x BN (rows of x x rows of w), K step 64, four waves in a
-// 2 x 2 arrangement, LDS double buffer filled from registers one K step ahead.
+// Two kernels: gemm_dma_kernel (K % 64 == 0; 256 x 256 tiles, 8 waves,
+// global->LDS streaming) for the block's GEMMs, and gemm_bias_act_kernel
+// (128 x 128 tiles, register-staged loads) for any other K.
 #include "common.h"
 
 namespace strata {
@@ -27,9 +28,11 @@ struct GemmParams {
 };
 
 __device__ __forceinline__ float gelu_tanh(float x) {
-  // 0.5 x (1 + tanh(sqrt(2/pi) (x + 0.044715 x^3)))
-  const float u = 0.7978845608028654f * fmaf(0.044715f * x * x, x, x);
-  return 0.5f * x * (1.f + tanhf(u));
+  // 0.5 x (1 + tanh(u)) with u = sqrt(2/pi) (x + 0.044715 x^3) equals
+  // x * sigmoid(2u) = x / (1 + 2^(-2u log2(e))): one exp2 and one reciprocal.
+  constexpr float k1 = 2.f * 1.4426950408889634f * 0.7978845608028654f;
+  const float t = x * fmaf(k1 * 0.044715f, x * x, k1);
+  return x * __builtin_amdgcn_rcpf(1.f + __builtin_amdgcn_exp2f(-t));
 }
 __device__ __forceinline__ float gelu_erf(float x) { return 0.5f * x * (1.f + erff(x * 0.7071067811865476f)); }
 
@@ -209,6 +212,226 @@ __global__ __launch_bounds__(64 * WGM * WGN) void gemm_bias_act_kernel(GemmParam
   }
 }
 
+// Epilogue for 4 consecutive output columns gn..gn+3 of row gm.
+__device__ __forceinline__ void store_quad(const GemmParams& p, int64_t gm, int64_t gn, float v0, float v1, float v2,
+                                           float v3) {
+  float v[4] = {v0, v1, v2, v3};
+  if (gm >= p.M || gn >= p.N) return;
+  const bool full = gn + 4 <= p.N;
+  if (p.bias) {
+    if (full) {
+      const u32x2 bw = *(const u32x2*)(p.bias + gn);
+      v[0] += bf16_lo(bw[0]);
+      v[1] += bf16_hi(bw[0]);
+      v[2] += bf16_lo(bw[1]);
+      v[3] += bf16_hi(bw[1]);
+    } else {
+      for (int e = 0; e < 4 && gn + e < p.N; ++e) v[e] += (float)p.bias[gn + e];
+    }
+  }
+  if (p.act == STRATA_HIP_ACT_GELU_TANH) {
+#pragma unroll
+    for (int e = 0; e < 4; ++e) v[e] = gelu_tanh(v[e]);
+  } else if (p.act == STRATA_HIP_ACT_GELU_ERF) {
+#pragma unroll
+    for (int e = 0; e < 4; ++e) v[e] = gelu_erf(v[e]);
+  }
+  if (full) {
+    if (p.res) {
+      const u32x2 rw = *(const u32x2*)(p.res + gm * p.ldr + gn);
+      v[0] += bf16_lo(rw[0]);
+      v[1] += bf16_hi(rw[0]);
+      v[2] += bf16_lo(rw[1]);
+      v[3] += bf16_hi(rw[1]);
+    }
+    const u32x2 ow = {pack_bf16x2(v[0], v[1]), pack_bf16x2(v[2], v[3])};
+    *(u32x2*)(p.out + gm * p.ldo + gn) = ow;
+  } else {
+    for (int e = 0; e < 4 && gn + e < p.N; ++e) {
+      float o = v[e];
+      if (p.res) o += (float)p.res[gm * p.ldr + gn + e];
+      p.out[gm * p.ldo + gn + e] = (bf16)o;
+    }
+  }
+}
+
+// Swizzle of the eight 16-byte chunks of a 128-byte LDS row: 32 consecutive
+// rows read at one logical chunk by ds_read_b128 land on distinct bank groups
+// whether the LDS serves 8 or 16 lanes per pass.
+__device__ __forceinline__ int gswz(int chunk, int row) { return chunk ^ ((row & 7) ^ ((row >> 3) & 1)); }
+
+// Large-tile GEMM for K % 64 == 0: a 256 x 256 output tile per workgroup of
+// 8 waves (2 along m x 4 along n, 128 x 64 each, v_mfma_f32_32x32x16_bf16),
+// K step 64, A/B tiles streamed from global memory straight into a
+// double-buffered LDS ring (buffer_load ... lds), one barrier per K step.
+#ifndef G_WAVES_M
+#define G_WAVES_M 2
+#define G_WAVES_N 4
+#endif
+constexpr int G_BM = 256, G_BN = 256, G_BK = 64, G_WGM = G_WAVES_M, G_WGN = G_WAVES_N;
+
+__global__ __launch_bounds__(64 * G_WAVES_M * G_WAVES_N, 1) void gemm_dma_kernel(GemmParams p) {
+  constexpr int NW = G_WGM * G_WGN;
+  constexpr int WTM = G_BM / G_WGM;  // 128
+  constexpr int WTN = G_BN / G_WGN;  // 64
+  constexpr int FM = WTM / 32, FN = WTN / 32;
+  constexpr int XB = G_BM * G_BK * 2;    // bytes of the x tile (32 KiB)
+  constexpr int STAGE = XB + G_BN * G_BK * 2;
+  constexpr int LPW = STAGE / 1024 / NW;  // 1-KiB loads per wave per stage (8)
+  __shared__ __attribute__((aligned(1024))) char lds[2 * STAGE];
+
+  const int wg = [&] {
+    const int id = (int)__builtin_amdgcn_workgroup_id_x(), n = p.mt * p.nt;
+    const int xcd = id & 7, local = id >> 3, q = n >> 3, rem = n & 7;
+    return xcd < rem ? xcd * (q + 1) + local : rem * (q + 1) + (xcd - rem) * q + local;
+  }();
+  const int tn = wg % p.nt;
+  const int tm = wg / p.nt;
+  const int64_t m0 = (int64_t)tm * G_BM;
+  const int64_t n0 = (int64_t)tn * G_BN;
+
+  const int tid = (int)__builtin_amdgcn_workitem_id_x();
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int lane = tid & 63;
+  const int wm = wave / G_WGN, wn = wave % G_WGN;
+  const int l32 = lane & 31, hi = lane >> 5;
+  const uint32_t lds_base = (uint32_t)(uintptr_t)(__attribute__((address_space(3))) char*)lds;
+
+  // DMA lane offsets: chunk c = j*NW + wave of a stage covers 8 rows of the x
+  // tile (c < 32) or of the w tile; lane i fills row 8*(c%32) + i/8, slot i%8.
+  uint32_t voff[LPW];
+#pragma unroll
+  for (int j = 0; j < LPW; ++j) {
+    const int c = j * NW + wave;
+    const bool isw = c >= 32;
+    const int row = 8 * (c & 31) + lane / 8;
+    const int lc = gswz(lane & 7, row);
+    const int64_t grow = (isw ? n0 : m0) + row;
+    const int64_t ld = isw ? p.ldw : p.ldx;
+    const bool ok = grow < (isw ? p.N : p.M);
+    voff[j] = ok ? (uint32_t)(row * ld * 2 + lc * 16) : OOB;
+  }
+  const char* xrow0 = (const char*)(p.x + m0 * p.ldx);
+  const char* wrow0 = (const char*)(p.w + n0 * p.ldw);
+  auto issue = [&](int kt, int buf) {
+    const u32x4 rx = make_rsrc(xrow0 + (int64_t)kt * G_BK * 2, OOB);
+    const u32x4 rw = make_rsrc(wrow0 + (int64_t)kt * G_BK * 2, OOB);
+    const uint32_t dst = lds_base + buf * STAGE + wave * 1024;
+#pragma unroll
+    for (int j = 0; j < LPW; ++j) dma_row16(j * NW + wave >= 32 ? rw : rx, dst + j * NW * 1024, voff[j]);
+  };
+
+  // LDS read offsets for the MFMA operands (kk adds 32 bytes before the swizzle).
+  uint32_t aoff[FN][2], boff[FM][2];  // [block][hi-chunk parity of kk]
+#pragma unroll
+  for (int i = 0; i < FN; ++i) {
+    const int row = wn * WTN + 32 * i + l32;
+    for (int kk = 0; kk < 2; ++kk) aoff[i][kk] = XB + row * 128 + gswz(2 * kk + hi, row) * 16;
+  }
+#pragma unroll
+  for (int j = 0; j < FM; ++j) {
+    const int row = wm * WTM + 32 * j + l32;
+    for (int kk = 0; kk < 2; ++kk) boff[j][kk] = row * 128 + gswz(2 * kk + hi, row) * 16;
+  }
+
+  f32x16 acc[FN][FM];
+#pragma unroll
+  for (int i = 0; i < FN; ++i)
+#pragma unroll
+    for (int j = 0; j < FM; ++j)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.f;
+
+  const int nk = (int)(p.K / G_BK);
+  issue(0, 0);
+  for (int kt = 0; kt < nk; ++kt) {
+    wait_vmcnt(0);
+    lds_barrier();
+    if (kt + 1 < nk) issue(kt + 1, (kt + 1) & 1);
+    const char* st = lds + (kt & 1) * STAGE;
+#pragma unroll
+    for (int kk = 0; kk < G_BK / 16; ++kk) {
+      // chunk 2*kk + hi = 4*(kk/2) + (2*(kk&1) + hi): the kk/2 part flips bit 2 of the slot
+      bf16x8 af[FN], bfr[FM];
+#pragma unroll
+      for (int i = 0; i < FN; ++i) af[i] = *(const bf16x8*)(st + (aoff[i][kk & 1] ^ ((kk >> 1) * 64)));
+#pragma unroll
+      for (int j = 0; j < FM; ++j) bfr[j] = *(const bf16x8*)(st + (boff[j][kk & 1] ^ ((kk >> 1) * 64)));
+#pragma unroll
+      for (int i = 0; i < FN; ++i)
+#pragma unroll
+        for (int j = 0; j < FM; ++j)
+          acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(af[i], bfr[j], acc[i][j], 0, 0, 0);
+    }
+  }
+
+  // ---- epilogue through LDS ----
+  // Phase 1: bias + activation on the accumulators, bf16 into this wave's
+  // 128 x 64 slab of LDS (rows of 128 bytes, 16-byte chunks swizzled by row).
+  // Phase 2: each lane reads 16 contiguous bytes of a row, adds the residual
+  // read the same way, and writes 16 bytes: 8 lanes cover a 128-byte row.
+  lds_barrier();  // every wave is done reading the last stage
+  char* slab = lds + wave * (WTM * WTN * 2);
+  const int64_t gn0 = n0 + wn * WTN, gm0 = m0 + wm * WTM;
+#pragma unroll
+  for (int i = 0; i < FN; ++i)
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      const int nl = 32 * i + 8 * q + 4 * hi;  // local column of this lane's quad
+      float bv[4] = {0.f, 0.f, 0.f, 0.f};
+      if (p.bias) {
+        const int64_t gn = gn0 + nl;
+        if (gn + 4 <= p.N) {
+          const u32x2 bw = *(const u32x2*)(p.bias + gn);
+          bv[0] = bf16_lo(bw[0]);
+          bv[1] = bf16_hi(bw[0]);
+          bv[2] = bf16_lo(bw[1]);
+          bv[3] = bf16_hi(bw[1]);
+        } else {
+          for (int e = 0; e < 4; ++e) bv[e] = gn + e < p.N ? (float)p.bias[gn + e] : 0.f;
+        }
+      }
+#pragma unroll
+      for (int j = 0; j < FM; ++j) {
+        float v[4];
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          v[e] = acc[i][j][4 * q + e] + bv[e];
+          if (p.act == STRATA_HIP_ACT_GELU_TANH) v[e] = gelu_tanh(v[e]);
+          else if (p.act == STRATA_HIP_ACT_GELU_ERF) v[e] = gelu_erf(v[e]);
+        }
+        const int ml = 32 * j + l32;
+        const u32x2 w2 = {pack_bf16x2(v[0], v[1]), pack_bf16x2(v[2], v[3])};
+        *(u32x2*)(slab + ml * 128 + (((nl >> 3) ^ (ml & 7)) << 4) + 8 * hi) = w2;
+      }
+    }
+#pragma unroll 4
+  for (int it = 0; it < WTM / 8; ++it) {
+    const int ml = 8 * it + (lane >> 3);
+    const int c = lane & 7;  // logical 16-byte chunk = 8 output columns
+    const u32x4 w4 = *(const u32x4*)(slab + ml * 128 + ((c ^ (ml & 7)) << 4));
+    const int64_t gm = gm0 + ml, gn = gn0 + 8 * c;
+    if (gm >= p.M || gn >= p.N) continue;
+    if (gn + 8 <= p.N) {
+      u32x4 o = w4;
+      if (p.res) {
+        const u32x4 r4 = *(const u32x4*)(p.res + gm * p.ldr + gn);
+#pragma unroll
+        for (int e = 0; e < 4; ++e)
+          o[e] = pack_bf16x2(bf16_lo(w4[e]) + bf16_lo(r4[e]), bf16_hi(w4[e]) + bf16_hi(r4[e]));
+      }
+      *(u32x4*)(p.out + gm * p.ldo + gn) = o;
+    } else {
+      for (int e = 0; e < 8 && gn + e < p.N; ++e) {
+        const uint32_t wd = w4[e >> 1];
+        float o = (e & 1) ? bf16_hi(wd) : bf16_lo(wd);
+        if (p.res) o += (float)p.res[gm * p.ldr + gn + e];
+        p.out[gm * p.ldo + gn + e] = (bf16)o;
+      }
+    }
+  }
+}
+
 template <int BM, int BN, int WGM, int WGN>
 static int launch_gemm(GemmParams p, hipStream_t st) {
   p.mt = (int)((p.M + BM - 1) / BM);
@@ -251,5 +474,17 @@ extern "C" int strata_hip_gemm_bias_act(const strata_hip_gemm_args* a, void* str
   p.ldr = a->ldr;
   p.ldo = a->ldo;
   p.act = a->act;
-  return launch_gemm<128, 128, 2, 2>(p, (hipStream_t)stream);
+  hipStream_t st = (hipStream_t)stream;
+  // The large-tile kernel streams 64-wide K steps with 32-bit lane offsets
+  // inside a 256-row block: K a multiple of 64, row strides small enough.
+  const bool big = p.K % G_BK == 0 && 256 * p.ldx * 2 + 4096 < (int64_t)OOB && 256 * p.ldw * 2 + 4096 < (int64_t)OOB;
+  if (big) {
+    p.mt = (int)((p.M + G_BM - 1) / G_BM);
+    p.nt = (int)((p.N + G_BN - 1) / G_BN);
+    const int64_t total = (int64_t)p.mt * p.nt;
+    if (total > 0x7fffffff) return fail(STRATA_HIP_EUNSUPPORTED, "gemm: problem too large for one launch");
+    hipLaunchKernelGGL(gemm_dma_kernel, dim3((unsigned)total), dim3(64 * G_WGM * G_WGN), 0, st, p);
+    return check_launch("gemm_dma_kernel");
+  }
+  return launch_gemm<128, 128, 2, 2>(p, st);
 }

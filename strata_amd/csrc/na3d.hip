@@ -147,54 +147,8 @@ __device__ __forceinline__ float colmax(float x) {
   return fmaxf(__uint_as_float(b[0]), __uint_as_float(b[1]));
 }
 
-__device__ __forceinline__ void wait_vmcnt(int n) {
-  // gfx9 s_waitcnt immediate: vmcnt[3:0] | expcnt[6:4] | lgkmcnt[11:8] | vmcnt[5:4] at [15:14]
-  switch (n) {
-#define STRATA_VMCNT(N) \
-  case N:               \
-    __builtin_amdgcn_s_waitcnt(((N) & 15) | (7 << 4) | (15 << 8) | (((N) >> 4) << 14)); \
-    break;
-    STRATA_VMCNT(0) STRATA_VMCNT(1) STRATA_VMCNT(2) STRATA_VMCNT(3) STRATA_VMCNT(4) STRATA_VMCNT(5)
-    STRATA_VMCNT(6) STRATA_VMCNT(7) STRATA_VMCNT(8) STRATA_VMCNT(9) STRATA_VMCNT(10) STRATA_VMCNT(11)
-    STRATA_VMCNT(12) STRATA_VMCNT(13) STRATA_VMCNT(14) STRATA_VMCNT(15) STRATA_VMCNT(16)
-#undef STRATA_VMCNT
-    default:
-      __builtin_amdgcn_s_waitcnt((7 << 4) | (15 << 8));  // vmcnt(0)
-  }
-}
-
-// One 1-KiB global->LDS copy: lane i's 16 bytes at `voff` within the buffer
-// described by `rsrc` land at LDS byte address `lds_addr + 16*i`; offsets
-// beyond the descriptor's record count read as zero.  Issued as inline asm so
-// that the compiler does not add its own conservative vmcnt(0) before every
-// later LDS read (it cannot tell the ring slots apart); completion is tracked
-// explicitly with wait_vmcnt() before the barrier that publishes a stage.
-__device__ __forceinline__ void dma_row16(u32x4 rsrc, uint32_t lds_addr, uint32_t voff) {
-  asm volatile(
-      "s_mov_b32 m0, %0\n\t"
-      "s_nop 0\n\t"
-      "buffer_load_dwordx4 %1, %2, 0 offen lds" ::"s"(lds_addr),
-      "v"(voff), "s"(rsrc)
-      : "memory", "m0");
-}
-
-__device__ __forceinline__ u32x4 make_rsrc(const void* base, uint32_t num_records) {
-  const uint64_t a = (uint64_t)base;
-  // dword1 holds base[47:32] with stride 0; dword3 = gfx9 data/num format for raw buffers.
-  // Every operand is workgroup-uniform; readfirstlane pins the descriptor in SGPRs.
-  const uint32_t lo = (uint32_t)__builtin_amdgcn_readfirstlane((int)(uint32_t)a);
-  const uint32_t hi = (uint32_t)__builtin_amdgcn_readfirstlane((int)((uint32_t)(a >> 32) & 0xffffu));
-  const uint32_t nr = (uint32_t)__builtin_amdgcn_readfirstlane((int)num_records);
-  return (u32x4){lo, hi, nr, 0x00020000u};
-}
-
-// Workgroup barrier without the release/acquire fences of __syncthreads():
-// those would also wait for the in-flight global->LDS loads of later stages.
-// LDS visibility is established by each wave's own vmcnt wait before it.
-__device__ __forceinline__ void lds_barrier() { asm volatile("s_barrier" ::: "memory"); }
 
 constexpr int NA3D_NWX = 4;          // waves per workgroup, side by side along x
-constexpr uint32_t OOB = 0x7ffffff0u;  // lane offset that reads as zero (beyond any record count)
 
 // Sum over lanes l, l^16, l^32 (the four lanes of one MFMA output column).
 __device__ __forceinline__ float colsum(float x) {
