@@ -7,10 +7,11 @@ One step = one NA3D launch over the whole batch; inputs are resident in HBM.
 FLOPs = 4 * N_q(interior) * |W| * D per head.
 
 Also reported: the full Strata block tokens/s with a per-kernel
-breakdown and the RoPE+QKV-pack prologue's HBM GB/s, the roofline of the
-dominant kernel, and the CPU oracle timed on a bounded sample on this host.
+breakdown and the RoPE+QKV-pack prologue's HBM GB/s, the configs[4] two-stage
+4-step rollout, the roofline of the dominant kernel, and the CPU oracle timed
+on a bounded sample on this host.
 
-    python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-block] [--no-cpu]
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-block] [--no-rollout] [--no-cpu]
 """
 
 from __future__ import annotations
@@ -153,6 +154,47 @@ def bench_block(device, steps, warmup):
     }
 
 
+def bench_rollout(device, reps, warmup):
+    """two-stage model (12 blocks @768 on (16,64,64), 2x merge, 12 blocks
+    @1024 on (8,32,32)), batch 6 face tiles, 80 channels, 4 autoregressive steps."""
+    import torch
+
+    from strata_amd import rope as P
+    from strata_amd.model import TwoStageStrata
+    from strata_amd.modules import init_xavier_
+
+    model = TwoStageStrata()
+    init_xavier_(model, torch.Generator().manual_seed(1))
+    model = model.to(device).bfloat16().eval()
+    g = torch.Generator(device=device).manual_seed(0)
+    x = torch.randn(6, 80, 16, 64, 64, generator=g, device=device).bfloat16()
+    lat, lon = P.synthetic_tile_latlon(6, 64, 64, torch.Generator().manual_seed(0))
+    rope1, rope2 = model.rope_tables(lat.to(device), lon.to(device))
+    steps = 4
+    for _ in range(warmup):
+        model.rollout(x, steps, rope1, rope2)
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record()
+    for _ in range(reps):
+        y = model.rollout(x, steps, rope1, rope2)
+    e1.record()
+    torch.cuda.synchronize()
+    ms = e0.elapsed_time(e1) / reps
+    flops = model.step_flops(6, (16, 64, 64)) * steps
+    tokens = 6 * 16 * 64 * 64 * steps
+    assert torch.isfinite(y.float()).all(), "rollout produced non-finite values"
+    return {
+        "workload": "configs[4] two-stage rollout: B=6 tiles, 80 ch, s1 12x(768, 12x64, W=(3,7,7)) on (16,64,64), "
+        "2x merge, s2 12x(1024, 16x64, W=(3,9,9)) on (8,32,32), 4 steps, Xavier seed 1",
+        "rollout_ms": round(ms, 2),
+        "step_ms": round(ms / steps, 2),
+        "tokens_per_s": tokens / (ms * 1e-3),
+        "block_tflops": round(flops / (ms * 1e-3) / 1e12, 1),
+        "pct_bf16_peak": round(100.0 * flops / (ms * 1e-3) / 1e12 / PEAK_BF16_TFLOPS, 2),
+    }
+
+
 def cpu_baseline():
     """The CPU oracle on a bounded sample of configs[2]: tile 0, head 0, 4 z-slices."""
     import torch
@@ -202,6 +244,7 @@ def main():
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--no-block", action="store_true")
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--no-rollout", action="store_true")
     ap.add_argument(
         "--copy-calibration",
         action="store_true",
@@ -281,6 +324,9 @@ def main():
     if not args.no_block:
         log("bench: timing the configs[3] block")
         result["block"] = bench_block(dev, max(3, args.steps // 2), 2)
+    if not args.no_rollout:
+        log("bench: timing the configs[4] rollout")
+        result["rollout"] = bench_rollout(dev, 2, 1)
     if not args.no_cpu:
         log("bench: timing the CPU oracle sample")
         result["cpu_baseline"] = cpu_baseline()

@@ -82,3 +82,11 @@ def apply_rope(t: Tensor, cos: Tensor, sin: Tensor, layout: str = "half") -> Ten
         a, b = t[..., 0::2], t[..., 1::2]
         return torch.stack([a * c - b * s, a * s + b * c], dim=-1).reshape(t.shape)
     raise ValueError(f"unknown rope layout {layout!r}")
+
+
+def pooled_latlon(lat: Tensor, lon: Tensor, f: int = 2) -> tuple[Tensor, Tensor]:
+    """Spherical centroid of each f x f block of pixels: ``[B, Y, X]`` -> ``[B, Y/f, X/f]``."""
+    B, Y, X = lat.shape
+    v = unit_vectors(lat, lon).view(B, Y // f, f, X // f, f, 3).sum(dim=(2, 4))
+    v = v / v.norm(dim=-1, keepdim=True)
+    return torch.asin(v[..., 2]), torch.atan2(v[..., 1], v[..., 0])
