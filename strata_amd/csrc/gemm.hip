@@ -255,30 +255,47 @@ __device__ __forceinline__ void store_quad(const GemmParams& p, int64_t gm, int6
   }
 }
 
-// Swizzle of the eight 16-byte chunks of a 128-byte LDS row: 32 consecutive
-// rows read at one logical chunk by ds_read_b128 land on distinct bank groups
-// whether the LDS serves 8 or 16 lanes per pass.
-__device__ __forceinline__ int gswz(int chunk, int row) { return chunk ^ ((row & 7) ^ ((row >> 3) & 1)); }
+// Swizzle of the 16-byte chunks of an LDS row (CH chunks of a BK-wide row):
+// the 16 consecutive rows that one pass of a ds_read_b128 serves, all at the
+// same logical chunk, land on 16 distinct 16-byte bank groups.
+//   CH = 8 (128-byte rows): two rows share a 256-byte bank line;
+//   CH = 4 (64-byte rows): four rows share one.
+template <int CH>
+__device__ __forceinline__ int gswz(int chunk, int row) {
+  if constexpr (CH == 8) return chunk ^ ((row & 7) ^ ((row >> 3) & 1));
+  else return chunk ^ ((row >> 2) & 3);
+}
 
-// Large-tile GEMM for K % 64 == 0: a 256 x 256 output tile per workgroup of
-// 8 waves (2 along m x 4 along n, 128 x 64 each, v_mfma_f32_32x32x16_bf16),
-// K step 64, A/B tiles streamed from global memory straight into a
-// double-buffered LDS ring (buffer_load ... lds), one barrier per K step.
-#ifndef G_WAVES_M
-#define G_WAVES_M 2
-#define G_WAVES_N 4
+// Large-tile GEMM for K % G_BK == 0: a 256 x 256 output tile per workgroup of
+// 8 waves (2 along m x 4 along n, 128 x 64 each, v_mfma_f32_32x32x16_bf16).
+// A/B tiles of G_BK columns stream from global memory straight into an LDS
+// ring of G_NST stages (buffer_load ... lds) that runs G_NST - 1 stages ahead
+// of the MFMAs, one barrier per stage.
+#ifndef G_BK_COLS
+#define G_BK_COLS 64
 #endif
-constexpr int G_BM = 256, G_BN = 256, G_BK = 64, G_WGM = G_WAVES_M, G_WGN = G_WAVES_N;
+#ifndef G_STAGES
+#define G_STAGES 2
+#endif
+constexpr int G_BM = 256, G_BN = 256, G_BK = G_BK_COLS, G_NST = G_STAGES, G_WGM = 2, G_WGN = 4;
 
-__global__ __launch_bounds__(64 * G_WAVES_M * G_WAVES_N, 1) void gemm_dma_kernel(GemmParams p) {
+__global__ __launch_bounds__(64 * G_WGM * G_WGN, 1) void gemm_dma_kernel(GemmParams p) {
   constexpr int NW = G_WGM * G_WGN;
   constexpr int WTM = G_BM / G_WGM;  // 128
   constexpr int WTN = G_BN / G_WGN;  // 64
   constexpr int FM = WTM / 32, FN = WTN / 32;
-  constexpr int XB = G_BM * G_BK * 2;    // bytes of the x tile (32 KiB)
-  constexpr int STAGE = XB + G_BN * G_BK * 2;
-  constexpr int LPW = STAGE / 1024 / NW;  // 1-KiB loads per wave per stage (8)
-  __shared__ __attribute__((aligned(1024))) char lds[2 * STAGE];
+  constexpr int ROWB = G_BK * 2;          // bytes of one tile row in a stage
+  constexpr int CH = ROWB / 16;           // 16-byte chunks per row
+  constexpr int RPC = 1024 / ROWB;        // rows per 1-KiB DMA
+  constexpr int XB = G_BM * ROWB;         // bytes of the x tile
+  constexpr int XCH = XB / 1024;          // 1-KiB DMAs of the x tile
+  constexpr int STAGE = XB + G_BN * ROWB;
+  constexpr int LPW = STAGE / 1024 / NW;  // 1-KiB DMAs per wave per stage
+  constexpr int PD = G_NST - 1;           // stages in flight ahead of the MFMAs
+  static_assert(CH == 4 || CH == 8, "G_BK must be 32 or 64");
+  constexpr int LDS_BYTES = G_NST * STAGE > NW * WTM * WTN * 2 ? G_NST * STAGE : NW * WTM * WTN * 2;
+  static_assert((PD - 1) * LPW <= 16, "wait_vmcnt range");
+  __shared__ __attribute__((aligned(1024))) char lds[LDS_BYTES];  // ring, then the epilogue slabs
 
   const int wg = [&] {
     const int id = (int)__builtin_amdgcn_workgroup_id_x(), n = p.mt * p.nt;
@@ -297,15 +314,15 @@ __global__ __launch_bounds__(64 * G_WAVES_M * G_WAVES_N, 1) void gemm_dma_kernel
   const int l32 = lane & 31, hi = lane >> 5;
   const uint32_t lds_base = (uint32_t)(uintptr_t)(__attribute__((address_space(3))) char*)lds;
 
-  // DMA lane offsets: chunk c = j*NW + wave of a stage covers 8 rows of the x
-  // tile (c < 32) or of the w tile; lane i fills row 8*(c%32) + i/8, slot i%8.
+  // DMA lane offsets: DMA c = j*NW + wave of a stage covers RPC rows of the x
+  // tile (c < XCH) or of the w tile; lane i fills row RPC*(c%XCH) + i/CH, slot i%CH.
   uint32_t voff[LPW];
 #pragma unroll
   for (int j = 0; j < LPW; ++j) {
     const int c = j * NW + wave;
-    const bool isw = c >= 32;
-    const int row = 8 * (c & 31) + lane / 8;
-    const int lc = gswz(lane & 7, row);
+    const bool isw = c >= XCH;
+    const int row = RPC * (c % XCH) + lane / CH;
+    const int lc = gswz<CH>(lane % CH, row);
     const int64_t grow = (isw ? n0 : m0) + row;
     const int64_t ld = isw ? p.ldw : p.ldx;
     const bool ok = grow < (isw ? p.N : p.M);
@@ -318,20 +335,21 @@ __global__ __launch_bounds__(64 * G_WAVES_M * G_WAVES_N, 1) void gemm_dma_kernel
     const u32x4 rw = make_rsrc(wrow0 + (int64_t)kt * G_BK * 2, OOB);
     const uint32_t dst = lds_base + buf * STAGE + wave * 1024;
 #pragma unroll
-    for (int j = 0; j < LPW; ++j) dma_row16(j * NW + wave >= 32 ? rw : rx, dst + j * NW * 1024, voff[j]);
+    for (int j = 0; j < LPW; ++j) dma_row16(j * NW + wave >= XCH ? rw : rx, dst + j * NW * 1024, voff[j]);
   };
 
-  // LDS read offsets for the MFMA operands (kk adds 32 bytes before the swizzle).
-  uint32_t aoff[FN][2], boff[FM][2];  // [block][hi-chunk parity of kk]
+  // LDS read offsets of the MFMA operands for K sub-steps kk = 0, 1; kk = 2, 3
+  // (64-wide stages) flip bit 2 of the chunk, i.e. byte offset ^ 64.
+  uint32_t aoff[FN][2], boff[FM][2];
 #pragma unroll
   for (int i = 0; i < FN; ++i) {
     const int row = wn * WTN + 32 * i + l32;
-    for (int kk = 0; kk < 2; ++kk) aoff[i][kk] = XB + row * 128 + gswz(2 * kk + hi, row) * 16;
+    for (int kk = 0; kk < 2; ++kk) aoff[i][kk] = XB + row * ROWB + gswz<CH>(2 * kk + hi, row) * 16;
   }
 #pragma unroll
   for (int j = 0; j < FM; ++j) {
     const int row = wm * WTM + 32 * j + l32;
-    for (int kk = 0; kk < 2; ++kk) boff[j][kk] = row * 128 + gswz(2 * kk + hi, row) * 16;
+    for (int kk = 0; kk < 2; ++kk) boff[j][kk] = row * ROWB + gswz<CH>(2 * kk + hi, row) * 16;
   }
 
   f32x16 acc[FN][FM];
@@ -343,15 +361,23 @@ __global__ __launch_bounds__(64 * G_WAVES_M * G_WAVES_N, 1) void gemm_dma_kernel
       for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.f;
 
   const int nk = (int)(p.K / G_BK);
-  issue(0, 0);
+#pragma unroll
+  for (int s = 0; s < PD; ++s)
+    if (s < nk) issue(s, s);
+  int rd = 0, wr = PD;  // ring slots read by this stage / filled by the next issue
   for (int kt = 0; kt < nk; ++kt) {
-    wait_vmcnt(0);
+    // stage kt has landed once at most (stages issued after it) x LPW DMAs are pending
+    const int later = min(PD - 1, nk - 1 - kt);
+    wait_vmcnt(later * LPW);
     lds_barrier();
-    if (kt + 1 < nk) issue(kt + 1, (kt + 1) & 1);
-    const char* st = lds + (kt & 1) * STAGE;
+    if (kt + PD < nk) {
+      issue(kt + PD, wr);
+      wr = wr + 1 == G_NST ? 0 : wr + 1;
+    }
+    const char* st = lds + rd * STAGE;
+    rd = rd + 1 == G_NST ? 0 : rd + 1;
 #pragma unroll
     for (int kk = 0; kk < G_BK / 16; ++kk) {
-      // chunk 2*kk + hi = 4*(kk/2) + (2*(kk&1) + hi): the kk/2 part flips bit 2 of the slot
       bf16x8 af[FN], bfr[FM];
 #pragma unroll
       for (int i = 0; i < FN; ++i) af[i] = *(const bf16x8*)(st + (aoff[i][kk & 1] ^ ((kk >> 1) * 64)));
@@ -475,7 +501,7 @@ extern "C" int strata_hip_gemm_bias_act(const strata_hip_gemm_args* a, void* str
   p.ldo = a->ldo;
   p.act = a->act;
   hipStream_t st = (hipStream_t)stream;
-  // The large-tile kernel streams 64-wide K steps with 32-bit lane offsets
+  // The large-tile kernel streams G_BK-wide K steps with 32-bit lane offsets
   // inside a 256-row block: K a multiple of 64, row strides small enough.
   const bool big = p.K % G_BK == 0 && 256 * p.ldx * 2 + 4096 < (int64_t)OOB && 256 * p.ldw * 2 + 4096 < (int64_t)OOB;
   if (big) {

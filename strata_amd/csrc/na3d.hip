@@ -127,14 +127,41 @@ __device__ __forceinline__ int xcd_tile_order(int n) {
   return xcd < rem ? xcd * (q + 1) + local : rem * (q + 1) + (xcd - rem) * q + local;
 }
 
-// Swizzle of the 16-byte chunks of one key row in LDS.  f(key) permutes
-// 0..7 so that (a) any 8 consecutive keys read at one chunk hit 8 distinct
-// chunk slots (K reads, ds_read_b128) and (b) any 4 consecutive keys read at
-// a chunk pair {2c, 2c+1} hit 4 distinct pairs (V transpose reads).
-__device__ __forceinline__ int swz(int chunk, int key, int cmask) {
-  const int f = 2 * (key & 3) + ((key >> 2) & 1);
-  return chunk ^ (f & cmask);
+// Tile (z, y, x) of the w-th workgroup of one (batch, head, residue class):
+// 4 x 4 x 4 blocks of tiles (smaller at the grid's far edges), x fastest
+// inside a block.  The ~64 workgroups an XCD runs at once then cover one
+// compact block whose z and x/y halos overlap, so the overlapping key rows
+// are read from HBM once and from L2 by the neighbours.
+__device__ __forceinline__ void blocked_tile(int w, int nz, int ny, int nx, int& z, int& y, int& x) {
+  constexpr int BZ = 4, BY = 4, BX = 4;
+  const int zb = w / (BZ * ny * nx);
+  int r = w - zb * BZ * ny * nx;
+  const int bz = min(BZ, nz - zb * BZ);
+  const int yb = r / (bz * BY * nx);
+  r -= yb * bz * BY * nx;
+  const int by = min(BY, ny - yb * BY);
+  const int xb = r / (bz * by * BX);
+  r -= xb * bz * by * BX;
+  const int bx = min(BX, nx - xb * BX);
+  x = xb * BX + r % bx;
+  r /= bx;
+  y = yb * BY + r % by;
+  z = zb * BZ + r / by;
 }
+
+// Swizzle of the 16-byte chunks of one key row (D bf16 = D/8 chunks) in LDS:
+// logical chunk c of key `key` sits at slot c ^ f(key).  f is chosen by
+// measurement (SQ_LDS_BANK_CONFLICT of the exact K ds_read_b128 and V
+// ds_read_b64_tr_b16 address streams of the kernel, every window offset):
+//   D = 32: f = (key >> 1) & 3,  D = 64: f = key & 7,  D = 128: f = (key & 7) << 1
+// -- no conflicts on either read for any window offset.
+template <int D>
+__device__ __forceinline__ int swz(int chunk, int key) {
+  if constexpr (D == 32) return chunk ^ ((key >> 1) & 3);
+  else if constexpr (D == 64) return chunk ^ (key & 7);
+  else return chunk ^ ((key & 7) << 1);
+}
+
 
 // Cross-lane max over lanes l, l^16 and l^32 (the four lanes of one MFMA
 // output column) with the gfx950 permlane swaps.
@@ -180,8 +207,10 @@ __device__ __forceinline__ uint32_t bit_range(int lo, int hi) {
 // Softmax: scores live in log2 units, u = s*scale*log2(e) - m, where m is a
 // per-query reference that starts at the query's score against its own key
 // (always inside its window) and only moves up, lazily, when a stage's
-// maximum exceeds it by more than TAU.  The subtraction and the window mask
-// fold into one FMA per score: u = fma(s, c2, bias - m), bias in {0, -inf}.
+// maximum exceeds it by more than TAU.  Q is pre-scaled by scale*log2(e) and
+// the QK MFMA starts from C = bias - m (bias in {0, -inf} per key for the x
+// mask), so the MFMA itself returns u and no VALU work sits between the scores
+// and the exponentials outside the boundary rows of the y mask.
 template <int D, int TX, int NTY, int NBUF>
 __device__ __forceinline__ void na3d_mfma_body(const Na3dParams p, const Na3dTiles tg) {
 #if defined(__HIP_DEVICE_COMPILE__)  // the body is device code only; the host pass needs just the signature
@@ -199,7 +228,6 @@ __device__ __forceinline__ void na3d_mfma_body(const Na3dParams p, const Na3dTil
   constexpr int CPK = D / 8;              // 16-byte chunks per key
   constexpr int KS = D / 32;              // k-steps of the QK MFMA
   constexpr int DB = D / 16;              // d-blocks of the PV MFMA
-  constexpr int CMASK = CPK >= 8 ? 7 : CPK - 1;
   // Lazy-rescale slack (log2 units): probabilities reach at most 2^TAU and the
   // fp32 sums at most |W| * 2^TAU * max|v|, far inside fp32/bf16 range; terms
   // more than 126 below the reference underflow, i.e. are < 2^-126 of the max.
@@ -209,12 +237,10 @@ __device__ __forceinline__ void na3d_mfma_body(const Na3dParams p, const Na3dTil
   __shared__ __attribute__((aligned(1024))) char lds[NBUF * STAGE_B];
 
   const int wg = xcd_tile_order(tg.total);
-  const int xt = wg % tg.nxt;
-  int t = wg / tg.nxt;
-  const int yt = t % tg.nyt;
-  t /= tg.nyt;
-  const int zt = t % tg.nzt;
-  t /= tg.nzt;
+  const int per = tg.nxt * tg.nyt * tg.nzt;
+  int t = wg / per;
+  int zt, yt, xt;
+  blocked_tile(wg - t * per, tg.nzt, tg.nyt, tg.nxt, zt, yt, xt);
   const int res = t % tg.nres;
   t /= tg.nres;
   const int h = t % p.H;
@@ -312,8 +338,11 @@ __device__ __forceinline__ void na3d_mfma_body(const Na3dParams p, const Na3dTil
 #pragma unroll
       for (int ks = 0; ks < KS; ++ks)
 #pragma unroll
-        for (int e = 0; e < 8; ++e) d = fmaf((float)qreg[tt][ks][e], (float)kself[tt][ks][e], d);
-      mref[tt] = colsum(d) * c2;
+        for (int e = 0; e < 8; ++e) {
+          qreg[tt][ks][e] = (bf16)((float)qreg[tt][ks][e] * c2);  // scores in log2 units
+          d = fmaf((float)qreg[tt][ks][e], (float)kself[tt][ks][e], d);
+        }
+      mref[tt] = colsum(d);
     }
   }
 
@@ -332,7 +361,7 @@ __device__ __forceinline__ void na3d_mfma_body(const Na3dParams p, const Na3dTil
     const int reg = gc / RKB;
     const int tensor = reg >> 1, row = reg & 1;
     const int key = (gc % RKB) * KPK + lane / CPK;
-    const int c = swz(lane % CPK, key, CMASK);  // logical chunk stored at this slot
+    const int c = swz<D>(lane % CPK, key);  // logical chunk stored at this slot
     const int64_t sx3 = tensor ? p.vs[3] : p.ks[3];
     const int64_t rowb = tensor ? rowv : rowk;
     voff[j] = (key < LW && X0 + key < Lx)
@@ -340,21 +369,22 @@ __device__ __forceinline__ void na3d_mfma_body(const Na3dParams p, const Na3dTil
                   : OOB;
     vten[j] = tensor;
   }
-  // Issue cursor: z-slice `cz`, pair `cp`; row pointers at the cursor.
-  const char* kz0p = (const char*)p.k + 2 * ((int64_t)b * p.ks[0] + (int64_t)h * p.ks[4] +
-                                             (int64_t)(gz + dz * sz) * p.ks[1] + (int64_t)(gy + dy * Y0) * p.ks[2]);
-  const char* vz0p = (const char*)p.v + 2 * ((int64_t)b * p.vs[0] + (int64_t)h * p.vs[4] +
-                                             (int64_t)(gz + dz * sz) * p.vs[1] + (int64_t)(gy + dy * Y0) * p.vs[2]);
+  // Issue cursor: pair `cp` (outer), z-slice `cz` (inner): the kz slices of a
+  // pair are fetched back to back, so workgroups at neighbouring z read the
+  // same rows close together in time (L2 reuse across the z window).
+  const char* kp0 = (const char*)p.k + 2 * ((int64_t)b * p.ks[0] + (int64_t)h * p.ks[4] +
+                                           (int64_t)(gz + dz * sz) * p.ks[1] + (int64_t)(gy + dy * Y0) * p.ks[2]);
+  const char* vp0 = (const char*)p.v + 2 * ((int64_t)b * p.vs[0] + (int64_t)h * p.vs[4] +
+                                           (int64_t)(gz + dz * sz) * p.vs[1] + (int64_t)(gy + dy * Y0) * p.vs[2]);
   const int64_t zstepk = 2 * (int64_t)dz * p.ks[1], zstepv = 2 * (int64_t)dz * p.vs[1];
   int cz = 0, cp = 0;
-  const char* kcur = kz0p;
-  const char* vcur = vz0p;
+  const char* kcur = kp0;
+  const char* vcur = vp0;
   uint32_t issue_off = 0;  // LDS byte offset of the ring slot the cursor fills
 
   auto issue = [&]() {
-    const bool zok = cz < kz;
-    const uint32_t nk = !zok ? 0u : (2 * cp + 1 < NR ? (uint32_t)(2 * rowk) : (2 * cp < NR ? (uint32_t)rowk : 0u));
-    const uint32_t nv = !zok ? 0u : (2 * cp + 1 < NR ? (uint32_t)(2 * rowv) : (2 * cp < NR ? (uint32_t)rowv : 0u));
+    const uint32_t nk = 2 * cp + 1 < NR ? (uint32_t)(2 * rowk) : (2 * cp < NR ? (uint32_t)rowk : 0u);
+    const uint32_t nv = 2 * cp + 1 < NR ? (uint32_t)(2 * rowv) : (2 * cp < NR ? (uint32_t)rowv : 0u);
     const u32x4 rk = make_rsrc(kcur, nk);
     const u32x4 rv = make_rsrc(vcur, nv);
     const uint32_t m0 = lds_base + issue_off + (uint32_t)wave * 1024;
@@ -362,16 +392,16 @@ __device__ __forceinline__ void na3d_mfma_body(const Na3dParams p, const Na3dTil
     for (int j = 0; j < LPT; ++j) dma_row16(vten[j] ? rv : rk, m0 + j * NWX * 1024, voff[j]);
     // advance the cursor
     issue_off = issue_off + STAGE_B == NBUF * STAGE_B ? 0 : issue_off + STAGE_B;
-    if (++cp == NP) {
-      cp = 0;
-      ++cz;
-      kz0p += zstepk;
-      vz0p += zstepv;
-      kcur = kz0p;
-      vcur = vz0p;
+    if (++cz == kz) {
+      cz = 0;
+      ++cp;
+      kp0 += 2 * rowk;
+      vp0 += 2 * rowv;
+      kcur = kp0;
+      vcur = vp0;
     } else {
-      kcur += 2 * rowk;
-      vcur += 2 * rowv;
+      kcur += zstepk;
+      vcur += zstepv;
     }
   };
 
@@ -380,7 +410,7 @@ __device__ __forceinline__ void na3d_mfma_body(const Na3dParams p, const Na3dTil
 #pragma unroll
   for (int ks = 0; ks < KS; ++ks) {
     const int key = off_w + n16;
-    koff[ks] = (key * D + 8 * swz(4 * ks + g, key, CMASK)) * 2;
+    koff[ks] = (key * D + 8 * swz<D>(4 * ks + g, key)) * 2;
   }
   uint32_t voffs[DB];
   {
@@ -388,12 +418,12 @@ __device__ __forceinline__ void na3d_mfma_body(const Na3dParams p, const Na3dTil
     const int dq = n16 & 3;
 #pragma unroll
     for (int db = 0; db < DB; ++db)
-      voffs[db] = 2 * RB + (keyv * D + 8 * swz(2 * db + (dq >> 1), keyv, CMASK) + 4 * (dq & 1)) * 2;
+      voffs[db] = 2 * RB + (keyv * D + 8 * swz<D>(2 * db + (dq >> 1), keyv) + 4 * (dq & 1)) * 2;
   }
 
   f32x4 oacc[NTY][DB];
   f32x4 lacc[NTY];
-  float nb[NTY][4];  // xbias - mref
+  f32x4 nb[NTY];  // xbias - mref: the C operand of the QK MFMA
 #pragma unroll
   for (int tt = 0; tt < NTY; ++tt) {
 #pragma unroll
@@ -409,7 +439,7 @@ __device__ __forceinline__ void na3d_mfma_body(const Na3dParams p, const Na3dTil
   for (int s = 0; s < NBUF - 1; ++s) issue();
 
   uint32_t cur_off = 0;  // ring slot of the stage being computed
-  int pr = 0;
+  int pr = 0, zc = 0;
   for (int s = 0; s < nstage; ++s) {
     wait_vmcnt((NBUF - 2) * LPT);  // constant: the tail issues empty (zero-record) stages
     lds_barrier();
@@ -436,25 +466,24 @@ __device__ __forceinline__ void na3d_mfma_body(const Na3dParams p, const Na3dTil
       f32x4 sacc[2];
 #pragma unroll
       for (int r = 0; r < 2; ++r) {
-        sacc[r] = (f32x4){0.f, 0.f, 0.f, 0.f};
+        sacc[r] = nb[tt];
 #pragma unroll
         for (int ks = 0; ks < KS; ++ks)
           sacc[r] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ak[r][ks], qreg[tt][ks], sacc[r], 0, 0, 0);
       }
       float u[8];
-      if (!((ym_mask[tt] >> pr) & 1)) {
-        // both rows inside every window of the tile: only the x mask applies
 #pragma unroll
-        for (int r = 0; r < 2; ++r)
+      for (int r = 0; r < 2; ++r)
 #pragma unroll
-          for (int i = 0; i < 4; ++i) u[4 * r + i] = fmaf(sacc[r][i], c2, nb[tt][i]);
-      } else {
+        for (int i = 0; i < 4; ++i) u[4 * r + i] = sacc[r][i];
+      if ((ym_mask[tt] >> pr) & 1) {
+        // a row outside some query's y window (else only the x mask applies)
 #pragma unroll
         for (int r = 0; r < 2; ++r) {
           const int yr = r0 + r;
           const bool yok = yr >= syl[tt] && yr < syl[tt] + ky;
 #pragma unroll
-          for (int i = 0; i < 4; ++i) u[4 * r + i] = fmaf(sacc[r][i], c2, yok ? nb[tt][i] : -INFINITY);
+          for (int i = 0; i < 4; ++i) u[4 * r + i] = yok ? u[4 * r + i] : -INFINITY;
         }
       }
       // The reference only has to move when some score exceeds it by TAU; the
@@ -484,7 +513,10 @@ __device__ __forceinline__ void na3d_mfma_body(const Na3dParams p, const Na3dTil
         oacc[tt][db] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(av[db], pb, oacc[tt][db], 0, 0, 0);
     }
     cur_off = cur_off + STAGE_B == NBUF * STAGE_B ? 0 : cur_off + STAGE_B;
-    pr = pr + 1 == NP ? 0 : pr + 1;
+    if (++zc == kz) {  // stages run pair-major, z-minor
+      zc = 0;
+      ++pr;
+    }
   }
   wait_vmcnt(0);
 
