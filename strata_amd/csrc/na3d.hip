@@ -211,7 +211,7 @@ __device__ __forceinline__ uint32_t bit_range(int lo, int hi) {
 // the QK MFMA starts from C = bias - m (bias in {0, -inf} per key for the x
 // mask), so the MFMA itself returns u and no VALU work sits between the scores
 // and the exponentials outside the boundary rows of the y mask.
-template <int D, int TX, int NTY, int NBUF>
+template <int D, int TX, int NTY, int RPS, int NBUF>
 __device__ __forceinline__ void na3d_mfma_body(const Na3dParams p, const Na3dTiles tg) {
 #if defined(__HIP_DEVICE_COMPILE__)  // the body is device code only; the host pass needs just the signature
   constexpr int NWX = NA3D_NWX;
@@ -223,8 +223,9 @@ __device__ __forceinline__ void na3d_mfma_body(const Na3dParams p, const Na3dTil
   constexpr int LWP = (LW + KPK - 1) / KPK * KPK;
   constexpr int RB = LWP * D * 2;         // bytes per (tensor, row) region
   constexpr int RKB = RB / 1024;
-  constexpr int STAGE_B = 4 * RB;         // K row 0, K row 1, V row 0, V row 1
-  constexpr int LPT = 4 * RKB / NWX;      // 1-KiB DMA loads per wave per stage
+  constexpr int STAGE_B = 2 * RPS * RB;   // K rows 0..RPS-1, then V rows 0..RPS-1
+  constexpr int LPT = 2 * RPS * RKB / NWX;  // 1-KiB DMA loads per wave per stage
+  constexpr int NRP = RPS / 2;            // row pairs per stage (one PV MFMA k-step each)
   constexpr int CPK = D / 8;              // 16-byte chunks per key
   constexpr int KS = D / 32;              // k-steps of the QK MFMA
   constexpr int DB = D / 16;              // d-blocks of the PV MFMA
@@ -232,7 +233,7 @@ __device__ __forceinline__ void na3d_mfma_body(const Na3dParams p, const Na3dTil
   // fp32 sums at most |W| * 2^TAU * max|v|, far inside fp32/bf16 range; terms
   // more than 126 below the reference underflow, i.e. are < 2^-126 of the max.
   constexpr float TAU = 64.f;
-  static_assert(RB % 1024 == 0 && (4 * RKB) % NWX == 0, "stage layout");
+  static_assert(RB % 1024 == 0 && (2 * RPS * RKB) % NWX == 0 && (RPS == 2 || RPS == 4), "stage layout");
 
   __shared__ __attribute__((aligned(1024))) char lds[NBUF * STAGE_B];
 
@@ -265,9 +266,9 @@ __device__ __forceinline__ void na3d_mfma_body(const Na3dParams p, const Na3dTil
   const int sz = win_start(iz, Lz, kz);
   const int Y0 = win_start(y0, Ly, ky);
   const int NR = win_start(min(y0 + WY - 1, qy1 - 1), Ly, ky) + ky - Y0;  // rows of the y-union (<= 64)
-  const int NP = (NR + 1) >> 1;                                          // pairs per z-slice (<= 32)
+  const int NQ = (NR + RPS - 1) / RPS;                                   // stages per z-slice (<= 32)
   const int X0 = win_start(x0, Lx, kx);
-  const int nstage = kz * NP;
+  const int nstage = kz * NQ;
 
   const int tid = (int)__builtin_amdgcn_workitem_id_x();
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // uniform: keeps DMA descriptors in SGPRs
@@ -289,7 +290,7 @@ __device__ __forceinline__ void na3d_mfma_body(const Na3dParams p, const Na3dTil
     xbias[i] = (kxs >= sx && kxs < sx + kx) ? 0.f : -INFINITY;
   }
 
-  // ---- per-tile y geometry: which pairs each tile touches / needs a y mask for ----
+  // ---- per-tile y geometry: which stages each tile touches / needs a y mask in ----
   uint32_t act_mask[NTY], ym_mask[NTY];
   int syl[NTY], qyl[NTY];
 #pragma unroll
@@ -299,8 +300,8 @@ __device__ __forceinline__ void na3d_mfma_body(const Na3dParams p, const Na3dTil
       const int ytl = min(yt0 + TY - 1, qy1 - 1);
       const int U0 = win_start(yt0, Ly, ky) - Y0, U1 = win_start(ytl, Ly, ky) + ky - Y0;  // union rows
       const int F0 = win_start(ytl, Ly, ky) - Y0, F1 = win_start(yt0, Ly, ky) + ky - Y0;  // rows in every window
-      act_mask[tt] = bit_range(U0 >> 1, (U1 + 1) >> 1);
-      ym_mask[tt] = act_mask[tt] & ~bit_range((F0 + 1) >> 1, F1 >> 1);
+      act_mask[tt] = bit_range(U0 / RPS, (U1 + RPS - 1) / RPS);
+      ym_mask[tt] = act_mask[tt] & ~bit_range((F0 + RPS - 1) / RPS, F1 / RPS);
     } else {
       act_mask[tt] = ym_mask[tt] = 0;
     }
@@ -347,11 +348,11 @@ __device__ __forceinline__ void na3d_mfma_body(const Na3dParams p, const Na3dTil
   }
 
   // ---- DMA descriptors ----
-  // A stage is 4 regions (K row 0, K row 1, V row 0, V row 1), each LWP keys of
-  // D bf16 in swizzled 16-byte chunks; wave w loads 1-KiB chunks w, w+4, ...
-  // One buffer descriptor per tensor covers both rows of the pair (the row
-  // offset is part of the lane offset; the record count stops at the last
-  // valid row, so rows past the window union read as zero).
+  // A stage is 2*RPS regions (K rows 0..RPS-1, V rows 0..RPS-1), each LWP keys
+  // of D bf16 in swizzled 16-byte chunks; wave w loads 1-KiB chunks w, w+4, ...
+  // One buffer descriptor per tensor covers the stage's rows (the row offset is
+  // part of the lane offset; the record count stops at the last valid row, so
+  // rows past the window union read as zero).
   const int64_t rowk = 2 * (int64_t)dy * p.ks[2], rowv = 2 * (int64_t)dy * p.vs[2];  // bytes per sub-grid row
   uint32_t voff[LPT];
   bool vten[LPT];
@@ -359,7 +360,7 @@ __device__ __forceinline__ void na3d_mfma_body(const Na3dParams p, const Na3dTil
   for (int j = 0; j < LPT; ++j) {
     const int gc = j * NWX + wave;  // 1-KiB chunk of the stage
     const int reg = gc / RKB;
-    const int tensor = reg >> 1, row = reg & 1;
+    const int tensor = reg / RPS, row = reg % RPS;
     const int key = (gc % RKB) * KPK + lane / CPK;
     const int c = swz<D>(lane % CPK, key);  // logical chunk stored at this slot
     const int64_t sx3 = tensor ? p.vs[3] : p.ks[3];
@@ -369,9 +370,9 @@ __device__ __forceinline__ void na3d_mfma_body(const Na3dParams p, const Na3dTil
                   : OOB;
     vten[j] = tensor;
   }
-  // Issue cursor: pair `cp` (outer), z-slice `cz` (inner): the kz slices of a
-  // pair are fetched back to back, so workgroups at neighbouring z read the
-  // same rows close together in time (L2 reuse across the z window).
+  // Issue cursor: row group `cp` (outer), z-slice `cz` (inner): the kz slices
+  // of a row group are fetched back to back, so workgroups at neighbouring z
+  // read the same rows close together in time (L2 reuse across the z window).
   const char* kp0 = (const char*)p.k + 2 * ((int64_t)b * p.ks[0] + (int64_t)h * p.ks[4] +
                                            (int64_t)(gz + dz * sz) * p.ks[1] + (int64_t)(gy + dy * Y0) * p.ks[2]);
   const char* vp0 = (const char*)p.v + 2 * ((int64_t)b * p.vs[0] + (int64_t)h * p.vs[4] +
@@ -383,8 +384,9 @@ __device__ __forceinline__ void na3d_mfma_body(const Na3dParams p, const Na3dTil
   uint32_t issue_off = 0;  // LDS byte offset of the ring slot the cursor fills
 
   auto issue = [&]() {
-    const uint32_t nk = 2 * cp + 1 < NR ? (uint32_t)(2 * rowk) : (2 * cp < NR ? (uint32_t)rowk : 0u);
-    const uint32_t nv = 2 * cp + 1 < NR ? (uint32_t)(2 * rowv) : (2 * cp < NR ? (uint32_t)rowv : 0u);
+    const int nrow = min(max(NR - RPS * cp, 0), RPS);  // valid rows of the stage at the cursor
+    const uint32_t nk = (uint32_t)(nrow * rowk);
+    const uint32_t nv = (uint32_t)(nrow * rowv);
     const u32x4 rk = make_rsrc(kcur, nk);
     const u32x4 rv = make_rsrc(vcur, nv);
     const uint32_t m0 = lds_base + issue_off + (uint32_t)wave * 1024;
@@ -395,8 +397,8 @@ __device__ __forceinline__ void na3d_mfma_body(const Na3dParams p, const Na3dTil
     if (++cz == kz) {
       cz = 0;
       ++cp;
-      kp0 += 2 * rowk;
-      vp0 += 2 * rowv;
+      kp0 += RPS * rowk;
+      vp0 += RPS * rowv;
       kcur = kp0;
       vcur = vp0;
     } else {
@@ -418,7 +420,7 @@ __device__ __forceinline__ void na3d_mfma_body(const Na3dParams p, const Na3dTil
     const int dq = n16 & 3;
 #pragma unroll
     for (int db = 0; db < DB; ++db)
-      voffs[db] = 2 * RB + (keyv * D + 8 * swz<D>(2 * db + (dq >> 1), keyv) + 4 * (dq & 1)) * 2;
+      voffs[db] = RPS * RB + (keyv * D + 8 * swz<D>(2 * db + (dq >> 1), keyv) + 4 * (dq & 1)) * 2;
   }
 
   f32x4 oacc[NTY][DB];
@@ -433,7 +435,7 @@ __device__ __forceinline__ void na3d_mfma_body(const Na3dParams p, const Na3dTil
     for (int i = 0; i < 4; ++i) nb[tt][i] = xbias[i] - mref[tt];
   }
   typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
-  const bf16x8_t ones = {(bf16)1.f, (bf16)1.f, (bf16)1.f, (bf16)1.f, (bf16)1.f, (bf16)1.f, (bf16)1.f, (bf16)1.f};
+  bf16x8_t ones = {(bf16)1.f, (bf16)1.f, (bf16)1.f, (bf16)1.f, (bf16)1.f, (bf16)1.f, (bf16)1.f, (bf16)1.f};
 
 #pragma unroll
   for (int s = 0; s < NBUF - 1; ++s) issue();
@@ -445,41 +447,44 @@ __device__ __forceinline__ void na3d_mfma_body(const Na3dParams p, const Na3dTil
     lds_barrier();
     issue();
 
+    asm volatile("" : "+v"(ones));  // keep the ones operand resident (else rebuilt per tile)
     const char* st = lds + cur_off;
-    bf16x8 ak[2][KS];
+    bf16x8 ak[RPS][KS];
 #pragma unroll
-    for (int r = 0; r < 2; ++r)
+    for (int r = 0; r < RPS; ++r)
 #pragma unroll
       for (int ks = 0; ks < KS; ++ks) ak[r][ks] = *(const bf16x8*)(st + r * RB + koff[ks]);
-    bf16x8 av[DB];
+    bf16x8 av[NRP][DB];  // V^T of row pair rp: keys of row 2rp then row 2rp+1
 #pragma unroll
-    for (int db = 0; db < DB; ++db) {
-      const bf16x4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4bf16(LDS_PTR(bf16x4, st + voffs[db]));
-      const bf16x4 hi = __builtin_amdgcn_ds_read_tr16_b64_v4bf16(LDS_PTR(bf16x4, st + voffs[db] + RB));
-      av[db] = __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7);
-    }
-    const int r0 = 2 * pr;
+    for (int rp = 0; rp < NRP; ++rp)
+#pragma unroll
+      for (int db = 0; db < DB; ++db) {
+        const bf16x4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4bf16(LDS_PTR(bf16x4, st + voffs[db] + 2 * rp * RB));
+        const bf16x4 hi = __builtin_amdgcn_ds_read_tr16_b64_v4bf16(LDS_PTR(bf16x4, st + voffs[db] + (2 * rp + 1) * RB));
+        av[rp][db] = __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7);
+      }
+    const int r0 = RPS * pr;
 
 #pragma unroll
     for (int tt = 0; tt < NTY; ++tt) {
       if (!((act_mask[tt] >> pr) & 1)) continue;  // rows outside this tile's window union
-      f32x4 sacc[2];
+      f32x4 sacc[RPS];
 #pragma unroll
-      for (int r = 0; r < 2; ++r) {
+      for (int r = 0; r < RPS; ++r) {
         sacc[r] = nb[tt];
 #pragma unroll
         for (int ks = 0; ks < KS; ++ks)
           sacc[r] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ak[r][ks], qreg[tt][ks], sacc[r], 0, 0, 0);
       }
-      float u[8];
+      float u[4 * RPS];
 #pragma unroll
-      for (int r = 0; r < 2; ++r)
+      for (int r = 0; r < RPS; ++r)
 #pragma unroll
         for (int i = 0; i < 4; ++i) u[4 * r + i] = sacc[r][i];
       if ((ym_mask[tt] >> pr) & 1) {
         // a row outside some query's y window (else only the x mask applies)
 #pragma unroll
-        for (int r = 0; r < 2; ++r) {
+        for (int r = 0; r < RPS; ++r) {
           const int yr = r0 + r;
           const bool yok = yr >= syl[tt] && yr < syl[tt] + ky;
 #pragma unroll
@@ -488,7 +493,11 @@ __device__ __forceinline__ void na3d_mfma_body(const Na3dParams p, const Na3dTil
       }
       // The reference only has to move when some score exceeds it by TAU; the
       // in-lane max decides that, the column max is needed only to move it.
-      const float ml = fmaxf(fmaxf(fmaxf(u[0], u[1]), fmaxf(u[2], u[3])), fmaxf(fmaxf(u[4], u[5]), fmaxf(u[6], u[7])));
+      float ml = -INFINITY;
+#pragma unroll
+      for (int j = 0; j < 4 * RPS; j += 8)
+        ml = fmaxf(ml, fmaxf(fmaxf(fmaxf(u[j], u[j + 1]), u[j + 2]),
+                             fmaxf(fmaxf(fmaxf(u[j + 3], u[j + 4]), u[j + 5]), fmaxf(u[j + 6], u[j + 7]))));
       if (__builtin_amdgcn_ballot_w64(ml > TAU) != 0) {
         const float mx = colmax(ml);
         const float d = mx > TAU ? mx : 0.f;
@@ -499,21 +508,29 @@ __device__ __forceinline__ void na3d_mfma_body(const Na3dParams p, const Na3dTil
 #pragma unroll
         for (int i = 0; i < 4; ++i) nb[tt][i] -= d;
 #pragma unroll
-        for (int j = 0; j < 8; ++j) u[j] -= d;
+        for (int j = 0; j < 4 * RPS; ++j) u[j] -= d;
       }
-      float pv[8];
+      // One straight-line block: P of every row pair, then the PV MFMAs.
+      bf16x8 pb[NRP];
 #pragma unroll
-      for (int j = 0; j < 8; ++j) pv[j] = __builtin_amdgcn_exp2f(u[j]);
-      const u32x4 pw = {pack_bf16x2(pv[0], pv[1]), pack_bf16x2(pv[2], pv[3]), pack_bf16x2(pv[4], pv[5]),
-                        pack_bf16x2(pv[6], pv[7])};
-      const bf16x8 pb = __builtin_bit_cast(bf16x8, pw);
-      lacc[tt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ones, pb, lacc[tt], 0, 0, 0);
+      for (int rp = 0; rp < NRP; ++rp) {
+        float pv[8];
 #pragma unroll
-      for (int db = 0; db < DB; ++db)
-        oacc[tt][db] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(av[db], pb, oacc[tt][db], 0, 0, 0);
+        for (int j = 0; j < 8; ++j) pv[j] = __builtin_amdgcn_exp2f(u[8 * rp + j]);
+        const u32x4 pw = {pack_bf16x2(pv[0], pv[1]), pack_bf16x2(pv[2], pv[3]), pack_bf16x2(pv[4], pv[5]),
+                          pack_bf16x2(pv[6], pv[7])};
+        pb[rp] = __builtin_bit_cast(bf16x8, pw);
+      }
+#pragma unroll
+      for (int rp = 0; rp < NRP; ++rp) {
+        lacc[tt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ones, pb[rp], lacc[tt], 0, 0, 0);
+#pragma unroll
+        for (int db = 0; db < DB; ++db)
+          oacc[tt][db] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(av[rp][db], pb[rp], oacc[tt][db], 0, 0, 0);
+      }
     }
     cur_off = cur_off + STAGE_B == NBUF * STAGE_B ? 0 : cur_off + STAGE_B;
-    if (++zc == kz) {  // stages run pair-major, z-minor
+    if (++zc == kz) {  // stages run row-group-major, z-minor
       zc = 0;
       ++pr;
     }
@@ -542,14 +559,15 @@ __device__ __forceinline__ void na3d_mfma_body(const Na3dParams p, const Na3dTil
 }
 
 // Two workgroups per CU for head_dim <= 64; head_dim 128 needs the full register file.
-template <int D, int TX, int NTY, int NBUF>
+template <int D, int TX, int NTY, int RPS, int NBUF>
 __global__ __launch_bounds__(256, 2) void na3d_mfma_kernel(Na3dParams p, Na3dTiles tg) {
-  na3d_mfma_body<D, TX, NTY, NBUF>(p, tg);
+  na3d_mfma_body<D, TX, NTY, RPS, NBUF>(p, tg);
 }
-template <int D, int TX, int NTY, int NBUF>
+template <int D, int TX, int NTY, int RPS, int NBUF>
 __global__ __launch_bounds__(256, 1) void na3d_mfma_wide_kernel(Na3dParams p, Na3dTiles tg) {
-  na3d_mfma_body<D, TX, NTY, NBUF>(p, tg);
+  na3d_mfma_body<D, TX, NTY, RPS, NBUF>(p, tg);
 }
+
 
 // ---------------------------------------------------------------------------
 // Host side
@@ -577,7 +595,7 @@ static int launch_scalar(const Na3dParams& p, hipStream_t st) {
   return check_launch("na3d_scalar_kernel");
 }
 
-template <int D, int TX, int NTY, int NBUF>
+template <int D, int TX, int NTY, int RPS, int NBUF>
 static int launch_mfma_cfg(const Na3dParams& p, hipStream_t st) {
   Na3dTiles tg;
   int nq[3] = {0, 0, 0};
@@ -596,30 +614,46 @@ static int launch_mfma_cfg(const Na3dParams& p, hipStream_t st) {
   if (total > 0x7fffffff) return fail(STRATA_HIP_EUNSUPPORTED, "na3d: problem too large for one launch");
   tg.total = (int)total;
   if (D >= 128)
-    hipLaunchKernelGGL((na3d_mfma_wide_kernel<D, TX, NTY, NBUF>), dim3((unsigned)total), dim3(64 * NA3D_NWX), 0, st, p, tg);
+    hipLaunchKernelGGL((na3d_mfma_wide_kernel<D, TX, NTY, RPS, NBUF>), dim3((unsigned)total), dim3(64 * NA3D_NWX), 0,
+                       st, p, tg);
   else
-    hipLaunchKernelGGL((na3d_mfma_kernel<D, TX, NTY, NBUF>), dim3((unsigned)total), dim3(64 * NA3D_NWX), 0, st, p, tg);
+    hipLaunchKernelGGL((na3d_mfma_kernel<D, TX, NTY, RPS, NBUF>), dim3((unsigned)total), dim3(64 * NA3D_NWX), 0, st, p,
+                       tg);
   return check_launch("na3d_mfma_kernel");
 }
 
-// LDS ring depth for a stage of `stage_bytes`: as deep as fits in ~80 KiB
-// (two workgroups per CU), at least double buffered.
-constexpr int ring_depth(int stage_bytes) {
-  return 81920 / stage_bytes >= 4 ? 4 : (81920 / stage_bytes >= 3 ? 3 : 2);
+// LDS budget per workgroup: ~80 KiB (two workgroups per CU).  A stage holds
+// RPS key rows of K and of V.  Wide windows (4-column tiles, kx >= 10) take
+// four rows per stage when a double-buffered ring of them fits the budget:
+// half the stages, so half the per-stage barrier, DMA issue and LDS latency
+// (configs[2]: 8.6 -> 8.2 ms).  Narrower windows keep two rows and a deeper
+// ring: their shorter y-unions pad a 4-row stage and the ring would be 2 deep.
+template <int D, int TX, int RPS>
+constexpr int stage_bytes() {
+  return 2 * RPS * (((NA3D_NWX - 1) * TX + 16 + 512 / D - 1) / (512 / D) * (512 / D)) * D * 2;
 }
 template <int D, int TX>
-constexpr int stage_bytes() {
-  return 4 * (((NA3D_NWX - 1) * TX + 16 + 512 / D - 1) / (512 / D) * (512 / D)) * D * 2;
+constexpr int rows_per_stage() {
+  return TX <= 4 && 2 * stage_bytes<D, TX, 4>() <= 81920 ? 4 : 2;
 }
+// Ring depth: as deep as fits the budget, at most 4, at least double buffered.
+constexpr int ring_depth(int stage_b) { return 81920 / stage_b >= 4 ? 4 : (81920 / stage_b >= 3 ? 3 : 2); }
+
+template <int D, int TX, int NTY>
+static int launch_mfma_tx(const Na3dParams& p, hipStream_t st) {
+  constexpr int RPS = rows_per_stage<D, TX>();
+  return launch_mfma_cfg<D, TX, NTY, RPS, ring_depth(stage_bytes<D, TX, RPS>())>(p, st);
+}
+
 
 template <int D>
 static int launch_mfma_d(const Na3dParams& p, hipStream_t st) {
   constexpr int NTY = D >= 128 ? 2 : 4;
   const int kx = p.ker[2];
-  if (kx == 1) return launch_mfma_cfg<D, 16, NTY, ring_depth(stage_bytes<D, 16>())>(p, st);
-  if (kx <= 9) return launch_mfma_cfg<D, 8, NTY, ring_depth(stage_bytes<D, 8>())>(p, st);
-  if (kx <= 13) return launch_mfma_cfg<D, 4, NTY, ring_depth(stage_bytes<D, 4>())>(p, st);
-  return launch_mfma_cfg<D, 2, (NTY > 2 ? 2 : NTY), ring_depth(stage_bytes<D, 2>())>(p, st);  // kx <= 15
+  if (kx == 1) return launch_mfma_tx<D, 16, NTY>(p, st);
+  if (kx <= 9) return launch_mfma_tx<D, 8, NTY>(p, st);
+  if (kx <= 13) return launch_mfma_tx<D, 4, NTY>(p, st);
+  return launch_mfma_tx<D, 2, (NTY > 2 ? 2 : NTY)>(p, st);  // kx <= 15
 }
 
 static bool aligned16(const void* ptr) { return ((uintptr_t)ptr & 15u) == 0; }
