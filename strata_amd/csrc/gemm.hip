@@ -266,34 +266,28 @@ __device__ __forceinline__ int gswz(int chunk, int row) {
   else return chunk ^ ((row >> 2) & 3);
 }
 
-// Large-tile GEMM for K % G_BK == 0: a 256 x 256 output tile per workgroup of
-// 8 waves (2 along m x 4 along n, 128 x 64 each, v_mfma_f32_32x32x16_bf16).
-// A/B tiles of G_BK columns stream from global memory straight into an LDS
-// ring of G_NST stages (buffer_load ... lds) that runs G_NST - 1 stages ahead
-// of the MFMAs, one barrier per stage.
-#ifndef G_BK_COLS
-#define G_BK_COLS 64
-#endif
-#ifndef G_STAGES
-#define G_STAGES 2
-#endif
-constexpr int G_BM = 256, G_BN = 256, G_BK = G_BK_COLS, G_NST = G_STAGES, G_WGM = 2, G_WGN = 4;
-
-__global__ __launch_bounds__(64 * G_WGM * G_WGN, 1) void gemm_dma_kernel(GemmParams p) {
-  constexpr int NW = G_WGM * G_WGN;
-  constexpr int WTM = G_BM / G_WGM;  // 128
-  constexpr int WTN = G_BN / G_WGN;  // 64
+// Large-tile GEMM for K % BK == 0: a BM x BN output tile per workgroup of
+// WGM x WGN waves (128 x 64 each, v_mfma_f32_32x32x16_bf16).  A/B tiles of BK
+// columns stream from global memory straight into an LDS ring of NST stages
+// (buffer_load ... lds) that runs NST - 1 stages ahead of the MFMAs, one
+// barrier per stage.
+template <int BM, int BN, int WGM, int WGN, int BK, int NST>
+__device__ __forceinline__ void gemm_dma_body(const GemmParams& p) {
+  constexpr int NW = WGM * WGN;
+  constexpr int WTM = BM / WGM;  // 128
+  constexpr int WTN = BN / WGN;  // 64
   constexpr int FM = WTM / 32, FN = WTN / 32;
-  constexpr int ROWB = G_BK * 2;          // bytes of one tile row in a stage
+  constexpr int ROWB = BK * 2;            // bytes of one tile row in a stage
   constexpr int CH = ROWB / 16;           // 16-byte chunks per row
   constexpr int RPC = 1024 / ROWB;        // rows per 1-KiB DMA
-  constexpr int XB = G_BM * ROWB;         // bytes of the x tile
+  constexpr int XB = BM * ROWB;           // bytes of the x tile
   constexpr int XCH = XB / 1024;          // 1-KiB DMAs of the x tile
-  constexpr int STAGE = XB + G_BN * ROWB;
+  constexpr int STAGE = XB + BN * ROWB;
   constexpr int LPW = STAGE / 1024 / NW;  // 1-KiB DMAs per wave per stage
-  constexpr int PD = G_NST - 1;           // stages in flight ahead of the MFMAs
-  static_assert(CH == 4 || CH == 8, "G_BK must be 32 or 64");
-  constexpr int LDS_BYTES = G_NST * STAGE > NW * WTM * WTN * 2 ? G_NST * STAGE : NW * WTM * WTN * 2;
+  constexpr int PD = NST - 1;             // stages in flight ahead of the MFMAs
+  static_assert(CH == 4 || CH == 8, "BK must be 32 or 64");
+  static_assert(WTM == 128 && (WTN == 64 || WTN == 128) && STAGE % (1024 * NW) == 0, "wave tile / stage layout");
+  constexpr int LDS_BYTES = NST * STAGE > NW * WTM * WTN * 2 ? NST * STAGE : NW * WTM * WTN * 2;
   static_assert((PD - 1) * LPW <= 16, "wait_vmcnt range");
   __shared__ __attribute__((aligned(1024))) char lds[LDS_BYTES];  // ring, then the epilogue slabs
 
@@ -304,13 +298,13 @@ __global__ __launch_bounds__(64 * G_WGM * G_WGN, 1) void gemm_dma_kernel(GemmPar
   }();
   const int tn = wg % p.nt;
   const int tm = wg / p.nt;
-  const int64_t m0 = (int64_t)tm * G_BM;
-  const int64_t n0 = (int64_t)tn * G_BN;
+  const int64_t m0 = (int64_t)tm * BM;
+  const int64_t n0 = (int64_t)tn * BN;
 
   const int tid = (int)__builtin_amdgcn_workitem_id_x();
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int lane = tid & 63;
-  const int wm = wave / G_WGN, wn = wave % G_WGN;
+  const int wm = wave / WGN, wn = wave % WGN;
   const int l32 = lane & 31, hi = lane >> 5;
   const uint32_t lds_base = (uint32_t)(uintptr_t)(__attribute__((address_space(3))) char*)lds;
 
@@ -321,7 +315,7 @@ __global__ __launch_bounds__(64 * G_WGM * G_WGN, 1) void gemm_dma_kernel(GemmPar
   for (int j = 0; j < LPW; ++j) {
     const int c = j * NW + wave;
     const bool isw = c >= XCH;
-    const int row = RPC * (c % XCH) + lane / CH;
+    const int row = RPC * (isw ? c - XCH : c) + lane / CH;
     const int lc = gswz<CH>(lane % CH, row);
     const int64_t grow = (isw ? n0 : m0) + row;
     const int64_t ld = isw ? p.ldw : p.ldx;
@@ -331,8 +325,8 @@ __global__ __launch_bounds__(64 * G_WGM * G_WGN, 1) void gemm_dma_kernel(GemmPar
   const char* xrow0 = (const char*)(p.x + m0 * p.ldx);
   const char* wrow0 = (const char*)(p.w + n0 * p.ldw);
   auto issue = [&](int kt, int buf) {
-    const u32x4 rx = make_rsrc(xrow0 + (int64_t)kt * G_BK * 2, OOB);
-    const u32x4 rw = make_rsrc(wrow0 + (int64_t)kt * G_BK * 2, OOB);
+    const u32x4 rx = make_rsrc(xrow0 + (int64_t)kt * BK * 2, OOB);
+    const u32x4 rw = make_rsrc(wrow0 + (int64_t)kt * BK * 2, OOB);
     const uint32_t dst = lds_base + buf * STAGE + wave * 1024;
 #pragma unroll
     for (int j = 0; j < LPW; ++j) dma_row16(j * NW + wave >= XCH ? rw : rx, dst + j * NW * 1024, voff[j]);
@@ -360,7 +354,7 @@ __global__ __launch_bounds__(64 * G_WGM * G_WGN, 1) void gemm_dma_kernel(GemmPar
 #pragma unroll
       for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.f;
 
-  const int nk = (int)(p.K / G_BK);
+  const int nk = (int)(p.K / BK);
 #pragma unroll
   for (int s = 0; s < PD; ++s)
     if (s < nk) issue(s, s);
@@ -372,12 +366,12 @@ __global__ __launch_bounds__(64 * G_WGM * G_WGN, 1) void gemm_dma_kernel(GemmPar
     lds_barrier();
     if (kt + PD < nk) {
       issue(kt + PD, wr);
-      wr = wr + 1 == G_NST ? 0 : wr + 1;
+      wr = wr + 1 == NST ? 0 : wr + 1;
     }
     const char* st = lds + rd * STAGE;
-    rd = rd + 1 == G_NST ? 0 : rd + 1;
+    rd = rd + 1 == NST ? 0 : rd + 1;
 #pragma unroll
-    for (int kk = 0; kk < G_BK / 16; ++kk) {
+    for (int kk = 0; kk < BK / 16; ++kk) {
       bf16x8 af[FN], bfr[FM];
 #pragma unroll
       for (int i = 0; i < FN; ++i) af[i] = *(const bf16x8*)(st + (aoff[i][kk & 1] ^ ((kk >> 1) * 64)));
@@ -393,9 +387,10 @@ __global__ __launch_bounds__(64 * G_WGM * G_WGN, 1) void gemm_dma_kernel(GemmPar
 
   // ---- epilogue through LDS ----
   // Phase 1: bias + activation on the accumulators, bf16 into this wave's
-  // 128 x 64 slab of LDS (rows of 128 bytes, 16-byte chunks swizzled by row).
+  // WTM x WTN slab of LDS (rows of SRB bytes, 16-byte chunks swizzled by row).
   // Phase 2: each lane reads 16 contiguous bytes of a row, adds the residual
-  // read the same way, and writes 16 bytes: 8 lanes cover a 128-byte row.
+  // read the same way, and writes 16 bytes: CPR lanes cover a row.
+  constexpr int SRB = WTN * 2, CPR = WTN / 8, RPI = 64 / CPR;
   lds_barrier();  // every wave is done reading the last stage
   char* slab = lds + wave * (WTM * WTN * 2);
   const int64_t gn0 = n0 + wn * WTN, gm0 = m0 + wm * WTM;
@@ -428,14 +423,14 @@ __global__ __launch_bounds__(64 * G_WGM * G_WGN, 1) void gemm_dma_kernel(GemmPar
         }
         const int ml = 32 * j + l32;
         const u32x2 w2 = {pack_bf16x2(v[0], v[1]), pack_bf16x2(v[2], v[3])};
-        *(u32x2*)(slab + ml * 128 + (((nl >> 3) ^ (ml & 7)) << 4) + 8 * hi) = w2;
+        *(u32x2*)(slab + ml * SRB + (((nl >> 3) ^ (ml & 7)) << 4) + 8 * hi) = w2;
       }
     }
 #pragma unroll 4
-  for (int it = 0; it < WTM / 8; ++it) {
-    const int ml = 8 * it + (lane >> 3);
-    const int c = lane & 7;  // logical 16-byte chunk = 8 output columns
-    const u32x4 w4 = *(const u32x4*)(slab + ml * 128 + ((c ^ (ml & 7)) << 4));
+  for (int it = 0; it < WTM / RPI; ++it) {
+    const int ml = RPI * it + lane / CPR;
+    const int c = lane % CPR;  // logical 16-byte chunk = 8 output columns
+    const u32x4 w4 = *(const u32x4*)(slab + ml * SRB + ((c ^ (ml & 7)) << 4));
     const int64_t gm = gm0 + ml, gn = gn0 + 8 * c;
     if (gm >= p.M || gn >= p.N) continue;
     if (gn + 8 <= p.N) {
@@ -457,6 +452,12 @@ __global__ __launch_bounds__(64 * G_WGM * G_WGN, 1) void gemm_dma_kernel(GemmPar
     }
   }
 }
+
+// One 256 x 256 workgroup of 8 waves per CU, K step 64, double-buffered
+// 128 KiB ring.  (Measured alternatives at the block's shapes, all slower:
+// 256 x 128 tiles at two workgroups per CU; K step 32 with 3-5 stages; four
+// waves of 128 x 128 with the accumulators in AGPRs.)
+__global__ __launch_bounds__(512, 1) void gemm_dma_kernel(GemmParams p) { gemm_dma_body<256, 256, 2, 4, 64, 2>(p); }
 
 template <int BM, int BN, int WGM, int WGN>
 static int launch_gemm(GemmParams p, hipStream_t st) {
@@ -501,15 +502,15 @@ extern "C" int strata_hip_gemm_bias_act(const strata_hip_gemm_args* a, void* str
   p.ldo = a->ldo;
   p.act = a->act;
   hipStream_t st = (hipStream_t)stream;
-  // The large-tile kernel streams G_BK-wide K steps with 32-bit lane offsets
+  // The large-tile kernels stream 64-wide K steps with 32-bit lane offsets
   // inside a 256-row block: K a multiple of 64, row strides small enough.
-  const bool big = p.K % G_BK == 0 && 256 * p.ldx * 2 + 4096 < (int64_t)OOB && 256 * p.ldw * 2 + 4096 < (int64_t)OOB;
+  const bool big = p.K % 64 == 0 && 256 * p.ldx * 2 + 4096 < (int64_t)OOB && 256 * p.ldw * 2 + 4096 < (int64_t)OOB;
   if (big) {
-    p.mt = (int)((p.M + G_BM - 1) / G_BM);
-    p.nt = (int)((p.N + G_BN - 1) / G_BN);
+    p.mt = (int)((p.M + 255) / 256);
+    p.nt = (int)((p.N + 255) / 256);
     const int64_t total = (int64_t)p.mt * p.nt;
     if (total > 0x7fffffff) return fail(STRATA_HIP_EUNSUPPORTED, "gemm: problem too large for one launch");
-    hipLaunchKernelGGL(gemm_dma_kernel, dim3((unsigned)total), dim3(64 * G_WGM * G_WGN), 0, st, p);
+    hipLaunchKernelGGL(gemm_dma_kernel, dim3((unsigned)total), dim3(512), 0, st, p);
     return check_launch("gemm_dma_kernel");
   }
   return launch_gemm<128, 128, 2, 2>(p, st);
