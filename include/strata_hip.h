@@ -25,7 +25,7 @@
 extern "C" {
 #endif
 
-#define STRATA_HIP_ABI_VERSION 1
+#define STRATA_HIP_ABI_VERSION 2
 
 enum strata_hip_status {
   STRATA_HIP_OK = 0,
@@ -36,7 +36,14 @@ enum strata_hip_status {
 
 enum strata_hip_dtype { STRATA_HIP_F32 = 0, STRATA_HIP_BF16 = 1 };
 
-enum strata_hip_act { STRATA_HIP_ACT_NONE = 0, STRATA_HIP_ACT_GELU_TANH = 1, STRATA_HIP_ACT_GELU_ERF = 2 };
+enum strata_hip_act {
+  STRATA_HIP_ACT_NONE = 0,
+  STRATA_HIP_ACT_GELU_TANH = 1,
+  STRATA_HIP_ACT_GELU_ERF = 2,
+  STRATA_HIP_ACT_SIGMOID = 3 /* the attention gate */
+};
+/* How the GEMM epilogue combines act(x @ w^T + bias) with `residual`. */
+enum strata_hip_res_op { STRATA_HIP_RES_ADD = 0, STRATA_HIP_RES_MUL = 1 };
 
 enum strata_hip_rope_layout {
   STRATA_HIP_ROPE_HALF = 0,       /* pair p = (d=p, d=p+D/2)   ("rotate_half") */
@@ -97,6 +104,13 @@ int strata_hip_na3d_fwd(const strata_hip_na3d_args* args, void* stream);
  * broadcasts one table over all levels).
  * q, k, v: [M, H, D] bf16 contiguous (heads-last token layout).  RoPE rotates
  * the pairs of q and k; v is copied.  Any of q/k/v may alias nothing else.
+ *
+ * qk_norm = 1 applies RMSNorm over D to every (token, head) of q and k before
+ * the rotation, x * rsqrt(mean(x^2) + qk_norm_eps) * weight (fp32 math;
+ * weight bf16 [D], or NULL for no elementwise affine): the block's optional
+ * qk normalisation (screamcast/config.py:91-93 qk_norm /
+ * qk_norm_elementwise_affine, passed at screamcast/strata_wrappers.py:324-325).
+ * It needs D/16 (half layout) or D/8 (interleaved) to be a power of two.
  * ------------------------------------------------------------------------- */
 typedef struct strata_hip_rope_pack_args {
   const void* qkv;
@@ -112,22 +126,30 @@ typedef struct strata_hip_rope_pack_args {
   int32_t head_dim;
   int32_t layout;     /* strata_hip_rope_layout */
   int64_t qkv_row_stride;
+  int32_t qk_norm;    /* 0: off, 1: RMSNorm of q and k per (token, head) */
+  float qk_norm_eps;
+  const void* q_norm_weight; /* bf16 [D] or NULL */
+  const void* k_norm_weight; /* bf16 [D] or NULL */
 } strata_hip_rope_pack_args;
 
 int strata_hip_rope_qkv_pack(const strata_hip_rope_pack_args* args, void* stream);
 
 /* ---------------------------------------------------------------------------
- * GEMM with fused epilogue:  out = act(x @ w^T + bias) + residual
+ * GEMM with fused epilogue:  out = act(x @ w^T + bias) (+ or *) residual
  * Replaces nn.Linear (+ GELU) of the block: attn.qkv, attn.proj and the Mlp
  * fc1 -> GELU(tanh) -> fc2 chain (Mlp layers.0 / layers.2 at
  * screamcast/checkpoint_compat.py:243-249; tanh GELU forced by
- * screamcast/strata_wrappers.py:76-100).
+ * screamcast/strata_wrappers.py:76-100), and the gated-attention gate
+ * a * sigmoid(gate_proj(x)) (attn.gate_proj in the manifests,
+ * tests/regression_data/sweep1_...param_order.txt:7-8): act = SIGMOID,
+ * res_op = MUL, residual = the attention output a.
  *
  * x: [M, K] bf16 (row stride ldx), w: [N, K] bf16 (nn.Linear layout, row
  * stride ldw), bias: [N] bf16 or NULL, residual: [M, N] bf16 (row stride ldr)
  * or NULL, out: [M, N] bf16 (row stride ldo).  fp32 accumulation.  The
- * residual is added after the activation.  K must be a multiple of 8 and
- * every row stride a multiple of 8 elements.  `out` may alias `residual`.
+ * residual is added (res_op ADD) or multiplied (res_op MUL) after the
+ * activation.  K must be a multiple of 8 and every row stride a multiple of
+ * 8 elements.  `out` may alias `residual`.
  * ------------------------------------------------------------------------- */
 typedef struct strata_hip_gemm_args {
   const void* x;
@@ -142,8 +164,8 @@ typedef struct strata_hip_gemm_args {
   int64_t ldw;
   int64_t ldr;
   int64_t ldo;
-  int32_t act; /* strata_hip_act */
-  int32_t reserved;
+  int32_t act;    /* strata_hip_act */
+  int32_t res_op; /* strata_hip_res_op */
 } strata_hip_gemm_args;
 
 int strata_hip_gemm_bias_act(const strata_hip_gemm_args* args, void* stream);

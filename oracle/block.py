@@ -10,6 +10,12 @@ screamcast/strata_wrappers.py:76-100; RoPE mode/base :153-162,:333-338):
     x = x + fc2(gelu_tanh(fc1(LN(x))))
 
 LayerNorm is non-affine (no LN parameters in the manifests), eps 1e-6.
+Optional production variants: gated attention ``a * sigmoid(gate_proj(h))``
+(attn.gate_proj in the manifests) and qk RMSNorm over the head dim before
+RoPE (screamcast/config.py:91-93; weights ``attn.q_norm.weight`` /
+``attn.k_norm.weight`` when elementwise-affine).  Their exact placement inside
+physicsnemo's block is not visible here: parity for those two is unpinned
+beyond this restatement.
 Composition of torch's own F.linear / F.layer_norm / F.gelu with the pinned
 ``oracle.na3d`` and ``oracle.rope``.
 """
@@ -24,9 +30,15 @@ from . import na3d as _na3d
 from . import rope as _rope
 
 
+def rms_norm(t: Tensor, eps: float, weight: Tensor | None = None) -> Tensor:
+    """RMSNorm over the last dim: t * rsqrt(mean(t^2) + eps) * weight."""
+    y = t * torch.rsqrt(t.pow(2).mean(dim=-1, keepdim=True) + eps)
+    return y * weight if weight is not None else y
+
+
 def block_forward(x: Tensor, params: dict, heads: int, kernel_size, cos: Tensor | None, sin: Tensor | None,
                   dilation=1, eps: float = 1e-6, layout: str = "half", gated: bool = False,
-                  dtype: torch.dtype = torch.float32) -> Tensor:
+                  dtype: torch.dtype = torch.float32, qk_norm: bool = False, qk_norm_eps: float = 1e-6) -> Tensor:
     """x ``[B, Z, Y, X, C]``; params keyed like the block's state dict."""
     p = {k: v.to(dtype) for k, v in params.items()}
     x = x.to(dtype)
@@ -35,6 +47,9 @@ def block_forward(x: Tensor, params: dict, heads: int, kernel_size, cos: Tensor 
     h = F.layer_norm(x, (C,), eps=eps)
     qkv = F.linear(h, p["attn.qkv.weight"], p.get("attn.qkv.bias")).view(B, Z, Y, X, 3, heads, D)
     q, k, v = qkv.unbind(dim=4)
+    if qk_norm:
+        q = rms_norm(q, qk_norm_eps, p.get("attn.q_norm.weight"))
+        k = rms_norm(k, qk_norm_eps, p.get("attn.k_norm.weight"))
     if cos is not None:
         q = _rope.apply_rope(q, cos, sin, layout)
         k = _rope.apply_rope(k, cos, sin, layout)

@@ -14,7 +14,7 @@ from pathlib import Path
 
 LIB_PATH = Path(__file__).resolve().parent / "libstrata_hip.so"
 
-ABI_VERSION = 1
+ABI_VERSION = 2
 
 OK = 0
 EINVAL = -1
@@ -27,6 +27,10 @@ BF16 = 1
 ACT_NONE = 0
 ACT_GELU_TANH = 1
 ACT_GELU_ERF = 2
+ACT_SIGMOID = 3
+
+RES_ADD = 0
+RES_MUL = 1
 
 ROPE_HALF = 0
 ROPE_INTERLEAVED = 1
@@ -75,6 +79,10 @@ class RopePackArgs(ctypes.Structure):
         ("head_dim", ctypes.c_int32),
         ("layout", ctypes.c_int32),
         ("qkv_row_stride", ctypes.c_int64),
+        ("qk_norm", ctypes.c_int32),
+        ("qk_norm_eps", ctypes.c_float),
+        ("q_norm_weight", ctypes.c_void_p),
+        ("k_norm_weight", ctypes.c_void_p),
     ]
 
 
@@ -93,7 +101,7 @@ class GemmArgs(ctypes.Structure):
         ("ldr", ctypes.c_int64),
         ("ldo", ctypes.c_int64),
         ("act", ctypes.c_int32),
-        ("reserved", ctypes.c_int32),
+        ("res_op", ctypes.c_int32),
     ]
 
 

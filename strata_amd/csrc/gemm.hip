@@ -24,6 +24,7 @@ struct GemmParams {
   int64_t M, N, K;
   int64_t ldx, ldw, ldr, ldo;
   int act;
+  int res_op;  // strata_hip_res_op: the residual is added or multiplied
   int mt, nt;  // tiles along M and N
 };
 
@@ -35,6 +36,19 @@ __device__ __forceinline__ float gelu_tanh(float x) {
   return x * __builtin_amdgcn_rcpf(1.f + __builtin_amdgcn_exp2f(-t));
 }
 __device__ __forceinline__ float gelu_erf(float x) { return 0.5f * x * (1.f + erff(x * 0.7071067811865476f)); }
+// sigmoid(x) = 1 / (1 + 2^(-x log2 e)); saturates to 0 / 1 through inf / 0.
+__device__ __forceinline__ float sigmoid_fast(float x) {
+  return __builtin_amdgcn_rcpf(1.f + __builtin_amdgcn_exp2f(-1.4426950408889634f * x));
+}
+__device__ __forceinline__ float apply_act(float v, int act) {
+  if (act == STRATA_HIP_ACT_GELU_TANH) return gelu_tanh(v);
+  if (act == STRATA_HIP_ACT_GELU_ERF) return gelu_erf(v);
+  if (act == STRATA_HIP_ACT_SIGMOID) return sigmoid_fast(v);
+  return v;
+}
+__device__ __forceinline__ float combine(float o, float r, int res_op) {
+  return res_op == STRATA_HIP_RES_MUL ? o * r : o + r;
+}
 
 template <int BM, int BN, int WGM, int WGN>
 __global__ __launch_bounds__(64 * WGM * WGN) void gemm_bias_act_kernel(GemmParams p) {
@@ -183,27 +197,22 @@ __global__ __launch_bounds__(64 * WGM * WGN) void gemm_bias_act_kernel(GemmParam
             for (int e = 0; e < 4 && gn + e < p.N; ++e) v[e] += (float)p.bias[gn + e];
           }
         }
-        if (p.act == STRATA_HIP_ACT_GELU_TANH) {
 #pragma unroll
-          for (int e = 0; e < 4; ++e) v[e] = gelu_tanh(v[e]);
-        } else if (p.act == STRATA_HIP_ACT_GELU_ERF) {
-#pragma unroll
-          for (int e = 0; e < 4; ++e) v[e] = gelu_erf(v[e]);
-        }
+        for (int e = 0; e < 4; ++e) v[e] = apply_act(v[e], p.act);
         if (full) {
           if (p.res) {
             const u32x2 rw = *(const u32x2*)(p.res + gm * p.ldr + gn);
-            v[0] += bf16_lo(rw[0]);
-            v[1] += bf16_hi(rw[0]);
-            v[2] += bf16_lo(rw[1]);
-            v[3] += bf16_hi(rw[1]);
+            v[0] = combine(v[0], bf16_lo(rw[0]), p.res_op);
+            v[1] = combine(v[1], bf16_hi(rw[0]), p.res_op);
+            v[2] = combine(v[2], bf16_lo(rw[1]), p.res_op);
+            v[3] = combine(v[3], bf16_hi(rw[1]), p.res_op);
           }
           const u32x2 ow = {pack_bf16x2(v[0], v[1]), pack_bf16x2(v[2], v[3])};
           *(u32x2*)(p.out + gm * p.ldo + gn) = ow;
         } else {
           for (int e = 0; e < 4 && gn + e < p.N; ++e) {
             float o = v[e];
-            if (p.res) o += (float)p.res[gm * p.ldr + gn + e];
+            if (p.res) o = combine(o, (float)p.res[gm * p.ldr + gn + e], p.res_op);
             p.out[gm * p.ldo + gn + e] = (bf16)o;
           }
         }
@@ -229,27 +238,22 @@ __device__ __forceinline__ void store_quad(const GemmParams& p, int64_t gm, int6
       for (int e = 0; e < 4 && gn + e < p.N; ++e) v[e] += (float)p.bias[gn + e];
     }
   }
-  if (p.act == STRATA_HIP_ACT_GELU_TANH) {
 #pragma unroll
-    for (int e = 0; e < 4; ++e) v[e] = gelu_tanh(v[e]);
-  } else if (p.act == STRATA_HIP_ACT_GELU_ERF) {
-#pragma unroll
-    for (int e = 0; e < 4; ++e) v[e] = gelu_erf(v[e]);
-  }
+  for (int e = 0; e < 4; ++e) v[e] = apply_act(v[e], p.act);
   if (full) {
     if (p.res) {
       const u32x2 rw = *(const u32x2*)(p.res + gm * p.ldr + gn);
-      v[0] += bf16_lo(rw[0]);
-      v[1] += bf16_hi(rw[0]);
-      v[2] += bf16_lo(rw[1]);
-      v[3] += bf16_hi(rw[1]);
+      v[0] = combine(v[0], bf16_lo(rw[0]), p.res_op);
+      v[1] = combine(v[1], bf16_hi(rw[0]), p.res_op);
+      v[2] = combine(v[2], bf16_lo(rw[1]), p.res_op);
+      v[3] = combine(v[3], bf16_hi(rw[1]), p.res_op);
     }
     const u32x2 ow = {pack_bf16x2(v[0], v[1]), pack_bf16x2(v[2], v[3])};
     *(u32x2*)(p.out + gm * p.ldo + gn) = ow;
   } else {
     for (int e = 0; e < 4 && gn + e < p.N; ++e) {
       float o = v[e];
-      if (p.res) o += (float)p.res[gm * p.ldr + gn + e];
+      if (p.res) o = combine(o, (float)p.res[gm * p.ldr + gn + e], p.res_op);
       p.out[gm * p.ldo + gn + e] = (bf16)o;
     }
   }
@@ -418,8 +422,7 @@ __device__ __forceinline__ void gemm_dma_body(const GemmParams& p) {
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
           v[e] = acc[i][j][4 * q + e] + bv[e];
-          if (p.act == STRATA_HIP_ACT_GELU_TANH) v[e] = gelu_tanh(v[e]);
-          else if (p.act == STRATA_HIP_ACT_GELU_ERF) v[e] = gelu_erf(v[e]);
+          v[e] = apply_act(v[e], p.act);
         }
         const int ml = 32 * j + l32;
         const u32x2 w2 = {pack_bf16x2(v[0], v[1]), pack_bf16x2(v[2], v[3])};
@@ -439,14 +442,15 @@ __device__ __forceinline__ void gemm_dma_body(const GemmParams& p) {
         const u32x4 r4 = *(const u32x4*)(p.res + gm * p.ldr + gn);
 #pragma unroll
         for (int e = 0; e < 4; ++e)
-          o[e] = pack_bf16x2(bf16_lo(w4[e]) + bf16_lo(r4[e]), bf16_hi(w4[e]) + bf16_hi(r4[e]));
+          o[e] = pack_bf16x2(combine(bf16_lo(w4[e]), bf16_lo(r4[e]), p.res_op),
+                             combine(bf16_hi(w4[e]), bf16_hi(r4[e]), p.res_op));
       }
       *(u32x4*)(p.out + gm * p.ldo + gn) = o;
     } else {
       for (int e = 0; e < 8 && gn + e < p.N; ++e) {
         const uint32_t wd = w4[e >> 1];
         float o = (e & 1) ? bf16_hi(wd) : bf16_lo(wd);
-        if (p.res) o += (float)p.res[gm * p.ldr + gn + e];
+        if (p.res) o = combine(o, (float)p.res[gm * p.ldr + gn + e], p.res_op);
         p.out[gm * p.ldo + gn + e] = (bf16)o;
       }
     }
@@ -486,7 +490,8 @@ extern "C" int strata_hip_gemm_bias_act(const strata_hip_gemm_args* a, void* str
   if (((uintptr_t)a->x & 15) || ((uintptr_t)a->w & 15) || ((uintptr_t)a->out & 7) ||
       (a->residual && ((uintptr_t)a->residual & 7)) || (a->bias && ((uintptr_t)a->bias & 7)))
     return fail(STRATA_HIP_EINVAL, "gemm: x/w must be 16-byte aligned, out/residual/bias 8-byte aligned");
-  if (a->act < STRATA_HIP_ACT_NONE || a->act > STRATA_HIP_ACT_GELU_ERF) return fail(STRATA_HIP_EINVAL, "gemm: bad act");
+  if (a->act < STRATA_HIP_ACT_NONE || a->act > STRATA_HIP_ACT_SIGMOID) return fail(STRATA_HIP_EINVAL, "gemm: bad act");
+  if (a->res_op != STRATA_HIP_RES_ADD && a->res_op != STRATA_HIP_RES_MUL) return fail(STRATA_HIP_EINVAL, "gemm: bad res_op");
   GemmParams p;
   p.x = (const bf16*)a->x;
   p.w = (const bf16*)a->w;
@@ -501,6 +506,7 @@ extern "C" int strata_hip_gemm_bias_act(const strata_hip_gemm_args* a, void* str
   p.ldr = a->ldr;
   p.ldo = a->ldo;
   p.act = a->act;
+  p.res_op = a->res_op;
   hipStream_t st = (hipStream_t)stream;
   // The large-tile kernels stream 64-wide K steps with 32-bit lane offsets
   // inside a 256-row block: K a multiple of 64, row strides small enough.

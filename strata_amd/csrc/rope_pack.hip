@@ -4,7 +4,11 @@
 // tables, rotates the channel pairs of q and k, copies v, and writes three
 // heads-last [M, H, D] tensors.  Each thread handles one 16-byte run of
 // pairs of one (token, head): 8 pairs for the half layout (two 16-byte runs
-// D/2 apart), 4 pairs for the interleaved layout (one 16-byte run).
+// D/2 apart), 4 pairs for the interleaved layout (one 16-byte run).  With
+// qk_norm, q and k of each (token, head) are RMS-normalised over D first: the
+// D/16 (or D/8) threads of a head are consecutive lanes and reduce their sums
+// of squares with lane shuffles; the values stay fp32 until after the
+// rotation.
 #include "common.h"
 
 namespace strata {
@@ -19,7 +23,33 @@ struct RopeParams {
   int64_t M;
   int Z, Y, X, Zt, H, D;
   int64_t ld;
+  int qk_norm;
+  float eps;
+  const bf16* qw;  // RMSNorm weights [D] or null
+  const bf16* kw;
 };
+
+__device__ __forceinline__ void unpack8(const u32x4& a, float* f) {
+#pragma unroll
+  for (int w = 0; w < 4; ++w) {
+    f[2 * w] = bf16_lo(a[w]);
+    f[2 * w + 1] = bf16_hi(a[w]);
+  }
+}
+
+// RMS-normalise the n values f[] a lane holds of one head; `lanes`
+// consecutive lanes (a power of two) hold the head's D values.  dof[i] is the
+// channel of f[i] for the weight.
+template <int NV>
+__device__ __forceinline__ void rms_norm(float* f, const int* dof, int lanes, int D, float eps, const bf16* w) {
+  float ss = 0.f;
+#pragma unroll
+  for (int i = 0; i < NV; ++i) ss = fmaf(f[i], f[i], ss);
+  for (int o = 1; o < lanes; o <<= 1) ss += __shfl_xor(ss, o);
+  const float r = rsqrtf(ss / (float)D + eps);
+#pragma unroll
+  for (int i = 0; i < NV; ++i) f[i] *= w ? r * (float)w[dof[i]] : r;
+}
 
 __device__ __forceinline__ int64_t table_row(const RopeParams& p, int64_t tok) {
   const int64_t x = tok % p.X;
@@ -32,16 +62,38 @@ __device__ __forceinline__ int64_t table_row(const RopeParams& p, int64_t tok) {
   return ((b * p.Zt + zt) * p.Y + y) * p.X + x;
 }
 
-__device__ __forceinline__ void rot8(const u32x4& a, const u32x4& b, const float* c, const float* s, u32x4& oa,
+// Rotate 8 half-layout pairs (a[j], b[j]) = (d, d + D/2) and pack to bf16.
+__device__ __forceinline__ void rot8(const float* a, const float* b, const float* c, const float* s, u32x4& oa,
                                      u32x4& ob) {
 #pragma unroll
   for (int w = 0; w < 4; ++w) {
-    const float a0 = bf16_lo(a[w]), a1 = bf16_hi(a[w]);
-    const float b0 = bf16_lo(b[w]), b1 = bf16_hi(b[w]);
+    const float a0 = a[2 * w], a1 = a[2 * w + 1], b0 = b[2 * w], b1 = b[2 * w + 1];
     const float c0 = c[2 * w], c1 = c[2 * w + 1], s0 = s[2 * w], s1 = s[2 * w + 1];
     oa[w] = pack_bf16x2(a0 * c0 - b0 * s0, a1 * c1 - b1 * s1);
     ob[w] = pack_bf16x2(a0 * s0 + b0 * c0, a1 * s1 + b1 * c1);
   }
+}
+
+// One head's q or k run of the half layout: optional RMSNorm, then rotation.
+__device__ __forceinline__ void half_run(const RopeParams& p, const bf16* src, bf16* dst, const float* cs,
+                                         const float* sn, int c, int cph, const bf16* w) {
+  const int half = p.D / 2;
+  float f[16];  // f[0..7]: d = 8c + j, f[8..15]: d = 8c + j + D/2
+  unpack8(*(const u32x4*)(src), f);
+  unpack8(*(const u32x4*)(src + half), f + 8);
+  if (p.qk_norm) {
+    int dof[16];
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      dof[j] = 8 * c + j;
+      dof[8 + j] = 8 * c + j + half;
+    }
+    rms_norm<16>(f, dof, cph, p.D, p.eps, w);
+  }
+  u32x4 oa, ob;
+  rot8(f, f + 8, cs, sn, oa, ob);
+  *(u32x4*)(dst) = oa;
+  *(u32x4*)(dst + half) = ob;
 }
 
 // Half layout: pair p = (d = p, d = p + D/2).
@@ -65,31 +117,29 @@ __global__ __launch_bounds__(256) void rope_pack_half_kernel(RopeParams p, int64
   *(f32x4*)&sn[4] = *(const f32x4*)(p.sin + trow + 4);
 
   const int64_t dst = tok * C + (int64_t)h * p.D + 8 * c;
-  {
-    const u32x4 a = *(const u32x4*)(src), b = *(const u32x4*)(src + half);
-    u32x4 oa, ob;
-    rot8(a, b, cs, sn, oa, ob);
-    *(u32x4*)(p.q + dst) = oa;
-    *(u32x4*)(p.q + dst + half) = ob;
-  }
-  {
-    const u32x4 a = *(const u32x4*)(src + C), b = *(const u32x4*)(src + C + half);
-    u32x4 oa, ob;
-    rot8(a, b, cs, sn, oa, ob);
-    *(u32x4*)(p.k + dst) = oa;
-    *(u32x4*)(p.k + dst + half) = ob;
-  }
+  half_run(p, src, p.q + dst, cs, sn, c, cph, p.qw);
+  half_run(p, src + C, p.k + dst, cs, sn, c, cph, p.kw);
   *(u32x4*)(p.v + dst) = *(const u32x4*)(src + 2 * C);
   *(u32x4*)(p.v + dst + half) = *(const u32x4*)(src + 2 * C + half);
 }
 
 // Interleaved layout: pair p = (d = 2p, d = 2p + 1).
-__device__ __forceinline__ u32x4 rot_inter(const u32x4& a, const float* c, const float* s) {
+// One head's 8 consecutive q or k values (4 pairs): optional RMSNorm, rotation.
+__device__ __forceinline__ u32x4 rot_inter(const RopeParams& p, const u32x4& a, const float* c, const float* s, int cc,
+                                           int cph, const bf16* w) {
+  float f[8];
+  unpack8(a, f);
+  if (p.qk_norm) {
+    int dof[8];
+#pragma unroll
+    for (int j = 0; j < 8; ++j) dof[j] = 8 * cc + j;
+    rms_norm<8>(f, dof, cph, p.D, p.eps, w);
+  }
   u32x4 o;
 #pragma unroll
-  for (int w = 0; w < 4; ++w) {
-    const float x0 = bf16_lo(a[w]), x1 = bf16_hi(a[w]);
-    o[w] = pack_bf16x2(x0 * c[w] - x1 * s[w], x0 * s[w] + x1 * c[w]);
+  for (int k = 0; k < 4; ++k) {
+    const float x0 = f[2 * k], x1 = f[2 * k + 1];
+    o[k] = pack_bf16x2(x0 * c[k] - x1 * s[k], x0 * s[k] + x1 * c[k]);
   }
   return o;
 }
@@ -111,8 +161,8 @@ __global__ __launch_bounds__(256) void rope_pack_inter_kernel(RopeParams p, int6
   *(f32x4*)&cs[0] = *(const f32x4*)(p.cos + trow);
   *(f32x4*)&sn[0] = *(const f32x4*)(p.sin + trow);
   const int64_t dst = tok * C + (int64_t)h * p.D + 8 * c;
-  *(u32x4*)(p.q + dst) = rot_inter(*(const u32x4*)(src), cs, sn);
-  *(u32x4*)(p.k + dst) = rot_inter(*(const u32x4*)(src + C), cs, sn);
+  *(u32x4*)(p.q + dst) = rot_inter(p, *(const u32x4*)(src), cs, sn, c, cph, p.qw);
+  *(u32x4*)(p.k + dst) = rot_inter(p, *(const u32x4*)(src + C), cs, sn, c, cph, p.kw);
   *(u32x4*)(p.v + dst) = *(const u32x4*)(src + 2 * C);
 }
 
@@ -154,6 +204,19 @@ extern "C" int strata_hip_rope_qkv_pack(const strata_hip_rope_pack_args* a, void
   p.ld = a->qkv_row_stride;
   p.M = (int64_t)a->batch * p.Z * p.Y * p.X;
   const int cph = a->layout == STRATA_HIP_ROPE_HALF ? p.D / 16 : p.D / 8;
+  if (a->qk_norm != 0 && a->qk_norm != 1) return fail(STRATA_HIP_EINVAL, "rope_qkv_pack: qk_norm must be 0 or 1");
+  if (a->qk_norm) {
+    // the lanes of one head reduce by shuffles within an aligned power-of-two group
+    if ((cph & (cph - 1)) || cph > 64)
+      return fail(STRATA_HIP_EINVAL, "rope_qkv_pack: qk_norm needs D/16 (half) or D/8 (interleaved) a power of two <= 64");
+    if (!(a->qk_norm_eps >= 0.f)) return fail(STRATA_HIP_EINVAL, "rope_qkv_pack: qk_norm_eps must be >= 0");
+    if (((uintptr_t)a->q_norm_weight & 1) || ((uintptr_t)a->k_norm_weight & 1))
+      return fail(STRATA_HIP_EINVAL, "rope_qkv_pack: norm weights must be 2-byte aligned");
+  }
+  p.qk_norm = a->qk_norm;
+  p.eps = a->qk_norm_eps;
+  p.qw = a->qk_norm ? (const bf16*)a->q_norm_weight : nullptr;
+  p.kw = a->qk_norm ? (const bf16*)a->k_norm_weight : nullptr;
   const int64_t total = p.M * p.H * cph;
   if (total == 0) return STRATA_HIP_OK;
   const int threads = 256;

@@ -66,15 +66,20 @@ class GemmGeluMlp(nn.Module):
 
 
 class FusedNA3DAttention(nn.Module):
-    """qkv GEMM -> RoPE + QKV pack -> NA3D -> (gate) -> proj GEMM (+ residual).
+    """qkv GEMM -> (qk RMSNorm +) RoPE + QKV pack -> NA3D -> (gate) -> proj GEMM (+ residual).
 
     Drop-in for the physicsnemo Strata attention's ``qkv -> split -> RoPE ->
     natten.na3d -> proj`` chain (keys attn.qkv / attn.proj / attn.gate_proj;
-    gate applied as ``a * sigmoid(gate_proj(x))`` before proj).
+    gate applied as ``a * sigmoid(gate_proj(x))`` before proj, fused into the
+    gate GEMM's epilogue).  ``qk_norm`` (screamcast/config.py:91-93) RMS-
+    normalises q and k per head inside the RoPE pack kernel; with
+    ``qk_norm_affine`` the weights live in ``attn.q_norm`` / ``attn.k_norm``
+    (nn.RMSNorm, registered after the manifest keys).
     """
 
     def __init__(self, dim: int, num_heads: int, kernel_size, dilation=1, qkv_bias: bool = True,
-                 gated: bool = False, rope_layout: int = _lib.ROPE_HALF, scale: Optional[float] = None):
+                 gated: bool = False, rope_layout: int = _lib.ROPE_HALF, scale: Optional[float] = None,
+                 qk_norm: bool = False, qk_norm_affine: bool = False, qk_norm_eps: float = 1e-6):
         super().__init__()
         if dim % num_heads:
             raise ValueError("dim must be divisible by num_heads")
@@ -90,22 +95,33 @@ class FusedNA3DAttention(nn.Module):
             self.gate_proj = nn.Linear(dim, dim)
         else:
             self.gate_proj = None
+        self.qk_norm, self.qk_norm_eps = qk_norm, qk_norm_eps
+        if qk_norm and qk_norm_affine:
+            self.q_norm = nn.RMSNorm(self.head_dim, eps=qk_norm_eps)
+            self.k_norm = nn.RMSNorm(self.head_dim, eps=qk_norm_eps)
+        else:
+            self.q_norm = self.k_norm = None
 
     def attention(self, x: Tensor, rope: Optional[tuple[Tensor, Tensor]] = None) -> Tensor:
         """Attention output before the projection, ``[B, Z, Y, X, C]``."""
         B, Z, Y, X, C = x.shape
         H, D = self.num_heads, self.head_dim
         qkv = ops.gemm_bias_act(x, self.qkv.weight, self.qkv.bias, None, _lib.ACT_NONE)
+        if rope is None and self.qk_norm:  # normalise in the pack kernel with identity rotations
+            ident = torch.ones(B, 1, Y, X, D // 2, device=x.device)
+            rope = (ident, torch.zeros_like(ident))
         if rope is not None:
-            q, k, v = ops.rope_qkv_pack(qkv, rope[0], rope[1], H, self.rope_layout)
+            qw = self.q_norm.weight if self.q_norm is not None else None
+            kw = self.k_norm.weight if self.k_norm is not None else None
+            q, k, v = ops.rope_qkv_pack(qkv, rope[0], rope[1], H, self.rope_layout, self.qk_norm, self.qk_norm_eps,
+                                        qw, kw)
         else:
             qkv6 = qkv.view(B, Z, Y, X, 3, H, D)
             q, k, v = qkv6[..., 0, :, :], qkv6[..., 1, :, :], qkv6[..., 2, :, :]
         a = ops.na3d_fwd(q, k, v, self.kernel_size, self.dilation, self.scale, [0, 0, 0], [Z, Y, X])
         a = a.view(B, Z, Y, X, C)
-        if self.gate_proj is not None:
-            gate = ops.gemm_bias_act(x, self.gate_proj.weight, self.gate_proj.bias, None, _lib.ACT_NONE)
-            a = a * torch.sigmoid(gate)
+        if self.gate_proj is not None:  # a * sigmoid(x @ Wg^T + bg) in one GEMM
+            a = ops.gemm_bias_act(x, self.gate_proj.weight, self.gate_proj.bias, a, _lib.ACT_SIGMOID, _lib.RES_MUL)
         return a
 
     def forward(self, x: Tensor, rope: Optional[tuple[Tensor, Tensor]] = None,
@@ -124,10 +140,12 @@ class StrataBlock(nn.Module):
     """
 
     def __init__(self, dim: int, num_heads: int, kernel_size, mlp_ratio: float = 4.0, dilation=1,
-                 qkv_bias: bool = True, gated: bool = False, eps: float = 1e-6):
+                 qkv_bias: bool = True, gated: bool = False, eps: float = 1e-6, qk_norm: bool = False,
+                 qk_norm_affine: bool = False, qk_norm_eps: float = 1e-6):
         super().__init__()
         self.eps = eps
-        self.attn = FusedNA3DAttention(dim, num_heads, kernel_size, dilation, qkv_bias, gated)
+        self.attn = FusedNA3DAttention(dim, num_heads, kernel_size, dilation, qkv_bias, gated,
+                                       qk_norm=qk_norm, qk_norm_affine=qk_norm_affine, qk_norm_eps=qk_norm_eps)
         self.mlp = GemmGeluMlp(dim, int(dim * mlp_ratio))
 
     def forward(self, x: Tensor, rope: Optional[tuple[Tensor, Tensor]] = None) -> Tensor:

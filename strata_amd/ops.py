@@ -141,13 +141,18 @@ na3d_fwd.register_autograd(_no_backward("strata_hip::na3d_fwd"))
 # RoPE + QKV pack
 # ---------------------------------------------------------------------------
 @torch.library.custom_op("strata_hip::rope_qkv_pack", mutates_args=())
-def rope_qkv_pack(qkv: Tensor, cos: Tensor, sin: Tensor, heads: int, rope_layout: int) -> tuple[Tensor, Tensor, Tensor]:
+def rope_qkv_pack(qkv: Tensor, cos: Tensor, sin: Tensor, heads: int, rope_layout: int, qk_norm: bool = False,
+                  qk_norm_eps: float = 1e-6, q_norm_weight: Optional[Tensor] = None,
+                  k_norm_weight: Optional[Tensor] = None) -> tuple[Tensor, Tensor, Tensor]:
     """Split ``attn.qkv``'s output into heads-last q, k, v and rotate q, k.
 
     qkv: ``[B, Z, Y, X, 3*H*D]`` bf16 (column order (3, H, D), last dim
     contiguous, rows possibly strided).  cos, sin: fp32 ``[B, Zt, Y, X, D/2]``
     with Zt in {1, Z}.  rope_layout: 0 = half split (pair p = (p, p + D/2)),
-    1 = interleaved (pair p = (2p, 2p+1)).  Returns q, k, v ``[B, Z, Y, X, H, D]``.
+    1 = interleaved (pair p = (2p, 2p+1)).  qk_norm: RMSNorm over D of each
+    (token, head) of q and k before the rotation, ``x * rsqrt(mean(x^2) + eps)
+    * weight`` (weights bf16 ``[D]`` or None; screamcast/config.py:91-93).
+    Returns q, k, v ``[B, Z, Y, X, H, D]``.
     """
     name = "rope_qkv_pack"
     _require_gpu(name, qkv, cos, sin)
@@ -168,6 +173,16 @@ def rope_qkv_pack(qkv: Tensor, cos: Tensor, sin: Tensor, heads: int, rope_layout
     if flat.stride(1) != 1:
         raise ValueError(f"{name}: the last dim of qkv must be contiguous")
     cos_c, sin_c = cos.contiguous(), sin.contiguous()
+    wts = []
+    for t, nm in ((q_norm_weight, "q_norm_weight"), (k_norm_weight, "k_norm_weight")):
+        if t is not None:
+            if not qk_norm:
+                raise ValueError(f"{name}: {nm} given without qk_norm")
+            _require_gpu(name, t)
+            if t.dtype != torch.bfloat16 or tuple(t.shape) != (D,):
+                raise ValueError(f"{name}: {nm} must be bfloat16 [{D}]")
+            t = t.contiguous()
+        wts.append(t)
     shape = (B, Z, Y, X, heads, D)
     q = torch.empty(shape, dtype=qkv.dtype, device=qkv.device)
     k = torch.empty_like(q)
@@ -182,13 +197,17 @@ def rope_qkv_pack(qkv: Tensor, cos: Tensor, sin: Tensor, heads: int, rope_layout
     a.table_z = cos.shape[1]
     a.heads, a.head_dim, a.layout = heads, D, int(rope_layout)
     a.qkv_row_stride = flat.stride(0)
+    a.qk_norm = 1 if qk_norm else 0
+    a.qk_norm_eps = float(qk_norm_eps)
+    a.q_norm_weight = wts[0].data_ptr() if wts[0] is not None else None
+    a.k_norm_weight = wts[1].data_ptr() if wts[1] is not None else None
     with torch.cuda.device(qkv.device):
         _lib.call("strata_hip_rope_qkv_pack", a, _stream(qkv))
     return q, k, v
 
 
 @rope_qkv_pack.register_fake
-def _(qkv, cos, sin, heads, rope_layout):
+def _(qkv, cos, sin, heads, rope_layout, qk_norm=False, qk_norm_eps=1e-6, q_norm_weight=None, k_norm_weight=None):
     B, Z, Y, X, C3 = qkv.shape
     D = C3 // (3 * heads)
     shape = (B, Z, Y, X, heads, D)
@@ -201,7 +220,7 @@ rope_qkv_pack.register_autograd(_no_backward("strata_hip::rope_qkv_pack"))
 # ---------------------------------------------------------------------------
 # GEMM + bias + activation + residual
 # ---------------------------------------------------------------------------
-ACTS = {"none": _lib.ACT_NONE, "gelu_tanh": _lib.ACT_GELU_TANH, "gelu": _lib.ACT_GELU_ERF}
+ACTS = {"none": _lib.ACT_NONE, "gelu_tanh": _lib.ACT_GELU_TANH, "gelu": _lib.ACT_GELU_ERF, "sigmoid": _lib.ACT_SIGMOID}
 
 
 def _rows(name: str, t: Tensor, what: str) -> Tensor:
@@ -213,13 +232,16 @@ def _rows(name: str, t: Tensor, what: str) -> Tensor:
 
 
 @torch.library.custom_op("strata_hip::gemm_bias_act", mutates_args=())
-def gemm_bias_act(x: Tensor, w: Tensor, bias: Optional[Tensor], residual: Optional[Tensor], act: int) -> Tensor:
-    """``act(x @ w.T + bias) + residual`` with fp32 accumulation, bf16 in/out.
+def gemm_bias_act(x: Tensor, w: Tensor, bias: Optional[Tensor], residual: Optional[Tensor], act: int,
+                  res_op: int = 0) -> Tensor:
+    """``act(x @ w.T + bias) + residual`` (res_op 0) or ``* residual`` (res_op 1),
+    fp32 accumulation, bf16 in/out.
 
     x ``[..., K]``, w ``[N, K]`` (nn.Linear layout), bias ``[N]``, residual
-    ``[..., N]``.  act: 0 none, 1 GELU(tanh), 2 GELU(erf).  Replaces
+    ``[..., N]``.  act: 0 none, 1 GELU(tanh), 2 GELU(erf), 3 sigmoid.  Replaces
     nn.Linear (+ nn.GELU) in the block's attn.qkv / attn.proj / Mlp
-    (screamcast/checkpoint_compat.py:243-249, screamcast/strata_wrappers.py:76-100).
+    (screamcast/checkpoint_compat.py:243-249, screamcast/strata_wrappers.py:76-100)
+    and, with act 3 / res_op 1, the attention gate ``a * sigmoid(gate_proj(x))``.
     """
     name = "gemm_bias_act"
     _require_gpu(name, x, w, bias, residual)
@@ -253,13 +275,14 @@ def gemm_bias_act(x: Tensor, w: Tensor, bias: Optional[Tensor], residual: Option
     a.ldr = (r2.stride(0) if M > 1 else N) if r2 is not None else 0
     a.ldo = N
     a.act = int(act)
+    a.res_op = int(res_op)
     with torch.cuda.device(x.device):
         _lib.call("strata_hip_gemm_bias_act", a, _stream(x))
     return out
 
 
 @gemm_bias_act.register_fake
-def _(x, w, bias, residual, act):
+def _(x, w, bias, residual, act, res_op=0):
     return x.new_empty((*x.shape[:-1], w.shape[0]))
 
 

@@ -13,13 +13,17 @@ from .conftest import rel_l2
 pytestmark = pytest.mark.gpu
 
 
-def _block_case(gpu, B, Z, Y, X, C, H, kernel, seed=0, gated=False):
+def _block_case(gpu, B, Z, Y, X, C, H, kernel, seed=0, gated=False, qk_norm=False, qk_norm_affine=False):
     g = torch.Generator().manual_seed(1)
-    blk = StrataBlock(C, H, kernel, gated=gated)
+    blk = StrataBlock(C, H, kernel, gated=gated, qk_norm=qk_norm, qk_norm_affine=qk_norm_affine)
     init_xavier_(blk, g)
     if gated:
         with torch.no_grad():
             blk.attn.gate_proj.bias.normal_(generator=g)
+    if qk_norm_affine:
+        with torch.no_grad():
+            blk.attn.q_norm.weight.normal_(1.0, 0.3, generator=g)
+            blk.attn.k_norm.weight.normal_(1.0, 0.3, generator=g)
     params = {k: v.detach().clone() for k, v in blk.state_dict().items()}
     blk = blk.to(gpu).bfloat16()
     gx = torch.Generator().manual_seed(seed)
@@ -32,7 +36,7 @@ def _block_case(gpu, B, Z, Y, X, C, H, kernel, seed=0, gated=False):
     # fp32 oracle on the same bf16 inputs and bf16-rounded weights
     params = {k: v.bfloat16().float() for k, v in params.items()}
     c64, s64 = R.tables(lat, lon, C // H, 10000.0, ls)
-    ref = OB.block_forward(x.float(), params, H, kernel, c64.float(), s64.float(), gated=gated)
+    ref = OB.block_forward(x.float(), params, H, kernel, c64.float(), s64.float(), gated=gated, qk_norm=qk_norm)
     return out, ref
 
 
@@ -43,6 +47,17 @@ def test_block_small(gpu):
 
 def test_block_gated(gpu):
     out, ref = _block_case(gpu, 1, 4, 12, 20, 256, 4, (3, 5, 5), gated=True)
+    assert rel_l2(out.float(), ref) <= 1e-2
+
+
+def test_block_qk_norm(gpu):
+    out, ref = _block_case(gpu, 1, 4, 12, 16, 256, 4, (3, 5, 5), qk_norm=True)
+    assert rel_l2(out.float(), ref) <= 1e-2
+
+
+def test_block_production_variant(gpu):
+    """Gated attention + qk RMSNorm with elementwise weights, 1024 wide (16 x 64 heads)."""
+    out, ref = _block_case(gpu, 1, 4, 12, 12, 1024, 16, (3, 7, 7), gated=True, qk_norm=True, qk_norm_affine=True)
     assert rel_l2(out.float(), ref) <= 1e-2
 
 

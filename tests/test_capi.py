@@ -123,6 +123,19 @@ def test_gemm_and_layernorm_validation(lib):
     r.qkv_row_stride = 384
     assert lib.strata_hip_rope_qkv_pack(ctypes.byref(r), None) == _lib.EINVAL
     assert "table_z" in lib.strata_hip_last_error().decode()
+    r.table_z, r.qk_norm = 1, 2
+    assert lib.strata_hip_rope_qkv_pack(ctypes.byref(r), None) == _lib.EINVAL
+    assert "qk_norm" in lib.strata_hip_last_error().decode()
+    r.qk_norm, r.head_dim, r.qkv_row_stride = 1, 48, 288  # D/16 = 3 is not a power of two
+    assert lib.strata_hip_rope_qkv_pack(ctypes.byref(r), None) == _lib.EINVAL
+    assert "power of two" in lib.strata_hip_last_error().decode()
+    g.k = g.ldx = g.ldw = 16
+    g.res_op = 5
+    assert lib.strata_hip_gemm_bias_act(ctypes.byref(g), None) == _lib.EINVAL
+    assert "res_op" in lib.strata_hip_last_error().decode()
+    g.res_op, g.act = 0, 4
+    assert lib.strata_hip_gemm_bias_act(ctypes.byref(g), None) == _lib.EINVAL
+    assert "act" in lib.strata_hip_last_error().decode()
 
 
 def test_empty_problem_is_a_no_op(lib):

@@ -53,6 +53,33 @@ def test_gemm_vs_fp64(gpu, case):
     assert rel_l2(out.float(), ref) <= 1e-2
 
 
+@pytest.mark.parametrize("M,N,K", [(300, 256, 128), (4096, 1024, 1024), (77, 200, 64)])
+def test_gemm_sigmoid_gate_vs_fp64(gpu, M, N, K):
+    """Gate epilogue: a * sigmoid(x @ w.T + b) with a passed as the residual (res_op MUL)."""
+    print(f"gemm gate {M}x{N}x{K}", flush=True)
+    g = torch.Generator().manual_seed(M + N)
+    x = _randn((M, K), g)
+    w = _randn((N, K), g, 2 * K**-0.5)
+    b = _randn((N,), g)
+    a = _randn((M, N), g)
+    out = torch.ops.strata_hip.gemm_bias_act(x.to(gpu), w.to(gpu), b.to(gpu), a.to(gpu), _lib.ACT_SIGMOID, _lib.RES_MUL)
+    ref = a.double() * torch.sigmoid(x.double() @ w.double().T + b.double())
+    assert rel_l2(out.float(), ref) <= 1e-2
+
+
+def test_gemm_sigmoid_saturates(gpu):
+    """Pre-activations of +-200 give exactly the residual and exactly zero."""
+    M, N, K = 64, 64, 64
+    x = torch.zeros(M, K, dtype=torch.bfloat16)
+    w = torch.zeros(N, K, dtype=torch.bfloat16)
+    b = torch.tensor([200.0, -200.0] * (N // 2), dtype=torch.bfloat16)
+    a = torch.randn(M, N).bfloat16()
+    out = torch.ops.strata_hip.gemm_bias_act(x.to(gpu), w.to(gpu), b.to(gpu), a.to(gpu), _lib.ACT_SIGMOID,
+                                             _lib.RES_MUL).cpu()
+    assert torch.equal(out[:, 0::2], a[:, 0::2])
+    assert torch.equal(out[:, 1::2], torch.zeros_like(a[:, 1::2]))
+
+
 def test_gemm_batched_shape_and_aliasing(gpu):
     g = torch.Generator().manual_seed(1)
     x = _randn((2, 3, 5, 64), g).to(gpu)
@@ -82,6 +109,36 @@ def test_rope_pack_vs_oracle(gpu, layout, zt):
         d = (got.double().cpu() - ref).abs()
         assert (d <= ref.abs() * 2**-8 + 1e-6).all(), d.max()
     assert torch.equal(v.cpu(), qkv.view(B, Z, Y, X, 3, H, D)[..., 2, :, :])
+
+
+@pytest.mark.parametrize("layout", [_lib.ROPE_HALF, _lib.ROPE_INTERLEAVED])
+@pytest.mark.parametrize("affine", [False, True])
+def test_rope_pack_qk_norm_vs_oracle(gpu, layout, affine):
+    """qk RMSNorm over D (per token, head) fused before the rotation."""
+    from oracle import block as OB
+    B, Z, Y, X, H, D = 1, 3, 6, 10, 4, 64
+    g = torch.Generator().manual_seed(11 + layout + 2 * affine)
+    qkv = _randn((B, Z, Y, X, 3 * H * D), g, 3.0)
+    ang = torch.rand(B, 1, Y, X, D // 2, generator=g, dtype=torch.float64) * 20 - 10
+    cos, sin = torch.cos(ang), torch.sin(ang)
+    qw = (1 + 0.3 * torch.randn(D, generator=g)).bfloat16() if affine else None
+    kw = (1 + 0.3 * torch.randn(D, generator=g)).bfloat16() if affine else None
+    eps = 1e-6
+    q, k, v = torch.ops.strata_hip.rope_qkv_pack(
+        qkv.to(gpu), cos.float().to(gpu), sin.float().to(gpu), H, layout, True, eps,
+        None if qw is None else qw.to(gpu), None if kw is None else kw.to(gpu))
+    t = qkv.double().view(B, Z, Y, X, 3, H, D)
+    name = "half" if layout == _lib.ROPE_HALF else "interleaved"
+    rq = R.apply_rope(OB.rms_norm(t[..., 0, :, :], eps, None if qw is None else qw.double()), cos, sin, name)
+    rk = R.apply_rope(OB.rms_norm(t[..., 1, :, :], eps, None if kw is None else kw.double()), cos, sin, name)
+    for got, ref in ((q, rq), (k, rk)):
+        d = (got.double().cpu() - ref).abs()
+        assert (d <= ref.abs() * 2**-7 + 1e-3).all(), d.max()
+    assert torch.equal(v.cpu(), qkv.view(B, Z, Y, X, 3, H, D)[..., 2, :, :])
+    # each normalised (unrotated) head has RMS 1: the rotation preserves it
+    if not affine:
+        rms = q.double().cpu().pow(2).mean(-1).sqrt()
+        assert (rms - 1).abs().max() < 1e-2
 
 
 def test_rope_pack_stereographic_tables(gpu):
