@@ -195,6 +195,36 @@ def bench_rollout(device, reps, warmup):
     }
 
 
+def bench_halo(device, reps, warmup):
+    """Cube-sphere halo fill + crop at the rollout tile geometry: 80 channels x
+    6 faces of 512 x 512 fp32, 32-cell halo (create_padded_faces_batched and
+    TileTopology.crop).  Algorithmic bytes = input read once + output written once."""
+    import torch
+
+    L, n, p = 80, 512, 32
+    g = torch.Generator(device=device).manual_seed(0)
+    x = torch.randn(L, 6, n, n, generator=g, device=device)
+    pad = lambda: torch.ops.strata_hip.cube_pad_faces(x, p)  # noqa: E731
+    y = pad()
+    crop = lambda: torch.ops.strata_hip.cube_crop(y, p)  # noqa: E731
+    out = {"workload": f"cube-sphere halo fill: [{L}, 6, {n}, {n}] fp32, halo {p}; crop back"}
+    for name, fn, nbytes in (("pad", pad, (x.numel() + y.numel()) * 4), ("crop", crop, (x.numel() + y.numel()) * 4)):
+        for _ in range(warmup):
+            fn()
+        torch.cuda.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        for _ in range(reps):
+            fn()
+        e1.record()
+        torch.cuda.synchronize()
+        ms = e0.elapsed_time(e1) / reps
+        out[f"{name}_ms"] = round(ms, 4)
+        out[f"{name}_GBps"] = round(nbytes / (ms * 1e-3) / 1e9, 1)
+        out[f"{name}_pct_hbm"] = round(100.0 * nbytes / (ms * 1e-3) / 1e9 / PEAK_HBM_GBPS, 1)
+    return out
+
+
 def cpu_baseline():
     """The CPU oracle on a bounded sample of configs[2]: tile 0, head 0, 4 z-slices."""
     import torch
@@ -245,6 +275,7 @@ def main():
     ap.add_argument("--no-block", action="store_true")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-rollout", action="store_true")
+    ap.add_argument("--no-halo", action="store_true")
     ap.add_argument(
         "--copy-calibration",
         action="store_true",
@@ -327,6 +358,9 @@ def main():
     if not args.no_rollout:
         log("bench: timing the configs[4] rollout")
         result["rollout"] = bench_rollout(dev, 2, 1)
+    if not args.no_halo:
+        log("bench: timing the cube-sphere halo fill")
+        result["halo"] = bench_halo(dev, 10, 2)
     if not args.no_cpu:
         log("bench: timing the CPU oracle sample")
         result["cpu_baseline"] = cpu_baseline()

@@ -189,6 +189,44 @@ typedef struct strata_hip_layer_norm_args {
 
 int strata_hip_layer_norm(const strata_hip_layer_norm_args* args, void* stream);
 
+/* ---------------------------------------------------------------------------
+ * Cube-sphere halo fill: the single-GPU local counterpart of the rollout's
+ * halo exchange, create_padded_faces_batched
+ * (screamcast/cubesphere_transforms.py:369-445; neighbour table :149-196, edge
+ * strips and quarter turns :199-273, corner fill :276-366).
+ * src: [lead, 6, n, n], dst: [lead, 6, n + 2*pad, n + 2*pad], contiguous,
+ * f32 or bf16 (strata_hip_dtype).  pad <= n; dst must not alias src.
+ * ------------------------------------------------------------------------- */
+typedef struct strata_hip_cube_pad_args {
+  const void* src;
+  void* dst;
+  int32_t dtype;
+  int32_t face_size; /* n */
+  int32_t pad;
+  int32_t reserved;
+  int64_t lead;      /* product of the leading dims */
+} strata_hip_cube_pad_args;
+
+int strata_hip_cube_pad_faces(const strata_hip_cube_pad_args* args, void* stream);
+
+/* ---------------------------------------------------------------------------
+ * Crop of padded tiles/faces: TileTopology.crop
+ * (screamcast/distributed_halo.py:143-147).
+ * src: [planes, extent, extent], dst: [planes, extent - 2*halo, extent - 2*halo],
+ * contiguous, f32 or bf16.
+ * ------------------------------------------------------------------------- */
+typedef struct strata_hip_cube_crop_args {
+  const void* src;
+  void* dst;
+  int32_t dtype;
+  int32_t extent; /* side of the padded square */
+  int32_t halo;
+  int32_t reserved;
+  int64_t planes;
+} strata_hip_cube_crop_args;
+
+int strata_hip_cube_crop(const strata_hip_cube_crop_args* args, void* stream);
+
 /* Library bookkeeping (no counterpart in the reference). */
 const char* strata_hip_last_error(void);
 int strata_hip_abi_version(void);

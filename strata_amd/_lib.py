@@ -119,11 +119,37 @@ class LayerNormArgs(ctypes.Structure):
 
 
 # Every function the header declares, with its ctypes signature.
+class CubePadArgs(ctypes.Structure):
+    _fields_ = [
+        ("src", ctypes.c_void_p),
+        ("dst", ctypes.c_void_p),
+        ("dtype", ctypes.c_int32),
+        ("face_size", ctypes.c_int32),
+        ("pad", ctypes.c_int32),
+        ("reserved", ctypes.c_int32),
+        ("lead", ctypes.c_int64),
+    ]
+
+
+class CubeCropArgs(ctypes.Structure):
+    _fields_ = [
+        ("src", ctypes.c_void_p),
+        ("dst", ctypes.c_void_p),
+        ("dtype", ctypes.c_int32),
+        ("extent", ctypes.c_int32),
+        ("halo", ctypes.c_int32),
+        ("reserved", ctypes.c_int32),
+        ("planes", ctypes.c_int64),
+    ]
+
+
 EXPORTS = {
     "strata_hip_na3d_fwd": ([ctypes.POINTER(Na3dArgs), ctypes.c_void_p], ctypes.c_int),
     "strata_hip_rope_qkv_pack": ([ctypes.POINTER(RopePackArgs), ctypes.c_void_p], ctypes.c_int),
     "strata_hip_gemm_bias_act": ([ctypes.POINTER(GemmArgs), ctypes.c_void_p], ctypes.c_int),
     "strata_hip_layer_norm": ([ctypes.POINTER(LayerNormArgs), ctypes.c_void_p], ctypes.c_int),
+    "strata_hip_cube_pad_faces": ([ctypes.POINTER(CubePadArgs), ctypes.c_void_p], ctypes.c_int),
+    "strata_hip_cube_crop": ([ctypes.POINTER(CubeCropArgs), ctypes.c_void_p], ctypes.c_int),
     "strata_hip_last_error": ([], ctypes.c_char_p),
     "strata_hip_abi_version": ([], ctypes.c_int),
 }

@@ -18,7 +18,7 @@ from torch import Tensor
 
 from . import _lib
 
-__all__ = ["na3d_fwd", "rope_qkv_pack", "gemm_bias_act", "layer_norm"]
+__all__ = ["na3d_fwd", "rope_qkv_pack", "gemm_bias_act", "layer_norm", "cube_pad_faces", "cube_crop"]
 
 
 def _stream(t: Tensor) -> int:
@@ -324,3 +324,81 @@ layer_norm.register_autograd(_no_backward("strata_hip::layer_norm"))
 
 def default_scale(head_dim: int) -> float:
     return 1.0 / math.sqrt(head_dim)
+
+
+# ---------------------------------------------------------------------------
+# Cube-sphere halo fill and crop
+# ---------------------------------------------------------------------------
+_CUBE_DTYPES = {torch.float32: _lib.F32, torch.bfloat16: _lib.BF16}
+
+
+@torch.library.custom_op("strata_hip::cube_pad_faces", mutates_args=())
+def cube_pad_faces(data: Tensor, pad: int) -> Tensor:
+    """``[..., 6, n, n]`` -> ``[..., 6, n + 2*pad, n + 2*pad]``: each face framed
+    by its neighbours' edge strips and diagonal-filled corners
+    (create_padded_faces_batched, screamcast/cubesphere_transforms.py:369-445).
+    f32 or bf16."""
+    name = "cube_pad_faces"
+    _require_gpu(name, data)
+    if data.dtype not in _CUBE_DTYPES:
+        raise ValueError(f"{name}: dtype must be float32 or bfloat16")
+    if data.dim() < 3 or data.shape[-3] != 6 or data.shape[-1] != data.shape[-2]:
+        raise ValueError(f"{name}: expected [..., 6, n, n], got {tuple(data.shape)}")
+    n = data.shape[-1]
+    if pad < 0 or pad > n:
+        raise ValueError(f"{name}: pad must be in [0, {n}]")
+    if pad == 0:
+        return data.clone()
+    src = data.contiguous()
+    out = torch.empty((*data.shape[:-2], n + 2 * pad, n + 2 * pad), dtype=data.dtype, device=data.device)
+    a = _lib.CubePadArgs()
+    a.src, a.dst = src.data_ptr(), out.data_ptr()
+    a.dtype, a.face_size, a.pad = _CUBE_DTYPES[data.dtype], n, int(pad)
+    a.lead = src.numel() // (6 * n * n)
+    with torch.cuda.device(data.device):
+        _lib.call("strata_hip_cube_pad_faces", a, _stream(data))
+    return out
+
+
+@cube_pad_faces.register_fake
+def _(data, pad):
+    n = data.shape[-1]
+    return data.new_empty((*data.shape[:-2], n + 2 * pad, n + 2 * pad))
+
+
+cube_pad_faces.register_autograd(_no_backward("strata_hip::cube_pad_faces"))
+
+
+@torch.library.custom_op("strata_hip::cube_crop", mutates_args=())
+def cube_crop(x: Tensor, halo: int) -> Tensor:
+    """``[..., S, S]`` -> ``[..., S - 2*halo, S - 2*halo]`` (TileTopology.crop,
+    screamcast/distributed_halo.py:143-147), as a contiguous tensor."""
+    name = "cube_crop"
+    _require_gpu(name, x)
+    if x.dtype not in _CUBE_DTYPES:
+        raise ValueError(f"{name}: dtype must be float32 or bfloat16")
+    if x.dim() < 2 or x.shape[-1] != x.shape[-2]:
+        raise ValueError(f"{name}: expected [..., S, S], got {tuple(x.shape)}")
+    S = x.shape[-1]
+    if halo < 0 or 2 * halo >= S:
+        raise ValueError(f"{name}: need 0 <= 2*halo < {S}")
+    src = x.contiguous()
+    out = torch.empty((*x.shape[:-2], S - 2 * halo, S - 2 * halo), dtype=x.dtype, device=x.device)
+    if out.numel() == 0:
+        return out
+    a = _lib.CubeCropArgs()
+    a.src, a.dst = src.data_ptr(), out.data_ptr()
+    a.dtype, a.extent, a.halo = _CUBE_DTYPES[x.dtype], S, int(halo)
+    a.planes = src.numel() // (S * S)
+    with torch.cuda.device(x.device):
+        _lib.call("strata_hip_cube_crop", a, _stream(x))
+    return out
+
+
+@cube_crop.register_fake
+def _(x, halo):
+    S = x.shape[-1]
+    return x.new_empty((*x.shape[:-2], S - 2 * halo, S - 2 * halo))
+
+
+cube_crop.register_autograd(_no_backward("strata_hip::cube_crop"))

@@ -19,6 +19,8 @@ STRUCTS = {
     "strata_hip_rope_pack_args": _lib.RopePackArgs,
     "strata_hip_gemm_args": _lib.GemmArgs,
     "strata_hip_layer_norm_args": _lib.LayerNormArgs,
+    "strata_hip_cube_pad_args": _lib.CubePadArgs,
+    "strata_hip_cube_crop_args": _lib.CubeCropArgs,
 }
 
 
@@ -141,3 +143,21 @@ def test_gemm_and_layernorm_validation(lib):
 def test_empty_problem_is_a_no_op(lib):
     a = _na3d_args(batch=0)
     assert lib.strata_hip_na3d_fwd(ctypes.byref(a), None) == _lib.OK
+
+
+def test_cube_validation(lib):
+    a = _lib.CubePadArgs()
+    a.src, a.dst, a.dtype, a.face_size, a.pad, a.lead = 0x1000, 0x2000, _lib.F32, 8, 9, 1
+    assert lib.strata_hip_cube_pad_faces(ctypes.byref(a), None) == _lib.EINVAL
+    assert "pad wider" in lib.strata_hip_last_error().decode()
+    a.pad, a.dst = 2, 0x1000
+    assert lib.strata_hip_cube_pad_faces(ctypes.byref(a), None) == _lib.EINVAL
+    assert "alias" in lib.strata_hip_last_error().decode()
+    a.dtype = 7
+    assert lib.strata_hip_cube_pad_faces(ctypes.byref(a), None) == _lib.EINVAL
+    c = _lib.CubeCropArgs()
+    c.src, c.dst, c.dtype, c.extent, c.halo, c.planes = 0x1000, 0x2000, _lib.BF16, 8, 4, 3
+    assert lib.strata_hip_cube_crop(ctypes.byref(c), None) == _lib.EINVAL
+    assert "2*halo" in lib.strata_hip_last_error().decode()
+    c.planes, c.halo = 0, 1
+    assert lib.strata_hip_cube_crop(ctypes.byref(c), None) == _lib.OK
