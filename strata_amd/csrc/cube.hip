@@ -84,29 +84,94 @@ __device__ __forceinline__ T pad_value(const CubeParams& q, const T* src, int64_
   return sgn == 0 ? mean2<T>(v, h) : (sgn == vsgn ? v : h);
 }
 
-// Grid: x over 16-byte runs of one plane's rows, y/z over the L * 6 planes.
+// Pad, one launch per call; grid x = [interior runs | halo tiles | corner
+// cells] of one plane, grid y/z = the L * 6 planes.
+//  - interior: 16-byte runs of the face copied into the centre;
+//  - halo: 32 x 32 tiles of each side's halo block; the tile's source is a
+//    32 x 32 block of the neighbour face (the side's map is a signed
+//    permutation), read row by row into LDS and written out row by row, so
+//    both the reads and the writes coalesce whatever the quarter turn;
+//  - corners: one cell per thread from the two halo lines beside it.
+constexpr int CT = 32;  // halo tile side
+
+struct PadLayout {
+  int int_blocks;     // interior blocks (256 runs each)
+  int halo_blocks[5]; // prefix sums of the tiles of the 4 sides
+  int corner_blocks;
+};
+
 template <typename T>
-__global__ __launch_bounds__(256) void cube_pad_kernel(CubeParams q) {
+__device__ __forceinline__ void halo_tile(const CubeParams& q, const T* src, T* dst, int64_t l, int f, int side,
+                                          int tile, T (*sm)[CT + 1]) {
+  const int n = q.n, p = q.p, S = q.S;
+  const bool tb = side == SIDE_TOP || side == SIDE_BOTTOM;
+  const int hu = tb ? p : n, hv = tb ? n : p;  // halo block shape
+  const int ntv = (hv + CT - 1) / CT;
+  const int u0 = (tile / ntv) * CT, v0 = (tile % ntv) * CT;
+  const int tu = min(CT, hu - u0), tv = min(CT, hv - v0);
+  const HaloMap& m = q.map[f][side];
+  // source block: the image of [u0, u0 + tu) x [v0, v0 + tv)
+  const int xa = m.c0 + m.a00 * u0 + m.a01 * v0, xb = m.c0 + m.a00 * (u0 + tu - 1) + m.a01 * (v0 + tv - 1);
+  const int ya = m.c1 + m.a10 * u0 + m.a11 * v0, yb = m.c1 + m.a10 * (u0 + tu - 1) + m.a11 * (v0 + tv - 1);
+  const int x0 = min(xa, xb), y0 = min(ya, yb), sx = max(xa, xb) - x0 + 1, sy = max(ya, yb) - y0 + 1;
+  const T* sp = src + (l * 6 + m.nbr) * (int64_t)n * n;
+  const int tx = threadIdx.x & (CT - 1), ty = threadIdx.x / CT;  // 32 x 8 threads
+  for (int r = ty; r < sx; r += 256 / CT) {
+    if (tx < sy) {
+      const int x = x0 + r, y = y0 + tx;
+      const int dx = x - m.c0, dy = y - m.c1;
+      const int u = m.a00 * dx + m.a10 * dy, v = m.a01 * dx + m.a11 * dy;  // A^T: the map is orthogonal
+      sm[u - u0][v - v0] = sp[(int64_t)x * n + y];
+    }
+  }
+  __syncthreads();
+  T* dp = dst + (l * 6 + f) * (int64_t)S * S;
+  const int ro = side == SIDE_TOP ? p + n : side == SIDE_BOTTOM ? 0 : p;
+  const int co = side == SIDE_LEFT ? 0 : side == SIDE_RIGHT ? p + n : p;
+  for (int r = ty; r < tu; r += 256 / CT)
+    if (tx < tv) dp[(int64_t)(ro + u0 + r) * S + co + v0 + tx] = sm[r][tx];
+}
+
+template <typename T>
+__global__ __launch_bounds__(256) void cube_pad_kernel(CubeParams q, PadLayout lay) {
   constexpr int V = 16 / sizeof(T);
+  __shared__ T sm[CT][CT + 1];
   const int64_t plane = blockIdx.y + (int64_t)gridDim.y * blockIdx.z;
-  if (plane >= q.L * 6) return;
+  if (plane >= q.L * 6) return;  // uniform over the block
   const T* src = (const T*)q.src;
-  T* dst = (T*)q.dst + plane * q.S * (int64_t)q.S;
+  T* dst = (T*)q.dst;
   const int64_t l = plane / 6;
   const int f = (int)(plane - l * 6);
-  const int S = q.S, runs = (S + V - 1) / V;
-  const int t = blockIdx.x * blockDim.x + threadIdx.x;
-  if (t >= S * runs) return;
-  const int i = t / runs, j0 = (t - i * runs) * V;
-  T* out = dst + (int64_t)i * S + j0;
-  if (q.vec && j0 + V <= S) {  // whole aligned run: one 16-byte store
-    T vals[V];
-#pragma unroll
-    for (int e = 0; e < V; ++e) vals[e] = pad_value<T>(q, src, l, f, i, j0 + e);
-    *(u32x4*)out = *(const u32x4*)vals;
-  } else {
-    for (int e = 0; e < V && j0 + e < S; ++e) out[e] = pad_value<T>(q, src, l, f, i, j0 + e);
+  const int n = q.n, p = q.p, S = q.S;
+  int b = blockIdx.x;
+  if (b < lay.int_blocks) {
+    const int runs = (n + V - 1) / V;
+    const int t = b * 256 + threadIdx.x;
+    if (t >= n * runs) return;
+    const int i = t / runs, j0 = (t - i * runs) * V;
+    const T* in = src + (plane * n + i) * (int64_t)n + j0;
+    T* out = dst + (plane * S + p + i) * (int64_t)S + p + j0;
+    if (q.vec && j0 + V <= n) {
+      *(u32x4*)out = *(const u32x4*)in;
+    } else {
+      for (int e = 0; e < V && j0 + e < n; ++e) out[e] = in[e];
+    }
+    return;
   }
+  b -= lay.int_blocks;
+  if (b < lay.halo_blocks[4]) {
+    int side = 0;
+    while (b >= lay.halo_blocks[side + 1]) ++side;
+    halo_tile<T>(q, src, dst, l, f, side, b - lay.halo_blocks[side], sm);
+    return;
+  }
+  b -= lay.halo_blocks[4];
+  const int c = b * 256 + threadIdx.x;  // corner cell: 4 corners of p x p
+  if (c >= 4 * p * p) return;
+  const int k = c / (p * p), a = (c / p) % p, bb = c % p;
+  const bool top = k >= 2, right = k & 1;
+  const int i = top ? p + n + a : a, j = right ? p + n + bb : bb;
+  dst[(plane * S + i) * (int64_t)S + j] = pad_value<T>(q, src, l, f, i, j);
 }
 
 template <typename T>
@@ -224,15 +289,27 @@ extern "C" int strata_hip_cube_pad_faces(const strata_hip_cube_pad_args* a, void
   q.n = a->face_size;
   q.p = a->pad;
   q.S = (int)S;
-  q.vec = (S % (a->dtype == STRATA_HIP_F32 ? 4 : 8)) == 0 && ((uintptr_t)a->dst & 15) == 0;
+  {  // interior runs: 16-byte loads and stores when every row of src and of dst's centre is aligned
+    const int V = a->dtype == STRATA_HIP_F32 ? 4 : 8;
+    q.vec = a->face_size % V == 0 && S % V == 0 && a->pad % V == 0 && ((uintptr_t)a->dst & 15) == 0 &&
+            ((uintptr_t)a->src & 15) == 0;
+  }
   build_maps(q);
   hipStream_t st = (hipStream_t)stream;
   const int V = a->dtype == STRATA_HIP_F32 ? 4 : 8;
-  const dim3 grid = plane_grid(a->lead * 6, S * ((S + V - 1) / V));
+  PadLayout lay;
+  const int n = q.n, p = q.p;
+  lay.int_blocks = (int)(((int64_t)n * ((n + V - 1) / V) + 255) / 256);
+  const int tiles_tb = ((p + CT - 1) / CT) * ((n + CT - 1) / CT);  // top / bottom: p x n; left / right: n x p
+  lay.halo_blocks[0] = 0;
+  for (int s = 0; s < 4; ++s) lay.halo_blocks[s + 1] = lay.halo_blocks[s] + tiles_tb;
+  lay.corner_blocks = (4 * p * p + 255) / 256;
+  const int64_t blocks = (int64_t)lay.int_blocks + lay.halo_blocks[4] + lay.corner_blocks;
+  const dim3 grid = plane_grid(a->lead * 6, blocks * 256);
   if (a->dtype == STRATA_HIP_F32)
-    hipLaunchKernelGGL(cube_pad_kernel<float>, grid, dim3(256), 0, st, q);
+    hipLaunchKernelGGL(cube_pad_kernel<float>, grid, dim3(256), 0, st, q, lay);
   else
-    hipLaunchKernelGGL(cube_pad_kernel<bf16>, grid, dim3(256), 0, st, q);
+    hipLaunchKernelGGL(cube_pad_kernel<bf16>, grid, dim3(256), 0, st, q, lay);
   return check_launch("cube_pad_kernel");
 }
 
