@@ -374,19 +374,32 @@ __device__ __forceinline__ void gemm_dma_body(const GemmParams& p) {
     }
     const char* st = lds + rd * STAGE;
     rd = rd + 1 == NST ? 0 : rd + 1;
+    // Operand fragments double-buffered in registers: the LDS reads of K
+    // sub-step kk + 1 are issued before the MFMAs of kk, so their latency
+    // hides behind those MFMAs.
+    bf16x8 af[2][FN], bfr[2][FM];
+    auto load_frags = [&](int kk, int buf) {
+#pragma unroll
+      for (int i = 0; i < FN; ++i) af[buf][i] = *(const bf16x8*)(st + (aoff[i][kk & 1] ^ ((kk >> 1) * 64)));
+#pragma unroll
+      for (int j = 0; j < FM; ++j) bfr[buf][j] = *(const bf16x8*)(st + (boff[j][kk & 1] ^ ((kk >> 1) * 64)));
+    };
+    load_frags(0, 0);
 #pragma unroll
     for (int kk = 0; kk < BK / 16; ++kk) {
-      bf16x8 af[FN], bfr[FM];
-#pragma unroll
-      for (int i = 0; i < FN; ++i) af[i] = *(const bf16x8*)(st + (aoff[i][kk & 1] ^ ((kk >> 1) * 64)));
-#pragma unroll
-      for (int j = 0; j < FM; ++j) bfr[j] = *(const bf16x8*)(st + (boff[j][kk & 1] ^ ((kk >> 1) * 64)));
+      const int cb = kk & 1;
+      if (kk + 1 < BK / 16) load_frags(kk + 1, cb ^ 1);
 #pragma unroll
       for (int i = 0; i < FN; ++i)
 #pragma unroll
         for (int j = 0; j < FM; ++j)
-          acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(af[i], bfr[j], acc[i][j], 0, 0, 0);
+          acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(af[cb][i], bfr[cb][j], acc[i][j], 0, 0, 0);
     }
+    // Let the scheduler interleave the LDS reads of the next sub-step with
+    // the MFMAs of the current one (measured 1-3% faster than the default
+    // order at the block's shapes; explicit sched_group_barrier groups gave
+    // the default order back).
+    __builtin_amdgcn_iglp_opt(1);
   }
 
   // ---- epilogue through LDS ----
