@@ -1,7 +1,7 @@
 // NA3D forward for gfx950.
 //
 // Semantics follow NATTEN's na3d (0.21.5): clamped windows, optional dilation,
-// non-causal, softmax over kz*ky*kx keys scaled by `scale`.  Two kernels:
+// non-causal, softmax over kz*ky*kx keys scaled by `scale`.  Three kernels:
 //
 //  * na3d_scalar_kernel: one thread per (batch, query, head), fp32 math, used
 //    for fp32 inputs and for shapes the MFMA kernel does not cover.
@@ -16,6 +16,9 @@
 //    runs an online softmax with lazy rescaling, and accumulates
 //    O^T += V^T P^T (V^T via ds_read_b64_tr_b16) and the row sums (ones x P^T)
 //    on the same MFMA.
+//  * na3d_strip_kernel:  the same tile math for 4-column tiles (kx 10..13,
+//    head_dim 64), but a workgroup walks a whole column of tiles along y and
+//    streams every key row once, four tiles in flight per wave.
 #include "common.h"
 
 namespace strata {
@@ -568,6 +571,457 @@ __global__ __launch_bounds__(256, 1) void na3d_mfma_wide_kernel(Na3dParams p, Na
   na3d_mfma_body<D, TX, NTY, RPS, NBUF>(p, tg);
 }
 
+// ---------------------------------------------------------------------------
+// Strip kernel: one workgroup walks a whole column of query tiles along y
+// ---------------------------------------------------------------------------
+// Work unit: (batch, head, dilation residue, z, 4*TX query columns) and a
+// chunk of query rows [ys, ye) (the whole y range unless that leaves too few
+// workgroups).  The chunk's tiles of (TY, TX) queries are j = 0, 1, ... along
+// y; tile j needs the key rows U_j = [ws(first row), ws(last row) + ky) of
+// every z-slice of the window.  Key rows stream through the LDS ring once, in
+// groups of RPS rows (all kz slices of a group back to back), and each group
+// feeds every tile whose union it meets.  A wave keeps four tiles in flight in
+// four register slots (tile j in slot j & 3): when a tile's union has passed
+// it is normalised and stored, and the tile four rows further takes its slot.
+// For an unclamped window with ky + TY - 1 = 4 * RPS (configs like 3x13x13
+// with 4x4 tiles) every group feeds exactly four tiles with all its rows,
+// where a fixed box of four tiles per wave is active in only ky+3 of
+// ky+15 rows.
+//
+// Clamped windows at the grid's edges can make tile j + 4 start before tile
+// j has finished, or two tiles start in one group.  The walk is then split
+// into segments: a new segment starts at such a tile and streams from its
+// union's first row again (a few groups are read twice; exact results).
+//
+// Q and the query's own key (which seeds the softmax reference) of the tile
+// that starts in group g + 1 are copied into LDS while group g runs; the
+// tiles that start in a segment's first group are staged through the ring.
+struct Na3dStrips {
+  int nxt, nzt;  // query column boxes and z-slices per (batch, head, residue)
+  int nch, cty;  // y chunks and tiles per chunk
+  int nres;      // dil_z * dil_y * dil_x
+  int total;     // workgroups in the launch
+};
+
+__device__ __forceinline__ void wait_lgkm0() {
+  __builtin_amdgcn_s_waitcnt(15 | (7 << 4) | (3 << 14));  // lgkmcnt(0), vmcnt/expcnt untouched
+}
+
+template <int D, int TX, int RPS, int NBUF>
+__device__ __forceinline__ void na3d_strip_body(const Na3dParams p, const Na3dStrips sg) {
+#if defined(__HIP_DEVICE_COMPILE__)
+  constexpr int NWX = NA3D_NWX;
+  constexpr int NS = 4;                   // tile slots per wave
+  constexpr int TY = 16 / TX;
+  constexpr int WQX = NWX * TX;           // workgroup query columns
+  constexpr int LW = (NWX - 1) * TX + 16; // keys per LDS row that are read
+  constexpr int KPK = 512 / D;            // keys per KiB
+  constexpr int LWP = (LW + KPK - 1) / KPK * KPK;
+  constexpr int RB = LWP * D * 2;         // bytes per (tensor, row) region
+  constexpr int RKB = RB / 1024;
+  constexpr int STAGE_B = 2 * RPS * RB;   // K rows 0..RPS-1, then V rows 0..RPS-1
+  constexpr int LPT = 2 * RPS * RKB / NWX;  // 1-KiB DMA loads per wave per stage
+  constexpr int NRP = RPS / 2;
+  constexpr int CPK = D / 8;              // 16-byte chunks per key
+  constexpr int KS = D / 32;              // k-steps of the QK MFMA; also 1-KiB loads per wave for 16 query rows
+  constexpr int DB = D / 16;
+  constexpr int QWB = 16 * D * 2;         // one wave's 16 rows of Q (or of self keys), bytes
+  constexpr int QTB = NWX * 2 * QWB;      // Q and self keys of one tile row of the workgroup
+  constexpr int RING_B = NBUF * STAGE_B;
+  constexpr float TAU = 64.f;             // lazy-rescale slack, log2 units (as in na3d_mfma_body)
+  static_assert(RKB == NWX && (RPS == 2 || RPS == 4), "stage layout: wave w loads the w-th KiB of every row");
+  static_assert(LPT == 2 * RPS, "a wave loads the same key block of every row of a stage");
+  static_assert(QWB == KS * 1024, "16 query rows are KS 1-KiB loads");
+  static_assert(NS * QTB <= RING_B, "a segment's first tiles are staged through the ring");
+  static_assert(TY <= RPS, "at most one tile starts per group");
+
+  __shared__ __attribute__((aligned(1024))) char lds[RING_B + QTB];
+
+  // ---- work unit ----
+  int t = xcd_tile_order(sg.total);
+  const int xb = t % sg.nxt;
+  t /= sg.nxt;
+  const int zt = t % sg.nzt;
+  t /= sg.nzt;
+  const int ch = t % sg.nch;
+  t /= sg.nch;
+  const int res = t % sg.nres;
+  t /= sg.nres;
+  const int h = t % p.H;
+  const int b = t / p.H;
+  const int dz = p.dil[0], dy = p.dil[1], dx = p.dil[2];
+  const int gx = res % dx;
+  const int gy = (res / dx) % dy;
+  const int gz = res / (dx * dy);
+
+  const int Lz = sub_len(p.L[0], gz, dz);
+  const int Ly = sub_len(p.L[1], gy, dy);
+  const int Lx = sub_len(p.L[2], gx, dx);
+  const int qz0 = sub_first(p.org[0], gz, dz), qz1 = sub_end(p.org[0], p.ext[0], gz, dz);
+  const int qy0 = sub_first(p.org[1], gy, dy), qy1 = sub_end(p.org[1], p.ext[1], gy, dy);
+  const int qx0 = sub_first(p.org[2], gx, dx), qx1 = sub_end(p.org[2], p.ext[2], gx, dx);
+  const int iz = qz0 + zt;
+  const int ys = qy0 + ch * sg.cty * TY;
+  const int ye = min(ys + sg.cty * TY, qy1);
+  const int x0 = qx0 + xb * WQX;
+  if (iz >= qz1 || ys >= ye || x0 >= qx1) return;  // uniform over the workgroup
+  const int NT = (ye - ys + TY - 1) / TY;
+
+  const int kz = p.ker[0], ky = p.ker[1], kx = p.ker[2];
+  const int sz = win_start(iz, Lz, kz);
+  const int X0 = win_start(x0, Lx, kx);
+
+  const int tid = (int)__builtin_amdgcn_workitem_id_x();
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int lane = tid & 63;
+  const int n16 = lane & 15;
+  const int g = lane >> 4;
+  const int trow = n16 / TX;  // this lane's query row within a tile
+  const uint32_t lds_base = (uint32_t)(uintptr_t)(__attribute__((address_space(3))) char*)lds;
+
+  // ---- per-lane x geometry (shared by every tile of the wave) ----
+  const int xw0 = x0 + wave * TX;
+  const int off_w = win_start(min(xw0, qx1 - 1), Lx, kx) - X0;
+  const int qx = xw0 + n16 % TX;
+  uint32_t xmask = 0;  // bit i: key 4g+i of the wave's block is outside this lane's x window
+  {
+    const int sx = win_start(min(qx, qx1 - 1), Lx, kx);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int kxs = X0 + off_w + 4 * g + i;
+      xmask |= (kxs >= sx && kxs < sx + kx) ? 0u : (1u << i);
+    }
+  }
+
+  // Union [u0, u1) of tile j's windows and the rows [f0, f1) inside all of them.
+  auto tile_rows = [&](int j, int& u0, int& u1, int& f0, int& f1) {
+    const int y = ys + TY * j;
+    const int yl = min(y + TY - 1, ye - 1);
+    const int w0 = win_start(y, Ly, ky), w1 = win_start(yl, Ly, ky);
+    u0 = w0;
+    u1 = w1 + ky;
+    f0 = w1;
+    f1 = w0 + ky;
+  };
+
+  const int rz = gz + dz * iz;
+  const float c2 = p.scale * 1.4426950408889634f;  // scores in log2 units
+
+  // ---- K/V ring lane offsets: wave w loads keys [w*KPK, (w+1)*KPK) of every row ----
+  const int64_t rowk = 2 * (int64_t)dy * p.ks[2], rowv = 2 * (int64_t)dy * p.vs[2];
+  uint32_t xoffk, xoffv;
+  {
+    const int key = (wave % RKB) * KPK + lane / CPK;
+    const int c = swz<D>(lane % CPK, key);
+    const bool in = key < LW && X0 + key < Lx;
+    xoffk = in ? (uint32_t)((int64_t)(gx + dx * (X0 + key)) * p.ks[3] * 2 + 16 * c) : OOB;
+    xoffv = in ? (uint32_t)((int64_t)(gx + dx * (X0 + key)) * p.vs[3] * 2 + 16 * c) : OOB;
+  }
+  // ---- Q and self-key copies: one (batch, z, head) slice, 31-bit offsets ----
+  const u32x4 rq = make_rsrc((const char*)p.q + 2 * ((int64_t)b * p.qs[0] + (int64_t)rz * p.qs[1] + (int64_t)h * p.qs[4]),
+                             0x7fffffffu);
+  const u32x4 rks = make_rsrc((const char*)p.k + 2 * ((int64_t)b * p.ks[0] + (int64_t)rz * p.ks[1] + (int64_t)h * p.ks[4]),
+                              0x7fffffffu);
+  const uint32_t qs2 = (uint32_t)(2 * dy * p.qs[2]), ks2 = (uint32_t)(2 * dy * p.ks[2]);
+  uint32_t qxo[KS], kxo[KS];  // x part of the lane's offsets; y part added per tile
+#pragma unroll
+  for (int i = 0; i < KS; ++i) {
+    const int n = lane / CPK + i * (64 / CPK);
+    const int rx = gx + dx * min(xw0 + n % TX, qx1 - 1);
+    qxo[i] = (uint32_t)((int64_t)rx * p.qs[3] * 2 + (int64_t)gy * p.qs[2] * 2) + 16 * (lane % CPK);
+    kxo[i] = (uint32_t)((int64_t)rx * p.ks[3] * 2 + (int64_t)gy * p.ks[2] * 2) + 16 * (lane % CPK);
+  }
+  // Copy Q and the self keys of tile j (this wave's 16 queries) to LDS at `off`:
+  // query n's row at n*2D bytes, self keys QWB further.
+  auto dma_q = [&](int j, uint32_t off) {
+    const int yt0 = ys + TY * j;
+    const uint32_t m0 = lds_base + off + (uint32_t)wave * 2 * QWB;
+#pragma unroll
+    for (int i = 0; i < KS; ++i) {
+      const int n = lane / CPK + i * (64 / CPK);
+      const uint32_t qy = (uint32_t)min(yt0 + n / TX, ye - 1);
+      dma_row16(rq, m0 + i * 1024, qxo[i] + qy * qs2);
+      dma_row16(rks, m0 + QWB + i * 1024, kxo[i] + qy * ks2);
+    }
+  };
+  // ---- output: one (batch, z, head) slice, lane offset of its column and row 0 ----
+  char* obase = (char*)p.o + 2 * ((int64_t)b * p.os[0] + (int64_t)(rz - p.org[0]) * p.os[1] + (int64_t)h * p.os[4]);
+  const int64_t orow = 2 * (int64_t)dy * p.os[2];
+  const int64_t ooff = 2 * ((int64_t)(gx + dx * qx - p.org[2]) * p.os[3] + (int64_t)(gy - p.org[1]) * p.os[2]) + 8 * g;
+
+  // ---- LDS read offsets of the K/V operands (bytes within a stage) ----
+  uint32_t koff[KS];
+#pragma unroll
+  for (int ks = 0; ks < KS; ++ks) {
+    const int key = off_w + n16;
+    koff[ks] = (key * D + 8 * swz<D>(4 * ks + g, key)) * 2;
+  }
+  uint32_t voffs[DB];
+  {
+    const int keyv = off_w + 4 * g + (n16 >> 2);
+    const int dq = n16 & 3;
+#pragma unroll
+    for (int db = 0; db < DB; ++db)
+      voffs[db] = RPS * RB + (keyv * D + 8 * swz<D>(2 * db + (dq >> 1), keyv) + 4 * (dq & 1)) * 2;
+  }
+
+  // ---- tile slots ----
+  bf16x8 qreg[NS][KS];
+  f32x4 oacc[NS][DB];
+  f32x4 lacc[NS];
+  f32x4 nb[NS];  // x bias - reference: the C operand of the QK MFMA
+  int syl[NS];   // first window row of this lane's query row (relative to the segment)
+  // Uniform slot state: tile index (-1: empty) and packed groups
+  // [ylo | yhi << 10 | end << 20]: groups below ylo or from yhi on have rows
+  // outside some query's window; `end` is the tile's last group.
+  int s_tile[NS], s_grp[NS];
+#pragma unroll
+  for (int k = 0; k < NS; ++k) s_tile[k] = -1, s_grp[k] = 0;
+  typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
+  bf16x8_t ones = {(bf16)1.f, (bf16)1.f, (bf16)1.f, (bf16)1.f, (bf16)1.f, (bf16)1.f, (bf16)1.f, (bf16)1.f};
+
+  int S = 0;  // first key row of the current segment
+  // Tile j enters slot k: Q (pre-scaled) and its score against its own key from LDS.
+  auto start_tile = [&](int k, int j, uint32_t off) {
+    const char* qb = lds + off + wave * 2 * QWB;
+    bf16x8 kself[KS];
+#pragma unroll
+    for (int ks = 0; ks < KS; ++ks) {
+      qreg[k][ks] = *(const bf16x8*)(qb + n16 * D * 2 + (4 * ks + g) * 16);
+      kself[ks] = *(const bf16x8*)(qb + QWB + n16 * D * 2 + (4 * ks + g) * 16);
+    }
+    float d = 0.f;
+#pragma unroll
+    for (int ks = 0; ks < KS; ++ks)
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        qreg[k][ks][e] = (bf16)((float)qreg[k][ks][e] * c2);
+        d = fmaf((float)qreg[k][ks][e], (float)kself[ks][e], d);
+      }
+    const float mref = colsum(d);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) nb[k][i] = ((xmask >> i) & 1) ? -INFINITY : -mref;
+#pragma unroll
+    for (int db = 0; db < DB; ++db) oacc[k][db] = (f32x4){0.f, 0.f, 0.f, 0.f};
+    lacc[k] = (f32x4){0.f, 0.f, 0.f, 0.f};
+    int u0, u1, f0, f1;
+    tile_rows(j, u0, u1, f0, f1);
+    s_tile[k] = j;
+    s_grp[k] = (f0 - S + RPS - 1) / RPS | ((f1 - S) / RPS) << 10 | ((u1 - 1 - S) / RPS) << 20;
+    syl[k] = win_start(min(ys + TY * j + trow, ye - 1), Ly, ky) - S;
+  };
+  auto finish_tile = [&](int k) {
+    const int qy = ys + TY * s_tile[k] + trow;
+    s_tile[k] = -1;
+    if (qy >= ye || qx >= qx1) return;
+    const float inv = 1.f / lacc[k][0];
+    char* op = obase + ooff + (int64_t)qy * orow;
+#pragma unroll
+    for (int db = 0; db < DB; ++db) {
+      const u32x2 w = {pack_bf16x2(oacc[k][db][0] * inv, oacc[k][db][1] * inv),
+                       pack_bf16x2(oacc[k][db][2] * inv, oacc[k][db][3] * inv)};
+      *(u32x2*)(op + 32 * db) = w;
+    }
+  };
+
+  const int64_t zstepk = 2 * (int64_t)dz * p.ks[1], zstepv = 2 * (int64_t)dz * p.vs[1];
+  const char* kz0 = (const char*)p.k + 2 * ((int64_t)b * p.ks[0] + (int64_t)h * p.ks[4] + (int64_t)(gz + dz * sz) * p.ks[1] +
+                                           (int64_t)gy * p.ks[2]);
+  const char* vz0 = (const char*)p.v + 2 * ((int64_t)b * p.vs[0] + (int64_t)h * p.vs[4] + (int64_t)(gz + dz * sz) * p.vs[1] +
+                                           (int64_t)gy * p.vs[2]);
+  int js = 0;
+  while (js < NT) {
+    // ---- segment [js, je]: no slot conflict, at most one start per later group ----
+    int u0, u1, f0, f1;
+    tile_rows(js, u0, u1, f0, f1);
+    S = u0;
+    int je = js, prev_a = 0;
+    while (je + 1 < NT) {
+      const int j = je + 1;
+      tile_rows(j, u0, u1, f0, f1);
+      const int aj = (u0 - S) / RPS;
+      if (aj > 0 && aj == prev_a) break;
+      if (j - NS >= js) {
+        int v0, v1, e0, e1;
+        tile_rows(j - NS, v0, v1, e0, e1);
+        if (aj <= (v1 - 1 - S) / RPS) break;
+      }
+      prev_a = aj;
+      je = j;
+    }
+    tile_rows(je, u0, u1, f0, f1);
+    const int NR = u1 - S;  // key rows the segment streams
+    const int nstage = kz * ((NR + RPS - 1) / RPS);
+
+    // ---- tiles that start in the first group: Q staged through the ring ----
+    lds_barrier();  // the previous segment's ring reads are done
+    int jn = js;
+    for (; jn <= je; ++jn) {
+      tile_rows(jn, u0, u1, f0, f1);
+      if (u0 - S >= RPS) break;
+      dma_q(jn, (uint32_t)((jn - js) * QTB));
+    }
+    wait_vmcnt(0);
+#pragma unroll
+    for (int k = 0; k < NS; ++k)
+      for (int j = js; j < jn; ++j)
+        if ((j & (NS - 1)) == k) start_tile(k, j, (uint32_t)((j - js) * QTB));
+    wait_lgkm0();
+    lds_barrier();  // staged Q read before the ring overwrites it
+    int a_next = NR;  // first group of tile jn
+    if (jn <= je) {
+      tile_rows(jn, u0, u1, f0, f1);
+      a_next = (u0 - S) / RPS;
+    }
+
+    // ---- K/V ring over the segment's rows, row-group-major, z-minor ----
+    const char* kseg = kz0 + (int64_t)S * rowk;
+    const char* vseg = vz0 + (int64_t)S * rowv;
+    int cz = 0, cp = 0;
+    uint32_t issue_off = 0;
+    auto issue = [&]() {
+      const int nrow = min(max(NR - RPS * cp, 0), RPS);
+      const u32x4 rk = make_rsrc(kseg + (int64_t)cp * RPS * rowk + (int64_t)cz * zstepk, (uint32_t)(nrow * rowk));
+      const u32x4 rv = make_rsrc(vseg + (int64_t)cp * RPS * rowv + (int64_t)cz * zstepv, (uint32_t)(nrow * rowv));
+      const uint32_t m0 = lds_base + issue_off + (uint32_t)(wave / RKB) * RB + (uint32_t)(wave % RKB) * 1024;
+#pragma unroll
+      for (int r = 0; r < RPS; ++r) dma_row16(rk, m0 + r * RB, xoffk + (uint32_t)(r * rowk));
+#pragma unroll
+      for (int r = 0; r < RPS; ++r) dma_row16(rv, m0 + (RPS + r) * RB, xoffv + (uint32_t)(r * rowv));
+      issue_off = issue_off + STAGE_B == RING_B ? 0 : issue_off + STAGE_B;
+      if (++cz == kz) {
+        cz = 0;
+        ++cp;
+      }
+    };
+#pragma unroll
+    for (int s = 0; s < NBUF - 1; ++s) issue();
+
+    uint32_t cur_off = 0;
+    int gr = 0, zc = 0;  // group and z-slice of the stage being computed
+    for (int s = 0; s < nstage; ++s) {
+      const bool starting = zc == 0 && gr > 0 && gr == a_next;
+      if (starting)
+        wait_vmcnt(0);  // the tile's Q copy as well
+      else
+        wait_vmcnt((NBUF - 2) * LPT);
+      lds_barrier();
+      issue();
+      if (starting) {
+#pragma unroll
+        for (int k = 0; k < NS; ++k)
+          if ((jn & (NS - 1)) == k) start_tile(k, jn, (uint32_t)RING_B);
+        ++jn;
+        a_next = NR;
+        if (jn <= je) {
+          tile_rows(jn, u0, u1, f0, f1);
+          a_next = (u0 - S) / RPS;
+        }
+      }
+      // Q of the tile starting in the next group (each wave reads and refills
+      // only its own part of the buffer; the start above has consumed it).
+      if (zc == 1 && a_next == gr + 1) dma_q(jn, (uint32_t)RING_B);
+
+      asm volatile("" : "+v"(ones));
+      const char* st = lds + cur_off;
+      bf16x8 ak[RPS][KS];
+#pragma unroll
+      for (int r = 0; r < RPS; ++r)
+#pragma unroll
+        for (int ks = 0; ks < KS; ++ks) ak[r][ks] = *(const bf16x8*)(st + r * RB + koff[ks]);
+      bf16x8 av[NRP][DB];
+#pragma unroll
+      for (int rp = 0; rp < NRP; ++rp)
+#pragma unroll
+        for (int db = 0; db < DB; ++db) {
+          const bf16x4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4bf16(LDS_PTR(bf16x4, st + voffs[db] + 2 * rp * RB));
+          const bf16x4 hi =
+              __builtin_amdgcn_ds_read_tr16_b64_v4bf16(LDS_PTR(bf16x4, st + voffs[db] + (2 * rp + 1) * RB));
+          av[rp][db] = __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7);
+        }
+      const int r0 = RPS * gr;
+
+#pragma unroll
+      for (int k = 0; k < NS; ++k) {
+        if (s_tile[k] < 0) continue;
+        f32x4 sacc[RPS];
+#pragma unroll
+        for (int r = 0; r < RPS; ++r) {
+          sacc[r] = nb[k];
+#pragma unroll
+          for (int ks = 0; ks < KS; ++ks)
+            sacc[r] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ak[r][ks], qreg[k][ks], sacc[r], 0, 0, 0);
+        }
+        float u[4 * RPS];
+#pragma unroll
+        for (int r = 0; r < RPS; ++r)
+#pragma unroll
+          for (int i = 0; i < 4; ++i) u[4 * r + i] = sacc[r][i];
+        if (gr < (s_grp[k] & 1023) || gr >= ((s_grp[k] >> 10) & 1023)) {
+          // rows outside some query's y window (else only the x mask applies)
+#pragma unroll
+          for (int r = 0; r < RPS; ++r) {
+            const int yr = r0 + r;
+            const bool yok = yr >= syl[k] && yr < syl[k] + ky;
+#pragma unroll
+            for (int i = 0; i < 4; ++i) u[4 * r + i] = yok ? u[4 * r + i] : -INFINITY;
+          }
+        }
+        float ml = -INFINITY;
+#pragma unroll
+        for (int j = 0; j < 4 * RPS; j += 8)
+          ml = fmaxf(ml, fmaxf(fmaxf(fmaxf(u[j], u[j + 1]), u[j + 2]),
+                               fmaxf(fmaxf(fmaxf(u[j + 3], u[j + 4]), u[j + 5]), fmaxf(u[j + 6], u[j + 7]))));
+        if (__builtin_amdgcn_ballot_w64(ml > TAU) != 0) {
+          const float mx = colmax(ml);
+          const float d = mx > TAU ? mx : 0.f;
+          const float alpha = __builtin_amdgcn_exp2f(-d);
+#pragma unroll
+          for (int db = 0; db < DB; ++db) oacc[k][db] *= alpha;
+          lacc[k] *= alpha;
+#pragma unroll
+          for (int i = 0; i < 4; ++i) nb[k][i] -= d;
+#pragma unroll
+          for (int j = 0; j < 4 * RPS; ++j) u[j] -= d;
+        }
+        bf16x8 pb[NRP];
+#pragma unroll
+        for (int rp = 0; rp < NRP; ++rp) {
+          float pv[8];
+#pragma unroll
+          for (int j = 0; j < 8; ++j) pv[j] = __builtin_amdgcn_exp2f(u[8 * rp + j]);
+          const u32x4 pw = {pack_bf16x2(pv[0], pv[1]), pack_bf16x2(pv[2], pv[3]), pack_bf16x2(pv[4], pv[5]),
+                            pack_bf16x2(pv[6], pv[7])};
+          pb[rp] = __builtin_bit_cast(bf16x8, pw);
+        }
+#pragma unroll
+        for (int rp = 0; rp < NRP; ++rp) {
+          lacc[k] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ones, pb[rp], lacc[k], 0, 0, 0);
+#pragma unroll
+          for (int db = 0; db < DB; ++db)
+            oacc[k][db] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(av[rp][db], pb[rp], oacc[k][db], 0, 0, 0);
+        }
+      }
+      cur_off = cur_off + STAGE_B == RING_B ? 0 : cur_off + STAGE_B;
+      if (++zc == kz) {
+        zc = 0;
+#pragma unroll
+        for (int k = 0; k < NS; ++k)
+          if (s_tile[k] >= 0 && (s_grp[k] >> 20) == gr) finish_tile(k);
+        ++gr;
+      }
+    }
+    wait_vmcnt(0);  // the ring's trailing (empty) stages
+    js = je + 1;
+  }
+#endif
+}
+
+template <int D, int TX, int RPS, int NBUF>
+__global__ __launch_bounds__(256, 2) void na3d_strip_kernel(Na3dParams p, Na3dStrips sg) {
+  na3d_strip_body<D, TX, RPS, NBUF>(p, sg);
+}
+
 
 // ---------------------------------------------------------------------------
 // Host side
@@ -645,6 +1099,51 @@ static int launch_mfma_tx(const Na3dParams& p, hipStream_t st) {
   return launch_mfma_cfg<D, TX, NTY, RPS, ring_depth(stage_bytes<D, TX, RPS>())>(p, st);
 }
 
+
+// Strip kernel launch.  Work units are (batch, head, residue, z, column box)
+// strips over the whole y range; the y range is cut into chunks only when the
+// strips alone would not fill the GPU several times over.
+template <int D, int TX, int RPS, int NBUF>
+static int launch_strip(const Na3dParams& p, hipStream_t st) {
+  constexpr int TY = 16 / TX;
+  Na3dStrips sg;
+  int nq[3] = {0, 0, 0};
+  for (int a = 0; a < 3; ++a)
+    for (int g = 0; g < p.dil[a]; ++g) {
+      const int n = sub_end(p.org[a], p.ext[a], g, p.dil[a]) - sub_first(p.org[a], g, p.dil[a]);
+      nq[a] = n > nq[a] ? n : nq[a];
+    }
+  sg.nzt = nq[0];
+  sg.nxt = (nq[2] + NA3D_NWX * TX - 1) / (NA3D_NWX * TX);
+  sg.nres = p.dil[0] * p.dil[1] * p.dil[2];
+  const int nty = (nq[1] + TY - 1) / TY;
+  const int64_t strips = (int64_t)sg.nxt * sg.nzt * sg.nres * p.H * p.B;
+  if (strips == 0 || nty == 0) return STRATA_HIP_OK;
+  int nch = 1;
+  while (strips * nch < 2048 && nch < nty) ++nch;
+  sg.cty = (nty + nch - 1) / nch;
+  sg.nch = (nty + sg.cty - 1) / sg.cty;
+  const int64_t total = strips * sg.nch;
+  if (total > 0x7fffffff) return fail(STRATA_HIP_EUNSUPPORTED, "na3d: problem too large for one launch");
+  sg.total = (int)total;
+  hipLaunchKernelGGL((na3d_strip_kernel<D, TX, RPS, NBUF>), dim3((unsigned)total), dim3(64 * NA3D_NWX), 0, st, p, sg);
+  return check_launch("na3d_strip_kernel");
+}
+
+// The strip kernel covers 4-column tiles (kx 10..13, ky <= 13) of head_dim 64
+// with a window at least two slices deep (the next tile's Q is copied while the
+// second slice of a group runs); its Q and self-key descriptors address one
+// (batch, z, head) slice with 31-bit byte offsets.
+static bool strip_fits(const Na3dParams& p) {
+  if (p.D != 64 || p.ker[0] < 2 || p.ker[2] < 10 || p.ker[2] > 13) return false;
+  // Taller windows keep more than four tiles alive per row group (the walk
+  // would split into many short segments); row groups are packed in 10 bits.
+  if (p.ker[1] > 13 || p.L[1] >= 4096) return false;
+  const int64_t* sd[2] = {p.qs, p.ks};
+  for (int t = 0; t < 2; ++t)
+    if (((int64_t)(p.L[1] - 1) * sd[t][2] + (int64_t)(p.L[2] - 1) * sd[t][3] + p.D) * 2 >= 0x7fffffffLL) return false;
+  return true;
+}
 
 template <int D>
 static int launch_mfma_d(const Na3dParams& p, hipStream_t st) {
@@ -739,6 +1238,7 @@ extern "C" int strata_hip_na3d_fwd(const strata_hip_na3d_args* a, void* stream) 
     case 32:
       return launch_mfma_d<32>(p, st);
     case 64:
+      if (strip_fits(p)) return launch_strip<64, 4, 4, 2>(p, st);
       return launch_mfma_d<64>(p, st);
     default:
       return launch_mfma_d<128>(p, st);

@@ -76,6 +76,15 @@ MFMA_CASES = [
     ((1, 4, 20, 20, 2, 64), (3, 7, 7), (1, 1, 1), (1, 3, 2), (2, 14, 15)),
     ((2, 4, 24, 24, 2, 64), (3, 13, 13), (1, 1, 1), (0, 4, 4), (4, 16, 16)),
     ((1, 3, 7, 9, 2, 64), (3, 7, 9), (1, 1, 1), None, None),  # window spans the y/x grid
+    # strip walk (4-column tiles): clamped edges that split the walk into segments,
+    # a window as tall as the grid, dilation, ragged y/x, deeper z windows, y chunks
+    ((1, 3, 40, 20, 2, 64), (3, 11, 11), (1, 1, 1), None, None),
+    ((1, 3, 13, 26, 1, 64), (3, 13, 13), (1, 1, 1), None, None),
+    ((1, 4, 30, 27, 2, 64), (3, 11, 13), (1, 2, 2), None, None),
+    ((2, 3, 37, 35, 1, 64), (3, 5, 11), (1, 1, 1), None, None),
+    ((1, 6, 21, 18, 1, 64), (5, 13, 11), (1, 1, 1), (1, 2, 1), (4, 17, 15)),
+    ((1, 3, 64, 16, 1, 64), (3, 1, 13), (1, 1, 1), None, None),
+    ((1, 3, 150, 16, 1, 64), (3, 9, 13), (1, 1, 1), None, None),
 ]
 
 
