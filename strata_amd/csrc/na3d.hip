@@ -19,6 +19,8 @@
 //  * na3d_strip_kernel:  the same tile math for 4-column tiles (kx 10..13,
 //    head_dim 64), but a workgroup walks a whole column of tiles along y and
 //    streams every key row once, four tiles in flight per wave.
+#include <type_traits>
+
 #include "common.h"
 
 namespace strata {
@@ -607,6 +609,78 @@ __device__ __forceinline__ void wait_lgkm0() {
   __builtin_amdgcn_s_waitcnt(15 | (7 << 4) | (3 << 14));  // lgkmcnt(0), vmcnt/expcnt untouched
 }
 
+// Where one strip tile's queries sit: batch, head, residue (gz, gy, gx), the
+// tile's sub-grid z, first query row and first column, and the chunk's ends.
+struct StripTile {
+  int b, h, gz, gy, gx, iz, qy0, ye, qx0, qx1;
+};
+
+// Rare path of the strip kernel: recompute one 4x4 tile of queries exactly,
+// straight from global memory, with a running maximum (fp32 online softmax).
+// Called by a whole wave when the tile's unnormalised sums left the range
+// the fast path guarantees (a score far above the query's own-key score, or
+// non-finite inputs).  Lane l handles query l >> 2 (row-major in the tile)
+// and the head-dim quarter l & 3 (16 values); invalid queries (past the
+// chunk's last row or column) compute a clamped copy and store nothing.
+__device__ __forceinline__ void na3d_strip_tile_exact(const Na3dParams* pp, StripTile t) {
+#if defined(__HIP_DEVICE_COMPILE__)
+  const Na3dParams& p = *pp;
+  const int lane = (int)__builtin_amdgcn_workitem_id_x() & 63;
+  const int n = lane >> 2, dq = lane & 3;
+  const int dz = p.dil[0], dy = p.dil[1], dx = p.dil[2];
+  const int Lz = sub_len(p.L[0], t.gz, dz), Ly = sub_len(p.L[1], t.gy, dy), Lx = sub_len(p.L[2], t.gx, dx);
+  const bool valid = t.qy0 + n / 4 < t.ye && t.qx0 + n % 4 < t.qx1;
+  const int qy = min(t.qy0 + n / 4, t.ye - 1), qx = min(t.qx0 + n % 4, t.qx1 - 1);
+  const int sz = win_start(t.iz, Lz, p.ker[0]), sy = win_start(qy, Ly, p.ker[1]), sx = win_start(qx, Lx, p.ker[2]);
+  const int rz = t.gz + dz * t.iz, ry = t.gy + dy * qy, rx = t.gx + dx * qx;
+  const bf16* qp = (const bf16*)p.q + (int64_t)t.b * p.qs[0] + (int64_t)rz * p.qs[1] + (int64_t)ry * p.qs[2] +
+                   (int64_t)rx * p.qs[3] + (int64_t)t.h * p.qs[4] + 16 * dq;
+  const float c2 = p.scale * 1.4426950408889634f;
+  float qf[16], acc[16];
+#pragma unroll
+  for (int i = 0; i < 16; ++i) {
+    qf[i] = (float)qp[i] * c2;
+    acc[i] = 0.f;
+  }
+  float m = -INFINITY, l = 0.f;
+  const bf16* kb = (const bf16*)p.k + (int64_t)t.b * p.ks[0] + (int64_t)t.h * p.ks[4] + 16 * dq;
+  const bf16* vb = (const bf16*)p.v + (int64_t)t.b * p.vs[0] + (int64_t)t.h * p.vs[4] + 16 * dq;
+  for (int a = 0; a < p.ker[0]; ++a) {
+    const int kzr = t.gz + dz * (sz + a);
+    for (int c = 0; c < p.ker[1]; ++c) {
+      const int kyr = t.gy + dy * (sy + c);
+      for (int e = 0; e < p.ker[2]; ++e) {
+        const int kxr = t.gx + dx * (sx + e);
+        const bf16* kp = kb + (int64_t)kzr * p.ks[1] + (int64_t)kyr * p.ks[2] + (int64_t)kxr * p.ks[3];
+        const bf16* vp = vb + (int64_t)kzr * p.vs[1] + (int64_t)kyr * p.vs[2] + (int64_t)kxr * p.vs[3];
+        float s = 0.f;
+#pragma unroll
+        for (int i = 0; i < 16; ++i) s = fmaf(qf[i], (float)kp[i], s);
+        s += __shfl_xor(s, 1);
+        s += __shfl_xor(s, 2);
+        const float mn = fmaxf(m, s);
+        const float alpha = exp2f(m - mn), w = exp2f(s - mn);
+        l = l * alpha + w;
+#pragma unroll
+        for (int i = 0; i < 16; ++i) acc[i] = fmaf(acc[i], alpha, w * (float)vp[i]);
+        m = mn;
+      }
+    }
+  }
+  if (!valid) return;
+  const float inv = 1.f / l;
+  char* op = (char*)p.o + 2 * ((int64_t)t.b * p.os[0] + (int64_t)(rz - p.org[0]) * p.os[1] +
+                               (int64_t)(ry - p.org[1]) * p.os[2] + (int64_t)(rx - p.org[2]) * p.os[3] +
+                               (int64_t)t.h * p.os[4] + 16 * dq);
+#pragma unroll
+  for (int i = 0; i < 16; i += 8) {
+    const u32x4 w = {pack_bf16x2(acc[i] * inv, acc[i + 1] * inv), pack_bf16x2(acc[i + 2] * inv, acc[i + 3] * inv),
+                     pack_bf16x2(acc[i + 4] * inv, acc[i + 5] * inv), pack_bf16x2(acc[i + 6] * inv, acc[i + 7] * inv)};
+    *(u32x4*)(op + 2 * i) = w;
+  }
+#endif
+}
+
 template <int D, int TX, int RPS, int NBUF>
 __device__ __forceinline__ void na3d_strip_body(const Na3dParams p, const Na3dStrips sg) {
 #if defined(__HIP_DEVICE_COMPILE__)
@@ -1024,6 +1098,388 @@ __global__ __launch_bounds__(256, 2) void na3d_strip_kernel(Na3dParams p, Na3dSt
 
 
 // ---------------------------------------------------------------------------
+// Strip kernel, fixed-reference instance for regular strips
+// ---------------------------------------------------------------------------
+// Regular strip: ky = 13, 4x4 tiles, four key rows per group, and no query row
+// of the chunk with a clamped y window (the host checks; configs like
+// 3x13x13 on a halo-padded tile).  Then tile j's y-union is rows
+// [4j, 4j + 16) of the strip: it starts in group j and ends in group j + 3,
+// in slot j & 3, so in group gr the tile in its first group sits in slot
+// gr & 3 and the one in its last group in slot (gr + 1) & 3.  The group loop
+// is unrolled four times, which makes both slots compile-time constants: the
+// y masks (query row t sees rows r >= t of its first group and r <= t of its
+// last; every row of the two middle groups) are a few v_cndmask on the packed
+// probabilities, and no stage has a per-tile branch.  Ramp-up and ramp-down
+// groups compute every slot; the slots without a live tile are discarded.
+//
+// The softmax reference is fixed per tile: m = (own-key score) + SLACK, in
+// log2 units, so the stage loop has no running maximum and no rescaling.  A
+// score s has p = 2^(s - m), the own key p = 2^-SLACK; keys more than
+// 126 - SLACK below the own key underflow (relative weight below 2^-30 each).
+// The sums stay finite while no score exceeds the own-key score by more than
+// about SLACK + 40 - log2|W|; the row sum is checked when the tile finishes
+// (above 2^40, infinite or NaN) and such tiles are recomputed exactly after
+// the strip by na3d_strip_tile_exact.  2^40 also keeps sum(p * v) finite for
+// |v| < 2^88.  (gfx950's v_dot2c_f32_bf16 does not keep an fp32 sum: the row
+// sums stay on the ones-operand MFMA.)
+template <int D, int TX, int RPS, int NBUF>
+__device__ __forceinline__ void na3d_strip_fast_body(const Na3dParams p, const Na3dStrips sg) {
+#if defined(__HIP_DEVICE_COMPILE__)
+  constexpr int NWX = NA3D_NWX;
+  constexpr int NS = 4;                   // tile slots per wave
+  constexpr int TY = 16 / TX;
+  constexpr int WQX = NWX * TX;           // workgroup query columns
+  constexpr int LW = (NWX - 1) * TX + 16; // keys per LDS row that are read
+  constexpr int KPK = 512 / D;            // keys per KiB
+  constexpr int LWP = (LW + KPK - 1) / KPK * KPK;
+  constexpr int RB = LWP * D * 2;         // bytes per (tensor, row) region
+  constexpr int RKB = RB / 1024;
+  constexpr int STAGE_B = 2 * RPS * RB;   // K rows 0..RPS-1, then V rows 0..RPS-1
+  constexpr int LPT = 2 * RPS * RKB / NWX;  // 1-KiB DMA loads per wave per stage
+  constexpr int NRP = RPS / 2;
+  constexpr int CPK = D / 8;              // 16-byte chunks per key
+  constexpr int KS = D / 32;              // k-steps of the QK MFMA; also 1-KiB loads per wave for 16 query rows
+  constexpr int DB = D / 16;
+  constexpr int QWB = 16 * D * 2;         // one wave's 16 rows of Q (or of self keys), bytes
+  constexpr int QTB = NWX * 2 * QWB;      // Q and self keys of one tile row of the workgroup
+  constexpr int RING_B = NBUF * STAGE_B;
+  constexpr int KY = 13, KR = KY / 2;     // window rows and radius in y
+  constexpr float SLACK = 96.f;
+  constexpr uint32_t LMAX_BITS = (127u + 40u) << 23;  // 2^40 as an fp32 bit pattern
+  static_assert(TX == 4 && TY == 4 && RPS == 4 && TY + KY - 1 == NS * RPS, "regular strip geometry");
+  static_assert(RKB == NWX && LPT == 2 * RPS, "stage layout: wave w loads the w-th KiB of every row");
+  static_assert(QWB == KS * 1024, "16 query rows are KS 1-KiB loads");
+  static_assert(QTB <= RING_B, "tile 0's Q is staged through the ring");
+
+  __shared__ __attribute__((aligned(1024))) char lds[RING_B + QTB];
+
+  // ---- work unit (as na3d_strip_body) ----
+  int t = xcd_tile_order(sg.total);
+  const int xb = t % sg.nxt;
+  t /= sg.nxt;
+  const int zt = t % sg.nzt;
+  t /= sg.nzt;
+  const int ch = t % sg.nch;
+  t /= sg.nch;
+  const int res = t % sg.nres;
+  t /= sg.nres;
+  const int h = t % p.H;
+  const int b = t / p.H;
+  const int dz = p.dil[0], dy = p.dil[1], dx = p.dil[2];
+  const int gx = res % dx;
+  const int gy = (res / dx) % dy;
+  const int gz = res / (dx * dy);
+
+  const int Lz = sub_len(p.L[0], gz, dz);
+  const int Lx = sub_len(p.L[2], gx, dx);
+  const int qz0 = sub_first(p.org[0], gz, dz), qz1 = sub_end(p.org[0], p.ext[0], gz, dz);
+  const int qy0 = sub_first(p.org[1], gy, dy), qy1 = sub_end(p.org[1], p.ext[1], gy, dy);
+  const int qx0 = sub_first(p.org[2], gx, dx), qx1 = sub_end(p.org[2], p.ext[2], gx, dx);
+  const int iz = qz0 + zt;
+  const int ys = qy0 + ch * sg.cty * TY;
+  const int ye = min(ys + sg.cty * TY, qy1);
+  const int x0 = qx0 + xb * WQX;
+  if (iz >= qz1 || ys >= ye || x0 >= qx1) return;  // uniform over the workgroup
+  const int NT = (ye - ys + TY - 1) / TY;
+  const int S = ys - KR;                 // first key row of tile 0's union (unclamped)
+  const int NR = ye - ys + 2 * KR;       // key rows the strip streams
+  const int NG = (NR + RPS - 1) / RPS;   // row groups (NT + 3)
+
+  const int kz = p.ker[0], kx = p.ker[2];
+  const int sz = win_start(iz, Lz, kz);
+  const int X0 = win_start(x0, Lx, kx);
+
+  const int tid = (int)__builtin_amdgcn_workitem_id_x();
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int lane = tid & 63;
+  const int n16 = lane & 15;
+  const int g = lane >> 4;
+  const int trow = n16 / TX;  // this lane's query row within a tile
+  const uint32_t lds_base = (uint32_t)(uintptr_t)(__attribute__((address_space(3))) char*)lds;
+
+  // ---- per-lane x geometry (shared by every tile of the wave) ----
+  const int xw0 = x0 + wave * TX;
+  const int off_w = win_start(min(xw0, qx1 - 1), Lx, kx) - X0;
+  const int qx = xw0 + n16 % TX;
+  uint32_t xmask = 0;  // bit i: key 4g+i of the wave's block is outside this lane's x window
+  {
+    const int sx = win_start(min(qx, qx1 - 1), Lx, kx);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int kxs = X0 + off_w + 4 * g + i;
+      xmask |= (kxs >= sx && kxs < sx + kx) ? 0u : (1u << i);
+    }
+  }
+
+  const int rz = gz + dz * iz;
+  const float c2 = p.scale * 1.4426950408889634f;  // scores in log2 units
+
+  // ---- K/V ring lane offsets: wave w loads keys [w*KPK, (w+1)*KPK) of every row ----
+  const int64_t rowk = 2 * (int64_t)dy * p.ks[2], rowv = 2 * (int64_t)dy * p.vs[2];
+  uint32_t xoffk, xoffv;
+  {
+    const int key = (wave % RKB) * KPK + lane / CPK;
+    const int c = swz<D>(lane % CPK, key);
+    const bool in = key < LW && X0 + key < Lx;
+    xoffk = in ? (uint32_t)((int64_t)(gx + dx * (X0 + key)) * p.ks[3] * 2 + 16 * c) : OOB;
+    xoffv = in ? (uint32_t)((int64_t)(gx + dx * (X0 + key)) * p.vs[3] * 2 + 16 * c) : OOB;
+  }
+  // ---- Q and self-key copies: one (batch, z, head) slice, 31-bit offsets ----
+  const u32x4 rq = make_rsrc((const char*)p.q + 2 * ((int64_t)b * p.qs[0] + (int64_t)rz * p.qs[1] + (int64_t)h * p.qs[4]),
+                             0x7fffffffu);
+  const u32x4 rks = make_rsrc((const char*)p.k + 2 * ((int64_t)b * p.ks[0] + (int64_t)rz * p.ks[1] + (int64_t)h * p.ks[4]),
+                              0x7fffffffu);
+  const uint32_t qs2 = (uint32_t)(2 * dy * p.qs[2]), ks2 = (uint32_t)(2 * dy * p.ks[2]);
+  uint32_t qxo[KS], kxo[KS];
+#pragma unroll
+  for (int i = 0; i < KS; ++i) {
+    const int n = lane / CPK + i * (64 / CPK);
+    const int rx = gx + dx * min(xw0 + n % TX, qx1 - 1);
+    qxo[i] = (uint32_t)((int64_t)rx * p.qs[3] * 2 + (int64_t)gy * p.qs[2] * 2) + 16 * (lane % CPK);
+    kxo[i] = (uint32_t)((int64_t)rx * p.ks[3] * 2 + (int64_t)gy * p.ks[2] * 2) + 16 * (lane % CPK);
+  }
+  // Copy Q and the self keys of tile j (this wave's 16 queries) to LDS at `off`.
+  auto dma_q = [&](int j, uint32_t off) {
+    const int yt0 = ys + TY * j;
+    const uint32_t m0 = lds_base + off + (uint32_t)wave * 2 * QWB;
+#pragma unroll
+    for (int i = 0; i < KS; ++i) {
+      const int n = lane / CPK + i * (64 / CPK);
+      const uint32_t qy = (uint32_t)min(yt0 + n / TX, ye - 1);
+      dma_row16(rq, m0 + i * 1024, qxo[i] + qy * qs2);
+      dma_row16(rks, m0 + QWB + i * 1024, kxo[i] + qy * ks2);
+    }
+  };
+  // ---- output: one (batch, z, head) slice ----
+  char* obase = (char*)p.o + 2 * ((int64_t)b * p.os[0] + (int64_t)(rz - p.org[0]) * p.os[1] + (int64_t)h * p.os[4]);
+  const int64_t orow = 2 * (int64_t)dy * p.os[2];
+  const int64_t ooff = 2 * ((int64_t)(gx + dx * qx - p.org[2]) * p.os[3] + (int64_t)(gy - p.org[1]) * p.os[2]) + 8 * g;
+
+  // ---- LDS read offsets of the K/V operands (bytes within a stage) ----
+  uint32_t koff[KS];
+#pragma unroll
+  for (int ks = 0; ks < KS; ++ks) {
+    const int key = off_w + n16;
+    koff[ks] = (key * D + 8 * swz<D>(4 * ks + g, key)) * 2;
+  }
+  uint32_t voffs[DB];
+  {
+    const int keyv = off_w + 4 * g + (n16 >> 2);
+    const int dq = n16 & 3;
+#pragma unroll
+    for (int db = 0; db < DB; ++db)
+      voffs[db] = RPS * RB + (keyv * D + 8 * swz<D>(2 * db + (dq >> 1), keyv) + 4 * (dq & 1)) * 2;
+  }
+
+  // ---- tile slots ----
+  bf16x8 qreg[NS][KS];
+  f32x4 oacc[NS][DB];
+  f32x4 lacc[NS];  // row sums (ones x P^T: every row of a column holds the column's sum)
+  f32x4 nb[NS];    // x bias - reference: the C operand of the QK MFMA
+  typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
+  bf16x8_t ones = {(bf16)1.f, (bf16)1.f, (bf16)1.f, (bf16)1.f, (bf16)1.f, (bf16)1.f, (bf16)1.f, (bf16)1.f};
+  const bool ylo[3] = {trow > 0, trow > 1, trow > 2};  // first group: rows 0..2 masked for later query rows
+  const bool yhi[3] = {trow < 1, trow < 2, trow < 3};  // last group: rows 1..3 masked for earlier query rows
+
+  // Tile j enters slot k: Q (pre-scaled) and its score against its own key from LDS.
+  auto start_tile = [&](int k, uint32_t off) {
+    const char* qb = lds + off + wave * 2 * QWB;
+    bf16x8 kself[KS];
+#pragma unroll
+    for (int ks = 0; ks < KS; ++ks) {
+      qreg[k][ks] = *(const bf16x8*)(qb + n16 * D * 2 + (4 * ks + g) * 16);
+      kself[ks] = *(const bf16x8*)(qb + QWB + n16 * D * 2 + (4 * ks + g) * 16);
+    }
+    float d = 0.f;
+#pragma unroll
+    for (int ks = 0; ks < KS; ++ks)
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        qreg[k][ks][e] = (bf16)((float)qreg[k][ks][e] * c2);
+        d = fmaf((float)qreg[k][ks][e], (float)kself[ks][e], d);
+      }
+    const float mref = colsum(d) + SLACK;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) nb[k][i] = ((xmask >> i) & 1) ? -INFINITY : -mref;
+#pragma unroll
+    for (int db = 0; db < DB; ++db) oacc[k][db] = (f32x4){0.f, 0.f, 0.f, 0.f};
+    lacc[k] = (f32x4){0.f, 0.f, 0.f, 0.f};
+  };
+  // Normalise and store tile j from slot k; true if the tile needs the exact path.
+  auto finish_tile = [&](int k, int j) {
+    const float l = lacc[k][0];
+    const int qy = ys + TY * j + trow;
+    const bool valid = qy < ye && qx < qx1;
+    if (valid) {
+      const float inv = 1.f / l;
+      char* op = obase + ooff + (int64_t)qy * orow;
+#pragma unroll
+      for (int db = 0; db < DB; ++db) {
+        const u32x2 w = {pack_bf16x2(oacc[k][db][0] * inv, oacc[k][db][1] * inv),
+                         pack_bf16x2(oacc[k][db][2] * inv, oacc[k][db][3] * inv)};
+        *(u32x2*)(op + 32 * db) = w;
+      }
+    }
+    // row sum above 2^40, infinite or NaN (never negative: compare the bits)
+    return __builtin_amdgcn_ballot_w64(valid && __float_as_uint(l) > LMAX_BITS) != 0;
+  };
+
+  // One stage's tile math for every slot.  C: slot of the tile in its first group.
+  auto stage_math = [&](auto cst, const bf16x8 (&ak)[RPS][KS], const bf16x8 (&av)[NRP][DB]) {
+    constexpr int C = decltype(cst)::value;
+#pragma unroll
+    for (int tt = 0; tt < NS; ++tt) {
+      const int k = (C + tt) & (NS - 1);  // tt = 0: the tile's first group, tt = 1: its last
+      f32x4 sacc[RPS];
+#pragma unroll
+      for (int r = 0; r < RPS; ++r) {
+        sacc[r] = nb[k];
+#pragma unroll
+        for (int ks = 0; ks < KS; ++ks)
+          sacc[r] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ak[r][ks], qreg[k][ks], sacc[r], 0, 0, 0);
+      }
+      bf16x8 pb[NRP];
+#pragma unroll
+      for (int rp = 0; rp < NRP; ++rp) {
+        float pv[8];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          pv[i] = __builtin_amdgcn_exp2f(sacc[2 * rp][i]);
+          pv[4 + i] = __builtin_amdgcn_exp2f(sacc[2 * rp + 1][i]);
+        }
+        u32x4 pw = {pack_bf16x2(pv[0], pv[1]), pack_bf16x2(pv[2], pv[3]), pack_bf16x2(pv[4], pv[5]),
+                    pack_bf16x2(pv[6], pv[7])};
+#pragma unroll
+        for (int h2 = 0; h2 < 2; ++h2) {
+          const int r = 2 * rp + h2;  // key row of the group: dwords 2*h2, 2*h2+1 hold its 4 keys
+          if ((tt == 0 && r <= 2) || (tt == 1 && r >= 1)) {
+            const bool zero = tt == 0 ? ylo[r < 3 ? r : 2] : yhi[r >= 1 ? r - 1 : 0];
+            pw[2 * h2] = zero ? 0u : pw[2 * h2];
+            pw[2 * h2 + 1] = zero ? 0u : pw[2 * h2 + 1];
+          }
+        }
+        pb[rp] = __builtin_bit_cast(bf16x8, pw);
+      }
+#pragma unroll
+      for (int rp = 0; rp < NRP; ++rp) {
+        lacc[k] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ones, pb[rp], lacc[k], 0, 0, 0);
+#pragma unroll
+        for (int db = 0; db < DB; ++db)
+          oacc[k][db] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(av[rp][db], pb[rp], oacc[k][db], 0, 0, 0);
+      }
+    }
+  };
+
+  // ---- K/V ring over the strip's rows, row-group-major, z-minor ----
+  const int64_t zstepk = 2 * (int64_t)dz * p.ks[1], zstepv = 2 * (int64_t)dz * p.vs[1];
+  const char* kseg = (const char*)p.k + 2 * ((int64_t)b * p.ks[0] + (int64_t)h * p.ks[4] +
+                                             (int64_t)(gz + dz * sz) * p.ks[1] + (int64_t)gy * p.ks[2]) +
+                     (int64_t)S * rowk;
+  const char* vseg = (const char*)p.v + 2 * ((int64_t)b * p.vs[0] + (int64_t)h * p.vs[4] +
+                                             (int64_t)(gz + dz * sz) * p.vs[1] + (int64_t)gy * p.vs[2]) +
+                     (int64_t)S * rowv;
+  int cz = 0, cp = 0;
+  uint32_t issue_off = 0;
+  auto issue = [&]() {
+    const int nrow = min(max(NR - RPS * cp, 0), RPS);
+    const u32x4 rk = make_rsrc(kseg + (int64_t)cp * RPS * rowk + (int64_t)cz * zstepk, (uint32_t)(nrow * rowk));
+    const u32x4 rv = make_rsrc(vseg + (int64_t)cp * RPS * rowv + (int64_t)cz * zstepv, (uint32_t)(nrow * rowv));
+    const uint32_t m0 = lds_base + issue_off + (uint32_t)(wave / RKB) * RB + (uint32_t)(wave % RKB) * 1024;
+#pragma unroll
+    for (int r = 0; r < RPS; ++r) dma_row16(rk, m0 + r * RB, xoffk + (uint32_t)(r * rowk));
+#pragma unroll
+    for (int r = 0; r < RPS; ++r) dma_row16(rv, m0 + (RPS + r) * RB, xoffv + (uint32_t)(r * rowv));
+    issue_off = issue_off + STAGE_B == RING_B ? 0 : issue_off + STAGE_B;
+    if (++cz == kz) {
+      cz = 0;
+      ++cp;
+    }
+  };
+
+  // Tile 0's Q is staged through the ring before the ring starts.
+  dma_q(0, 0);
+  wait_vmcnt(0);
+  start_tile(0, 0);
+  wait_lgkm0();
+  lds_barrier();  // staged Q read before the ring overwrites it
+#pragma unroll
+  for (int s = 0; s < NBUF - 1; ++s) issue();
+
+  uint32_t cur_off = 0;
+  uint64_t bad_tiles = 0;  // tiles (index < 64) for the exact path
+  bool bad_high = false;   // some tile with index >= 64 needs it
+  // Group gr (slot gr & 3 = C starts tile gr, slot (C + 1) & 3 finishes tile gr - 3).
+  auto group = [&](auto cst, int gr) {
+    constexpr int C = decltype(cst)::value;
+    for (int zc = 0; zc < kz; ++zc) {
+      const bool starting = zc == 0 && gr > 0 && gr < NT;
+      if (starting)
+        wait_vmcnt(0);  // the tile's Q copy as well
+      else
+        wait_vmcnt((NBUF - 2) * LPT);
+      lds_barrier();
+      issue();
+      if (starting) start_tile(C, (uint32_t)RING_B);
+      // Q of the next group's tile (each wave refills only its own part of the buffer)
+      if (zc == 1 && gr + 1 < NT) dma_q(gr + 1, (uint32_t)RING_B);
+
+      asm volatile("" : "+v"(ones));  // keep the ones operand resident
+      const char* st = lds + cur_off;
+      bf16x8 ak[RPS][KS];
+#pragma unroll
+      for (int r = 0; r < RPS; ++r)
+#pragma unroll
+        for (int ks = 0; ks < KS; ++ks) ak[r][ks] = *(const bf16x8*)(st + r * RB + koff[ks]);
+      bf16x8 av[NRP][DB];
+#pragma unroll
+      for (int rp = 0; rp < NRP; ++rp)
+#pragma unroll
+        for (int db = 0; db < DB; ++db) {
+          const bf16x4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4bf16(LDS_PTR(bf16x4, st + voffs[db] + 2 * rp * RB));
+          const bf16x4 hi =
+              __builtin_amdgcn_ds_read_tr16_b64_v4bf16(LDS_PTR(bf16x4, st + voffs[db] + (2 * rp + 1) * RB));
+          av[rp][db] = __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7);
+        }
+      stage_math(cst, ak, av);
+      cur_off = cur_off + STAGE_B == RING_B ? 0 : cur_off + STAGE_B;
+    }
+    const int jf = gr - (NS - 1);
+    if (jf >= 0 && jf < NT && finish_tile((C + 1) & (NS - 1), jf)) {
+      if (jf < 64)
+        bad_tiles |= 1ull << jf;
+      else
+        bad_high = true;
+    }
+  };
+  for (int gr = 0; gr < NG; gr += NS) {
+    group(std::integral_constant<int, 0>{}, gr);
+    if (gr + 1 >= NG) break;
+    group(std::integral_constant<int, 1>{}, gr + 1);
+    if (gr + 2 >= NG) break;
+    group(std::integral_constant<int, 2>{}, gr + 2);
+    if (gr + 3 >= NG) break;
+    group(std::integral_constant<int, 3>{}, gr + 3);
+  }
+  wait_vmcnt(0);  // the ring's trailing (empty) stages
+
+  // Rare: tiles whose sums left the fixed reference's range, recomputed
+  // exactly after the strip (their stores above are overwritten).
+  if (bad_tiles != 0 || bad_high) {
+    __builtin_amdgcn_s_waitcnt(0);
+    for (int j = 0; j < NT; ++j)
+      if (j < 64 ? ((bad_tiles >> j) & 1) : bad_high)
+        na3d_strip_tile_exact(&p, StripTile{b, h, gz, gy, gx, iz, ys + TY * j, ye, xw0, qx1});
+  }
+#endif
+}
+
+template <int D, int TX, int RPS, int NBUF>
+__global__ __launch_bounds__(256, 2) void na3d_strip_fast_kernel(Na3dParams p, Na3dStrips sg) {
+  na3d_strip_fast_body<D, TX, RPS, NBUF>(p, sg);
+}
+
+
+// ---------------------------------------------------------------------------
 // Host side
 // ---------------------------------------------------------------------------
 template <typename T>
@@ -1103,7 +1559,7 @@ static int launch_mfma_tx(const Na3dParams& p, hipStream_t st) {
 // Strip kernel launch.  Work units are (batch, head, residue, z, column box)
 // strips over the whole y range; the y range is cut into chunks only when the
 // strips alone would not fill the GPU several times over.
-template <int D, int TX, int RPS, int NBUF>
+template <int D, int TX, int RPS, int NBUF, bool FAST>
 static int launch_strip(const Na3dParams& p, hipStream_t st) {
   constexpr int TY = 16 / TX;
   Na3dStrips sg;
@@ -1126,6 +1582,11 @@ static int launch_strip(const Na3dParams& p, hipStream_t st) {
   const int64_t total = strips * sg.nch;
   if (total > 0x7fffffff) return fail(STRATA_HIP_EUNSUPPORTED, "na3d: problem too large for one launch");
   sg.total = (int)total;
+  if (FAST) {
+    hipLaunchKernelGGL((na3d_strip_fast_kernel<D, TX, RPS, NBUF>), dim3((unsigned)total), dim3(64 * NA3D_NWX), 0, st,
+                       p, sg);
+    return check_launch("na3d_strip_fast_kernel");
+  }
   hipLaunchKernelGGL((na3d_strip_kernel<D, TX, RPS, NBUF>), dim3((unsigned)total), dim3(64 * NA3D_NWX), 0, st, p, sg);
   return check_launch("na3d_strip_kernel");
 }
@@ -1142,6 +1603,20 @@ static bool strip_fits(const Na3dParams& p) {
   const int64_t* sd[2] = {p.qs, p.ks};
   for (int t = 0; t < 2; ++t)
     if (((int64_t)(p.L[1] - 1) * sd[t][2] + (int64_t)(p.L[2] - 1) * sd[t][3] + p.D) * 2 >= 0x7fffffffLL) return false;
+  return true;
+}
+
+// Regular strips (na3d_strip_fast_kernel): ky = 13 and no query row of the box
+// has a clamped y window in any residue class, so every tile's y-union starts
+// one row group after the previous tile's.
+static bool strip_regular(const Na3dParams& p) {
+  if (p.ker[1] != 13) return false;
+  const int r = p.ker[1] / 2, dy = p.dil[1];
+  for (int g = 0; g < dy; ++g) {
+    const int y0 = sub_first(p.org[1], g, dy), y1 = sub_end(p.org[1], p.ext[1], g, dy);
+    if (y1 <= y0) continue;
+    if (y0 - r < 0 || y1 - 1 + r > sub_len(p.L[1], g, dy) - 1) return false;
+  }
   return true;
 }
 
@@ -1238,7 +1713,8 @@ extern "C" int strata_hip_na3d_fwd(const strata_hip_na3d_args* a, void* stream) 
     case 32:
       return launch_mfma_d<32>(p, st);
     case 64:
-      if (strip_fits(p)) return launch_strip<64, 4, 4, 2>(p, st);
+      if (strip_fits(p))
+        return strip_regular(p) ? launch_strip<64, 4, 4, 2, true>(p, st) : launch_strip<64, 4, 4, 2, false>(p, st);
       return launch_mfma_d<64>(p, st);
     default:
       return launch_mfma_d<128>(p, st);

@@ -165,3 +165,72 @@ def test_cfg2_halo_interior_subboxes(gpu):
             o = (org[0], org[1] - 8, org[2] - 8)
             got = out[b : b + 1, o[0] : o[0] + 2, o[1] : o[1] + 16, o[2] : o[2] + 16, h : h + 1]
             assert rel_l2(got.float(), ref) <= BF16_TOL, (b, h, org)
+
+
+# Regular strips: ky = 13 and every query's y window unclamped (a halo of at
+# least 6 rows in each dilation residue class).  These take the fixed-reference
+# strip kernel; the cases cover one to eight tiles per strip, a partial last
+# tile, ragged x, deeper z windows, dilation, and y chunks of the walk.
+REGULAR_CASES = [
+    # shape (B, Z, Y, X, H, D), kernel, dilation, origin, extent
+    ((1, 3, 16, 28, 2, 64), (3, 13, 13), (1, 1, 1), (0, 6, 6), (3, 4, 16)),
+    ((1, 4, 25, 29, 1, 64), (3, 13, 11), (1, 1, 1), (0, 6, 5), (4, 13, 19)),
+    ((2, 5, 44, 24, 2, 64), (5, 13, 13), (1, 1, 1), (0, 6, 6), (5, 32, 12)),
+    ((1, 4, 40, 40, 1, 64), (3, 13, 13), (1, 2, 2), (0, 12, 12), (4, 16, 16)),
+    ((1, 3, 24, 30, 3, 64), (3, 13, 11), (1, 1, 1), (0, 6, 7), (3, 10, 13)),
+]
+
+
+@pytest.mark.parametrize("case", REGULAR_CASES, ids=[f"{c[0]}-k{c[1]}-d{c[2]}-box{c[3]}" for c in REGULAR_CASES])
+def test_regular_strip_vs_oracle(gpu, case):
+    shape, kernel, dil, origin, extent = case
+    print(f"regular strip {shape} k{kernel} d{dil} o{origin} e{extent}", flush=True)
+    q, k, v = _rand(shape, 21, torch.bfloat16, gpu)
+    out = _run(q, k, v, kernel, dil, origin, extent)
+    ref = O.na3d(q.cpu(), k.cpu(), v.cpu(), kernel, dil, q_origin=origin, q_extent=extent)
+    assert rel_l2(out.float(), ref) <= BF16_TOL
+    assert torch.isfinite(out.float()).all()
+
+
+def test_regular_strip_chunks(gpu):
+    """Enough strips that the y range is walked in four chunks of four tiles;
+    the oracle checks boxes on both sides of the chunk seams."""
+    shape = (1, 4, 76, 44, 64, 64)
+    g = torch.Generator(device=gpu).manual_seed(4)
+    q, k, v = (torch.randn(shape, generator=g, device=gpu).bfloat16() for _ in range(3))
+    print("regular strip chunks", flush=True)
+    out = _run(q, k, v, (3, 13, 13), origin=(0, 6, 6), extent=(4, 64, 32))
+    torch.cuda.synchronize()
+    for h in (0, 37, 63):
+        sl = (slice(0, 1), slice(None), slice(None), slice(None), slice(h, h + 1))
+        qc, kc, vc = q[sl].cpu(), k[sl].cpu(), v[sl].cpu()
+        for org in ((0, 6, 6), (1, 18, 20), (2, 34, 10), (2, 58, 30)):
+            ext = (2, 12, 8)
+            ref = O.na3d(qc, kc, vc, (3, 13, 13), q_origin=org, q_extent=ext)
+            o = (org[0], org[1] - 6, org[2] - 6)
+            got = out[0:1, o[0] : o[0] + 2, o[1] : o[1] + 12, o[2] : o[2] + 8, h : h + 1]
+            assert rel_l2(got.float(), ref) <= BF16_TOL, (h, org)
+
+
+def test_regular_strip_score_far_above_own_key(gpu):
+    """A key scoring ~160 (log2 units) above a query's own-key score overflows
+    the fixed softmax reference of the fast strip kernel; that tile must be
+    recomputed exactly (its output is then the dominant key's value)."""
+    shape = (1, 3, 20, 28, 1, 64)
+    q, k, v = (t.float() for t in _rand(shape, 8, torch.bfloat16, "cpu"))
+    u = torch.zeros(64)
+    u[:32] = 1.0 / 32**0.5
+    w = torch.zeros(64)
+    w[32:] = 1.0 / 32**0.5
+    # query (1, 9, 10): large along u, its own key along w (score 0), one
+    # neighbour key (2, 12, 14) large along u: 30 * 30 / 8 nats ~ 162 log2 units.
+    q[0, 1, 9, 10, 0] = 30.0 * u
+    k[0, 1, 9, 10, 0] = 2.0 * w
+    k[0, 2, 12, 14, 0] = 30.0 * u
+    q, k, v = (t.bfloat16() for t in (q, k, v))
+    out = _run(q.to(gpu), k.to(gpu), v.to(gpu), (3, 13, 13), origin=(0, 6, 6), extent=(3, 8, 16))
+    ref = O.na3d(q, k, v, (3, 13, 13), q_origin=(0, 6, 6), q_extent=(3, 8, 16))
+    assert torch.isfinite(out.float()).all()
+    assert rel_l2(out.float(), ref) <= BF16_TOL
+    got = out[0, 1, 3, 4, 0].float().cpu()
+    assert rel_l2(got, v[0, 2, 12, 14, 0].float()) <= BF16_TOL
