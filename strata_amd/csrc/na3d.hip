@@ -1109,8 +1109,9 @@ __global__ __launch_bounds__(256, 2) void na3d_strip_kernel(Na3dParams p, Na3dSt
 // is unrolled four times, which makes both slots compile-time constants: the
 // y masks (query row t sees rows r >= t of its first group and r <= t of its
 // last; every row of the two middle groups) are a few v_cndmask on the packed
-// probabilities, and no stage has a per-tile branch.  Ramp-up and ramp-down
-// groups compute every slot; the slots without a live tile are discarded.
+// probabilities, and no stage has a per-tile branch.  The three ramp-up groups
+// compute only the slots holding a tile; the ramp-down groups compute every
+// slot and the emptied ones are discarded.
 //
 // The softmax reference is fixed per tile: m = (own-key score) + SLACK, in
 // log2 units, so the stage loop has no running maximum and no rescaling.  A
@@ -1325,11 +1326,14 @@ __device__ __forceinline__ void na3d_strip_fast_body(const Na3dParams p, const N
   };
 
   // One stage's tile math for every slot.  C: slot of the tile in its first group.
-  auto stage_math = [&](auto cst, const bf16x8 (&ak)[RPS][KS], const bf16x8 (&av)[NRP][DB]) {
+  // ACT: bit k set if slot k holds a live tile (ramp groups at a strip's ends skip the others).
+  auto stage_math = [&](auto cst, auto act, const bf16x8 (&ak)[RPS][KS], const bf16x8 (&av)[NRP][DB]) {
     constexpr int C = decltype(cst)::value;
+    constexpr int ACT = decltype(act)::value;
 #pragma unroll
     for (int tt = 0; tt < NS; ++tt) {
       const int k = (C + tt) & (NS - 1);  // tt = 0: the tile's first group, tt = 1: its last
+      if (!((ACT >> k) & 1)) continue;
       f32x4 sacc[RPS];
 #pragma unroll
       for (int r = 0; r < RPS; ++r) {
@@ -1409,7 +1413,7 @@ __device__ __forceinline__ void na3d_strip_fast_body(const Na3dParams p, const N
   uint64_t bad_tiles = 0;  // tiles (index < 64) for the exact path
   bool bad_high = false;   // some tile with index >= 64 needs it
   // Group gr (slot gr & 3 = C starts tile gr, slot (C + 1) & 3 finishes tile gr - 3).
-  auto group = [&](auto cst, int gr) {
+  auto group = [&](auto cst, auto act, int gr) {
     constexpr int C = decltype(cst)::value;
     for (int zc = 0; zc < kz; ++zc) {
       const bool starting = zc == 0 && gr > 0 && gr < NT;
@@ -1440,7 +1444,7 @@ __device__ __forceinline__ void na3d_strip_fast_body(const Na3dParams p, const N
               __builtin_amdgcn_ds_read_tr16_b64_v4bf16(LDS_PTR(bf16x4, st + voffs[db] + (2 * rp + 1) * RB));
           av[rp][db] = __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7);
         }
-      stage_math(cst, ak, av);
+      stage_math(cst, act, ak, av);
       cur_off = cur_off + STAGE_B == RING_B ? 0 : cur_off + STAGE_B;
     }
     const int jf = gr - (NS - 1);
@@ -1451,14 +1455,26 @@ __device__ __forceinline__ void na3d_strip_fast_body(const Na3dParams p, const N
         bad_high = true;
     }
   };
-  for (int gr = 0; gr < NG; gr += NS) {
-    group(std::integral_constant<int, 0>{}, gr);
+  using I0 = std::integral_constant<int, 0>;
+  using I1 = std::integral_constant<int, 1>;
+  using I2 = std::integral_constant<int, 2>;
+  using I3 = std::integral_constant<int, 3>;
+  using ALL = std::integral_constant<int, 15>;
+  // Ramp-up: tile g starts in group g (slot g), so groups 0-2 compute only
+  // the slots already holding a tile.  From group 3 on every slot computes
+  // (the ramp-down's emptied slots too: their masks would depend on NT mod 4).
+  group(I0{}, std::integral_constant<int, 1>{}, 0);
+  group(I1{}, std::integral_constant<int, 3>{}, 1);
+  group(I2{}, std::integral_constant<int, 7>{}, 2);
+  for (int gr = 3;; gr += NS) {  // NG = NT + 3 >= 4
+    group(I3{}, ALL{}, gr);
     if (gr + 1 >= NG) break;
-    group(std::integral_constant<int, 1>{}, gr + 1);
+    group(I0{}, ALL{}, gr + 1);
     if (gr + 2 >= NG) break;
-    group(std::integral_constant<int, 2>{}, gr + 2);
+    group(I1{}, ALL{}, gr + 2);
     if (gr + 3 >= NG) break;
-    group(std::integral_constant<int, 3>{}, gr + 3);
+    group(I2{}, ALL{}, gr + 3);
+    if (gr + 4 >= NG) break;
   }
   wait_vmcnt(0);  // the ring's trailing (empty) stages
 
