@@ -9,24 +9,13 @@
 // as one 8-byte write after bias, GELU and residual.
 //
 // Two kernels: gemm_dma_kernel (K % 64 == 0; 256 x 256 tiles, 8 waves,
-// global->LDS streaming) for the block's GEMMs, and gemm_bias_act_kernel
-// (128 x 128 tiles, register-staged loads) for any other K.
-#include "common.h"
+// global->LDS streaming) for the block's fused-epilogue GEMMs, and
+// gemm_bias_act_kernel (128 x 128 tiles, register-staged loads) for any other
+// K.  Plain GEMMs (no activation, bias and an added residual at most) are
+// handed to hipBLASLt first (gemm_lt.cpp).
+#include "gemm.h"
 
 namespace strata {
-
-struct GemmParams {
-  const bf16* x;
-  const bf16* w;
-  const bf16* bias;
-  const bf16* res;
-  bf16* out;
-  int64_t M, N, K;
-  int64_t ldx, ldw, ldr, ldo;
-  int act;
-  int res_op;  // strata_hip_res_op: the residual is added or multiplied
-  int mt, nt;  // tiles along M and N
-};
 
 __device__ __forceinline__ float gelu_tanh(float x) {
   // 0.5 x (1 + tanh(u)) with u = sqrt(2/pi) (x + 0.044715 x^3) equals
@@ -521,6 +510,9 @@ extern "C" int strata_hip_gemm_bias_act(const strata_hip_gemm_args* a, void* str
   p.act = a->act;
   p.res_op = a->res_op;
   hipStream_t st = (hipStream_t)stream;
+  // Plain GEMMs (no activation; bias and an added residual at most) go to
+  // hipBLASLt; the fused epilogues, and anything it declines, run here.
+  if (gemm_lt_enabled() && gemm_lt(p, st) == STRATA_HIP_OK) return STRATA_HIP_OK;
   // The large-tile kernels stream 64-wide K steps with 32-bit lane offsets
   // inside a 256-row block: K a multiple of 64, row strides small enough.
   const bool big = p.K % 64 == 0 && 256 * p.ldx * 2 + 4096 < (int64_t)OOB && 256 * p.ldw * 2 + 4096 < (int64_t)OOB;

@@ -1,0 +1,124 @@
+// Plain GEMMs through hipBLASLt: out = x @ w^T (+ bias) (+ residual).
+//
+// The block's projections without a fused activation (attn.qkv, attn.proj +
+// residual, mlp fc2 + residual, and the rollout's embed / merge / head) are
+// plain library GEMMs; hipBLASLt's 256x256x64 direct-to-LDS kernels run them
+// 1.4-1.75x faster than gemm_dma_kernel on MI355X.  The fused epilogues this
+// library exists for (GELU, the sigmoid gate with a multiplied residual) stay
+// on the hand-written kernels in gemm.hip.
+//
+// Mapping to hipBLASLt's column-major convention: out^T [N x M] (ld = ldo) =
+// op_T(w as K x N, ld = ldw) * (x as K x M, ld = ldx); the residual is the C
+// matrix with beta = 1 (it may alias out when both row strides agree); the
+// bias uses HIPBLASLT_EPILOGUE_BIAS (added before the residual, fp32 math, one
+// rounding to bf16).  No workspace: the library allocates nothing per call.
+//
+// State: one hipBLASLt handle per device (created on first use with that
+// device current) and a host-side plan cache (descriptors + the heuristic's
+// first algorithm) keyed by device, shape, strides and epilogue.  A plan's
+// bias pointer is set under the cache mutex right before the asynchronous
+// launch, so concurrent callers on different threads stay correct.
+#include <hip/hip_runtime.h>
+#include <hipblaslt/hipblaslt.h>
+
+#include <cstdlib>
+#include <cstring>
+#include <map>
+#include <mutex>
+#include <tuple>
+
+#include "gemm.h"
+
+namespace strata {
+
+namespace {
+
+struct LtPlan {
+  hipblasLtMatmulDesc_t desc = nullptr;
+  hipblasLtMatrixLayout_t la = nullptr, lb = nullptr, lc = nullptr, ld = nullptr;
+  hipblasLtMatmulAlgo_t algo;
+  bool ok = false;
+};
+
+using LtKey = std::tuple<int, int64_t, int64_t, int64_t, int64_t, int64_t, int64_t, int64_t, bool, bool>;
+
+std::mutex g_mu;
+hipblasLtHandle_t g_handle[64] = {};
+bool g_handle_failed[64] = {};
+std::map<LtKey, LtPlan> g_plans;
+
+bool build_plan(hipblasLtHandle_t h, const GemmParams& p, bool has_bias, bool has_res, LtPlan& pl) {
+  if (hipblasLtMatmulDescCreate(&pl.desc, HIPBLAS_COMPUTE_32F, HIP_R_32F) != HIPBLAS_STATUS_SUCCESS) return false;
+  hipblasOperation_t ta = HIPBLAS_OP_T, tb = HIPBLAS_OP_N;
+  hipblasLtMatmulDescSetAttribute(pl.desc, HIPBLASLT_MATMUL_DESC_TRANSA, &ta, sizeof(ta));
+  hipblasLtMatmulDescSetAttribute(pl.desc, HIPBLASLT_MATMUL_DESC_TRANSB, &tb, sizeof(tb));
+  hipblasLtEpilogue_t ep = has_bias ? HIPBLASLT_EPILOGUE_BIAS : HIPBLASLT_EPILOGUE_DEFAULT;
+  hipblasLtMatmulDescSetAttribute(pl.desc, HIPBLASLT_MATMUL_DESC_EPILOGUE, &ep, sizeof(ep));
+  if (has_bias) {
+    hipDataType bt = HIP_R_16BF;
+    hipblasLtMatmulDescSetAttribute(pl.desc, HIPBLASLT_MATMUL_DESC_BIAS_DATA_TYPE, &bt, sizeof(bt));
+    const void* bias = p.bias;
+    hipblasLtMatmulDescSetAttribute(pl.desc, HIPBLASLT_MATMUL_DESC_BIAS_POINTER, &bias, sizeof(bias));
+  }
+  if (hipblasLtMatrixLayoutCreate(&pl.la, HIP_R_16BF, p.K, p.N, p.ldw) != HIPBLAS_STATUS_SUCCESS ||
+      hipblasLtMatrixLayoutCreate(&pl.lb, HIP_R_16BF, p.K, p.M, p.ldx) != HIPBLAS_STATUS_SUCCESS ||
+      hipblasLtMatrixLayoutCreate(&pl.lc, HIP_R_16BF, p.N, p.M, has_res ? p.ldr : p.ldo) != HIPBLAS_STATUS_SUCCESS ||
+      hipblasLtMatrixLayoutCreate(&pl.ld, HIP_R_16BF, p.N, p.M, p.ldo) != HIPBLAS_STATUS_SUCCESS)
+    return false;
+  hipblasLtMatmulPreference_t pref = nullptr;
+  if (hipblasLtMatmulPreferenceCreate(&pref) != HIPBLAS_STATUS_SUCCESS) return false;
+  uint64_t ws = 0;
+  hipblasLtMatmulPreferenceSetAttribute(pref, HIPBLASLT_MATMUL_PREF_MAX_WORKSPACE_BYTES, &ws, sizeof(ws));
+  hipblasLtMatmulHeuristicResult_t res[1];
+  int nres = 0;
+  const hipblasStatus_t st =
+      hipblasLtMatmulAlgoGetHeuristic(h, pl.desc, pl.la, pl.lb, pl.lc, pl.ld, pref, 1, res, &nres);
+  hipblasLtMatmulPreferenceDestroy(pref);
+  if (st != HIPBLAS_STATUS_SUCCESS || nres < 1) return false;
+  pl.algo = res[0].algo;
+  return true;
+}
+
+}  // namespace
+
+bool gemm_lt_enabled() {
+  const char* e = std::getenv("STRATA_HIP_GEMM");
+  return !(e && std::strcmp(e, "native") == 0);
+}
+
+int gemm_lt(const GemmParams& p, hipStream_t stream) {
+  const bool has_bias = p.bias != nullptr, has_res = p.res != nullptr;
+  if (p.act != STRATA_HIP_ACT_NONE || (has_res && p.res_op != STRATA_HIP_RES_ADD)) return GEMM_LT_DECLINED;
+  // in place only with one layout for C and D
+  if (has_res && (const void*)p.res == (const void*)p.out && p.ldr != p.ldo) return GEMM_LT_DECLINED;
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return GEMM_LT_DECLINED;
+
+  std::lock_guard<std::mutex> lock(g_mu);
+  if (g_handle_failed[dev]) return GEMM_LT_DECLINED;
+  if (!g_handle[dev] && hipblasLtCreate(&g_handle[dev]) != HIPBLAS_STATUS_SUCCESS) {
+    g_handle[dev] = nullptr;
+    g_handle_failed[dev] = true;
+    return GEMM_LT_DECLINED;
+  }
+  const LtKey key{dev, p.M, p.N, p.K, p.ldx, p.ldw, has_res ? p.ldr : 0, p.ldo, has_bias, has_res};
+  auto it = g_plans.find(key);
+  if (it == g_plans.end()) {
+    LtPlan pl;
+    pl.ok = build_plan(g_handle[dev], p, has_bias, has_res, pl);
+    it = g_plans.emplace(key, pl).first;
+  }
+  LtPlan& pl = it->second;
+  if (!pl.ok) return GEMM_LT_DECLINED;
+  if (has_bias) {
+    const void* bias = p.bias;
+    hipblasLtMatmulDescSetAttribute(pl.desc, HIPBLASLT_MATMUL_DESC_BIAS_POINTER, &bias, sizeof(bias));
+  }
+  const float alpha = 1.f, beta = has_res ? 1.f : 0.f;
+  const void* c = has_res ? (const void*)p.res : (const void*)p.out;
+  const hipblasStatus_t st = hipblasLtMatmul(g_handle[dev], pl.desc, &alpha, p.w, pl.la, p.x, pl.lb, &beta, c, pl.lc,
+                                             p.out, pl.ld, &pl.algo, nullptr, 0, stream);
+  return st == HIPBLAS_STATUS_SUCCESS ? STRATA_HIP_OK : GEMM_LT_DECLINED;
+}
+
+}  // namespace strata
