@@ -38,6 +38,21 @@ __device__ __forceinline__ float apply_act(float v, int act) {
 __device__ __forceinline__ float combine(float o, float r, int res_op) {
   return res_op == STRATA_HIP_RES_MUL ? o * r : o + r;
 }
+// Compile-time forms for the large-tile kernel: one instance per activation
+// and residual mode keeps its epilogue straight-line (a runtime activation
+// code makes every element branch over all four activations).
+enum { RES_NONE_T = 0, RES_ADD_T = 1, RES_MUL_T = 2 };
+template <int ACT>
+__device__ __forceinline__ float act_t(float v) {
+  if constexpr (ACT == STRATA_HIP_ACT_GELU_TANH) return gelu_tanh(v);
+  else if constexpr (ACT == STRATA_HIP_ACT_GELU_ERF) return gelu_erf(v);
+  else if constexpr (ACT == STRATA_HIP_ACT_SIGMOID) return sigmoid_fast(v);
+  else return v;
+}
+template <int RES>
+__device__ __forceinline__ float combine_t(float o, float r) {
+  return RES == RES_MUL_T ? o * r : o + r;
+}
 
 template <int BM, int BN, int WGM, int WGN>
 __global__ __launch_bounds__(64 * WGM * WGN) void gemm_bias_act_kernel(GemmParams p) {
@@ -264,7 +279,7 @@ __device__ __forceinline__ int gswz(int chunk, int row) {
 // columns stream from global memory straight into an LDS ring of NST stages
 // (buffer_load ... lds) that runs NST - 1 stages ahead of the MFMAs, one
 // barrier per stage.
-template <int BM, int BN, int WGM, int WGN, int BK, int NST>
+template <int BM, int BN, int WGM, int WGN, int BK, int NST, int ACT, int RES>
 __device__ __forceinline__ void gemm_dma_body(const GemmParams& p) {
   constexpr int NW = WGM * WGN;
   constexpr int WTM = BM / WGM;  // 128
@@ -284,9 +299,16 @@ __device__ __forceinline__ void gemm_dma_body(const GemmParams& p) {
   static_assert((PD - 1) * LPW <= 16, "wait_vmcnt range");
   __shared__ __attribute__((aligned(1024))) char lds[LDS_BYTES];  // ring, then the epilogue slabs
 
+  // Persistent: a workgroup walks tiles id, id + grid, ...  With a grid that
+  // is a multiple of 8, tile index t stays on the XCD that runs workgroup id
+  // (the dispatcher deals workgroups round-robin over the 8 XCDs), and each
+  // XCD takes a contiguous block of tiles, 32 neighbours in flight at once.
+  const int ntiles = p.mt * p.nt;
+  const int wg_id = (int)__builtin_amdgcn_workgroup_id_x();
+  for (int t = wg_id; t < ntiles; t += (int)gridDim.x) {
+  if (t != wg_id) lds_barrier();  // the previous tile's epilogue has read its slabs
   const int wg = [&] {
-    const int id = (int)__builtin_amdgcn_workgroup_id_x(), n = p.mt * p.nt;
-    const int xcd = id & 7, local = id >> 3, q = n >> 3, rem = n & 7;
+    const int xcd = t & 7, local = t >> 3, q = ntiles >> 3, rem = ntiles & 7;
     return xcd < rem ? xcd * (q + 1) + local : rem * (q + 1) + (xcd - rem) * q + local;
   }();
   const int tn = wg % p.nt;
@@ -394,76 +416,114 @@ __device__ __forceinline__ void gemm_dma_body(const GemmParams& p) {
   // ---- epilogue through LDS ----
   // Phase 1: bias + activation on the accumulators, bf16 into this wave's
   // WTM x WTN slab of LDS (rows of SRB bytes, 16-byte chunks swizzled by row).
-  // Phase 2: each lane reads 16 contiguous bytes of a row, adds the residual
-  // read the same way, and writes 16 bytes: CPR lanes cover a row.
-  constexpr int SRB = WTN * 2, CPR = WTN / 8, RPI = 64 / CPR;
+  // Phase 2: each lane reads 16 contiguous bytes of a row, combines the
+  // residual read the same way, and writes 16 bytes: CPR lanes cover a row.
+  // Loads and stores share vmcnt on gfx9 (a load issued after a store waits
+  // for it), so every bias and residual load is issued before the first
+  // store: the bias before the barrier, the residual rows into registers the
+  // accumulators have freed.  Tiles inside the matrix skip every bounds check.
+  constexpr int SRB = WTN * 2, CPR = WTN / 8, RPI = 64 / CPR, NIT = WTM / RPI;
+  const int64_t gn0 = n0 + wn * WTN, gm0 = m0 + wm * WTM;
+  const bool full = m0 + BM <= p.M && n0 + BN <= p.N;  // uniform
+  u32x2 bw[FN][4];
+#pragma unroll
+  for (int i = 0; i < FN; ++i)
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      const int64_t gn = gn0 + 32 * i + 8 * q + 4 * hi;
+      bw[i][q] = (u32x2){0u, 0u};
+      if (p.bias && (full || gn + 4 <= p.N)) bw[i][q] = *(const u32x2*)(p.bias + gn);
+    }
   lds_barrier();  // every wave is done reading the last stage
   char* slab = lds + wave * (WTM * WTN * 2);
-  const int64_t gn0 = n0 + wn * WTN, gm0 = m0 + wm * WTM;
 #pragma unroll
   for (int i = 0; i < FN; ++i)
 #pragma unroll
     for (int q = 0; q < 4; ++q) {
       const int nl = 32 * i + 8 * q + 4 * hi;  // local column of this lane's quad
-      float bv[4] = {0.f, 0.f, 0.f, 0.f};
-      if (p.bias) {
+      float bv[4] = {bf16_lo(bw[i][q][0]), bf16_hi(bw[i][q][0]), bf16_lo(bw[i][q][1]), bf16_hi(bw[i][q][1])};
+      if (!full && p.bias && gn0 + nl + 4 > p.N) {  // ragged last columns
         const int64_t gn = gn0 + nl;
-        if (gn + 4 <= p.N) {
-          const u32x2 bw = *(const u32x2*)(p.bias + gn);
-          bv[0] = bf16_lo(bw[0]);
-          bv[1] = bf16_hi(bw[0]);
-          bv[2] = bf16_lo(bw[1]);
-          bv[3] = bf16_hi(bw[1]);
-        } else {
-          for (int e = 0; e < 4; ++e) bv[e] = gn + e < p.N ? (float)p.bias[gn + e] : 0.f;
-        }
+        for (int e = 0; e < 4; ++e) bv[e] = gn + e < p.N ? (float)p.bias[gn + e] : 0.f;
       }
 #pragma unroll
       for (int j = 0; j < FM; ++j) {
         float v[4];
 #pragma unroll
-        for (int e = 0; e < 4; ++e) {
-          v[e] = acc[i][j][4 * q + e] + bv[e];
-          v[e] = apply_act(v[e], p.act);
-        }
+        for (int e = 0; e < 4; ++e) v[e] = act_t<ACT>(acc[i][j][4 * q + e] + bv[e]);
         const int ml = 32 * j + l32;
         const u32x2 w2 = {pack_bf16x2(v[0], v[1]), pack_bf16x2(v[2], v[3])};
         *(u32x2*)(slab + ml * SRB + (((nl >> 3) ^ (ml & 7)) << 4) + 8 * hi) = w2;
       }
     }
-#pragma unroll 4
-  for (int it = 0; it < WTM / RPI; ++it) {
-    const int ml = RPI * it + lane / CPR;
-    const int c = lane % CPR;  // logical 16-byte chunk = 8 output columns
-    const u32x4 w4 = *(const u32x4*)(slab + ml * SRB + ((c ^ (ml & 7)) << 4));
-    const int64_t gm = gm0 + ml, gn = gn0 + 8 * c;
-    if (gm >= p.M || gn >= p.N) continue;
-    if (gn + 8 <= p.N) {
-      u32x4 o = w4;
-      if (p.res) {
-        const u32x4 r4 = *(const u32x4*)(p.res + gm * p.ldr + gn);
+  const int c = lane % CPR;  // logical 16-byte chunk = 8 output columns
+  const int64_t gn = gn0 + 8 * c;
+  u32x4 r4[NIT];
+  if constexpr (RES != RES_NONE_T) {
 #pragma unroll
-        for (int e = 0; e < 4; ++e)
-          o[e] = pack_bf16x2(combine(bf16_lo(w4[e]), bf16_lo(r4[e]), p.res_op),
-                             combine(bf16_hi(w4[e]), bf16_hi(r4[e]), p.res_op));
-      }
+    for (int it = 0; it < NIT; ++it) {
+      const int64_t gm = gm0 + RPI * it + lane / CPR;
+      r4[it] = (u32x4){0u, 0u, 0u, 0u};
+      if (full || (gm < p.M && gn + 8 <= p.N)) r4[it] = *(const u32x4*)(p.res + gm * p.ldr + gn);
+    }
+  }
+#pragma unroll
+  for (int it = 0; it < NIT; ++it) {
+    const int ml = RPI * it + lane / CPR;
+    const u32x4 w4 = *(const u32x4*)(slab + ml * SRB + ((c ^ (ml & 7)) << 4));
+    const int64_t gm = gm0 + ml;
+    u32x4 o = w4;
+    if constexpr (RES != RES_NONE_T) {
+#pragma unroll
+      for (int e = 0; e < 4; ++e)
+        o[e] = pack_bf16x2(combine_t<RES>(bf16_lo(w4[e]), bf16_lo(r4[it][e])),
+                           combine_t<RES>(bf16_hi(w4[e]), bf16_hi(r4[it][e])));
+    }
+    if (full || (gm < p.M && gn + 8 <= p.N)) {
       *(u32x4*)(p.out + gm * p.ldo + gn) = o;
-    } else {
-      for (int e = 0; e < 8 && gn + e < p.N; ++e) {
+    } else if (gm < p.M && gn < p.N) {
+      for (int e = 0; e < 8 && gn + e < p.N; ++e) {  // ragged last columns
         const uint32_t wd = w4[e >> 1];
-        float o = (e & 1) ? bf16_hi(wd) : bf16_lo(wd);
-        if (p.res) o = combine(o, (float)p.res[gm * p.ldr + gn + e], p.res_op);
-        p.out[gm * p.ldo + gn + e] = (bf16)o;
+        float ov = (e & 1) ? bf16_hi(wd) : bf16_lo(wd);
+        if constexpr (RES != RES_NONE_T) ov = combine_t<RES>(ov, (float)p.res[gm * p.ldr + gn + e]);
+        p.out[gm * p.ldo + gn + e] = (bf16)ov;
       }
     }
   }
+  }  // tiles
 }
 
 // One 256 x 256 workgroup of 8 waves per CU, K step 64, double-buffered
 // 128 KiB ring.  (Measured alternatives at the block's shapes, all slower:
 // 256 x 128 tiles at two workgroups per CU; K step 32 with 3-5 stages; four
 // waves of 128 x 128 with the accumulators in AGPRs.)
-__global__ __launch_bounds__(512, 1) void gemm_dma_kernel(GemmParams p) { gemm_dma_body<256, 256, 2, 4, 64, 2>(p); }
+template <int ACT, int RES>
+__global__ __launch_bounds__(512, 1) void gemm_dma_kernel(GemmParams p) {
+  gemm_dma_body<256, 256, 2, 4, 64, 2, ACT, RES>(p);
+}
+
+template <int ACT>
+static void launch_dma_act(const GemmParams& p, dim3 grid, hipStream_t st) {
+  if (!p.res)
+    hipLaunchKernelGGL((gemm_dma_kernel<ACT, RES_NONE_T>), grid, dim3(512), 0, st, p);
+  else if (p.res_op == STRATA_HIP_RES_MUL)
+    hipLaunchKernelGGL((gemm_dma_kernel<ACT, RES_MUL_T>), grid, dim3(512), 0, st, p);
+  else
+    hipLaunchKernelGGL((gemm_dma_kernel<ACT, RES_ADD_T>), grid, dim3(512), 0, st, p);
+}
+
+// Compute units of the current device (cached per device).
+static int device_cus() {
+  static int cached[64] = {};
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
+  if (cached[dev] == 0) {
+    int n = 0;
+    if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0) n = 256;
+    cached[dev] = n;
+  }
+  return cached[dev];
+}
 
 template <int BM, int BN, int WGM, int WGN>
 static int launch_gemm(GemmParams p, hipStream_t st) {
@@ -521,7 +581,15 @@ extern "C" int strata_hip_gemm_bias_act(const strata_hip_gemm_args* a, void* str
     p.nt = (int)((p.N + 255) / 256);
     const int64_t total = (int64_t)p.mt * p.nt;
     if (total > 0x7fffffff) return fail(STRATA_HIP_EUNSUPPORTED, "gemm: problem too large for one launch");
-    hipLaunchKernelGGL(gemm_dma_kernel, dim3((unsigned)total), dim3(512), 0, st, p);
+    // one persistent workgroup per CU (the 128 KiB ring admits one)
+    const int cus = device_cus();
+    const dim3 grid((unsigned)(total < cus ? total : cus));
+    switch (p.act) {
+      case STRATA_HIP_ACT_GELU_TANH: launch_dma_act<STRATA_HIP_ACT_GELU_TANH>(p, grid, st); break;
+      case STRATA_HIP_ACT_GELU_ERF: launch_dma_act<STRATA_HIP_ACT_GELU_ERF>(p, grid, st); break;
+      case STRATA_HIP_ACT_SIGMOID: launch_dma_act<STRATA_HIP_ACT_SIGMOID>(p, grid, st); break;
+      default: launch_dma_act<STRATA_HIP_ACT_NONE>(p, grid, st); break;
+    }
     return check_launch("gemm_dma_kernel");
   }
   return launch_gemm<128, 128, 2, 2>(p, st);
