@@ -618,8 +618,8 @@ struct StripTile {
 // Rare path of the strip kernel: recompute one 4x4 tile of queries exactly,
 // straight from global memory, with a running maximum (fp32 online softmax).
 // Called by a whole wave when the tile's unnormalised sums left the range
-// the fast path guarantees (a score far above the query's own-key score, or
-// non-finite inputs).  Lane l handles query l >> 2 (row-major in the tile)
+// the fast path guarantees (scores far from 0 in log2 units, or non-finite
+// inputs).  Lane l handles query l >> 2 (row-major in the tile)
 // and the head-dim quarter l & 3 (16 values); invalid queries (past the
 // chunk's last row or column) compute a clamped copy and store nothing.
 __device__ __forceinline__ void na3d_strip_tile_exact(const Na3dParams* pp, StripTile t) {
@@ -1098,7 +1098,7 @@ __global__ __launch_bounds__(256, 2) void na3d_strip_kernel(Na3dParams p, Na3dSt
 
 
 // ---------------------------------------------------------------------------
-// Strip kernel, fixed-reference instance for regular strips
+// Strip kernel, reference-free instance for regular strips
 // ---------------------------------------------------------------------------
 // Regular strip: ky = 13, 4x4 tiles, four key rows per group, and no query row
 // of the chunk with a clamped y window (the host checks; configs like
@@ -1113,16 +1113,17 @@ __global__ __launch_bounds__(256, 2) void na3d_strip_kernel(Na3dParams p, Na3dSt
 // compute only the slots holding a tile; the ramp-down groups compute every
 // slot and the emptied ones are discarded.
 //
-// The softmax reference is fixed per tile: m = (own-key score) + SLACK, in
-// log2 units, so the stage loop has no running maximum and no rescaling.  A
-// score s has p = 2^(s - m), the own key p = 2^-SLACK; keys more than
-// 126 - SLACK below the own key underflow (relative weight below 2^-30 each).
-// The sums stay finite while no score exceeds the own-key score by more than
-// about SLACK + 40 - log2|W|; the row sum is checked when the tile finishes
-// (above 2^40, infinite or NaN) and such tiles are recomputed exactly after
-// the strip by na3d_strip_tile_exact.  2^40 also keeps sum(p * v) finite for
-// |v| < 2^88.  (gfx950's v_dot2c_f32_bf16 does not keep an fp32 sum: the row
-// sums stay on the ones-operand MFMA.)
+// No softmax reference: a score s (log2 units) has p = 2^s directly, so the
+// stage loop has no maximum, no rescaling and no per-tile bias, and the QK
+// MFMA starts from the x bias (0 or -inf per key) shared by all slots.  The
+// normalisation cancels any common factor of p, so this is exact while p, the
+// row sum l and sum(p * v) stay finite and normal: the tile is checked when it
+// finishes (l outside [2^-100, inf), NaN, or a non-finite output sum) and such
+// tiles are recomputed exactly after the strip by na3d_strip_tile_exact.  Every
+// query with its largest score in about [-100, 118] passes; keys more than
+// ~26 log2 units below 2^-100 underflow (relative weight below 2^-26 each).
+// (gfx950's v_dot2c_f32_bf16 does not keep an fp32 sum: the row sums stay on
+// the ones-operand MFMA.)
 template <int D, int TX, int RPS, int NBUF>
 __device__ __forceinline__ void na3d_strip_fast_body(const Na3dParams p, const Na3dStrips sg) {
 #if defined(__HIP_DEVICE_COMPILE__)
@@ -1142,11 +1143,11 @@ __device__ __forceinline__ void na3d_strip_fast_body(const Na3dParams p, const N
   constexpr int KS = D / 32;              // k-steps of the QK MFMA; also 1-KiB loads per wave for 16 query rows
   constexpr int DB = D / 16;
   constexpr int QWB = 16 * D * 2;         // one wave's 16 rows of Q (or of self keys), bytes
-  constexpr int QTB = NWX * 2 * QWB;      // Q and self keys of one tile row of the workgroup
+  constexpr int QTB = NWX * QWB;          // Q of one tile row of the workgroup
   constexpr int RING_B = NBUF * STAGE_B;
   constexpr int KY = 13, KR = KY / 2;     // window rows and radius in y
-  constexpr float SLACK = 96.f;
-  constexpr uint32_t LMAX_BITS = (127u + 40u) << 23;  // 2^40 as an fp32 bit pattern
+  constexpr uint32_t LMIN_BITS = (127u - 100u) << 23;  // 2^-100 as an fp32 bit pattern
+  constexpr uint32_t INF_BITS = 0x7f800000u;
   static_assert(TX == 4 && TY == 4 && RPS == 4 && TY + KY - 1 == NS * RPS, "regular strip geometry");
   static_assert(RKB == NWX && LPT == 2 * RPS, "stage layout: wave w loads the w-th KiB of every row");
   static_assert(QWB == KS * 1024, "16 query rows are KS 1-KiB loads");
@@ -1228,27 +1229,23 @@ __device__ __forceinline__ void na3d_strip_fast_body(const Na3dParams p, const N
   // ---- Q and self-key copies: one (batch, z, head) slice, 31-bit offsets ----
   const u32x4 rq = make_rsrc((const char*)p.q + 2 * ((int64_t)b * p.qs[0] + (int64_t)rz * p.qs[1] + (int64_t)h * p.qs[4]),
                              0x7fffffffu);
-  const u32x4 rks = make_rsrc((const char*)p.k + 2 * ((int64_t)b * p.ks[0] + (int64_t)rz * p.ks[1] + (int64_t)h * p.ks[4]),
-                              0x7fffffffu);
-  const uint32_t qs2 = (uint32_t)(2 * dy * p.qs[2]), ks2 = (uint32_t)(2 * dy * p.ks[2]);
-  uint32_t qxo[KS], kxo[KS];
+  const uint32_t qs2 = (uint32_t)(2 * dy * p.qs[2]);
+  uint32_t qxo[KS];
 #pragma unroll
   for (int i = 0; i < KS; ++i) {
     const int n = lane / CPK + i * (64 / CPK);
     const int rx = gx + dx * min(xw0 + n % TX, qx1 - 1);
     qxo[i] = (uint32_t)((int64_t)rx * p.qs[3] * 2 + (int64_t)gy * p.qs[2] * 2) + 16 * (lane % CPK);
-    kxo[i] = (uint32_t)((int64_t)rx * p.ks[3] * 2 + (int64_t)gy * p.ks[2] * 2) + 16 * (lane % CPK);
   }
-  // Copy Q and the self keys of tile j (this wave's 16 queries) to LDS at `off`.
+  // Copy Q of tile j (this wave's 16 queries) to LDS at `off`.
   auto dma_q = [&](int j, uint32_t off) {
     const int yt0 = ys + TY * j;
-    const uint32_t m0 = lds_base + off + (uint32_t)wave * 2 * QWB;
+    const uint32_t m0 = lds_base + off + (uint32_t)wave * QWB;
 #pragma unroll
     for (int i = 0; i < KS; ++i) {
       const int n = lane / CPK + i * (64 / CPK);
       const uint32_t qy = (uint32_t)min(yt0 + n / TX, ye - 1);
       dma_row16(rq, m0 + i * 1024, qxo[i] + qy * qs2);
-      dma_row16(rks, m0 + QWB + i * 1024, kxo[i] + qy * ks2);
     }
   };
   // ---- output: one (batch, z, head) slice ----
@@ -1276,32 +1273,23 @@ __device__ __forceinline__ void na3d_strip_fast_body(const Na3dParams p, const N
   bf16x8 qreg[NS][KS];
   f32x4 oacc[NS][DB];
   f32x4 lacc[NS];  // row sums (ones x P^T: every row of a column holds the column's sum)
-  f32x4 nb[NS];    // x bias - reference: the C operand of the QK MFMA
+  f32x4 xbias;     // 0 or -inf per key (x window): the C operand of every QK MFMA
+#pragma unroll
+  for (int i = 0; i < 4; ++i) xbias[i] = ((xmask >> i) & 1) ? -INFINITY : 0.f;
   typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
   bf16x8_t ones = {(bf16)1.f, (bf16)1.f, (bf16)1.f, (bf16)1.f, (bf16)1.f, (bf16)1.f, (bf16)1.f, (bf16)1.f};
   const bool ylo[3] = {trow > 0, trow > 1, trow > 2};  // first group: rows 0..2 masked for later query rows
   const bool yhi[3] = {trow < 1, trow < 2, trow < 3};  // last group: rows 1..3 masked for earlier query rows
 
-  // Tile j enters slot k: Q (pre-scaled) and its score against its own key from LDS.
+  // Tile j enters slot k: Q from LDS, pre-scaled to log2 units.
   auto start_tile = [&](int k, uint32_t off) {
-    const char* qb = lds + off + wave * 2 * QWB;
-    bf16x8 kself[KS];
+    const char* qb = lds + off + wave * QWB;
 #pragma unroll
     for (int ks = 0; ks < KS; ++ks) {
       qreg[k][ks] = *(const bf16x8*)(qb + n16 * D * 2 + (4 * ks + g) * 16);
-      kself[ks] = *(const bf16x8*)(qb + QWB + n16 * D * 2 + (4 * ks + g) * 16);
+#pragma unroll
+      for (int e = 0; e < 8; ++e) qreg[k][ks][e] = (bf16)((float)qreg[k][ks][e] * c2);
     }
-    float d = 0.f;
-#pragma unroll
-    for (int ks = 0; ks < KS; ++ks)
-#pragma unroll
-      for (int e = 0; e < 8; ++e) {
-        qreg[k][ks][e] = (bf16)((float)qreg[k][ks][e] * c2);
-        d = fmaf((float)qreg[k][ks][e], (float)kself[ks][e], d);
-      }
-    const float mref = colsum(d) + SLACK;
-#pragma unroll
-    for (int i = 0; i < 4; ++i) nb[k][i] = ((xmask >> i) & 1) ? -INFINITY : -mref;
 #pragma unroll
     for (int db = 0; db < DB; ++db) oacc[k][db] = (f32x4){0.f, 0.f, 0.f, 0.f};
     lacc[k] = (f32x4){0.f, 0.f, 0.f, 0.f};
@@ -1309,6 +1297,10 @@ __device__ __forceinline__ void na3d_strip_fast_body(const Na3dParams p, const N
   // Normalise and store tile j from slot k; true if the tile needs the exact path.
   auto finish_tile = [&](int k, int j) {
     const float l = lacc[k][0];
+    float osum = 0.f;  // infinite or NaN if any output is
+#pragma unroll
+    for (int db = 0; db < DB; ++db)
+      osum += fabsf(oacc[k][db][0]) + fabsf(oacc[k][db][1]) + fabsf(oacc[k][db][2]) + fabsf(oacc[k][db][3]);
     const int qy = ys + TY * j + trow;
     const bool valid = qy < ye && qx < qx1;
     if (valid) {
@@ -1321,8 +1313,9 @@ __device__ __forceinline__ void na3d_strip_fast_body(const Na3dParams p, const N
         *(u32x2*)(op + 32 * db) = w;
       }
     }
-    // row sum above 2^40, infinite or NaN (never negative: compare the bits)
-    return __builtin_amdgcn_ballot_w64(valid && __float_as_uint(l) > LMAX_BITS) != 0;
+    // l in [2^-100, inf) and a finite output sum (l is never negative: compare the bits)
+    const bool ok = __float_as_uint(l) - LMIN_BITS < INF_BITS - LMIN_BITS && __float_as_uint(osum) < INF_BITS;
+    return __builtin_amdgcn_ballot_w64(valid && !ok) != 0;
   };
 
   // One stage's tile math for every slot.  C: slot of the tile in its first group.
@@ -1337,7 +1330,7 @@ __device__ __forceinline__ void na3d_strip_fast_body(const Na3dParams p, const N
       f32x4 sacc[RPS];
 #pragma unroll
       for (int r = 0; r < RPS; ++r) {
-        sacc[r] = nb[k];
+        sacc[r] = xbias;
 #pragma unroll
         for (int ks = 0; ks < KS; ++ks)
           sacc[r] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ak[r][ks], qreg[k][ks], sacc[r], 0, 0, 0);
@@ -1478,8 +1471,8 @@ __device__ __forceinline__ void na3d_strip_fast_body(const Na3dParams p, const N
   }
   wait_vmcnt(0);  // the ring's trailing (empty) stages
 
-  // Rare: tiles whose sums left the fixed reference's range, recomputed
-  // exactly after the strip (their stores above are overwritten).
+  // Rare: tiles whose sums left the range the reference-free softmax keeps
+  // exact, recomputed after the strip (their stores above are overwritten).
   if (bad_tiles != 0 || bad_high) {
     __builtin_amdgcn_s_waitcnt(0);
     for (int j = 0; j < NT; ++j)

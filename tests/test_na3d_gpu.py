@@ -213,9 +213,9 @@ def test_regular_strip_chunks(gpu):
 
 
 def test_regular_strip_score_far_above_own_key(gpu):
-    """A key scoring ~160 (log2 units) above a query's own-key score overflows
-    the fixed softmax reference of the fast strip kernel; that tile must be
-    recomputed exactly (its output is then the dominant key's value)."""
+    """A key scoring ~160 (log2 units) overflows the reference-free softmax of
+    the fast strip kernel (2^s above fp32 range); that tile must be recomputed
+    exactly (its output is then the dominant key's value)."""
     shape = (1, 3, 20, 28, 1, 64)
     q, k, v = (t.float() for t in _rand(shape, 8, torch.bfloat16, "cpu"))
     u = torch.zeros(64)
@@ -234,3 +234,39 @@ def test_regular_strip_score_far_above_own_key(gpu):
     assert rel_l2(out.float(), ref) <= BF16_TOL
     got = out[0, 1, 3, 4, 0].float().cpu()
     assert rel_l2(got, v[0, 2, 12, 14, 0].float()) <= BF16_TOL
+
+
+def test_regular_strip_all_scores_far_below_zero(gpu):
+    """Every key of one query scores ~-160 (log2 units): 2^s underflows, the row
+    sum falls below the fast path's range and the tile is recomputed exactly
+    (a near-uniform average over the window, as the fp32 oracle computes)."""
+    shape = (1, 3, 20, 28, 1, 64)
+    q, k, v = (t.float() for t in _rand(shape, 9, torch.bfloat16, "cpu"))
+    u = torch.zeros(64)
+    u[:32] = 1.0 / 32**0.5
+    k = k * 0.1 + 30.0 * u  # every key along u (plus a little noise)
+    q[0, 1, 9, 10, 0] = -30.0 * u
+    q, k, v = (t.bfloat16() for t in (q, k, v))
+    out = _run(q.to(gpu), k.to(gpu), v.to(gpu), (3, 13, 13), origin=(0, 6, 6), extent=(3, 8, 16))
+    ref = O.na3d(q, k, v, (3, 13, 13), q_origin=(0, 6, 6), q_extent=(3, 8, 16))
+    assert torch.isfinite(out.float()).all()
+    assert rel_l2(out.float(), ref) <= BF16_TOL
+    assert rel_l2(out[0, 1, 3, 4, 0].float().cpu(), ref[0, 1, 3, 4, 0]) <= BF16_TOL
+
+
+def test_regular_strip_large_scores_in_range(gpu):
+    """Scores of ~70 log2 units stay inside the fast path's range (2^70 and the
+    sums are finite) and must come out exact without the fallback's help."""
+    shape = (1, 3, 20, 28, 2, 64)
+    q, k, v = (t.float() for t in _rand(shape, 10, torch.bfloat16, "cpu"))
+    u = torch.zeros(64)
+    u[:32] = 1.0 / 32**0.5
+    q[0, 1, 9, 10, 1] = 20.0 * u
+    k[0, 2, 12, 14, 1] = 20.0 * u  # 400 / 8 nats ~ 72 log2 units
+    k[0, 1, 7, 8, 1] = 19.0 * u    # ~69 log2 units: a second, smaller weight
+    q, k, v = (t.bfloat16() for t in (q, k, v))
+    out = _run(q.to(gpu), k.to(gpu), v.to(gpu), (3, 13, 13), origin=(0, 6, 6), extent=(3, 8, 16))
+    ref = O.na3d(q, k, v, (3, 13, 13), q_origin=(0, 6, 6), q_extent=(3, 8, 16))
+    assert torch.isfinite(out.float()).all()
+    assert rel_l2(out.float(), ref) <= BF16_TOL
+    assert rel_l2(out[0, 1, 3, 4, 1].float().cpu(), ref[0, 1, 3, 4, 1]) <= BF16_TOL
