@@ -2,7 +2,8 @@
  * strata_hip.h — C ABI of the MI355X (gfx950) kernels for the Strata
  * transformer block's hot path: 3D neighbourhood attention (NA3D), the
  * stereographic-RoPE + QKV-pack prologue, the bias/GELU/residual GEMM and the
- * non-affine LayerNorm.
+ * non-affine LayerNorm; around it, the cube-sphere halo fill and the rollout
+ * step's state normalisation / patchify and state update.
  *
  * Conventions shared by every entry point
  *   - All pointers are device pointers owned by the caller.  The library never
@@ -25,7 +26,7 @@
 extern "C" {
 #endif
 
-#define STRATA_HIP_ABI_VERSION 2
+#define STRATA_HIP_ABI_VERSION 3
 
 enum strata_hip_status {
   STRATA_HIP_OK = 0,
@@ -226,6 +227,70 @@ typedef struct strata_hip_cube_crop_args {
 } strata_hip_cube_crop_args;
 
 int strata_hip_cube_crop(const strata_hip_cube_crop_args* args, void* stream);
+
+/* ---------------------------------------------------------------------------
+ * Pipeline step, input side: the input normalisation of the model state
+ * (RunningNorm2d.forward, screamcast/normalization.py:109-123, applied by
+ * MixedPredictionAsymmetric.forward_from_flat, screamcast/model_pipelines.py:210-211)
+ * fused with the patchify of a Conv3d(kernel = stride = patch) patch embedding:
+ *   tok[b, t, e] = bf16((state[b, c, pz*tz + dz, py*ty + dy, px*tx + dx] - mean[c]) / std[c]),
+ *                  0 where that state value is not finite,
+ * token t = (tz, ty, tx) row-major over the token grid, element
+ * e = ((c*pz + dz)*py + dy)*px + dx: the order of a Conv3d weight [E, C, pz, py, px]
+ * flattened, so tok @ weight.reshape(E, -1)^T + bias is the patch embedding of
+ * the normalised state.  std[c] = sqrt(var[c]) + eps, computed by the caller in
+ * fp32 as normalization.py:117 does; mean and std NULL: no normalisation.
+ * state: fp32 [B, C, Z, Y, X] contiguous; tok: bf16 [B, Z/pz, Y/py, X/px, C*pz*py*px]
+ * contiguous; each grid size a multiple of its patch size.
+ * ------------------------------------------------------------------------- */
+typedef struct strata_hip_state_patchify_args {
+  const float* state;
+  void* tokens;
+  const float* mean; /* [C] or NULL */
+  const float* std;  /* [C] or NULL (with mean) */
+  int32_t batch;
+  int32_t channels;  /* C */
+  int32_t grid[3];   /* Z, Y, X of the state */
+  int32_t patch[3];  /* pz, py, px */
+} strata_hip_state_patchify_args;
+
+int strata_hip_state_patchify(const strata_hip_state_patchify_args* args, void* stream);
+
+/* ---------------------------------------------------------------------------
+ * Pipeline step, output side: unpatchify of the prediction tokens, the target
+ * denormalisation (RunningNorm2d.denormalize, screamcast/normalization.py:102-107)
+ * and the prognostic state update of MixedPredictionAsymmetric.step
+ * (screamcast/model_pipelines.py:631-662, _process_mixed_statediff_predictions :664-676):
+ *   d = bf16(pred * std[c] + mean[c])            (fp32 multiply, then add, then bf16)
+ *   next[b, c, z, y, x] = d + state[b, src[c], z, y, x]   src[c] >= 0: difference prediction
+ *                       = d                               src[c] <  0: state prediction
+ *   then max(next, clamp_min[c]) where clamp_min[c] is not NaN (the qv floor, :652-658).
+ * pred: bf16 [B, Z/pz, Y/py, X/px, C*pz*py*px] contiguous, element order
+ *   order 0: ((c*pz + dz)*py + dy)*px + dx   (Conv3d / ConvTranspose3d weight order)
+ *   order 1: ((dz*py + dy)*px + dx)*C + c     (patch-major, channels last)
+ * state: fp32 [B, Cin, Z, Y, X] contiguous; next: fp32 [B, C, Z, Y, X] contiguous.
+ * NULL tables: mean 0, std 1, src[c] = c (every channel a difference), no clamp.
+ * src[c] outside [0, Cin) adds nothing; state may be NULL with state_channels 0
+ * (every channel a state prediction).  next may alias state only when every
+ * src[c] is c or negative.
+ * ------------------------------------------------------------------------- */
+typedef struct strata_hip_state_update_args {
+  const void* pred;
+  const float* state;
+  float* next;
+  const float* mean;          /* [C] or NULL */
+  const float* std;           /* [C] or NULL */
+  const int32_t* src_channel; /* [C] or NULL */
+  const float* clamp_min;     /* [C] or NULL */
+  int32_t batch;
+  int32_t channels;           /* C of pred and next */
+  int32_t state_channels;     /* Cin of state */
+  int32_t order;              /* 0 or 1, see above */
+  int32_t grid[3];            /* Z, Y, X of the state */
+  int32_t patch[3];           /* pz, py, px */
+} strata_hip_state_update_args;
+
+int strata_hip_state_update(const strata_hip_state_update_args* args, void* stream);
 
 /* Library bookkeeping (no counterpart in the reference). */
 const char* strata_hip_last_error(void);

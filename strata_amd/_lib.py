@@ -14,7 +14,7 @@ from pathlib import Path
 
 LIB_PATH = Path(__file__).resolve().parent / "libstrata_hip.so"
 
-ABI_VERSION = 2
+ABI_VERSION = 3
 
 OK = 0
 EINVAL = -1
@@ -143,6 +143,37 @@ class CubeCropArgs(ctypes.Structure):
     ]
 
 
+class StatePatchifyArgs(ctypes.Structure):
+    _fields_ = [
+        ("state", ctypes.c_void_p),
+        ("tokens", ctypes.c_void_p),
+        ("mean", ctypes.c_void_p),
+        ("std", ctypes.c_void_p),
+        ("batch", ctypes.c_int32),
+        ("channels", ctypes.c_int32),
+        ("grid", ctypes.c_int32 * 3),
+        ("patch", ctypes.c_int32 * 3),
+    ]
+
+
+class StateUpdateArgs(ctypes.Structure):
+    _fields_ = [
+        ("pred", ctypes.c_void_p),
+        ("state", ctypes.c_void_p),
+        ("next", ctypes.c_void_p),
+        ("mean", ctypes.c_void_p),
+        ("std", ctypes.c_void_p),
+        ("src_channel", ctypes.c_void_p),
+        ("clamp_min", ctypes.c_void_p),
+        ("batch", ctypes.c_int32),
+        ("channels", ctypes.c_int32),
+        ("state_channels", ctypes.c_int32),
+        ("order", ctypes.c_int32),
+        ("grid", ctypes.c_int32 * 3),
+        ("patch", ctypes.c_int32 * 3),
+    ]
+
+
 EXPORTS = {
     "strata_hip_na3d_fwd": ([ctypes.POINTER(Na3dArgs), ctypes.c_void_p], ctypes.c_int),
     "strata_hip_rope_qkv_pack": ([ctypes.POINTER(RopePackArgs), ctypes.c_void_p], ctypes.c_int),
@@ -150,6 +181,8 @@ EXPORTS = {
     "strata_hip_layer_norm": ([ctypes.POINTER(LayerNormArgs), ctypes.c_void_p], ctypes.c_int),
     "strata_hip_cube_pad_faces": ([ctypes.POINTER(CubePadArgs), ctypes.c_void_p], ctypes.c_int),
     "strata_hip_cube_crop": ([ctypes.POINTER(CubeCropArgs), ctypes.c_void_p], ctypes.c_int),
+    "strata_hip_state_patchify": ([ctypes.POINTER(StatePatchifyArgs), ctypes.c_void_p], ctypes.c_int),
+    "strata_hip_state_update": ([ctypes.POINTER(StateUpdateArgs), ctypes.c_void_p], ctypes.c_int),
     "strata_hip_last_error": ([], ctypes.c_char_p),
     "strata_hip_abi_version": ([], ctypes.c_int),
 }

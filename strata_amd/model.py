@@ -12,16 +12,21 @@ stand-in below keeps the hot path — the blocks — identical to the drop-in
     stage 2 depth2 x StrataBlock(dim2, heads2, kernel2)
     head    LayerNorm + Linear(dim2 -> 8*Cin) + depth-to-space -> [B, Cin, Z, Y, X]
 
-``rollout`` applies ``x <- x + model(x)`` for ``steps`` autoregressive steps
-(state plus predicted tendency).  All matmuls, LayerNorms, RoPE packs and
-NA3D calls run in the HIP library; the space/depth permutes and the state
-update are torch data movement.
+``step`` is one step of the pipeline (MixedPredictionAsymmetric.step,
+screamcast/model_pipelines.py:631-662) on an fp32 state: the input
+normalisation and the per-voxel patchify run as one HIP kernel
+(``state_patchify``), the head's tokens go back through one HIP kernel that
+un-patchifies (2x2x2, channels last), denormalises and adds the state
+(``state_update``).  With no ``StepNorms`` the tables are identities and the
+step is ``x <- x + bf16(model(x))``.  ``rollout`` repeats ``step``.  All
+matmuls, LayerNorms, RoPE packs and NA3D calls run in the HIP library; the
+2x2x2 merge permute is torch data movement.
 """
 
 from __future__ import annotations
 
 import math
-from typing import Sequence
+from typing import Optional, Sequence
 
 import torch
 import torch.nn as nn
@@ -30,6 +35,7 @@ from torch import Tensor
 from . import _lib, ops
 from . import rope as R
 from .modules import StrataBlock
+from .pipeline import StepNorms
 
 
 def space_to_depth(x: Tensor) -> Tensor:
@@ -85,9 +91,10 @@ class TwoStageStrata(nn.Module):
         t2 = R.stereographic_rope_tables(lat2, lon2, self.head_dims[1], base, R.default_rope_length_scale(2))
         return t1, t2
 
-    def forward(self, x: Tensor, rope1: tuple[Tensor, Tensor], rope2: tuple[Tensor, Tensor]) -> Tensor:
-        h = x.permute(0, 2, 3, 4, 1).contiguous()
-        h = ops.gemm_bias_act(h, self.embed.weight, self.embed.bias, None, _lib.ACT_NONE)
+    def network(self, tokens: Tensor, rope1: tuple[Tensor, Tensor], rope2: tuple[Tensor, Tensor]) -> Tensor:
+        """Input tokens ``[B, Z, Y, X, Cin]`` (bf16) -> head tokens ``[B, Z/2, Y/2, X/2, 8*Cin]``,
+        each the 2x2x2 cell's outputs in (dz, dy, dx, c) order."""
+        h = ops.gemm_bias_act(tokens, self.embed.weight, self.embed.bias, None, _lib.ACT_NONE)
         for blk in self.stage1:
             h = blk(h, rope1)
         h = space_to_depth(h).contiguous()
@@ -95,14 +102,29 @@ class TwoStageStrata(nn.Module):
         for blk in self.stage2:
             h = blk(h, rope2)
         h = ops.layer_norm(h, 1e-6)
-        h = ops.gemm_bias_act(h, self.head.weight, self.head.bias, None, _lib.ACT_NONE)
+        return ops.gemm_bias_act(h, self.head.weight, self.head.bias, None, _lib.ACT_NONE)
+
+    def forward(self, x: Tensor, rope1: tuple[Tensor, Tensor], rope2: tuple[Tensor, Tensor]) -> Tensor:
+        """The tendency ``[B, Cin, Z, Y, X]`` of a bf16 input state."""
+        h = self.network(x.permute(0, 2, 3, 4, 1).to(torch.bfloat16).contiguous(), rope1, rope2)
         return depth_to_space(h, self.in_channels).permute(0, 4, 1, 2, 3)
 
     @torch.no_grad()
-    def rollout(self, x: Tensor, steps: int, rope1, rope2) -> Tensor:
+    def step(self, state: Tensor, rope1, rope2, norms: Optional[StepNorms] = None) -> Tensor:
+        """One pipeline step on an fp32 state ``[B, Cin, Z, Y, X]``: next fp32 state."""
+        n = norms or StepNorms()
+        tok = ops.state_patchify(state.float(), n.in_mean, n.in_std, (1, 1, 1))
+        h = self.network(tok, rope1, rope2)
+        return ops.state_update(h, state.float(), n.tgt_mean, n.tgt_std, n.src_channel, n.clamp_min,
+                                tuple(state.shape[2:]), (2, 2, 2), 1)
+
+    @torch.no_grad()
+    def rollout(self, x: Tensor, steps: int, rope1, rope2, norms: Optional[StepNorms] = None) -> Tensor:
+        """``steps`` pipeline steps from ``x``; the fp32 state after the last."""
+        state = x.float()
         for _ in range(steps):
-            x = x + self(x, rope1, rope2)
-        return x
+            state = self.step(state, rope1, rope2, norms)
+        return state
 
     def step_flops(self, batch: int, grid: Sequence[int]) -> float:
         """Block FLOPs of one step (GEMMs 24*M*C^2 per block + NA3D 4*M*|W|*C)."""

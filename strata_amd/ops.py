@@ -18,7 +18,16 @@ from torch import Tensor
 
 from . import _lib
 
-__all__ = ["na3d_fwd", "rope_qkv_pack", "gemm_bias_act", "layer_norm", "cube_pad_faces", "cube_crop"]
+__all__ = [
+    "na3d_fwd",
+    "rope_qkv_pack",
+    "gemm_bias_act",
+    "layer_norm",
+    "cube_pad_faces",
+    "cube_crop",
+    "state_patchify",
+    "state_update",
+]
 
 
 def _stream(t: Tensor) -> int:
@@ -402,3 +411,144 @@ def _(x, halo):
 
 
 cube_crop.register_autograd(_no_backward("strata_hip::cube_crop"))
+
+
+# ---------------------------------------------------------------------------
+# Rollout step: state normalisation + patchify, and the state update
+# ---------------------------------------------------------------------------
+def _state_tables(name: str, dev: torch.device, C: int, **tabs: Optional[Tensor]) -> dict:
+    out = {}
+    for key, t in tabs.items():
+        if t is None:
+            out[key] = None
+            continue
+        want = torch.int32 if key == "src_channel" else torch.float32
+        if t.dim() != 1 or t.shape[0] != C:
+            raise ValueError(f"{name}: {key} must have shape [{C}], got {tuple(t.shape)}")
+        out[key] = t.to(device=dev, dtype=want).contiguous()
+    return out
+
+
+@torch.library.custom_op("strata_hip::state_patchify", mutates_args=())
+def state_patchify(
+    state: Tensor, mean: Optional[Tensor], std: Optional[Tensor], patch: Sequence[int]
+) -> Tensor:
+    """fp32 state ``[B, C, Z, Y, X]`` -> bf16 tokens ``[B, Z/pz, Y/py, X/px, C*pz*py*px]``:
+    ``(state - mean[c]) / std[c]`` with non-finite values set to 0
+    (RunningNorm2d.forward, screamcast/normalization.py:109-123; ``std = sqrt(var) + eps``),
+    patchified in Conv3d weight order (c, dz, dy, dx), so ``tokens @
+    conv.weight.reshape(E, -1).T + conv.bias`` is ``Conv3d(kernel=stride=patch)``.
+    ``mean``/``std`` None: no normalisation."""
+    name = "state_patchify"
+    dev = _require_gpu(name, state)
+    if state.dtype != torch.float32 or state.dim() != 5:
+        raise ValueError(f"{name}: state must be float32 [B, C, Z, Y, X], got {state.dtype} {tuple(state.shape)}")
+    if (mean is None) != (std is None):
+        raise ValueError(f"{name}: give both mean and std, or neither")
+    pz, py, px = _triple("patch", patch)
+    B, C, Z, Y, X = state.shape
+    if min(pz, py, px) <= 0 or Z % pz or Y % py or X % px:
+        raise ValueError(f"{name}: grid {(Z, Y, X)} is not a multiple of patch {(pz, py, px)}")
+    tabs = _state_tables(name, dev, C, mean=mean, std=std)
+    src = state.contiguous()
+    out = torch.empty((B, Z // pz, Y // py, X // px, C * pz * py * px), dtype=torch.bfloat16, device=dev)
+    if out.numel() == 0:
+        return out
+    a = _lib.StatePatchifyArgs()
+    a.state, a.tokens = src.data_ptr(), out.data_ptr()
+    a.mean = tabs["mean"].data_ptr() if tabs["mean"] is not None else None
+    a.std = tabs["std"].data_ptr() if tabs["std"] is not None else None
+    a.batch, a.channels = B, C
+    a.grid[:] = [Z, Y, X]
+    a.patch[:] = [pz, py, px]
+    with torch.cuda.device(dev):
+        _lib.call("strata_hip_state_patchify", a, _stream(state))
+    return out
+
+
+@state_patchify.register_fake
+def _(state, mean, std, patch):
+    pz, py, px = _triple("patch", patch)
+    B, C, Z, Y, X = state.shape
+    return state.new_empty((B, Z // pz, Y // py, X // px, C * pz * py * px), dtype=torch.bfloat16)
+
+
+state_patchify.register_autograd(_no_backward("strata_hip::state_patchify"))
+
+
+@torch.library.custom_op("strata_hip::state_update", mutates_args=())
+def state_update(
+    pred: Tensor,
+    state: Optional[Tensor],
+    mean: Optional[Tensor],
+    std: Optional[Tensor],
+    src_channel: Optional[Tensor],
+    clamp_min: Optional[Tensor],
+    grid: Sequence[int],
+    patch: Sequence[int],
+    order: int,
+) -> Tensor:
+    """bf16 prediction tokens ``[B, Z/pz, Y/py, X/px, C*pz*py*px]`` -> fp32 next state
+    ``[B, C, Z, Y, X]``: ``d = bf16(pred * std[c] + mean[c])`` (RunningNorm2d.denormalize,
+    screamcast/normalization.py:102-107), ``next = d + state[:, src_channel[c]]`` for
+    difference-predicted channels (``src_channel[c] >= 0``) and ``d`` for state-predicted
+    ones, then ``max(next, clamp_min[c])`` where ``clamp_min[c]`` is not NaN
+    (MixedPredictionAsymmetric.step, screamcast/model_pipelines.py:631-676).
+    ``order`` 0: token elements (c, dz, dy, dx); 1: (dz, dy, dx, c).  None tables:
+    mean 0, std 1, ``src_channel[c] = c``, no clamp."""
+    name = "state_update"
+    dev = _require_gpu(name, pred, state)
+    if pred.dtype != torch.bfloat16 or pred.dim() != 5:
+        raise ValueError(f"{name}: pred must be bfloat16 [B, Tz, Ty, Tx, K], got {pred.dtype} {tuple(pred.shape)}")
+    if (mean is None) != (std is None):
+        raise ValueError(f"{name}: give both mean and std, or neither")
+    if order not in (0, 1):
+        raise ValueError(f"{name}: order must be 0 or 1")
+    Z, Y, X = _triple("grid", grid)
+    pz, py, px = _triple("patch", patch)
+    if min(pz, py, px) <= 0 or Z % pz or Y % py or X % px:
+        raise ValueError(f"{name}: grid {(Z, Y, X)} is not a multiple of patch {(pz, py, px)}")
+    B = pred.shape[0]
+    P = pz * py * px
+    if tuple(pred.shape[1:4]) != (Z // pz, Y // py, X // px) or pred.shape[4] % P:
+        raise ValueError(f"{name}: pred {tuple(pred.shape)} does not match grid {(Z, Y, X)} / patch {(pz, py, px)}")
+    C = pred.shape[4] // P
+    Cin = 0
+    if state is not None:
+        if state.dtype != torch.float32 or state.dim() != 5 or state.shape[0] != B or tuple(state.shape[2:]) != (Z, Y, X):
+            raise ValueError(f"{name}: state must be float32 [{B}, Cin, {Z}, {Y}, {X}], got {tuple(state.shape)}")
+        Cin = state.shape[1]
+    tabs = _state_tables(name, dev, C, mean=mean, std=std, src_channel=src_channel, clamp_min=clamp_min)
+    if tabs["src_channel"] is not None:
+        # checked when the table lives on the host (a device table is not read
+        # back: the kernel adds nothing for entries outside [0, Cin))
+        if src_channel.device.type == "cpu" and bool((src_channel >= Cin).any()):
+            raise ValueError(f"{name}: src_channel entries must be < {Cin} (negative: state prediction)")
+    elif Cin < C:
+        raise ValueError(f"{name}: without src_channel the state needs at least {C} channels")
+    pr = pred.contiguous()
+    st = state.contiguous() if state is not None else None
+    out = torch.empty((B, C, Z, Y, X), dtype=torch.float32, device=dev)
+    if out.numel() == 0:
+        return out
+    a = _lib.StateUpdateArgs()
+    a.pred, a.next = pr.data_ptr(), out.data_ptr()
+    a.state = st.data_ptr() if st is not None else None
+    for key in ("mean", "std", "src_channel", "clamp_min"):
+        setattr(a, key, tabs[key].data_ptr() if tabs[key] is not None else None)
+    a.batch, a.channels, a.state_channels, a.order = B, C, Cin, int(order)
+    a.grid[:] = [Z, Y, X]
+    a.patch[:] = [pz, py, px]
+    with torch.cuda.device(dev):
+        _lib.call("strata_hip_state_update", a, _stream(pred))
+    return out
+
+
+@state_update.register_fake
+def _(pred, state, mean, std, src_channel, clamp_min, grid, patch, order):
+    Z, Y, X = _triple("grid", grid)
+    P = math.prod(_triple("patch", patch))
+    return pred.new_empty((pred.shape[0], pred.shape[4] // P, Z, Y, X), dtype=torch.float32)
+
+
+state_update.register_autograd(_no_backward("strata_hip::state_update"))

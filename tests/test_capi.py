@@ -21,6 +21,8 @@ STRUCTS = {
     "strata_hip_layer_norm_args": _lib.LayerNormArgs,
     "strata_hip_cube_pad_args": _lib.CubePadArgs,
     "strata_hip_cube_crop_args": _lib.CubeCropArgs,
+    "strata_hip_state_patchify_args": _lib.StatePatchifyArgs,
+    "strata_hip_state_update_args": _lib.StateUpdateArgs,
 }
 
 
@@ -161,3 +163,34 @@ def test_cube_validation(lib):
     assert "2*halo" in lib.strata_hip_last_error().decode()
     c.planes, c.halo = 0, 1
     assert lib.strata_hip_cube_crop(ctypes.byref(c), None) == _lib.OK
+
+
+def test_state_step_validation(lib):
+    a = _lib.StatePatchifyArgs()
+    a.state, a.tokens, a.batch, a.channels = 0x1000, 0x2000, 1, 4
+    a.grid[:] = [4, 8, 8]
+    a.patch[:] = [1, 3, 2]
+    assert lib.strata_hip_state_patchify(ctypes.byref(a), None) == _lib.EINVAL
+    assert "multiple of the patch" in lib.strata_hip_last_error().decode()
+    a.patch[:] = [1, 2, 2]
+    a.mean = 0x3000
+    assert lib.strata_hip_state_patchify(ctypes.byref(a), None) == _lib.EINVAL
+    assert "mean and std" in lib.strata_hip_last_error().decode()
+    a.mean, a.channels = None, 20000
+    assert lib.strata_hip_state_patchify(ctypes.byref(a), None) == _lib.EUNSUPPORTED
+    a.channels, a.batch = 4, 0
+    assert lib.strata_hip_state_patchify(ctypes.byref(a), None) == _lib.OK
+    u = _lib.StateUpdateArgs()
+    u.pred, u.next, u.batch, u.channels, u.order = 0x1000, 0x2000, 1, 4, 2
+    u.grid[:] = [4, 8, 8]
+    u.patch[:] = [1, 2, 2]
+    u.state, u.state_channels = 0x3000, 4
+    assert lib.strata_hip_state_update(ctypes.byref(u), None) == _lib.EINVAL
+    assert "order" in lib.strata_hip_last_error().decode()
+    u.order, u.state_channels = 1, 3
+    assert lib.strata_hip_state_update(ctypes.byref(u), None) == _lib.EINVAL
+    assert "fewer channels" in lib.strata_hip_last_error().decode()
+    u.state_channels, u.state = 4, None
+    assert lib.strata_hip_state_update(ctypes.byref(u), None) == _lib.EINVAL
+    u.state, u.batch = 0x3000, 0
+    assert lib.strata_hip_state_update(ctypes.byref(u), None) == _lib.OK
