@@ -225,6 +225,48 @@ def bench_halo(device, reps, warmup):
     return out
 
 
+def bench_step_io(device, reps, warmup):
+    """The rollout step's kernels around the network at the configs[4] geometry:
+    fp32 state [6, 80, 16, 64, 64] -> normalised bf16 tokens (patch 1), and head
+    tokens [6, 8, 32, 32, 640] (2x2x2 cells, channels last) -> denormalised,
+    state-updated fp32 state with a floor on one channel.  Algorithmic bytes =
+    each input read once + the output written once (the 80-entry tables aside)."""
+    import torch
+
+    from strata_amd import ops
+
+    B, C, grid = 6, 80, (16, 64, 64)
+    g = torch.Generator(device=device).manual_seed(0)
+    state = torch.randn(B, C, *grid, generator=g, device=device)
+    pred = torch.randn(B, 8, 32, 32, 8 * C, generator=g, device=device).bfloat16()
+    mean = torch.randn(C, generator=g, device=device)
+    std = torch.rand(C, generator=g, device=device) + 0.5
+    src = torch.arange(C, dtype=torch.int32, device=device)
+    floor = torch.full((C,), float("nan"), device=device)
+    floor[7] = 0.0
+    n = state.numel()
+    fns = (
+        ("patchify", lambda: ops.state_patchify(state, mean, std, (1, 1, 1)), n * (4 + 2)),
+        ("update", lambda: ops.state_update(pred, state, mean, std, src, floor, grid, (2, 2, 2), 1), n * (2 + 4 + 4)),
+    )
+    out = {"workload": f"rollout step I/O: state [{B}, {C}, 16, 64, 64] fp32 <-> bf16 tokens (patchify 1, update 2x2x2)"}
+    for name, fn, nbytes in fns:
+        for _ in range(warmup):
+            fn()
+        torch.cuda.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        for _ in range(reps):
+            fn()
+        e1.record()
+        torch.cuda.synchronize()
+        ms = e0.elapsed_time(e1) / reps
+        out[f"{name}_ms"] = round(ms, 4)
+        out[f"{name}_GBps"] = round(nbytes / (ms * 1e-3) / 1e9, 1)
+        out[f"{name}_pct_hbm"] = round(100.0 * nbytes / (ms * 1e-3) / 1e9 / PEAK_HBM_GBPS, 1)
+    return out
+
+
 def cpu_baseline():
     """The CPU oracle on a bounded sample of configs[2]: tile 0, head 0, 4 z-slices."""
     import torch
@@ -361,6 +403,8 @@ def main():
     if not args.no_halo:
         log("bench: timing the cube-sphere halo fill")
         result["halo"] = bench_halo(dev, 10, 2)
+        log("bench: timing the rollout step's state kernels")
+        result["step_io"] = bench_step_io(dev, 10, 2)
     if not args.no_cpu:
         log("bench: timing the CPU oracle sample")
         result["cpu_baseline"] = cpu_baseline()

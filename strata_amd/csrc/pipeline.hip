@@ -43,8 +43,35 @@ __device__ __forceinline__ int token_elem(const PipeParams& p, int order, int c,
   return order == 0 ? ((c * p.pz + dz) * p.py + dy) * p.px + dx : ((dz * p.py + dy) * p.px + dx) * p.C + c;
 }
 
+// Copy n bf16 between a token run in global memory and the LDS tile: 16-byte
+// pieces when the run is 16-byte aligned and n a multiple of 8, else 4-byte
+// pieces when p.vec allows, else single elements.
+template <bool TO_LDS>
+__device__ __forceinline__ void copy_run(const PipeParams& p, bf16* tile, bf16* g, int n, int tid) {
+  if (((uintptr_t)g & 15u) == 0 && (n & 7) == 0) {
+    u32x4* t = (u32x4*)tile;
+    u32x4* q = (u32x4*)g;
+    for (int i = tid; i < n / 8; i += PIPE_THREADS) {
+      if (TO_LDS) t[i] = q[i];
+      else q[i] = t[i];
+    }
+  } else if (p.vec) {
+    uint32_t* t = (uint32_t*)tile;
+    uint32_t* q = (uint32_t*)g;
+    for (int i = tid; i < n / 2; i += PIPE_THREADS) {
+      if (TO_LDS) t[i] = q[i];
+      else q[i] = t[i];
+    }
+  } else {
+    for (int i = tid; i < n; i += PIPE_THREADS) {
+      if (TO_LDS) tile[i] = g[i];
+      else g[i] = tile[i];
+    }
+  }
+}
+
 __global__ __launch_bounds__(PIPE_THREADS) void state_patchify_kernel(PipeParams p) {
-  __shared__ __attribute__((aligned(16))) bf16 tile[PIPE_LDS / 2];
+  extern __shared__ __attribute__((aligned(16))) bf16 tile[];  // NX tokens, pipe_lds_bytes(p)
   int w = (int)blockIdx.x;
   const int xb = w % p.nxb;
   w /= p.nxb;
@@ -61,35 +88,31 @@ __global__ __launch_bounds__(PIPE_THREADS) void state_patchify_kernel(PipeParams
   const int x0 = tx0 * p.px;
   const int tid = (int)threadIdx.x;
 
-  // state rows (c, dz, dy) -> tile[token][element], normalised, in bf16
-  for (int i = tid; i < rows * run; i += PIPE_THREADS) {
-    const int r = i / run, xi = i - r * run;
+  // state rows (c, dz, dy) -> tile[token][element], normalised, in bf16: a
+  // wave per row, a lane per x (run <= 64)
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6), lane = tid & 63;
+  const int t = lane / p.px, dx = lane - t * p.px;
+  for (int r = wave; r < rows; r += PIPE_THREADS / 64) {
     const int dy = r % p.py, dz = (r / p.py) % p.pz, c = r / (p.py * p.pz);
-    const int64_t src = (((int64_t)b * p.C + c) * p.Z + (tz * p.pz + dz)) * (int64_t)p.Y * p.X +
-                        (int64_t)(ty * p.py + dy) * p.X + x0 + xi;
-    const float v = p.state[src];
-    float n = v;
-    if (p.mean) n = (v - p.mean[c]) / p.std[c];
-    if (!__builtin_isfinite(v)) n = 0.f;
-    const int t = xi / p.px, dx = xi - t * p.px;
-    tile[t * K + token_elem(p, 0, c, dz, dy, dx)] = (bf16)n;
+    if (lane < run) {
+      const int64_t src = (((int64_t)b * p.C + c) * p.Z + (tz * p.pz + dz)) * (int64_t)p.Y * p.X +
+                          (int64_t)(ty * p.py + dy) * p.X + x0 + lane;
+      const float v = p.state[src];
+      float n = v;
+      if (p.mean) n = (v - p.mean[c]) / p.std[c];
+      if (!__builtin_isfinite(v)) n = 0.f;
+      tile[t * K + token_elem(p, 0, c, dz, dy, dx)] = (bf16)n;
+    }
   }
   __syncthreads();
   // tile -> nt contiguous tokens
   bf16* dst = (bf16*)p.tokens + ((((int64_t)b * p.Tz + tz) * p.Ty + ty) * p.Tx + tx0) * K;
-  const int total = nt * K;
-  if (p.vec) {  // pairs of bf16: 4-byte stores (every run starts 4-byte aligned)
-    const uint32_t* t32 = (const uint32_t*)tile;
-    uint32_t* d32 = (uint32_t*)dst;
-    for (int i = tid; i < total / 2; i += PIPE_THREADS) d32[i] = t32[i];
-  } else {
-    for (int i = tid; i < total; i += PIPE_THREADS) dst[i] = tile[i];
-  }
+  copy_run<false>(p, tile, dst, nt * K, tid);
 }
 
 __global__ __launch_bounds__(PIPE_THREADS) void state_update_kernel(PipeParams p) {
 #pragma clang fp contract(off)
-  __shared__ __attribute__((aligned(16))) bf16 tile[PIPE_LDS / 2];
+  extern __shared__ __attribute__((aligned(16))) bf16 tile[];  // NX tokens, pipe_lds_bytes(p)
   int w = (int)blockIdx.x;
   const int xb = w % p.nxb;
   w /= p.nxb;
@@ -107,21 +130,16 @@ __global__ __launch_bounds__(PIPE_THREADS) void state_update_kernel(PipeParams p
   const int tid = (int)threadIdx.x;
 
   // nt contiguous tokens -> tile
-  const bf16* src = (const bf16*)p.tokens + ((((int64_t)b * p.Tz + tz) * p.Ty + ty) * p.Tx + tx0) * K;
-  const int total = nt * K;
-  if (p.vec) {
-    const uint32_t* s32 = (const uint32_t*)src;
-    uint32_t* t32 = (uint32_t*)tile;
-    for (int i = tid; i < total / 2; i += PIPE_THREADS) t32[i] = s32[i];
-  } else {
-    for (int i = tid; i < total; i += PIPE_THREADS) tile[i] = src[i];
-  }
+  bf16* src = (bf16*)p.tokens + ((((int64_t)b * p.Tz + tz) * p.Ty + ty) * p.Tx + tx0) * K;
+  copy_run<true>(p, tile, src, nt * K, tid);
   __syncthreads();
-  // tile -> state rows (c, dz, dy)
-  for (int i = tid; i < rows * run; i += PIPE_THREADS) {
-    const int r = i / run, xi = i - r * run;
+  // tile -> state rows (c, dz, dy): a wave per row, a lane per x (run <= 64)
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6), lane = tid & 63;
+  const int t = lane / p.px, dx = lane - t * p.px;
+  for (int r = wave; r < rows; r += PIPE_THREADS / 64) {
     const int dy = r % p.py, dz = (r / p.py) % p.pz, c = r / (p.py * p.pz);
-    const int t = xi / p.px, dx = xi - t * p.px;
+    if (lane >= run) continue;
+    const int xi = lane;
     const float pr = (float)tile[t * K + token_elem(p, p.order, c, dz, dy, dx)];
     // denormalise in fp32 (a multiply, then an add, each rounded: the pragma
     // above keeps them from contracting to an fma), round to bf16
@@ -137,6 +155,12 @@ __global__ __launch_bounds__(PIPE_THREADS) void state_update_kernel(PipeParams p
     }
     p.next[((int64_t)b * p.C + c) * p.Z * (int64_t)p.Y * p.X + sp] = d;
   }
+}
+
+// LDS of one workgroup: NX tokens of C*P bf16, rounded up to 16 bytes (sized
+// to the need so that small tokens leave room for many workgroups per CU).
+static size_t pipe_lds_bytes(const PipeParams& p) {
+  return ((size_t)p.NX * p.C * p.pz * p.py * p.px * 2 + 15) / 16 * 16;
 }
 
 // Shared validation and launch geometry.  Returns OK and fills p, or an error.
@@ -164,10 +188,13 @@ static int pipe_setup(PipeParams& p, const char* name, int B, int C, const int32
   const int64_t K = (int64_t)C * p.pz * p.py * p.px;
   if (K * 2 > PIPE_LDS)
     return fail(STRATA_HIP_EUNSUPPORTED, n + ": a token of C*pz*py*px elements must fit 48 KiB of bf16");
-  // up to 64 state floats per row run, as many tokens as LDS holds
+  if (p.px > 64) return fail(STRATA_HIP_EUNSUPPORTED, n + ": patch width above 64");
+  // up to 64 state floats per row run (a lane each), as many tokens as LDS holds
   int NX = (int)(PIPE_LDS / (K * 2));
   const int nx_run = 64 / p.px > 1 ? 64 / p.px : 1;
   NX = NX < nx_run ? NX : nx_run;
+  // at most 16 KiB when that still leaves 16 tokens: more workgroups per CU
+  if (NX > 16 && (int64_t)NX * K * 2 > 16384) NX = (int)(16384 / (K * 2)) > 16 ? (int)(16384 / (K * 2)) : 16;
   NX = NX < p.Tx ? NX : p.Tx;
   p.NX = NX;
   p.nxb = (p.Tx + NX - 1) / NX;
@@ -196,7 +223,8 @@ extern "C" int strata_hip_state_patchify(const strata_hip_state_patchify_args* a
   p.vec = (p.C * p.pz * p.py * p.px) % 2 == 0 && ((uintptr_t)a->tokens & 3u) == 0;
   const int64_t blocks = (int64_t)p.B * p.Tz * p.Ty * p.nxb;
   if (blocks == 0) return STRATA_HIP_OK;
-  hipLaunchKernelGGL(state_patchify_kernel, dim3((unsigned)blocks), dim3(PIPE_THREADS), 0, (hipStream_t)stream, p);
+  hipLaunchKernelGGL(state_patchify_kernel, dim3((unsigned)blocks), dim3(PIPE_THREADS), pipe_lds_bytes(p),
+                     (hipStream_t)stream, p);
   return check_launch("state_patchify_kernel");
 }
 
@@ -226,6 +254,7 @@ extern "C" int strata_hip_state_update(const strata_hip_state_update_args* a, vo
   p.vec = (p.C * p.pz * p.py * p.px) % 2 == 0 && ((uintptr_t)a->pred & 3u) == 0;
   const int64_t blocks = (int64_t)p.B * p.Tz * p.Ty * p.nxb;
   if (blocks == 0) return STRATA_HIP_OK;
-  hipLaunchKernelGGL(state_update_kernel, dim3((unsigned)blocks), dim3(PIPE_THREADS), 0, (hipStream_t)stream, p);
+  hipLaunchKernelGGL(state_update_kernel, dim3((unsigned)blocks), dim3(PIPE_THREADS), pipe_lds_bytes(p),
+                     (hipStream_t)stream, p);
   return check_launch("state_update_kernel");
 }
