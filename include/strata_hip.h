@@ -3,7 +3,7 @@
  * transformer block's hot path: 3D neighbourhood attention (NA3D), the
  * stereographic-RoPE + QKV-pack prologue, the bias/GELU/residual GEMM and the
  * non-affine LayerNorm; around it, the cube-sphere halo fill and the rollout
- * step's state normalisation / patchify and state update.
+ * step's state normalisation / patchify and state update, and the NA3D backward.
  *
  * Conventions shared by every entry point
  *   - All pointers are device pointers owned by the caller.  The library never
@@ -91,6 +91,37 @@ typedef struct strata_hip_na3d_args {
 } strata_hip_na3d_args;
 
 int strata_hip_na3d_fwd(const strata_hip_na3d_args* args, void* stream);
+
+/* ---------------------------------------------------------------------------
+ * NA3D backward: dq, dk, dv of natten.na3d for out = na3d(q, k, v) over the
+ * whole grid (the autograd function of NATTEN 0.21.5 that training reaches
+ * through train.py:1161), same windows, kernel, dilation and scale as the
+ * forward.  q, k, v, out, dout, dq, dk, dv: contiguous heads-last
+ * [B, Z, Y, X, H, D], one dtype (f32 or bf16; fp32 math), 16-byte aligned;
+ * head_dim 32, 64 or 128.  workspace: 2 * B*Z*Y*X*H floats of caller memory
+ * (per-query log-sum-exp and rowsum(dout * out)), overwritten.
+ * ------------------------------------------------------------------------- */
+typedef struct strata_hip_na3d_bwd_args {
+  const void* q;
+  const void* k;
+  const void* v;
+  const void* out;  /* the forward's output */
+  const void* dout; /* gradient of the loss w.r.t. out */
+  void* dq;
+  void* dk;
+  void* dv;
+  float* workspace;
+  int32_t dtype;
+  int32_t batch;
+  int32_t heads;
+  int32_t head_dim;
+  int32_t grid[3];
+  int32_t kernel[3];
+  int32_t dilation[3];
+  float scale;
+} strata_hip_na3d_bwd_args;
+
+int strata_hip_na3d_bwd(const strata_hip_na3d_bwd_args* args, void* stream);
 
 /* ---------------------------------------------------------------------------
  * Stereographic-RoPE + QKV pack.

@@ -188,3 +188,15 @@ def na3d_flops(batch: int, heads: int, head_dim: int, n_queries: int, kernel_siz
     """Algorithmic FLOPs 4 * N_q * |W| * D per head (QK^T and PV, 2 flops per MAC)."""
     kz, ky, kx = _triple(kernel_size)
     return 4.0 * batch * heads * n_queries * kz * ky * kx * head_dim
+
+
+def na3d_backward(q: Tensor, k: Tensor, v: Tensor, dout: Tensor, kernel_size, dilation=1, scale: float | None = None,
+                  compute_dtype: torch.dtype = torch.float32) -> tuple[Tensor, Tensor, Tensor]:
+    """``(dq, dk, dv)`` of ``na3d`` over the whole grid for the upstream gradient ``dout``:
+    torch autograd through the restated forward (the gradient NATTEN's na3d autograd
+    function returns, reached in training through train.py:1161)."""
+    qc, kc, vc = (t.detach().to(compute_dtype).requires_grad_(True) for t in (q, k, v))
+    with torch.enable_grad():
+        out = na3d(qc, kc, vc, kernel_size, dilation, scale, compute_dtype=compute_dtype)
+        dq, dk, dv = torch.autograd.grad(out, (qc, kc, vc), dout.to(compute_dtype))
+    return dq, dk, dv

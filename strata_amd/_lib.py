@@ -143,6 +143,28 @@ class CubeCropArgs(ctypes.Structure):
     ]
 
 
+class Na3dBwdArgs(ctypes.Structure):
+    _fields_ = [
+        ("q", ctypes.c_void_p),
+        ("k", ctypes.c_void_p),
+        ("v", ctypes.c_void_p),
+        ("out", ctypes.c_void_p),
+        ("dout", ctypes.c_void_p),
+        ("dq", ctypes.c_void_p),
+        ("dk", ctypes.c_void_p),
+        ("dv", ctypes.c_void_p),
+        ("workspace", ctypes.c_void_p),
+        ("dtype", ctypes.c_int32),
+        ("batch", ctypes.c_int32),
+        ("heads", ctypes.c_int32),
+        ("head_dim", ctypes.c_int32),
+        ("grid", ctypes.c_int32 * 3),
+        ("kernel", ctypes.c_int32 * 3),
+        ("dilation", ctypes.c_int32 * 3),
+        ("scale", ctypes.c_float),
+    ]
+
+
 class StatePatchifyArgs(ctypes.Structure):
     _fields_ = [
         ("state", ctypes.c_void_p),
@@ -176,6 +198,7 @@ class StateUpdateArgs(ctypes.Structure):
 
 EXPORTS = {
     "strata_hip_na3d_fwd": ([ctypes.POINTER(Na3dArgs), ctypes.c_void_p], ctypes.c_int),
+    "strata_hip_na3d_bwd": ([ctypes.POINTER(Na3dBwdArgs), ctypes.c_void_p], ctypes.c_int),
     "strata_hip_rope_qkv_pack": ([ctypes.POINTER(RopePackArgs), ctypes.c_void_p], ctypes.c_int),
     "strata_hip_gemm_bias_act": ([ctypes.POINTER(GemmArgs), ctypes.c_void_p], ctypes.c_int),
     "strata_hip_layer_norm": ([ctypes.POINTER(LayerNormArgs), ctypes.c_void_p], ctypes.c_int),

@@ -4,8 +4,8 @@ Each op validates its tensors, allocates the output through torch's caching
 allocator, and enqueues the kernel on torch's current stream of the input's
 device.  There is no CPU or eager fallback: CPU tensors are rejected and a
 missing library raises.  Every op has a fake (meta) implementation so that
-``torch.compile`` traces through it, and an autograd formula that raises,
-because the kernels are forward-only (inference).
+``torch.compile`` traces through it.  ``na3d_fwd`` has a backward (the HIP
+NA3D backward, full-grid queries); the other ops' autograd formulas raise.
 """
 
 from __future__ import annotations
@@ -20,6 +20,7 @@ from . import _lib
 
 __all__ = [
     "na3d_fwd",
+    "na3d_bwd",
     "rope_qkv_pack",
     "gemm_bias_act",
     "layer_norm",
@@ -143,7 +144,74 @@ def _(q, k, v, kernel, dilation, scale, q_origin, q_extent):
     return q.new_empty((B, *[int(e) for e in q_extent], H, D))
 
 
-na3d_fwd.register_autograd(_no_backward("strata_hip::na3d_fwd"))
+@torch.library.custom_op("strata_hip::na3d_bwd", mutates_args=())
+def na3d_bwd(
+    q: Tensor,
+    k: Tensor,
+    v: Tensor,
+    out: Tensor,
+    dout: Tensor,
+    kernel: Sequence[int],
+    dilation: Sequence[int],
+    scale: Optional[float],
+) -> tuple[Tensor, Tensor, Tensor]:
+    """``(dq, dk, dv)`` of ``out = na3d(q, k, v)`` over the whole grid, given ``dout``
+    (NATTEN 0.21.5's na3d backward, reached in training through train.py:1161).
+    Heads-last ``[B, Z, Y, X, H, D]``, bf16 or fp32 (fp32 math), D in {32, 64, 128}."""
+    name = "na3d_bwd"
+    _require_gpu(name, q, k, v, out, dout)
+    shape = q.shape
+    for t, nm in ((k, "k"), (v, "v"), (out, "out"), (dout, "dout")):
+        if t.shape != shape or t.dtype != q.dtype:
+            raise ValueError(f"{name}: {nm} must match q ({tuple(shape)}, {q.dtype}), got {tuple(t.shape)}, {t.dtype}")
+    dt = _dtype_code(name, q)
+    if q.dim() != 6:
+        raise ValueError(f"{name}: expected heads-last [B, Z, Y, X, H, D], got {tuple(shape)}")
+    B, Z, Y, X, H, D = shape
+    kernel, dilation = _triple("kernel", kernel), _triple("dilation", dilation)
+    ins = [t.contiguous() for t in (q, k, v, out, dout)]
+    dq, dk, dv = (torch.empty_like(ins[0]) for _ in range(3))
+    if q.numel() == 0:
+        return dq, dk, dv
+    ws = torch.empty(2 * B * Z * Y * X * H, dtype=torch.float32, device=q.device)
+    a = _lib.Na3dBwdArgs()
+    a.q, a.k, a.v, a.out, a.dout = (t.data_ptr() for t in ins)
+    a.dq, a.dk, a.dv, a.workspace = dq.data_ptr(), dk.data_ptr(), dv.data_ptr(), ws.data_ptr()
+    a.dtype = dt
+    a.batch, a.heads, a.head_dim = B, H, D
+    a.grid[:] = [Z, Y, X]
+    a.kernel[:] = kernel
+    a.dilation[:] = dilation
+    a.scale = float(D**-0.5 if scale is None else scale)
+    with torch.cuda.device(q.device):
+        _lib.call("strata_hip_na3d_bwd", a, _stream(q))
+    return dq, dk, dv
+
+
+@na3d_bwd.register_fake
+def _(q, k, v, out, dout, kernel, dilation, scale):
+    return torch.empty_like(q), torch.empty_like(k), torch.empty_like(v)
+
+
+na3d_bwd.register_autograd(_no_backward("strata_hip::na3d_bwd"))
+
+
+def _na3d_setup_context(ctx, inputs, output):
+    q, k, v, kernel, dilation, scale, q_origin, q_extent = inputs
+    ctx.full_grid = list(q_origin) == [0, 0, 0] and list(q_extent) == list(q.shape[1:4])
+    ctx.kernel, ctx.dilation, ctx.scale = kernel, dilation, scale
+    ctx.save_for_backward(q, k, v, output)
+
+
+def _na3d_backward(ctx, dout):
+    if not ctx.full_grid:
+        raise RuntimeError("strata_hip::na3d_fwd: the backward covers full-grid queries only (no query box)")
+    q, k, v, out = ctx.saved_tensors
+    dq, dk, dv = na3d_bwd(q, k, v, out, dout.contiguous(), ctx.kernel, ctx.dilation, ctx.scale)
+    return dq, dk, dv, None, None, None, None, None
+
+
+na3d_fwd.register_autograd(_na3d_backward, setup_context=_na3d_setup_context)
 
 
 # ---------------------------------------------------------------------------

@@ -16,6 +16,7 @@ from .conftest import ROOT
 HEADER = ROOT / "include" / "strata_hip.h"
 STRUCTS = {
     "strata_hip_na3d_args": _lib.Na3dArgs,
+    "strata_hip_na3d_bwd_args": _lib.Na3dBwdArgs,
     "strata_hip_rope_pack_args": _lib.RopePackArgs,
     "strata_hip_gemm_args": _lib.GemmArgs,
     "strata_hip_layer_norm_args": _lib.LayerNormArgs,
@@ -194,3 +195,26 @@ def test_state_step_validation(lib):
     assert lib.strata_hip_state_update(ctypes.byref(u), None) == _lib.EINVAL
     u.state, u.batch = 0x3000, 0
     assert lib.strata_hip_state_update(ctypes.byref(u), None) == _lib.OK
+
+
+def test_na3d_bwd_validation(lib):
+    a = _lib.Na3dBwdArgs()
+    a.dtype, a.batch, a.heads, a.head_dim, a.scale = _lib.BF16, 1, 2, 64, 0.125
+    a.grid[:] = [4, 8, 8]
+    a.kernel[:] = [3, 5, 4]
+    a.dilation[:] = [1, 1, 1]
+    assert lib.strata_hip_na3d_bwd(ctypes.byref(a), None) == _lib.EINVAL
+    assert "odd" in lib.strata_hip_last_error().decode()
+    a.kernel[:] = [3, 5, 5]
+    a.dilation[:] = [1, 2, 1]
+    assert lib.strata_hip_na3d_bwd(ctypes.byref(a), None) == _lib.EINVAL
+    assert "exceeds" in lib.strata_hip_last_error().decode()
+    a.dilation[:] = [1, 1, 1]
+    assert lib.strata_hip_na3d_bwd(ctypes.byref(a), None) == _lib.EINVAL
+    assert "null" in lib.strata_hip_last_error().decode()
+    for name in ("q", "k", "v", "out", "dout", "dq", "dk", "dv", "workspace"):
+        setattr(a, name, 0x1000)
+    a.head_dim = 48
+    assert lib.strata_hip_na3d_bwd(ctypes.byref(a), None) == _lib.EUNSUPPORTED
+    a.batch = 0
+    assert lib.strata_hip_na3d_bwd(ctypes.byref(a), None) == _lib.OK

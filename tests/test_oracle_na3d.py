@@ -127,3 +127,47 @@ def test_flop_count_cfg2():
     # 6 tiles x interior (16,128,128) x 16 heads x W=507 x D=64
     f = O.na3d_flops(6, 16, 64, 16 * 128 * 128, (3, 13, 13))
     assert math.isclose(f, 3.266e12, rel_tol=1e-3)
+
+
+@pytest.mark.parametrize("kernel,dilation", [((3, 3, 5), (1, 1, 1)), ((1, 3, 3), (1, 2, 1)), ((3, 5, 3), (1, 1, 2))])
+def test_backward_matches_finite_differences(kernel, dilation):
+    """The oracle's backward against central finite differences (torch gradcheck, fp64),
+    on grids small enough that the windows clamp at every edge."""
+    g = torch.Generator().manual_seed(7)
+    shape = (1, 3, 6, 7, 2, 4)
+    q, k, v = (torch.randn(shape, generator=g, dtype=torch.float64, requires_grad=True) for _ in range(3))
+
+    def f(q, k, v):
+        return O.na3d(q, k, v, kernel, dilation, compute_dtype=torch.float64)
+
+    assert torch.autograd.gradcheck(f, (q, k, v), eps=1e-6, atol=1e-6, rtol=1e-5, fast_mode=True)
+
+
+def test_backward_full_window_is_dense_attention_backward():
+    """Kernel covering the grid: the gradients are those of dense softmax attention."""
+    g = torch.Generator().manual_seed(9)
+    B, Z, Y, X, H, D = 1, 3, 3, 5, 2, 4
+    q, k, v, dout = (torch.randn((B, Z, Y, X, H, D), generator=g, dtype=torch.float64) for _ in range(4))
+    dq, dk, dv = O.na3d_backward(q, k, v, dout, (Z, Y, X), compute_dtype=torch.float64)
+    qt, kt, vt = (t.clone().requires_grad_(True) for t in (q, k, v))
+
+    def heads(t):  # [B, Z, Y, X, H, D] -> [B, H, N, D]
+        return t.reshape(B, Z * Y * X, H, D).transpose(1, 2)
+
+    o = torch.nn.functional.scaled_dot_product_attention(heads(qt), heads(kt), heads(vt))
+    gq, gk, gv = torch.autograd.grad(o, (qt, kt, vt), heads(dout))
+    for a, b in zip((dq, dk, dv), (gq, gk, gv)):
+        assert torch.allclose(a, b, atol=1e-10, rtol=1e-9)
+
+
+def test_backward_dv_is_transposed_attention():
+    """dV = P^T dO: with dout = one-hot rows, dv sums the softmax weights each key receives."""
+    g = torch.Generator().manual_seed(8)
+    shape = (1, 2, 5, 5, 1, 3)
+    q, k, v = (torch.randn(shape, generator=g, dtype=torch.float64) for _ in range(3))
+    dout = torch.zeros(shape, dtype=torch.float64)
+    dout[..., 0] = 1.0
+    _, _, dv = O.na3d_backward(q, k, v, dout, (1, 3, 3), compute_dtype=torch.float64)
+    # total weight is conserved: every query distributes exactly 1
+    assert torch.allclose(dv[..., 0].sum(), torch.tensor(2 * 5 * 5, dtype=torch.float64))
+    assert torch.all(dv[..., 1:] == 0)
