@@ -28,6 +28,7 @@ ACT_NONE = 0
 ACT_GELU_TANH = 1
 ACT_GELU_ERF = 2
 ACT_SIGMOID = 3
+ACT_GELU_TANH_GRAD = 4
 
 RES_ADD = 0
 RES_MUL = 1

@@ -24,6 +24,16 @@ __device__ __forceinline__ float gelu_tanh(float x) {
   const float t = x * fmaf(k1 * 0.044715f, x * x, k1);
   return x * __builtin_amdgcn_rcpf(1.f + __builtin_amdgcn_exp2f(-t));
 }
+// d/dx gelu_tanh(x) = s + 2 x s (1 - s) u'(x) with s = sigmoid(2u) as above and
+// u' = sqrt(2/pi) (1 + 3 * 0.044715 x^2) (the backward of the MLP's GELU).
+__device__ __forceinline__ float gelu_tanh_grad(float x) {
+  constexpr float c = 0.7978845608028654f;
+  constexpr float k1 = 2.f * 1.4426950408889634f * c;
+  const float t = x * fmaf(k1 * 0.044715f, x * x, k1);
+  const float s = __builtin_amdgcn_rcpf(1.f + __builtin_amdgcn_exp2f(-t));
+  const float du2 = 2.f * c * fmaf(3.f * 0.044715f, x * x, 1.f);
+  return fmaf(x * s * (1.f - s), du2, s);
+}
 __device__ __forceinline__ float gelu_erf(float x) { return 0.5f * x * (1.f + erff(x * 0.7071067811865476f)); }
 // sigmoid(x) = 1 / (1 + 2^(-x log2 e)); saturates to 0 / 1 through inf / 0.
 __device__ __forceinline__ float sigmoid_fast(float x) {
@@ -33,6 +43,7 @@ __device__ __forceinline__ float apply_act(float v, int act) {
   if (act == STRATA_HIP_ACT_GELU_TANH) return gelu_tanh(v);
   if (act == STRATA_HIP_ACT_GELU_ERF) return gelu_erf(v);
   if (act == STRATA_HIP_ACT_SIGMOID) return sigmoid_fast(v);
+  if (act == STRATA_HIP_ACT_GELU_TANH_GRAD) return gelu_tanh_grad(v);
   return v;
 }
 __device__ __forceinline__ float combine(float o, float r, int res_op) {
@@ -47,6 +58,7 @@ __device__ __forceinline__ float act_t(float v) {
   if constexpr (ACT == STRATA_HIP_ACT_GELU_TANH) return gelu_tanh(v);
   else if constexpr (ACT == STRATA_HIP_ACT_GELU_ERF) return gelu_erf(v);
   else if constexpr (ACT == STRATA_HIP_ACT_SIGMOID) return sigmoid_fast(v);
+  else if constexpr (ACT == STRATA_HIP_ACT_GELU_TANH_GRAD) return gelu_tanh_grad(v);
   else return v;
 }
 template <int RES>
@@ -552,7 +564,7 @@ extern "C" int strata_hip_gemm_bias_act(const strata_hip_gemm_args* a, void* str
   if (((uintptr_t)a->x & 15) || ((uintptr_t)a->w & 15) || ((uintptr_t)a->out & 7) ||
       (a->residual && ((uintptr_t)a->residual & 7)) || (a->bias && ((uintptr_t)a->bias & 7)))
     return fail(STRATA_HIP_EINVAL, "gemm: x/w must be 16-byte aligned, out/residual/bias 8-byte aligned");
-  if (a->act < STRATA_HIP_ACT_NONE || a->act > STRATA_HIP_ACT_SIGMOID) return fail(STRATA_HIP_EINVAL, "gemm: bad act");
+  if (a->act < STRATA_HIP_ACT_NONE || a->act > STRATA_HIP_ACT_GELU_TANH_GRAD) return fail(STRATA_HIP_EINVAL, "gemm: bad act");
   if (a->res_op != STRATA_HIP_RES_ADD && a->res_op != STRATA_HIP_RES_MUL) return fail(STRATA_HIP_EINVAL, "gemm: bad res_op");
   GemmParams p;
   p.x = (const bf16*)a->x;
@@ -588,6 +600,7 @@ extern "C" int strata_hip_gemm_bias_act(const strata_hip_gemm_args* a, void* str
       case STRATA_HIP_ACT_GELU_TANH: launch_dma_act<STRATA_HIP_ACT_GELU_TANH>(p, grid, st); break;
       case STRATA_HIP_ACT_GELU_ERF: launch_dma_act<STRATA_HIP_ACT_GELU_ERF>(p, grid, st); break;
       case STRATA_HIP_ACT_SIGMOID: launch_dma_act<STRATA_HIP_ACT_SIGMOID>(p, grid, st); break;
+      case STRATA_HIP_ACT_GELU_TANH_GRAD: launch_dma_act<STRATA_HIP_ACT_GELU_TANH_GRAD>(p, grid, st); break;
       default: launch_dma_act<STRATA_HIP_ACT_NONE>(p, grid, st); break;
     }
     return check_launch("gemm_dma_kernel");
