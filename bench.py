@@ -11,7 +11,7 @@ breakdown and the RoPE+QKV-pack prologue's HBM GB/s, the configs[4] two-stage
 4-step rollout, the roofline of the dominant kernel, and the CPU oracle timed
 on a bounded sample on this host.
 
-    python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-block] [--no-rollout] [--no-cpu]
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-block] [--no-rollout] [--no-halo] [--no-backward] [--no-cpu]
 """
 
 from __future__ import annotations
@@ -267,6 +267,49 @@ def bench_step_io(device, reps, warmup):
     return out
 
 
+def bench_backward(device, reps, warmup):
+    """Training kernels: the NA3D backward at the configs[1] shape ([2, 8, 64, 64] tokens,
+    8 x 64 heads, W=(3,7,7), bf16; FLOPs = 2.5 x the forward's 4*N*|W|*D, the usual
+    attention-backward count) and the GEMM-GELU backward's fused epilogue GEMM
+    (gelu'(x @ w.T + b) * dout) at the configs[3] fc1 shape."""
+    import torch
+
+    from strata_amd import _lib, ops
+
+    g = torch.Generator(device=device).manual_seed(0)
+    shape, ker = (2, 8, 64, 64, 8, 64), [3, 7, 7]
+    q, k, v, do = (torch.randn(shape, generator=g, device=device).bfloat16() for _ in range(4))
+    out = torch.ops.strata_hip.na3d_fwd(q, k, v, ker, [1, 1, 1], None, [0, 0, 0], list(shape[1:4]))
+    M, N, K = 131072, 4096, 1024
+    x = torch.randn(M, K, generator=g, device=device).bfloat16()
+    w = (torch.randn(N, K, generator=g, device=device) * K**-0.5).bfloat16()
+    b = torch.randn(N, generator=g, device=device).bfloat16()
+    dy = torch.randn(M, N, generator=g, device=device).bfloat16()
+    B, Z, Y, X, H, D = shape
+    fns = (
+        ("na3d_bwd", lambda: ops.na3d_bwd(q, k, v, out, do, ker, [1, 1, 1], None),
+         2.5 * 4.0 * B * Z * Y * X * H * 147 * D),
+        ("gelu_grad_gemm", lambda: ops.gemm_bias_act(x, w, b, dy, _lib.ACT_GELU_TANH_GRAD, _lib.RES_MUL),
+         2.0 * M * N * K),
+    )
+    res = {"workload": "NA3D bwd at configs[1] (bf16, W=(3,7,7)); fused GELU-derivative GEMM at configs[3] fc1 "
+                       "(M=131072, N=4096, K=1024)"}
+    for name, fn, flops in fns:
+        for _ in range(warmup):
+            fn()
+        torch.cuda.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        for _ in range(reps):
+            fn()
+        e1.record()
+        torch.cuda.synchronize()
+        ms = e0.elapsed_time(e1) / reps
+        res[f"{name}_ms"] = round(ms, 4)
+        res[f"{name}_tflops"] = round(flops / (ms * 1e-3) / 1e12, 1)
+    return res
+
+
 def cpu_baseline():
     """The CPU oracle on a bounded sample of configs[2]: tile 0, head 0, 4 z-slices."""
     import torch
@@ -318,6 +361,7 @@ def main():
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-rollout", action="store_true")
     ap.add_argument("--no-halo", action="store_true")
+    ap.add_argument("--no-backward", action="store_true")
     ap.add_argument(
         "--copy-calibration",
         action="store_true",
@@ -405,6 +449,9 @@ def main():
         result["halo"] = bench_halo(dev, 10, 2)
         log("bench: timing the rollout step's state kernels")
         result["step_io"] = bench_step_io(dev, 10, 2)
+    if not args.no_backward:
+        log("bench: timing the backward kernels")
+        result["backward"] = bench_backward(dev, 5, 1)
     if not args.no_cpu:
         log("bench: timing the CPU oracle sample")
         result["cpu_baseline"] = cpu_baseline()

@@ -19,6 +19,8 @@ CASES = [  # shape [B, Z, Y, X, H, D], kernel, dilation
     ((1, 4, 12, 12, 2, 64), (3, 5, 3), (1, 2, 2)),
     ((1, 3, 14, 16, 1, 128), (3, 13, 13), (1, 1, 1)),
     ((1, 5, 7, 9, 2, 64), (5, 7, 9), (1, 1, 1)),
+    ((1, 3, 21, 30, 2, 64), (3, 13, 13), (1, 1, 1)),  # MFMA dq: x union of 16 keys, ragged tiles
+    ((2, 4, 6, 37, 1, 64), (3, 5, 11), (1, 1, 1)),
 ]
 
 
@@ -74,3 +76,17 @@ def test_backward_of_a_query_box_raises(gpu):
     out = torch.ops.strata_hip.na3d_fwd(q, kg, vg, [3, 3, 3], [1, 1, 1], None, [0, 2, 2], [3, 4, 4])
     with pytest.raises(RuntimeError, match="full-grid"):
         out.sum().backward()
+
+
+@pytest.mark.parametrize("case", [c for c in CASES if c[0][-1] == 64 and c[2] == (1, 1, 1)], ids=str)
+def test_bwd_mfma_matches_valu_path(gpu, case, monkeypatch):
+    """bf16, head_dim 64, dilation 1 runs the MFMA kernels; the VALU kernels
+    (STRATA_HIP_NA3D_BWD_VALU) must agree with them."""
+    shape, kernel, dil = case
+    _, (qg, kg, vg, dg) = _inputs(shape, 4, torch.bfloat16, gpu)
+    out = _fwd(qg, kg, vg, kernel, dil)
+    fast = torch.ops.strata_hip.na3d_bwd(qg, kg, vg, out, dg, list(kernel), list(dil), None)
+    monkeypatch.setenv("STRATA_HIP_NA3D_BWD_VALU", "1")
+    slow = torch.ops.strata_hip.na3d_bwd(qg, kg, vg, out, dg, list(kernel), list(dil), None)
+    for a, b in zip(fast, slow):
+        assert rel_l2(a.float(), b.float()) <= 1e-2
