@@ -168,6 +168,27 @@ typedef struct strata_hip_rope_pack_args {
 
 int strata_hip_rope_qkv_pack(const strata_hip_rope_pack_args* args, void* stream);
 
+/* Backward of the pack without qk_norm: dqkv [M, (3, H, D)] (row stride
+ * dqkv_row_stride) = (R(-theta) dq, R(-theta) dk, dv) for dq, dk, dv [M, H, D]
+ * contiguous bf16 and the forward's cos/sin tables and layout. */
+typedef struct strata_hip_rope_pack_bwd_args {
+  const void* dq;
+  const void* dk;
+  const void* dv;
+  const float* cos;
+  const float* sin;
+  void* dqkv;
+  int32_t batch;
+  int32_t grid[3];
+  int32_t table_z;
+  int32_t heads;
+  int32_t head_dim;
+  int32_t layout;
+  int64_t dqkv_row_stride;
+} strata_hip_rope_pack_bwd_args;
+
+int strata_hip_rope_qkv_pack_bwd(const strata_hip_rope_pack_bwd_args* args, void* stream);
+
 /* ---------------------------------------------------------------------------
  * GEMM with fused epilogue:  out = act(x @ w^T + bias) (+ or *) residual
  * Replaces nn.Linear (+ GELU) of the block: attn.qkv, attn.proj and the Mlp
@@ -222,6 +243,22 @@ typedef struct strata_hip_layer_norm_args {
 } strata_hip_layer_norm_args;
 
 int strata_hip_layer_norm(const strata_hip_layer_norm_args* args, void* stream);
+
+/* Backward of the non-affine LayerNorm: dx from x and dy (all [M, C] bf16 with
+ * one row stride `ld`), dx = rstd * (dy - mean(dy) - xh * mean(dy * xh)),
+ * xh = (x - mean) * rstd, fp32 statistics recomputed from x. */
+typedef struct strata_hip_layer_norm_bwd_args {
+  const void* x;
+  const void* dy;
+  void* dx;
+  int64_t m;
+  int64_t c;
+  int64_t ld;
+  float eps;
+  int32_t reserved;
+} strata_hip_layer_norm_bwd_args;
+
+int strata_hip_layer_norm_bwd(const strata_hip_layer_norm_bwd_args* args, void* stream);
 
 /* ---------------------------------------------------------------------------
  * Cube-sphere halo fill: the single-GPU local counterpart of the rollout's

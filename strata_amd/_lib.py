@@ -166,6 +166,37 @@ class Na3dBwdArgs(ctypes.Structure):
     ]
 
 
+class LayerNormBwdArgs(ctypes.Structure):
+    _fields_ = [
+        ("x", ctypes.c_void_p),
+        ("dy", ctypes.c_void_p),
+        ("dx", ctypes.c_void_p),
+        ("m", ctypes.c_int64),
+        ("c", ctypes.c_int64),
+        ("ld", ctypes.c_int64),
+        ("eps", ctypes.c_float),
+        ("reserved", ctypes.c_int32),
+    ]
+
+
+class RopePackBwdArgs(ctypes.Structure):
+    _fields_ = [
+        ("dq", ctypes.c_void_p),
+        ("dk", ctypes.c_void_p),
+        ("dv", ctypes.c_void_p),
+        ("cos", ctypes.c_void_p),
+        ("sin", ctypes.c_void_p),
+        ("dqkv", ctypes.c_void_p),
+        ("batch", ctypes.c_int32),
+        ("grid", ctypes.c_int32 * 3),
+        ("table_z", ctypes.c_int32),
+        ("heads", ctypes.c_int32),
+        ("head_dim", ctypes.c_int32),
+        ("layout", ctypes.c_int32),
+        ("dqkv_row_stride", ctypes.c_int64),
+    ]
+
+
 class StatePatchifyArgs(ctypes.Structure):
     _fields_ = [
         ("state", ctypes.c_void_p),
@@ -203,6 +234,8 @@ EXPORTS = {
     "strata_hip_rope_qkv_pack": ([ctypes.POINTER(RopePackArgs), ctypes.c_void_p], ctypes.c_int),
     "strata_hip_gemm_bias_act": ([ctypes.POINTER(GemmArgs), ctypes.c_void_p], ctypes.c_int),
     "strata_hip_layer_norm": ([ctypes.POINTER(LayerNormArgs), ctypes.c_void_p], ctypes.c_int),
+    "strata_hip_layer_norm_bwd": ([ctypes.POINTER(LayerNormBwdArgs), ctypes.c_void_p], ctypes.c_int),
+    "strata_hip_rope_qkv_pack_bwd": ([ctypes.POINTER(RopePackBwdArgs), ctypes.c_void_p], ctypes.c_int),
     "strata_hip_cube_pad_faces": ([ctypes.POINTER(CubePadArgs), ctypes.c_void_p], ctypes.c_int),
     "strata_hip_cube_crop": ([ctypes.POINTER(CubeCropArgs), ctypes.c_void_p], ctypes.c_int),
     "strata_hip_state_patchify": ([ctypes.POINTER(StatePatchifyArgs), ctypes.c_void_p], ctypes.c_int),

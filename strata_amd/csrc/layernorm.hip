@@ -60,9 +60,91 @@ __global__ __launch_bounds__(256) void layer_norm_kernel(const bf16* __restrict_
   }
 }
 
+// Backward of the non-affine LayerNorm, one wave per row as above:
+//   xh = (x - mean) * rstd,  dx = rstd * (dy - mean(dy) - xh * mean(dy * xh)).
+__global__ __launch_bounds__(256) void layer_norm_bwd_kernel(const bf16* __restrict__ x, const bf16* __restrict__ dy,
+                                                             bf16* __restrict__ dx, int64_t M, int C, int64_t ld,
+                                                             float eps) {
+  const int64_t row = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (row >= M) return;
+  const int lane = threadIdx.x & 63;
+  const int runs = C / 8;
+  u32x4 v[LN_MAX_RUNS], g[LN_MAX_RUNS];
+  float s = 0.f;
+#pragma unroll
+  for (int r = 0; r < LN_MAX_RUNS; ++r) {
+    const int run = lane + 64 * r;
+    v[r] = g[r] = (u32x4){0u, 0u, 0u, 0u};
+    if (run < runs) {
+      v[r] = *(const u32x4*)(x + row * ld + 8 * run);
+      g[r] = *(const u32x4*)(dy + row * ld + 8 * run);
+#pragma unroll
+      for (int w = 0; w < 4; ++w) s += bf16_lo(v[r][w]) + bf16_hi(v[r][w]);
+    }
+  }
+  const float mean = wave_sum(s) / C;
+  float q = 0.f;
+#pragma unroll
+  for (int r = 0; r < LN_MAX_RUNS; ++r) {
+    if (lane + 64 * r < runs) {
+#pragma unroll
+      for (int w = 0; w < 4; ++w) {
+        const float a = bf16_lo(v[r][w]) - mean, b = bf16_hi(v[r][w]) - mean;
+        q = fmaf(a, a, q);
+        q = fmaf(b, b, q);
+      }
+    }
+  }
+  const float rstd = rsqrtf(wave_sum(q) / C + eps);
+  float sg = 0.f, sgx = 0.f;
+#pragma unroll
+  for (int r = 0; r < LN_MAX_RUNS; ++r) {
+    if (lane + 64 * r < runs) {
+#pragma unroll
+      for (int w = 0; w < 4; ++w) {
+        const float g0 = bf16_lo(g[r][w]), g1 = bf16_hi(g[r][w]);
+        sg += g0 + g1;
+        sgx = fmaf(g0, (bf16_lo(v[r][w]) - mean) * rstd, sgx);
+        sgx = fmaf(g1, (bf16_hi(v[r][w]) - mean) * rstd, sgx);
+      }
+    }
+  }
+  const float mg = wave_sum(sg) / C, mgx = wave_sum(sgx) / C;
+#pragma unroll
+  for (int r = 0; r < LN_MAX_RUNS; ++r) {
+    const int run = lane + 64 * r;
+    if (run < runs) {
+      u32x4 o;
+#pragma unroll
+      for (int w = 0; w < 4; ++w) {
+        const float x0 = (bf16_lo(v[r][w]) - mean) * rstd, x1 = (bf16_hi(v[r][w]) - mean) * rstd;
+        o[w] = pack_bf16x2(rstd * (bf16_lo(g[r][w]) - mg - x0 * mgx), rstd * (bf16_hi(g[r][w]) - mg - x1 * mgx));
+      }
+      *(u32x4*)(dx + row * ld + 8 * run) = o;
+    }
+  }
+}
+
 }  // namespace strata
 
 using namespace strata;
+
+extern "C" int strata_hip_layer_norm_bwd(const strata_hip_layer_norm_bwd_args* a, void* stream) {
+  if (!a) return fail(STRATA_HIP_EINVAL, "layer_norm_bwd: null args");
+  if (a->m < 0 || a->c <= 0) return fail(STRATA_HIP_EINVAL, "layer_norm_bwd: bad m/c");
+  if (a->m == 0) return STRATA_HIP_OK;
+  if (!a->x || !a->dy || !a->dx) return fail(STRATA_HIP_EINVAL, "layer_norm_bwd: null pointer");
+  if (a->c % 8 || a->c > 8 * 64 * LN_MAX_RUNS)
+    return fail(STRATA_HIP_EUNSUPPORTED, "layer_norm_bwd: channels must be a multiple of 8 and at most 4096");
+  if (a->ld < a->c || a->ld % 8 || ((uintptr_t)a->x & 15) || ((uintptr_t)a->dy & 15) || ((uintptr_t)a->dx & 15))
+    return fail(STRATA_HIP_EINVAL, "layer_norm_bwd: rows must be 16-byte aligned with a stride >= c");
+  if (!(a->eps >= 0.f)) return fail(STRATA_HIP_EINVAL, "layer_norm_bwd: eps must be non-negative");
+  const int64_t blocks = (a->m + 3) / 4;
+  if (blocks > 0x7fffffff) return fail(STRATA_HIP_EUNSUPPORTED, "layer_norm_bwd: too many rows");
+  hipLaunchKernelGGL(layer_norm_bwd_kernel, dim3((unsigned)blocks), dim3(256), 0, (hipStream_t)stream,
+                     (const bf16*)a->x, (const bf16*)a->dy, (bf16*)a->dx, a->m, (int)a->c, a->ld, a->eps);
+  return check_launch("layer_norm_bwd_kernel");
+}
 
 extern "C" int strata_hip_layer_norm(const strata_hip_layer_norm_args* a, void* stream) {
   if (!a) return fail(STRATA_HIP_EINVAL, "layer_norm: null args");

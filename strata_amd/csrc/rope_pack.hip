@@ -166,9 +166,125 @@ __global__ __launch_bounds__(256) void rope_pack_inter_kernel(RopeParams p, int6
   *(u32x4*)(p.v + dst) = *(const u32x4*)(src + 2 * C);
 }
 
+// Backward of the pack without qk_norm: the gradient of a rotation by theta is
+// the rotation by -theta, so d(qkv) gets R(-theta) dq, R(-theta) dk and dv,
+// written back into the [M, (3, H, D)] layout of the qkv GEMM's output (the
+// row stride p.ld; p.qkv is the destination here, p.q / p.k / p.v the sources).
+__global__ __launch_bounds__(256) void rope_unpack_half_kernel(RopeParams p, int64_t total) {
+  const int64_t idx = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (idx >= total) return;
+  const int cph = p.D / 16;
+  const int c = (int)(idx % cph);
+  const int64_t th = idx / cph;
+  const int h = (int)(th % p.H);
+  const int64_t tok = th / p.H;
+  const int half = p.D / 2;
+  const int64_t C = (int64_t)p.H * p.D;
+  bf16* dst = const_cast<bf16*>(p.qkv) + tok * p.ld + (int64_t)h * p.D + 8 * c;
+  const int64_t trow = table_row(p, tok) * half + 8 * c;
+  float cs[8], sn[8];
+  *(f32x4*)&cs[0] = *(const f32x4*)(p.cos + trow);
+  *(f32x4*)&cs[4] = *(const f32x4*)(p.cos + trow + 4);
+  *(f32x4*)&sn[0] = *(const f32x4*)(p.sin + trow);
+  *(f32x4*)&sn[4] = *(const f32x4*)(p.sin + trow + 4);
+#pragma unroll
+  for (int i = 0; i < 8; ++i) sn[i] = -sn[i];
+  const int64_t src = tok * C + (int64_t)h * p.D + 8 * c;
+  const bf16* srcs[2] = {p.q, p.k};
+#pragma unroll
+  for (int t = 0; t < 2; ++t) {
+    float f[16];
+    unpack8(*(const u32x4*)(srcs[t] + src), f);
+    unpack8(*(const u32x4*)(srcs[t] + src + half), f + 8);
+    u32x4 oa, ob;
+    rot8(f, f + 8, cs, sn, oa, ob);
+    *(u32x4*)(dst + t * C) = oa;
+    *(u32x4*)(dst + t * C + half) = ob;
+  }
+  *(u32x4*)(dst + 2 * C) = *(const u32x4*)(p.v + src);
+  *(u32x4*)(dst + 2 * C + half) = *(const u32x4*)(p.v + src + half);
+}
+
+__global__ __launch_bounds__(256) void rope_unpack_inter_kernel(RopeParams p, int64_t total) {
+  const int64_t idx = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (idx >= total) return;
+  const int cph = p.D / 8;
+  const int c = (int)(idx % cph);
+  const int64_t th = idx / cph;
+  const int h = (int)(th % p.H);
+  const int64_t tok = th / p.H;
+  const int half = p.D / 2;
+  const int64_t C = (int64_t)p.H * p.D;
+  bf16* dst = const_cast<bf16*>(p.qkv) + tok * p.ld + (int64_t)h * p.D + 8 * c;
+  const int64_t trow = table_row(p, tok) * half + 4 * c;
+  float cs[4], sn[4];
+  *(f32x4*)&cs[0] = *(const f32x4*)(p.cos + trow);
+  *(f32x4*)&sn[0] = *(const f32x4*)(p.sin + trow);
+  const int64_t src = tok * C + (int64_t)h * p.D + 8 * c;
+  const bf16* srcs[2] = {p.q, p.k};
+#pragma unroll
+  for (int t = 0; t < 2; ++t) {
+    float f[8];
+    unpack8(*(const u32x4*)(srcs[t] + src), f);
+    u32x4 o;
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+      const float y0 = f[2 * k], y1 = f[2 * k + 1];
+      o[k] = pack_bf16x2(y0 * cs[k] + y1 * sn[k], y1 * cs[k] - y0 * sn[k]);
+    }
+    *(u32x4*)(dst + t * C) = o;
+  }
+  *(u32x4*)(dst + 2 * C) = *(const u32x4*)(p.v + src);
+}
+
 }  // namespace strata
 
 using namespace strata;
+
+extern "C" int strata_hip_rope_qkv_pack_bwd(const strata_hip_rope_pack_bwd_args* a, void* stream) {
+  if (!a) return fail(STRATA_HIP_EINVAL, "rope_qkv_pack_bwd: null args");
+  if (!a->dq || !a->dk || !a->dv || !a->cos || !a->sin || !a->dqkv)
+    return fail(STRATA_HIP_EINVAL, "rope_qkv_pack_bwd: null pointer");
+  if (a->batch < 0 || a->grid[0] <= 0 || a->grid[1] <= 0 || a->grid[2] <= 0 || a->heads <= 0)
+    return fail(STRATA_HIP_EINVAL, "rope_qkv_pack_bwd: bad batch/grid/heads");
+  if (a->table_z != 1 && a->table_z != a->grid[0])
+    return fail(STRATA_HIP_EINVAL, "rope_qkv_pack_bwd: table_z must be 1 or Z");
+  if (a->layout != STRATA_HIP_ROPE_HALF && a->layout != STRATA_HIP_ROPE_INTERLEAVED)
+    return fail(STRATA_HIP_EINVAL, "rope_qkv_pack_bwd: bad layout");
+  if (a->layout == STRATA_HIP_ROPE_HALF ? (a->head_dim % 16) : (a->head_dim % 8))
+    return fail(STRATA_HIP_EINVAL, "rope_qkv_pack_bwd: head_dim must be a multiple of 16 (half) or 8 (interleaved)");
+  const int64_t C = (int64_t)a->heads * a->head_dim;
+  if (a->dqkv_row_stride < 3 * C || a->dqkv_row_stride % 8)
+    return fail(STRATA_HIP_EINVAL, "rope_qkv_pack_bwd: dqkv row stride must be >= 3*H*D and a multiple of 8");
+  const void* ptrs[6] = {a->dq, a->dk, a->dv, a->cos, a->sin, a->dqkv};
+  for (int i = 0; i < 6; ++i)
+    if ((uintptr_t)ptrs[i] & 15) return fail(STRATA_HIP_EINVAL, "rope_qkv_pack_bwd: pointers must be 16-byte aligned");
+  RopeParams p = {};
+  p.qkv = (const bf16*)a->dqkv;
+  p.cos = a->cos;
+  p.sin = a->sin;
+  p.q = (bf16*)a->dq;
+  p.k = (bf16*)a->dk;
+  p.v = (bf16*)a->dv;
+  p.Z = a->grid[0];
+  p.Y = a->grid[1];
+  p.X = a->grid[2];
+  p.Zt = a->table_z;
+  p.H = a->heads;
+  p.D = a->head_dim;
+  p.ld = a->dqkv_row_stride;
+  p.M = (int64_t)a->batch * p.Z * p.Y * p.X;
+  const int cph = a->layout == STRATA_HIP_ROPE_HALF ? p.D / 16 : p.D / 8;
+  const int64_t total = p.M * p.H * cph;
+  if (total == 0) return STRATA_HIP_OK;
+  const int64_t blocks = (total + 255) / 256;
+  if (blocks > 0x7fffffff) return fail(STRATA_HIP_EUNSUPPORTED, "rope_qkv_pack_bwd: too many tokens");
+  if (a->layout == STRATA_HIP_ROPE_HALF)
+    hipLaunchKernelGGL(rope_unpack_half_kernel, dim3((unsigned)blocks), dim3(256), 0, (hipStream_t)stream, p, total);
+  else
+    hipLaunchKernelGGL(rope_unpack_inter_kernel, dim3((unsigned)blocks), dim3(256), 0, (hipStream_t)stream, p, total);
+  return check_launch("rope_unpack_kernel");
+}
 
 extern "C" int strata_hip_rope_qkv_pack(const strata_hip_rope_pack_args* a, void* stream) {
   if (!a) return fail(STRATA_HIP_EINVAL, "rope_qkv_pack: null args");

@@ -4,8 +4,10 @@ Each op validates its tensors, allocates the output through torch's caching
 allocator, and enqueues the kernel on torch's current stream of the input's
 device.  There is no CPU or eager fallback: CPU tensors are rejected and a
 missing library raises.  Every op has a fake (meta) implementation so that
-``torch.compile`` traces through it.  ``na3d_fwd`` has a backward (the HIP
-NA3D backward, full-grid queries); the other ops' autograd formulas raise.
+``torch.compile`` traces through it.  ``na3d_fwd`` (full-grid queries),
+``gemm_bias_act`` (act none / GELU(tanh), added residual), ``layer_norm`` and
+``rope_qkv_pack`` (without qk_norm) have backwards on HIP kernels; the other
+ops' autograd formulas raise.
 """
 
 from __future__ import annotations
@@ -291,7 +293,39 @@ def _(qkv, cos, sin, heads, rope_layout, qk_norm=False, qk_norm_eps=1e-6, q_norm
     return qkv.new_empty(shape), qkv.new_empty(shape), qkv.new_empty(shape)
 
 
-rope_qkv_pack.register_autograd(_no_backward("strata_hip::rope_qkv_pack"))
+def _rope_setup_context(ctx, inputs, output):
+    qkv, cos, sin, heads, rope_layout, qk_norm, qk_norm_eps, q_norm_weight, k_norm_weight = inputs
+    ctx.qk_norm, ctx.heads, ctx.layout = bool(qk_norm), int(heads), int(rope_layout)
+    ctx.qkv_shape = tuple(qkv.shape)
+    ctx.save_for_backward(cos, sin)
+
+
+def _rope_backward(ctx, dq, dk, dv):
+    """d(qkv) = (R(-theta) dq, R(-theta) dk, dv) in qkv's (3, H, D) column layout (no qk_norm)."""
+    if ctx.qk_norm:
+        raise RuntimeError("strata_hip::rope_qkv_pack: backward with qk_norm is not implemented")
+    cos, sin = ctx.saved_tensors
+    B, Z, Y, X, C3 = ctx.qkv_shape
+    D = C3 // (3 * ctx.heads)
+    grads = [g.contiguous() if g is not None else torch.zeros((B, Z, Y, X, ctx.heads, D), dtype=torch.bfloat16,
+                                                                 device=cos.device) for g in (dq, dk, dv)]
+    dqkv = torch.empty(ctx.qkv_shape, dtype=torch.bfloat16, device=cos.device)
+    a = _lib.RopePackBwdArgs()
+    a.dq, a.dk, a.dv = (g.data_ptr() for g in grads)
+    cos_c, sin_c = cos.contiguous(), sin.contiguous()
+    a.cos, a.sin, a.dqkv = cos_c.data_ptr(), sin_c.data_ptr(), dqkv.data_ptr()
+    a.batch = B
+    a.grid[:] = [Z, Y, X]
+    a.table_z = cos.shape[1]
+    a.heads, a.head_dim, a.layout = ctx.heads, D, ctx.layout
+    a.dqkv_row_stride = C3
+    if dqkv.numel():
+        with torch.cuda.device(cos.device):
+            _lib.call("strata_hip_rope_qkv_pack_bwd", a, _stream(dqkv))
+    return dqkv, None, None, None, None, None, None, None, None
+
+
+rope_qkv_pack.register_autograd(_rope_backward, setup_context=_rope_setup_context)
 
 
 # ---------------------------------------------------------------------------
@@ -424,7 +458,27 @@ def _(x, eps):
     return torch.empty_like(x)
 
 
-layer_norm.register_autograd(_no_backward("strata_hip::layer_norm"))
+def _ln_setup_context(ctx, inputs, output):
+    x, eps = inputs
+    ctx.eps = float(eps)
+    ctx.save_for_backward(x)
+
+
+def _ln_backward(ctx, dy):
+    (x,) = ctx.saved_tensors
+    x2 = x.contiguous().view(-1, x.shape[-1])
+    g2 = dy.to(torch.bfloat16).contiguous().view(-1, x.shape[-1])
+    dx = torch.empty_like(x2)
+    if x2.shape[0]:
+        a = _lib.LayerNormBwdArgs()
+        a.x, a.dy, a.dx = x2.data_ptr(), g2.data_ptr(), dx.data_ptr()
+        a.m, a.c, a.ld, a.eps = x2.shape[0], x2.shape[1], x2.shape[1], ctx.eps
+        with torch.cuda.device(x.device):
+            _lib.call("strata_hip_layer_norm_bwd", a, _stream(x))
+    return dx.view(x.shape), None
+
+
+layer_norm.register_autograd(_ln_backward, setup_context=_ln_setup_context)
 
 
 def default_scale(head_dim: int) -> float:

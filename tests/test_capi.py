@@ -17,6 +17,8 @@ HEADER = ROOT / "include" / "strata_hip.h"
 STRUCTS = {
     "strata_hip_na3d_args": _lib.Na3dArgs,
     "strata_hip_na3d_bwd_args": _lib.Na3dBwdArgs,
+    "strata_hip_layer_norm_bwd_args": _lib.LayerNormBwdArgs,
+    "strata_hip_rope_pack_bwd_args": _lib.RopePackBwdArgs,
     "strata_hip_rope_pack_args": _lib.RopePackArgs,
     "strata_hip_gemm_args": _lib.GemmArgs,
     "strata_hip_layer_norm_args": _lib.LayerNormArgs,
