@@ -42,8 +42,9 @@ enum strata_hip_act {
   STRATA_HIP_ACT_GELU_TANH = 1,
   STRATA_HIP_ACT_GELU_ERF = 2,
   STRATA_HIP_ACT_SIGMOID = 3,       /* the attention gate */
-  STRATA_HIP_ACT_GELU_TANH_GRAD = 4 /* d/dx GELU(tanh): with res_op MUL and residual = the upstream
-                                       gradient, the MLP backward's gradient at fc1's output */
+  STRATA_HIP_ACT_GELU_TANH_GRAD = 4, /* d/dx GELU(tanh): with res_op MUL and residual = the upstream
+                                        gradient, the MLP backward's gradient at fc1's output */
+  STRATA_HIP_ACT_SIGMOID_GRAD = 5     /* d/dx sigmoid: the gate's backward (res_op MUL) */
 };
 /* How the GEMM epilogue combines act(x @ w^T + bias) with `residual`. */
 enum strata_hip_res_op { STRATA_HIP_RES_ADD = 0, STRATA_HIP_RES_MUL = 1 };

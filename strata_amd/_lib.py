@@ -29,6 +29,7 @@ ACT_GELU_TANH = 1
 ACT_GELU_ERF = 2
 ACT_SIGMOID = 3
 ACT_GELU_TANH_GRAD = 4
+ACT_SIGMOID_GRAD = 5
 
 RES_ADD = 0
 RES_MUL = 1

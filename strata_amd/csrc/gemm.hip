@@ -39,11 +39,17 @@ __device__ __forceinline__ float gelu_erf(float x) { return 0.5f * x * (1.f + er
 __device__ __forceinline__ float sigmoid_fast(float x) {
   return __builtin_amdgcn_rcpf(1.f + __builtin_amdgcn_exp2f(-1.4426950408889634f * x));
 }
+// sigmoid'(x) = s (1 - s): the gate's backward.
+__device__ __forceinline__ float sigmoid_grad(float x) {
+  const float s = sigmoid_fast(x);
+  return s * (1.f - s);
+}
 __device__ __forceinline__ float apply_act(float v, int act) {
   if (act == STRATA_HIP_ACT_GELU_TANH) return gelu_tanh(v);
   if (act == STRATA_HIP_ACT_GELU_ERF) return gelu_erf(v);
   if (act == STRATA_HIP_ACT_SIGMOID) return sigmoid_fast(v);
   if (act == STRATA_HIP_ACT_GELU_TANH_GRAD) return gelu_tanh_grad(v);
+  if (act == STRATA_HIP_ACT_SIGMOID_GRAD) return sigmoid_grad(v);
   return v;
 }
 __device__ __forceinline__ float combine(float o, float r, int res_op) {
@@ -59,6 +65,7 @@ __device__ __forceinline__ float act_t(float v) {
   else if constexpr (ACT == STRATA_HIP_ACT_GELU_ERF) return gelu_erf(v);
   else if constexpr (ACT == STRATA_HIP_ACT_SIGMOID) return sigmoid_fast(v);
   else if constexpr (ACT == STRATA_HIP_ACT_GELU_TANH_GRAD) return gelu_tanh_grad(v);
+  else if constexpr (ACT == STRATA_HIP_ACT_SIGMOID_GRAD) return sigmoid_grad(v);
   else return v;
 }
 template <int RES>
@@ -564,7 +571,7 @@ extern "C" int strata_hip_gemm_bias_act(const strata_hip_gemm_args* a, void* str
   if (((uintptr_t)a->x & 15) || ((uintptr_t)a->w & 15) || ((uintptr_t)a->out & 7) ||
       (a->residual && ((uintptr_t)a->residual & 7)) || (a->bias && ((uintptr_t)a->bias & 7)))
     return fail(STRATA_HIP_EINVAL, "gemm: x/w must be 16-byte aligned, out/residual/bias 8-byte aligned");
-  if (a->act < STRATA_HIP_ACT_NONE || a->act > STRATA_HIP_ACT_GELU_TANH_GRAD) return fail(STRATA_HIP_EINVAL, "gemm: bad act");
+  if (a->act < STRATA_HIP_ACT_NONE || a->act > STRATA_HIP_ACT_SIGMOID_GRAD) return fail(STRATA_HIP_EINVAL, "gemm: bad act");
   if (a->res_op != STRATA_HIP_RES_ADD && a->res_op != STRATA_HIP_RES_MUL) return fail(STRATA_HIP_EINVAL, "gemm: bad res_op");
   GemmParams p;
   p.x = (const bf16*)a->x;
@@ -601,6 +608,7 @@ extern "C" int strata_hip_gemm_bias_act(const strata_hip_gemm_args* a, void* str
       case STRATA_HIP_ACT_GELU_ERF: launch_dma_act<STRATA_HIP_ACT_GELU_ERF>(p, grid, st); break;
       case STRATA_HIP_ACT_SIGMOID: launch_dma_act<STRATA_HIP_ACT_SIGMOID>(p, grid, st); break;
       case STRATA_HIP_ACT_GELU_TANH_GRAD: launch_dma_act<STRATA_HIP_ACT_GELU_TANH_GRAD>(p, grid, st); break;
+      case STRATA_HIP_ACT_SIGMOID_GRAD: launch_dma_act<STRATA_HIP_ACT_SIGMOID_GRAD>(p, grid, st); break;
       default: launch_dma_act<STRATA_HIP_ACT_NONE>(p, grid, st); break;
     }
     return check_launch("gemm_dma_kernel");

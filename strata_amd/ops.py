@@ -401,27 +401,37 @@ def _gemm_setup_context(ctx, inputs, output):
     x, w, bias, residual, act, res_op = inputs
     ctx.act, ctx.res_op = int(act), int(res_op)
     ctx.has_bias, ctx.has_res = bias is not None, residual is not None
-    ctx.save_for_backward(x, w, bias)
+    gate = int(act) == _lib.ACT_SIGMOID and residual is not None and int(res_op) == _lib.RES_MUL
+    ctx.save_for_backward(x, w, bias, residual if gate else None)
 
 
 def _gemm_backward(ctx, dout):
     """Backward of ``act(x @ w.T + bias) + residual`` for act none / GELU(tanh), residual
-    added (the MLP's fc1 -> GELU and fc2 + residual, attn.qkv and attn.proj + residual).
+    added (the MLP's fc1 -> GELU and fc2 + residual, attn.qkv and attn.proj + residual), and
+    of the attention gate ``sigmoid(x @ w.T + bias) * residual``.
     The gradient at the pre-activation of a GELU layer, ``gelu'(x @ w.T + bias) * dout``,
     recomputes the GEMM with that epilogue fused (hand-written kernel); the input and
     weight gradients are plain GEMMs."""
-    if ctx.act not in (_lib.ACT_NONE, _lib.ACT_GELU_TANH) or (ctx.has_res and ctx.res_op != _lib.RES_ADD):
-        raise RuntimeError("strata_hip::gemm_bias_act: backward covers act none / GELU(tanh) with an added residual")
-    x, w, bias = ctx.saved_tensors
+    gate = ctx.act == _lib.ACT_SIGMOID and ctx.has_res and ctx.res_op == _lib.RES_MUL
+    if not gate and (ctx.act not in (_lib.ACT_NONE, _lib.ACT_GELU_TANH) or (ctx.has_res and ctx.res_op != _lib.RES_ADD)):
+        raise RuntimeError("strata_hip::gemm_bias_act: backward covers act none / GELU(tanh) with an added "
+                           "residual and the sigmoid gate (multiplied residual)")
+    x, w, bias, res = ctx.saved_tensors
     g = dout.contiguous()
-    if ctx.act == _lib.ACT_GELU_TANH:
+    dres = None
+    if gate:  # out = sigmoid(z) * res: d res = dout * sigmoid(z), d z = dout * res * sigmoid'(z)
+        if ctx.needs_input_grad[3]:
+            dres = gemm_bias_act(x, w, bias, g, _lib.ACT_SIGMOID, _lib.RES_MUL)
+        g = gemm_bias_act(x, w, bias, (g * res).contiguous(), _lib.ACT_SIGMOID_GRAD, _lib.RES_MUL)
+    elif ctx.act == _lib.ACT_GELU_TANH:
         g = gemm_bias_act(x, w, bias, g, _lib.ACT_GELU_TANH_GRAD, _lib.RES_MUL)
     g2 = g.reshape(-1, g.shape[-1])
     x2 = x.reshape(-1, x.shape[-1])
     dx = (g2 @ w).reshape(x.shape) if ctx.needs_input_grad[0] else None
     dw = (g2.t() @ x2) if ctx.needs_input_grad[1] else None
     db = g2.float().sum(0).to(bias.dtype) if ctx.has_bias and ctx.needs_input_grad[2] else None
-    dres = dout if ctx.has_res and ctx.needs_input_grad[3] else None
+    if not gate:
+        dres = dout if ctx.has_res and ctx.needs_input_grad[3] else None
     return dx, dw, db, dres, None, None
 
 

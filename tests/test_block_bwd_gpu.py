@@ -61,10 +61,11 @@ def test_rope_pack_backward_is_the_inverse_rotation(gpu, layout, zt):
     assert rel_l2(q.detach().float().cpu(), outs[0].detach()) <= 1e-2
 
 
-def test_strata_block_backward_vs_oracle(gpu):
+@pytest.mark.parametrize("gated", [False, True])
+def test_strata_block_backward_vs_oracle(gpu, gated):
     C, H, kernel = 128, 2, (3, 5, 5)
     torch.manual_seed(0)
-    blk = StrataBlock(C, H, kernel)
+    blk = StrataBlock(C, H, kernel, gated=gated)
     init_xavier_(blk, torch.Generator().manual_seed(1))
     with torch.no_grad():  # nonzero biases so their gradients are checked too
         for m in blk.modules():
@@ -83,7 +84,7 @@ def test_strata_block_backward_vs_oracle(gpu):
     xg = x.to(gpu).requires_grad_(True)
     blk(xg, rope).backward(dy.to(gpu))
     xr = x.float().requires_grad_(True)
-    OB.block_forward(xr, params, H, kernel, c1.float(), s1.float()).backward(dy.float())
+    OB.block_forward(xr, params, H, kernel, c1.float(), s1.float(), gated=gated).backward(dy.float())
     assert rel_l2(xg.grad.float().cpu(), xr.grad) <= 2e-2
     for name, p in blk.named_parameters():
         assert rel_l2(p.grad.float().cpu(), params[name].grad) <= 2e-2, name

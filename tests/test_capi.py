@@ -140,7 +140,7 @@ def test_gemm_and_layernorm_validation(lib):
     g.res_op = 5
     assert lib.strata_hip_gemm_bias_act(ctypes.byref(g), None) == _lib.EINVAL
     assert "res_op" in lib.strata_hip_last_error().decode()
-    g.res_op, g.act = 0, 5
+    g.res_op, g.act = 0, 6
     assert lib.strata_hip_gemm_bias_act(ctypes.byref(g), None) == _lib.EINVAL
     assert "act" in lib.strata_hip_last_error().decode()
 

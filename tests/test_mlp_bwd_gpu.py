@@ -67,3 +67,17 @@ def test_mlp_module_backward(gpu):
     for (n1, p1), (n2, p2) in zip(mlp.named_parameters(), ref.named_parameters()):
         assert n1 == n2
         assert rel_l2(p1.grad.float().cpu(), p2.grad.bfloat16().float()) <= 1e-2, n1
+
+
+@pytest.mark.parametrize("shape", SHAPES, ids=str)
+def test_gate_autograd_vs_torch(gpu, shape):
+    """The attention gate sigmoid(x @ w.T + b) * a: gradients of x, w, b and a."""
+    M, N, K = shape
+    g = torch.Generator().manual_seed(3)
+    x, w, b, a, dout = _bf((M, K), g), _bf((N, K), g, K**-0.5), _bf((N,), g), _bf((M, N), g), _bf((M, N), g)
+    leaves = [t.to(gpu).requires_grad_(True) for t in (x, w, b, a)]
+    ops.gemm_bias_act(*leaves, _lib.ACT_SIGMOID, _lib.RES_MUL).backward(dout.to(gpu))
+    ref = [t.float().requires_grad_(True) for t in (x, w, b, a)]
+    (torch.sigmoid(F.linear(ref[0], ref[1], ref[2])) * ref[3]).backward(dout.float())
+    for name, got, want in zip("xwba", leaves, ref):
+        assert rel_l2(got.grad.float().cpu(), want.grad) <= 1e-2, name
