@@ -1131,13 +1131,11 @@ __device__ __forceinline__ void na3d_strip_fast_body(const Na3dParams p, const N
   constexpr int NS = 4;                   // tile slots per wave
   constexpr int TY = 16 / TX;
   constexpr int WQX = NWX * TX;           // workgroup query columns
-  constexpr int LW = (NWX - 1) * TX + 16; // keys per LDS row that are read
+  constexpr int LW = (NWX - 1) * TX + 16; // keys of a row the workgroup reads (no padding)
   constexpr int KPK = 512 / D;            // keys per KiB
-  constexpr int LWP = (LW + KPK - 1) / KPK * KPK;
-  constexpr int RB = LWP * D * 2;         // bytes per (tensor, row) region
-  constexpr int RKB = RB / 1024;
+  constexpr int RB = LW * D * 2;          // bytes per (tensor, row) region: rows packed back to back
   constexpr int STAGE_B = 2 * RPS * RB;   // K rows 0..RPS-1, then V rows 0..RPS-1
-  constexpr int LPT = 2 * RPS * RKB / NWX;  // 1-KiB DMA loads per wave per stage
+  constexpr int LPT = STAGE_B / 1024 / NWX;  // 1-KiB DMA loads per wave per stage
   constexpr int NRP = RPS / 2;
   constexpr int CPK = D / 8;              // 16-byte chunks per key
   constexpr int KS = D / 32;              // k-steps of the QK MFMA; also 1-KiB loads per wave for 16 query rows
@@ -1149,7 +1147,9 @@ __device__ __forceinline__ void na3d_strip_fast_body(const Na3dParams p, const N
   constexpr uint32_t LMIN_BITS = (127u - 100u) << 23;  // 2^-100 as an fp32 bit pattern
   constexpr uint32_t INF_BITS = 0x7f800000u;
   static_assert(TX == 4 && TY == 4 && RPS == 4 && TY + KY - 1 == NS * RPS, "regular strip geometry");
-  static_assert(RKB == NWX && LPT == 2 * RPS, "stage layout: wave w loads the w-th KiB of every row");
+  static_assert(D == 64 && LW % 8 == 4, "odd rows start half a swizzle period in: chunk slot bit 2 flips");
+  static_assert(LPT * NWX * 1024 == STAGE_B && 2 * LPT * 1024 == RPS * RB,
+                "stage layout: waves 0-1 load the K rows, waves 2-3 the V rows, LPT KiB each");
   static_assert(QWB == KS * 1024, "16 query rows are KS 1-KiB loads");
   static_assert(QTB <= RING_B, "tile 0's Q is staged through the ring");
 
@@ -1216,15 +1216,22 @@ __device__ __forceinline__ void na3d_strip_fast_body(const Na3dParams p, const N
   const int rz = gz + dz * iz;
   const float c2 = p.scale * 1.4426950408889634f;  // scores in log2 units
 
-  // ---- K/V ring lane offsets: wave w loads keys [w*KPK, (w+1)*KPK) of every row ----
+  // ---- K/V ring lane offsets ----
+  // A stage holds RPS rows of LW keys of K, then of V, each key's 16-byte chunks
+  // at swizzled slots of the stage-flat key index f = row * LW + x.  Wave w
+  // copies the (w & 1)-th half of K (w < 2) or V (w >= 2): LPT 1-KiB loads of
+  // 8 keys each, every lane one chunk, at offsets fixed for the whole strip.
   const int64_t rowk = 2 * (int64_t)dy * p.ks[2], rowv = 2 * (int64_t)dy * p.vs[2];
-  uint32_t xoffk, xoffv;
-  {
-    const int key = (wave % RKB) * KPK + lane / CPK;
-    const int c = swz<D>(lane % CPK, key);
-    const bool in = key < LW && X0 + key < Lx;
-    xoffk = in ? (uint32_t)((int64_t)(gx + dx * (X0 + key)) * p.ks[3] * 2 + 16 * c) : OOB;
-    xoffv = in ? (uint32_t)((int64_t)(gx + dx * (X0 + key)) * p.vs[3] * 2 + 16 * c) : OOB;
+  const bool vwave = wave >= 2;
+  const int64_t rowt = vwave ? rowv : rowk;
+  const int64_t colt = 2 * (vwave ? p.vs[3] : p.ks[3]);
+  uint32_t doff[LPT];
+#pragma unroll
+  for (int i = 0; i < LPT; ++i) {
+    const int f = ((wave & 1) * LPT + i) * KPK + lane / CPK;
+    const int row = f / LW, key = f % LW;
+    const int c = swz<D>(lane % CPK, f);
+    doff[i] = X0 + key < Lx ? (uint32_t)(row * rowt + (int64_t)(gx + dx * (X0 + key)) * colt + 16 * c) : OOB;
   }
   // ---- Q and self-key copies: one (batch, z, head) slice, 31-bit offsets ----
   const u32x4 rq = make_rsrc((const char*)p.q + 2 * ((int64_t)b * p.qs[0] + (int64_t)rz * p.qs[1] + (int64_t)h * p.qs[4]),
@@ -1253,7 +1260,9 @@ __device__ __forceinline__ void na3d_strip_fast_body(const Na3dParams p, const N
   const int64_t orow = 2 * (int64_t)dy * p.os[2];
   const int64_t ooff = 2 * ((int64_t)(gx + dx * qx - p.org[2]) * p.os[3] + (int64_t)(gy - p.org[1]) * p.os[2]) + 8 * g;
 
-  // ---- LDS read offsets of the K/V operands (bytes within a stage) ----
+  // ---- LDS read offsets of the K/V operands (bytes within row 0 of a stage;
+  // row r adds r * RB, and for odd r uses the offsets of chunk bit 2 flipped:
+  // entry ks ^ 1 for K, db ^ 2 for V) ----
   uint32_t koff[KS];
 #pragma unroll
   for (int ks = 0; ks < KS; ++ks) {
@@ -1379,13 +1388,11 @@ __device__ __forceinline__ void na3d_strip_fast_body(const Na3dParams p, const N
   uint32_t issue_off = 0;
   auto issue = [&]() {
     const int nrow = min(max(NR - RPS * cp, 0), RPS);
-    const u32x4 rk = make_rsrc(kseg + (int64_t)cp * RPS * rowk + (int64_t)cz * zstepk, (uint32_t)(nrow * rowk));
-    const u32x4 rv = make_rsrc(vseg + (int64_t)cp * RPS * rowv + (int64_t)cz * zstepv, (uint32_t)(nrow * rowv));
-    const uint32_t m0 = lds_base + issue_off + (uint32_t)(wave / RKB) * RB + (uint32_t)(wave % RKB) * 1024;
+    const u32x4 rs = vwave ? make_rsrc(vseg + (int64_t)cp * RPS * rowv + (int64_t)cz * zstepv, (uint32_t)(nrow * rowv))
+                           : make_rsrc(kseg + (int64_t)cp * RPS * rowk + (int64_t)cz * zstepk, (uint32_t)(nrow * rowk));
+    const uint32_t m0 = lds_base + issue_off + (uint32_t)wave * (LPT * 1024);
 #pragma unroll
-    for (int r = 0; r < RPS; ++r) dma_row16(rk, m0 + r * RB, xoffk + (uint32_t)(r * rowk));
-#pragma unroll
-    for (int r = 0; r < RPS; ++r) dma_row16(rv, m0 + (RPS + r) * RB, xoffv + (uint32_t)(r * rowv));
+    for (int i = 0; i < LPT; ++i) dma_row16(rs, m0 + i * 1024, doff[i]);
     issue_off = issue_off + STAGE_B == RING_B ? 0 : issue_off + STAGE_B;
     if (++cz == kz) {
       cz = 0;
@@ -1426,7 +1433,7 @@ __device__ __forceinline__ void na3d_strip_fast_body(const Na3dParams p, const N
 #pragma unroll
       for (int r = 0; r < RPS; ++r)
 #pragma unroll
-        for (int ks = 0; ks < KS; ++ks) ak[r][ks] = *(const bf16x8*)(st + r * RB + koff[ks]);
+        for (int ks = 0; ks < KS; ++ks) ak[r][ks] = *(const bf16x8*)(st + r * RB + koff[ks ^ (r & 1)]);
       bf16x8 av[NRP][DB];
 #pragma unroll
       for (int rp = 0; rp < NRP; ++rp)
@@ -1434,7 +1441,7 @@ __device__ __forceinline__ void na3d_strip_fast_body(const Na3dParams p, const N
         for (int db = 0; db < DB; ++db) {
           const bf16x4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4bf16(LDS_PTR(bf16x4, st + voffs[db] + 2 * rp * RB));
           const bf16x4 hi =
-              __builtin_amdgcn_ds_read_tr16_b64_v4bf16(LDS_PTR(bf16x4, st + voffs[db] + (2 * rp + 1) * RB));
+              __builtin_amdgcn_ds_read_tr16_b64_v4bf16(LDS_PTR(bf16x4, st + voffs[db ^ 2] + (2 * rp + 1) * RB));
           av[rp][db] = __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7);
         }
       stage_math(cst, act, ak, av);
