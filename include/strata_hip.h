@@ -26,7 +26,7 @@
 extern "C" {
 #endif
 
-#define STRATA_HIP_ABI_VERSION 3
+#define STRATA_HIP_ABI_VERSION 4
 
 enum strata_hip_status {
   STRATA_HIP_OK = 0,
@@ -169,9 +169,19 @@ typedef struct strata_hip_rope_pack_args {
 
 int strata_hip_rope_qkv_pack(const strata_hip_rope_pack_args* args, void* stream);
 
-/* Backward of the pack without qk_norm: dqkv [M, (3, H, D)] (row stride
- * dqkv_row_stride) = (R(-theta) dq, R(-theta) dk, dv) for dq, dk, dv [M, H, D]
- * contiguous bf16 and the forward's cos/sin tables and layout. */
+/* Backward of the pack: dqkv [M, (3, H, D)] (row stride dqkv_row_stride) =
+ * (R(-theta) dq, R(-theta) dk, dv) for dq, dk, dv [M, H, D] contiguous bf16
+ * and the forward's cos/sin tables and layout.  With qk_norm = 1 the q and k
+ * columns are further taken through the RMSNorm backward, recomputed from the
+ * forward's input qkv (row stride qkv_row_stride):
+ *   g = R(-theta) dout * w,  r = 1/sqrt(mean(x^2) + eps),
+ *   dx = r * g - x * r^3 * <g, x> / D,
+ * and, for a weight given (q_norm_weight / k_norm_weight, bf16 [D]), the
+ * weight gradient sum over tokens and heads of (R(-theta) dout) * x * r is
+ * ADDED to dq_norm_weight / dk_norm_weight (fp32 [D]; the caller zeroes them;
+ * the sum is accumulated with atomics, so its rounding order varies).
+ * Backward of the forward strata_hip_rope_qkv_pack with the same
+ * qk_norm / qk_norm_eps / weights. */
 typedef struct strata_hip_rope_pack_bwd_args {
   const void* dq;
   const void* dk;
@@ -186,6 +196,14 @@ typedef struct strata_hip_rope_pack_bwd_args {
   int32_t head_dim;
   int32_t layout;
   int64_t dqkv_row_stride;
+  const void* qkv;           /* forward input [M, (3, H, D)] bf16; read only with qk_norm */
+  int64_t qkv_row_stride;
+  const void* q_norm_weight; /* bf16 [D] or NULL */
+  const void* k_norm_weight; /* bf16 [D] or NULL */
+  float* dq_norm_weight;     /* fp32 [D], accumulated; NULL iff q_norm_weight is NULL */
+  float* dk_norm_weight;     /* fp32 [D], accumulated; NULL iff k_norm_weight is NULL */
+  int32_t qk_norm;           /* 0 or 1, as in the forward */
+  float qk_norm_eps;
 } strata_hip_rope_pack_bwd_args;
 
 int strata_hip_rope_qkv_pack_bwd(const strata_hip_rope_pack_bwd_args* args, void* stream);

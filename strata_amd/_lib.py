@@ -14,7 +14,7 @@ from pathlib import Path
 
 LIB_PATH = Path(__file__).resolve().parent / "libstrata_hip.so"
 
-ABI_VERSION = 3
+ABI_VERSION = 4
 
 OK = 0
 EINVAL = -1
@@ -195,6 +195,14 @@ class RopePackBwdArgs(ctypes.Structure):
         ("head_dim", ctypes.c_int32),
         ("layout", ctypes.c_int32),
         ("dqkv_row_stride", ctypes.c_int64),
+        ("qkv", ctypes.c_void_p),
+        ("qkv_row_stride", ctypes.c_int64),
+        ("q_norm_weight", ctypes.c_void_p),
+        ("k_norm_weight", ctypes.c_void_p),
+        ("dq_norm_weight", ctypes.c_void_p),
+        ("dk_norm_weight", ctypes.c_void_p),
+        ("qk_norm", ctypes.c_int32),
+        ("qk_norm_eps", ctypes.c_float),
     ]
 
 

@@ -27,6 +27,11 @@ struct RopeParams {
   float eps;
   const bf16* qw;  // RMSNorm weights [D] or null
   const bf16* kw;
+  // backward with qk_norm only
+  const bf16* x;   // the forward's input qkv
+  int64_t ldx;
+  float* dqw;      // fp32 [D] weight-gradient accumulators or null
+  float* dkw;
 };
 
 __device__ __forceinline__ void unpack8(const u32x4& a, float* f) {
@@ -237,6 +242,129 @@ __global__ __launch_bounds__(256) void rope_unpack_inter_kernel(RopeParams p, in
   *(u32x4*)(dst + 2 * C) = *(const u32x4*)(p.v + src);
 }
 
+// Backward with qk_norm: each of q and k goes back through the rotation,
+// dy = R(-theta) dout, and then through the RMSNorm y = x * r * w with
+// r = 1/sqrt(mean(x^2) + eps) recomputed from the forward's input:
+//   dx = r * g - x * r^3 * <g, x> / D,  g = dy * w,
+// and the weight gradient sums dy * x * r over tokens and heads.  A thread
+// holds 16 (half layout) or 8 (interleaved) values of one (token, head); the
+// head's D/16 or D/8 threads are consecutive lanes that reduce <x, x> and
+// <g, x> with shuffles, as the forward reduces <x, x>.  The grid-stride loop's
+// stride is a multiple of the threads per head, so a thread keeps the same
+// channels throughout and sums its weight-gradient terms in registers; at the
+// end the block adds them per channel in LDS and adds those to the fp32 [D]
+// accumulators with one global atomic per channel and block.
+template <bool HALF>
+__global__ __launch_bounds__(256) void rope_unpack_norm_kernel(RopeParams p, int64_t total) {
+  constexpr int NV = HALF ? 16 : 8;
+  __shared__ float red[2][1024];
+  const int D = p.D;
+  const int cph = HALF ? D / 16 : D / 8;
+  const int half = D / 2;
+  const int64_t C = (int64_t)p.H * D;
+  for (int i = threadIdx.x; i < 2 * D; i += blockDim.x) red[i / D][i % D] = 0.f;
+
+  int64_t idx = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  const int64_t stride = (int64_t)gridDim.x * blockDim.x;
+  const int c = (int)(idx % cph);
+  int dof[NV];
+#pragma unroll
+  for (int j = 0; j < 8; ++j) {
+    dof[j] = 8 * c + j;
+    if constexpr (HALF) dof[8 + j] = 8 * c + j + half;
+  }
+  float wv[2][NV], dw[2][NV];
+#pragma unroll
+  for (int t = 0; t < 2; ++t) {
+    const bf16* w = t ? p.kw : p.qw;
+#pragma unroll
+    for (int i = 0; i < NV; ++i) {
+      wv[t][i] = w ? (float)w[dof[i]] : 1.f;
+      dw[t][i] = 0.f;
+    }
+  }
+  const bf16* srcs[2] = {p.q, p.k};
+
+  for (; idx < total; idx += stride) {
+    const int64_t th = idx / cph;
+    const int h = (int)(th % p.H);
+    const int64_t tok = th / p.H;
+    const bf16* xin = p.x + tok * p.ldx + (int64_t)h * D + 8 * c;
+    bf16* dst = const_cast<bf16*>(p.qkv) + tok * p.ld + (int64_t)h * D + 8 * c;
+    const int64_t src = tok * C + (int64_t)h * D + 8 * c;
+    constexpr int NP = NV / 2;  // rotation pairs of the thread
+    float cs[NP], sn[NP];
+    const int64_t trow = table_row(p, tok) * half + NP * c;
+#pragma unroll
+    for (int i = 0; i < NP; i += 4) {
+      *(f32x4*)&cs[i] = *(const f32x4*)(p.cos + trow + i);
+      *(f32x4*)&sn[i] = *(const f32x4*)(p.sin + trow + i);
+    }
+#pragma unroll
+    for (int t = 0; t < 2; ++t) {
+      float x[NV], o[NV], dy[NV];
+      unpack8(*(const u32x4*)(xin + t * C), x);
+      unpack8(*(const u32x4*)(srcs[t] + src), o);
+      if constexpr (HALF) {
+        unpack8(*(const u32x4*)(xin + t * C + half), x + 8);
+        unpack8(*(const u32x4*)(srcs[t] + src + half), o + 8);
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {  // pair (j, 8 + j) = (d, d + D/2)
+          dy[j] = o[j] * cs[j] + o[8 + j] * sn[j];
+          dy[8 + j] = o[8 + j] * cs[j] - o[j] * sn[j];
+        }
+      } else {
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {  // pair (2k, 2k + 1)
+          dy[2 * k] = o[2 * k] * cs[k] + o[2 * k + 1] * sn[k];
+          dy[2 * k + 1] = o[2 * k + 1] * cs[k] - o[2 * k] * sn[k];
+        }
+      }
+      float ss = 0.f, gx = 0.f, g[NV];
+#pragma unroll
+      for (int i = 0; i < NV; ++i) {
+        ss = fmaf(x[i], x[i], ss);
+        g[i] = dy[i] * wv[t][i];
+        gx = fmaf(g[i], x[i], gx);
+      }
+      for (int o2 = 1; o2 < cph; o2 <<= 1) {
+        ss += __shfl_xor(ss, o2);
+        gx += __shfl_xor(gx, o2);
+      }
+      const float r = rsqrtf(ss / (float)D + p.eps);
+      const float coef = r * r * r * gx / (float)D;
+      float dx[NV];
+#pragma unroll
+      for (int i = 0; i < NV; ++i) {
+        dx[i] = r * g[i] - x[i] * coef;
+        dw[t][i] = fmaf(dy[i] * x[i], r, dw[t][i]);
+      }
+      u32x4 lo, hi;
+#pragma unroll
+      for (int w = 0; w < 4; ++w) {
+        lo[w] = pack_bf16x2(dx[2 * w], dx[2 * w + 1]);
+        if constexpr (HALF) hi[w] = pack_bf16x2(dx[8 + 2 * w], dx[8 + 2 * w + 1]);
+      }
+      *(u32x4*)(dst + t * C) = lo;
+      if constexpr (HALF) *(u32x4*)(dst + t * C + half) = hi;
+    }
+    *(u32x4*)(dst + 2 * C) = *(const u32x4*)(p.v + src);
+    if constexpr (HALF) *(u32x4*)(dst + 2 * C + half) = *(const u32x4*)(p.v + src + half);
+  }
+
+  if (!p.dqw && !p.dkw) return;  // uniform: no weight gradients wanted
+  __syncthreads();
+#pragma unroll
+  for (int t = 0; t < 2; ++t)
+#pragma unroll
+    for (int i = 0; i < NV; ++i) atomicAdd(&red[t][dof[i]], dw[t][i]);
+  __syncthreads();
+  for (int i = threadIdx.x; i < 2 * D; i += blockDim.x) {
+    float* acc = i < D ? p.dqw : p.dkw;
+    if (acc) unsafeAtomicAdd(acc + i % D, red[i / D][i % D]);
+  }
+}
+
 }  // namespace strata
 
 using namespace strata;
@@ -259,6 +387,21 @@ extern "C" int strata_hip_rope_qkv_pack_bwd(const strata_hip_rope_pack_bwd_args*
   const void* ptrs[6] = {a->dq, a->dk, a->dv, a->cos, a->sin, a->dqkv};
   for (int i = 0; i < 6; ++i)
     if ((uintptr_t)ptrs[i] & 15) return fail(STRATA_HIP_EINVAL, "rope_qkv_pack_bwd: pointers must be 16-byte aligned");
+  if (a->qk_norm != 0 && a->qk_norm != 1) return fail(STRATA_HIP_EINVAL, "rope_qkv_pack_bwd: qk_norm must be 0 or 1");
+  if (a->qk_norm) {
+    const int cph = a->layout == STRATA_HIP_ROPE_HALF ? a->head_dim / 16 : a->head_dim / 8;
+    if (cph < 1 || cph > 64 || (cph & (cph - 1)))
+      return fail(STRATA_HIP_EINVAL, "rope_qkv_pack_bwd: qk_norm needs D/16 (half) or D/8 (interleaved) a power of two <= 64");
+    if (!(a->qk_norm_eps >= 0.f)) return fail(STRATA_HIP_EINVAL, "rope_qkv_pack_bwd: qk_norm_eps must be >= 0");
+    if (!a->qkv || ((uintptr_t)a->qkv & 15))
+      return fail(STRATA_HIP_EINVAL, "rope_qkv_pack_bwd: qk_norm needs the forward's qkv, 16-byte aligned");
+    if (a->qkv_row_stride < 3 * C || a->qkv_row_stride % 8)
+      return fail(STRATA_HIP_EINVAL, "rope_qkv_pack_bwd: qkv row stride must be >= 3*H*D and a multiple of 8");
+    if (!a->q_norm_weight != !a->dq_norm_weight || !a->k_norm_weight != !a->dk_norm_weight)
+      return fail(STRATA_HIP_EINVAL, "rope_qkv_pack_bwd: a norm weight and its gradient accumulator go together");
+  } else if (a->q_norm_weight || a->k_norm_weight || a->dq_norm_weight || a->dk_norm_weight) {
+    return fail(STRATA_HIP_EINVAL, "rope_qkv_pack_bwd: norm weights given without qk_norm");
+  }
   RopeParams p = {};
   p.qkv = (const bf16*)a->dqkv;
   p.cos = a->cos;
@@ -279,6 +422,22 @@ extern "C" int strata_hip_rope_qkv_pack_bwd(const strata_hip_rope_pack_bwd_args*
   if (total == 0) return STRATA_HIP_OK;
   const int64_t blocks = (total + 255) / 256;
   if (blocks > 0x7fffffff) return fail(STRATA_HIP_EUNSUPPORTED, "rope_qkv_pack_bwd: too many tokens");
+  if (a->qk_norm) {
+    p.x = (const bf16*)a->qkv;
+    p.ldx = a->qkv_row_stride;
+    p.eps = a->qk_norm_eps;
+    p.qw = (const bf16*)a->q_norm_weight;
+    p.kw = (const bf16*)a->k_norm_weight;
+    p.dqw = a->dq_norm_weight;
+    p.dkw = a->dk_norm_weight;
+    // a bounded grid: the weight-gradient atomics are one per channel and block
+    const unsigned nb = (unsigned)(blocks < 2048 ? blocks : 2048);
+    if (a->layout == STRATA_HIP_ROPE_HALF)
+      hipLaunchKernelGGL(rope_unpack_norm_kernel<true>, dim3(nb), dim3(256), 0, (hipStream_t)stream, p, total);
+    else
+      hipLaunchKernelGGL(rope_unpack_norm_kernel<false>, dim3(nb), dim3(256), 0, (hipStream_t)stream, p, total);
+    return check_launch("rope_unpack_norm_kernel");
+  }
   if (a->layout == STRATA_HIP_ROPE_HALF)
     hipLaunchKernelGGL(rope_unpack_half_kernel, dim3((unsigned)blocks), dim3(256), 0, (hipStream_t)stream, p, total);
   else

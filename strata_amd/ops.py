@@ -5,9 +5,9 @@ allocator, and enqueues the kernel on torch's current stream of the input's
 device.  There is no CPU or eager fallback: CPU tensors are rejected and a
 missing library raises.  Every op has a fake (meta) implementation so that
 ``torch.compile`` traces through it.  ``na3d_fwd`` (full-grid queries),
-``gemm_bias_act`` (act none / GELU(tanh), added residual), ``layer_norm`` and
-``rope_qkv_pack`` (without qk_norm) have backwards on HIP kernels; the other
-ops' autograd formulas raise.
+``gemm_bias_act`` (act none / GELU(tanh) with an added residual, and the
+sigmoid gate), ``layer_norm`` and ``rope_qkv_pack`` (with or without qk_norm)
+have backwards on HIP kernels; the other ops' autograd formulas raise.
 """
 
 from __future__ import annotations
@@ -296,15 +296,19 @@ def _(qkv, cos, sin, heads, rope_layout, qk_norm=False, qk_norm_eps=1e-6, q_norm
 def _rope_setup_context(ctx, inputs, output):
     qkv, cos, sin, heads, rope_layout, qk_norm, qk_norm_eps, q_norm_weight, k_norm_weight = inputs
     ctx.qk_norm, ctx.heads, ctx.layout = bool(qk_norm), int(heads), int(rope_layout)
+    ctx.qk_norm_eps = float(qk_norm_eps)
     ctx.qkv_shape = tuple(qkv.shape)
-    ctx.save_for_backward(cos, sin)
+    if ctx.qk_norm:  # the RMSNorm backward recomputes the norms from the input
+        ctx.save_for_backward(cos, sin, qkv, q_norm_weight, k_norm_weight)
+    else:
+        ctx.save_for_backward(cos, sin)
 
 
 def _rope_backward(ctx, dq, dk, dv):
-    """d(qkv) = (R(-theta) dq, R(-theta) dk, dv) in qkv's (3, H, D) column layout (no qk_norm)."""
-    if ctx.qk_norm:
-        raise RuntimeError("strata_hip::rope_qkv_pack: backward with qk_norm is not implemented")
-    cos, sin = ctx.saved_tensors
+    """d(qkv) = (R(-theta) dq, R(-theta) dk, dv) in qkv's (3, H, D) column layout;
+    with qk_norm, q and k further through the RMSNorm backward (and the norm
+    weights' gradients, summed over tokens and heads in fp32)."""
+    cos, sin = ctx.saved_tensors[:2]
     B, Z, Y, X, C3 = ctx.qkv_shape
     D = C3 // (3 * ctx.heads)
     grads = [g.contiguous() if g is not None else torch.zeros((B, Z, Y, X, ctx.heads, D), dtype=torch.bfloat16,
@@ -319,10 +323,25 @@ def _rope_backward(ctx, dq, dk, dv):
     a.table_z = cos.shape[1]
     a.heads, a.head_dim, a.layout = ctx.heads, D, ctx.layout
     a.dqkv_row_stride = C3
+    dws = [None, None]
+    if ctx.qk_norm:
+        qkv, qw, kw = ctx.saved_tensors[2:]
+        qkv = qkv.contiguous()
+        a.qkv, a.qkv_row_stride = qkv.data_ptr(), C3
+        a.qk_norm, a.qk_norm_eps = 1, ctx.qk_norm_eps
+        for i, w in enumerate((qw, kw)):
+            if w is not None:
+                dws[i] = torch.zeros(D, dtype=torch.float32, device=cos.device)
+        a.q_norm_weight = qw.data_ptr() if qw is not None else None
+        a.k_norm_weight = kw.data_ptr() if kw is not None else None
+        a.dq_norm_weight = dws[0].data_ptr() if dws[0] is not None else None
+        a.dk_norm_weight = dws[1].data_ptr() if dws[1] is not None else None
     if dqkv.numel():
         with torch.cuda.device(cos.device):
             _lib.call("strata_hip_rope_qkv_pack_bwd", a, _stream(dqkv))
-    return dqkv, None, None, None, None, None, None, None, None
+    if ctx.qk_norm:
+        dws = [d.to(w.dtype) if d is not None else None for d, w in zip(dws, ctx.saved_tensors[3:])]
+    return dqkv, None, None, None, None, None, None, dws[0], dws[1]
 
 
 rope_qkv_pack.register_autograd(_rope_backward, setup_context=_rope_setup_context)

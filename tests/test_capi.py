@@ -220,3 +220,26 @@ def test_na3d_bwd_validation(lib):
     assert lib.strata_hip_na3d_bwd(ctypes.byref(a), None) == _lib.EUNSUPPORTED
     a.batch = 0
     assert lib.strata_hip_na3d_bwd(ctypes.byref(a), None) == _lib.OK
+
+
+def test_rope_pack_bwd_qk_norm_validation(lib):
+    a = _lib.RopePackBwdArgs()
+    a.dq = a.dk = a.dv = a.cos = a.sin = a.dqkv = 0x1000
+    a.batch, a.heads, a.head_dim, a.layout, a.table_z = 1, 2, 64, _lib.ROPE_HALF, 1
+    a.grid[:] = [4, 8, 8]
+    a.dqkv_row_stride = 384
+    a.q_norm_weight = 0x2000  # a weight without qk_norm
+    assert lib.strata_hip_rope_qkv_pack_bwd(ctypes.byref(a), None) == _lib.EINVAL
+    assert "without qk_norm" in lib.strata_hip_last_error().decode()
+    a.qk_norm = 1  # the forward's qkv is needed to recompute the norms
+    assert lib.strata_hip_rope_qkv_pack_bwd(ctypes.byref(a), None) == _lib.EINVAL
+    assert "forward's qkv" in lib.strata_hip_last_error().decode()
+    a.qkv, a.qkv_row_stride = 0x3000, 384
+    assert lib.strata_hip_rope_qkv_pack_bwd(ctypes.byref(a), None) == _lib.EINVAL
+    assert "accumulator" in lib.strata_hip_last_error().decode()
+    a.dq_norm_weight = 0x4000
+    a.head_dim, a.dqkv_row_stride, a.qkv_row_stride = 48, 288, 288  # D/16 = 3
+    assert lib.strata_hip_rope_qkv_pack_bwd(ctypes.byref(a), None) == _lib.EINVAL
+    assert "power of two" in lib.strata_hip_last_error().decode()
+    a.head_dim, a.dqkv_row_stride, a.qkv_row_stride, a.batch = 64, 384, 384, 0
+    assert lib.strata_hip_rope_qkv_pack_bwd(ctypes.byref(a), None) == _lib.OK
