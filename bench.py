@@ -230,7 +230,10 @@ def bench_step_io(device, reps, warmup):
     fp32 state [6, 80, 16, 64, 64] -> normalised bf16 tokens (patch 1), and head
     tokens [6, 8, 32, 32, 640] (2x2x2 cells, channels last) -> denormalised,
     state-updated fp32 state with a floor on one channel.  Algorithmic bytes =
-    each input read once + the output written once (the 80-entry tables aside)."""
+    each input read once + the output written once (the 80-entry tables aside).
+    ``dealias``: the two filter passes (y, x; the (1, 4, 6, 4, 1) low-pass with
+    patch (1, 2, 2), normalisation fused) of a dealiased patch embedding of the
+    same state, each pass reading and writing the fp32 state once."""
     import torch
 
     from strata_amd import ops
@@ -245,9 +248,12 @@ def bench_step_io(device, reps, warmup):
     floor = torch.full((C,), float("nan"), device=device)
     floor[7] = 0.0
     n = state.numel()
+    taps = [0.0625, 0.25, 0.375, 0.25, 0.0625]
     fns = (
         ("patchify", lambda: ops.state_patchify(state, mean, std, (1, 1, 1)), n * (4 + 2)),
         ("update", lambda: ops.state_update(pred, state, mean, std, src, floor, grid, (2, 2, 2), 1), n * (2 + 4 + 4)),
+        ("dealias", lambda: ops.dealias_axis(ops.dealias_axis(state, mean, std, 1, 2, taps), None, None, 2, 2, taps),
+         2 * n * (4 + 4)),
     )
     out = {"workload": f"rollout step I/O: state [{B}, {C}, 16, 64, 64] fp32 <-> bf16 tokens (patchify 1, update 2x2x2)"}
     for name, fn, nbytes in fns:

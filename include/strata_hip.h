@@ -26,7 +26,7 @@
 extern "C" {
 #endif
 
-#define STRATA_HIP_ABI_VERSION 4
+#define STRATA_HIP_ABI_VERSION 5
 
 enum strata_hip_status {
   STRATA_HIP_OK = 0,
@@ -344,6 +344,38 @@ typedef struct strata_hip_state_patchify_args {
 } strata_hip_state_patchify_args;
 
 int strata_hip_state_patchify(const strata_hip_state_patchify_args* args, void* stream);
+
+/* ---------------------------------------------------------------------------
+ * Dealiased patch embedding (DealiasedPatchEmbed3D, screamcast/dealias.py:28-143):
+ * a stride-1 valid Conv3d (kernel = patch) followed by a per-axis low-pass,
+ * replicate-padded by (k-1)/2 below and the rest above, decimated by the patch
+ * stride.  Both stages are linear and each axis filter sums to 1, so the
+ * embedding equals the plain patch embedding (state_patchify + GEMM with the
+ * same proj weight and bias) of the state filtered, per decimated axis, as
+ *   dst[.., i, ..] = sum_{t < taps} filter[t] *
+ *                    n(src[.., clamp(p*(i/p) - lo + t, 0, S - p) + i % p, ..])
+ * with S the grid size and p the patch size on that axis, lo = (taps - 1) / 2,
+ * and n(v) = (v - mean[c]) / std[c] (0 for non-finite v) when mean/std are
+ * given (the input normalisation, fused into the first pass), else v.
+ * src, dst: fp32 [B, C, Z, Y, X] contiguous, not aliased.  filter: the axis
+ * taps already divided by their sum (the reference's dealias_filter is their
+ * outer product over the axes); axes with patch 1 take no pass.
+ * ------------------------------------------------------------------------- */
+typedef struct strata_hip_dealias_axis_args {
+  const float* src;
+  float* dst;
+  const float* mean; /* [C] or NULL */
+  const float* std;  /* [C] or NULL (with mean) */
+  int32_t batch;
+  int32_t channels;
+  int32_t grid[3];   /* Z, Y, X */
+  int32_t axis;      /* 0: Z, 1: Y, 2: X */
+  int32_t patch;     /* patch size along the axis, divides grid[axis] */
+  int32_t taps;      /* 1..16 */
+  float filter[16];
+} strata_hip_dealias_axis_args;
+
+int strata_hip_dealias_axis(const strata_hip_dealias_axis_args* args, void* stream);
 
 /* ---------------------------------------------------------------------------
  * Pipeline step, output side: unpatchify of the prediction tokens, the target

@@ -7,6 +7,9 @@ Follows the pipeline of the reference:
     ``PatchEmbed3D`` (the ``proj`` conv that ``DealiasedPatchEmbed3D``,
     screamcast/dealias.py:88-97, keeps state-dict compatible with), written as a
     patchify in the conv weight's (c, dz, dy, dx) order and a matmul;
+  * ``DealiasedPatchEmbed3D.forward`` (screamcast/dealias.py:111-143) as the
+    reference writes it: stride-1 conv, replicate pad, depthwise low-pass with
+    stride = patch;
   * target denormalisation ``RunningNorm2d.denormalize`` (normalization.py:102-107):
     ``x * (sqrt(var) + eps) + mean`` in fp32, cast back to the prediction's dtype;
   * the prognostic update of ``MixedPredictionAsymmetric.step``
@@ -22,6 +25,7 @@ from __future__ import annotations
 from typing import Optional, Sequence
 
 import torch
+import torch.nn.functional as F
 from torch import Tensor
 
 
@@ -70,6 +74,33 @@ def patch_embed(state: Tensor, weight: Tensor, bias: Optional[Tensor], patch: Se
     t = patchify(state.float(), patch)
     y = t @ weight.float().reshape(weight.shape[0], -1).T
     return y + bias.float() if bias is not None else y
+
+
+def dealiased_patch_embed(
+    x: Tensor, weight: Tensor, bias: Optional[Tensor], patch: Sequence[int], resample_filter: Sequence[float]
+) -> Tensor:
+    """``DealiasedPatchEmbed3D.forward`` (screamcast/dealias.py:111-143) in float64,
+    channels-last out ``[B, Z/pz, Y/py, X/px, E]``: the stride-1 valid conv
+    (:113), the per-axis filter (identity on axes with patch 1, :101-108)
+    normalised by the product of the axis sums (:109), the replicate pad of
+    ``(k-1)//2`` below and the rest above (:120-133), and the depthwise conv
+    with stride = patch (:135-142)."""
+    pz, py, px = patch
+    E = weight.shape[0]
+    s1 = F.conv3d(x.double(), weight.double(), None if bias is None else bias.double(), stride=1, padding=0)
+    fa = torch.as_tensor(resample_filter, dtype=torch.float64)
+    one = torch.ones(1, dtype=torch.float64)
+    fd, fh, fw = (one if p == 1 else fa for p in (pz, py, px))
+    f3d = fd[:, None, None] * fh[None, :, None] * fw[None, None, :]
+    f3d = (f3d / (fd.sum() * fh.sum() * fw.sum()))[None, None]
+    kd, kh, kw = f3d.shape[2:]
+    pads = []
+    for k in (kw, kh, kd):  # F.pad order: last axis first
+        pads += [(k - 1) // 2, (k - 1) - (k - 1) // 2]
+    if kd > 1 or kh > 1 or kw > 1:
+        s1 = F.pad(s1, pads, mode="replicate")
+    y = F.conv3d(s1, f3d.repeat(E, 1, 1, 1, 1), groups=E, stride=(pz, py, px), padding=0)
+    return y.permute(0, 2, 3, 4, 1)
 
 
 def state_update(

@@ -14,7 +14,7 @@ from pathlib import Path
 
 LIB_PATH = Path(__file__).resolve().parent / "libstrata_hip.so"
 
-ABI_VERSION = 4
+ABI_VERSION = 5
 
 OK = 0
 EINVAL = -1
@@ -206,6 +206,22 @@ class RopePackBwdArgs(ctypes.Structure):
     ]
 
 
+class DealiasAxisArgs(ctypes.Structure):
+    _fields_ = [
+        ("src", ctypes.c_void_p),
+        ("dst", ctypes.c_void_p),
+        ("mean", ctypes.c_void_p),
+        ("std", ctypes.c_void_p),
+        ("batch", ctypes.c_int32),
+        ("channels", ctypes.c_int32),
+        ("grid", ctypes.c_int32 * 3),
+        ("axis", ctypes.c_int32),
+        ("patch", ctypes.c_int32),
+        ("taps", ctypes.c_int32),
+        ("filter", ctypes.c_float * 16),
+    ]
+
+
 class StatePatchifyArgs(ctypes.Structure):
     _fields_ = [
         ("state", ctypes.c_void_p),
@@ -248,6 +264,7 @@ EXPORTS = {
     "strata_hip_cube_pad_faces": ([ctypes.POINTER(CubePadArgs), ctypes.c_void_p], ctypes.c_int),
     "strata_hip_cube_crop": ([ctypes.POINTER(CubeCropArgs), ctypes.c_void_p], ctypes.c_int),
     "strata_hip_state_patchify": ([ctypes.POINTER(StatePatchifyArgs), ctypes.c_void_p], ctypes.c_int),
+    "strata_hip_dealias_axis": ([ctypes.POINTER(DealiasAxisArgs), ctypes.c_void_p], ctypes.c_int),
     "strata_hip_state_update": ([ctypes.POINTER(StateUpdateArgs), ctypes.c_void_p], ctypes.c_int),
     "strata_hip_last_error": ([], ctypes.c_char_p),
     "strata_hip_abi_version": ([], ctypes.c_int),

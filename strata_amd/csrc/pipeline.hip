@@ -204,9 +204,145 @@ static int pipe_setup(PipeParams& p, const char* name, int B, int C, const int32
   return STRATA_HIP_OK;
 }
 
+// One axis pass of the dealiasing low-pass (see strata_hip_dealias_axis).  The
+// tensor is viewed as [outer, S, inner] around the filtered axis.  A wave owns
+// DEALIAS_LPW lines and its lanes step through the lines' contiguous floats, so
+// every index below the lane level is wave-uniform (scalar registers, no
+// per-thread division), and the lines' loads of one tap are issued together:
+//   x axis (inner = 1): a line is one row of S floats; output i of the row
+//     reads its taps along the row;
+//   y, z axes: a line is (o, i), the `inner` floats of output row i; its taps
+//     are the rows clamp(P*(i/P) - lo + t, 0, S - P) + i%P of the same o.
+struct DealiasParams {
+  const float* src;
+  float* dst;
+  const float* mean;
+  const float* std;
+  int64_t lines;  // x: outer rows; y, z: outer * S
+  int64_t inner;  // stride of the axis in floats
+  int64_t cdiv;   // lines (x) or outer index (y, z) per channel step: c = (. / cdiv) % C
+  int C, S, P, lo, taps;
+  float f[16];
+};
+
+constexpr int DEALIAS_LPW = 8;  // lines per wave, their loads of one tap issued together
+
+template <bool XAXIS>
+__global__ __launch_bounds__(256) void dealias_axis_kernel(DealiasParams p) {
+  constexpr int R = DEALIAS_LPW;
+  const int64_t line0 = ((int64_t)blockIdx.x * 4 + __builtin_amdgcn_readfirstlane(threadIdx.x >> 6)) * R;
+  const int lane = threadIdx.x & 63;
+  if (line0 >= p.lines) return;  // uniform per wave
+  const float* src[R];
+  float* dst[R];
+  float m[R], sd[R];
+  int j0[R], u[R];
+  bool live[R];
+#pragma unroll
+  for (int r = 0; r < R; ++r) {
+    const int64_t line = line0 + r < p.lines ? line0 + r : p.lines - 1;  // a repeated last line is harmless
+    live[r] = line0 + r < p.lines;
+    int64_t o = line;  // x: the row; y, z: the outer index
+    int irow = 0;      // y, z: the output row
+    if constexpr (!XAXIS) {
+      o = line / p.S;
+      irow = (int)(line - o * p.S);
+    }
+    m[r] = 0.f;
+    sd[r] = 1.f;
+    if (p.mean) {
+      const int c = (int)((o / p.cdiv) % p.C);
+      m[r] = p.mean[c];
+      sd[r] = p.std[c];
+    }
+    if constexpr (XAXIS) {
+      src[r] = p.src + line * p.S;
+      dst[r] = p.dst + line * p.S;
+    } else {
+      j0[r] = p.P * (irow / p.P) - p.lo;
+      u[r] = irow % p.P;
+      src[r] = p.src + o * p.S * p.inner;
+      dst[r] = p.dst + line * p.inner;
+    }
+  }
+  const int64_t n = XAXIS ? p.S : p.inner;
+  for (int64_t k = lane; k < n; k += 64) {
+    int xj0 = 0, xu = 0;
+    if constexpr (XAXIS) {
+      xj0 = p.P * ((int)k / p.P) - p.lo;
+      xu = (int)k % p.P;
+    }
+    float acc[R];
+#pragma unroll
+    for (int r = 0; r < R; ++r) acc[r] = 0.f;
+    for (int t = 0; t < p.taps; ++t) {
+      float v[R];
+#pragma unroll
+      for (int r = 0; r < R; ++r) {
+        if constexpr (XAXIS)
+          v[r] = src[r][min(max(xj0 + t, 0), p.S - p.P) + xu];
+        else
+          v[r] = src[r][(int64_t)(min(max(j0[r] + t, 0), p.S - p.P) + u[r]) * p.inner + k];
+      }
+#pragma unroll
+      for (int r = 0; r < R; ++r) {
+        float nv = v[r];
+        if (p.mean) nv = (v[r] - m[r]) / sd[r];
+        if (!__builtin_isfinite(v[r])) nv = 0.f;
+        acc[r] = fmaf(p.f[t], nv, acc[r]);
+      }
+    }
+#pragma unroll
+    for (int r = 0; r < R; ++r)
+      if (live[r]) dst[r][k] = acc[r];
+  }
+}
+
 }  // namespace strata
 
 using namespace strata;
+
+extern "C" int strata_hip_dealias_axis(const strata_hip_dealias_axis_args* a, void* stream) {
+  if (!a) return fail(STRATA_HIP_EINVAL, "dealias_axis: null args");
+  if (!a->src || !a->dst) return fail(STRATA_HIP_EINVAL, "dealias_axis: null tensor pointer");
+  if ((a->mean == nullptr) != (a->std == nullptr))
+    return fail(STRATA_HIP_EINVAL, "dealias_axis: mean and std must both be given or both be NULL");
+  if (a->batch < 0 || a->channels <= 0) return fail(STRATA_HIP_EINVAL, "dealias_axis: bad batch/channels");
+  if (a->grid[0] <= 0 || a->grid[1] <= 0 || a->grid[2] <= 0) return fail(STRATA_HIP_EINVAL, "dealias_axis: bad grid");
+  if (a->axis < 0 || a->axis > 2) return fail(STRATA_HIP_EINVAL, "dealias_axis: axis must be 0, 1 or 2");
+  const int S = a->grid[a->axis];
+  if (a->patch <= 0 || S % a->patch != 0)
+    return fail(STRATA_HIP_EINVAL, "dealias_axis: patch must be positive and divide the grid on the axis");
+  if (a->taps < 1 || a->taps > 16) return fail(STRATA_HIP_EINVAL, "dealias_axis: taps must be in 1..16");
+  if (a->src == a->dst) return fail(STRATA_HIP_EINVAL, "dealias_axis: src and dst must not alias");
+  DealiasParams p = {};
+  p.src = a->src;
+  p.dst = a->dst;
+  p.mean = a->mean;
+  p.std = a->std;
+  p.C = a->channels;
+  p.S = S;
+  p.P = a->patch;
+  p.taps = a->taps;
+  p.lo = (a->taps - 1) / 2;
+  for (int t = 0; t < a->taps; ++t) p.f[t] = a->filter[t];
+  const int64_t Z = a->grid[0], Y = a->grid[1], X = a->grid[2];
+  const int64_t total = (int64_t)a->batch * a->channels * Z * Y * X;
+  if (total == 0) return STRATA_HIP_OK;
+  if (total > ((int64_t)1 << 40)) return fail(STRATA_HIP_EUNSUPPORTED, "dealias_axis: problem too large");
+  // [outer, S, inner] around the axis; cdiv: outer indices (y, z) or rows (x) per channel
+  p.inner = a->axis == 2 ? 1 : (a->axis == 1 ? X : Y * X);
+  const int64_t outer = total / (S * p.inner);
+  p.lines = a->axis == 2 ? outer : outer * S;
+  p.cdiv = a->axis == 0 ? 1 : (a->axis == 1 ? Z : Z * Y);
+  const int64_t blocks = (p.lines + 4 * DEALIAS_LPW - 1) / (4 * DEALIAS_LPW);
+  if (blocks > 0x7fffffff) return fail(STRATA_HIP_EUNSUPPORTED, "dealias_axis: problem too large for one launch");
+  if (a->axis == 2)
+    hipLaunchKernelGGL(dealias_axis_kernel<true>, dim3((unsigned)blocks), dim3(256), 0, (hipStream_t)stream, p);
+  else
+    hipLaunchKernelGGL(dealias_axis_kernel<false>, dim3((unsigned)blocks), dim3(256), 0, (hipStream_t)stream, p);
+  return check_launch("dealias_axis_kernel");
+}
 
 extern "C" int strata_hip_state_patchify(const strata_hip_state_patchify_args* a, void* stream) {
   if (!a) return fail(STRATA_HIP_EINVAL, "state_patchify: null args");

@@ -29,6 +29,7 @@ __all__ = [
     "cube_pad_faces",
     "cube_crop",
     "state_patchify",
+    "dealias_axis",
     "state_update",
 ]
 
@@ -653,6 +654,55 @@ def _(state, mean, std, patch):
 
 
 state_patchify.register_autograd(_no_backward("strata_hip::state_patchify"))
+
+
+@torch.library.custom_op("strata_hip::dealias_axis", mutates_args=())
+def dealias_axis(
+    state: Tensor, mean: Optional[Tensor], std: Optional[Tensor], axis: int, patch: int, taps: Sequence[float]
+) -> Tensor:
+    """One axis of the dealiasing low-pass of ``DealiasedPatchEmbed3D``
+    (screamcast/dealias.py:111-143) moved in front of the patch conv: along
+    ``axis`` (0: Z, 1: Y, 2: X) of the fp32 state ``[B, C, Z, Y, X]``,
+    ``out[.., i, ..] = sum_t taps[t] * n(state[.., clamp(p*(i//p) - lo + t, 0, S - p) + i % p, ..])``
+    with ``lo = (len(taps) - 1) // 2`` (the replicate pad of the stride-1 conv's
+    output) and ``n`` the input normalisation when ``mean``/``std`` are given.
+    ``taps``: the axis filter divided by its sum (1 to 16 taps)."""
+    name = "dealias_axis"
+    dev = _require_gpu(name, state)
+    if state.dtype != torch.float32 or state.dim() != 5:
+        raise ValueError(f"{name}: state must be float32 [B, C, Z, Y, X], got {state.dtype} {tuple(state.shape)}")
+    if (mean is None) != (std is None):
+        raise ValueError(f"{name}: give both mean and std, or neither")
+    taps = [float(t) for t in taps]
+    if not 1 <= len(taps) <= 16:
+        raise ValueError(f"{name}: 1 to 16 taps, got {len(taps)}")
+    B, C, Z, Y, X = state.shape
+    if axis not in (0, 1, 2) or patch <= 0 or (Z, Y, X)[axis] % patch:
+        raise ValueError(f"{name}: patch {patch} does not divide axis {axis} of the grid {(Z, Y, X)}")
+    tabs = _state_tables(name, dev, C, mean=mean, std=std)
+    src = state.contiguous()
+    out = torch.empty_like(src)
+    if out.numel() == 0:
+        return out
+    a = _lib.DealiasAxisArgs()
+    a.src, a.dst = src.data_ptr(), out.data_ptr()
+    a.mean = tabs["mean"].data_ptr() if tabs["mean"] is not None else None
+    a.std = tabs["std"].data_ptr() if tabs["std"] is not None else None
+    a.batch, a.channels = B, C
+    a.grid[:] = [Z, Y, X]
+    a.axis, a.patch, a.taps = axis, patch, len(taps)
+    a.filter[: len(taps)] = taps
+    with torch.cuda.device(dev):
+        _lib.call("strata_hip_dealias_axis", a, _stream(state))
+    return out
+
+
+@dealias_axis.register_fake
+def _(state, mean, std, axis, patch, taps):
+    return torch.empty_like(state.contiguous())
+
+
+dealias_axis.register_autograd(_no_backward("strata_hip::dealias_axis"))
 
 
 @torch.library.custom_op("strata_hip::state_update", mutates_args=())

@@ -26,6 +26,7 @@ STRUCTS = {
     "strata_hip_cube_crop_args": _lib.CubeCropArgs,
     "strata_hip_state_patchify_args": _lib.StatePatchifyArgs,
     "strata_hip_state_update_args": _lib.StateUpdateArgs,
+    "strata_hip_dealias_axis_args": _lib.DealiasAxisArgs,
 }
 
 
@@ -243,3 +244,26 @@ def test_rope_pack_bwd_qk_norm_validation(lib):
     assert "power of two" in lib.strata_hip_last_error().decode()
     a.head_dim, a.dqkv_row_stride, a.qkv_row_stride, a.batch = 64, 384, 384, 0
     assert lib.strata_hip_rope_qkv_pack_bwd(ctypes.byref(a), None) == _lib.OK
+
+
+def test_dealias_axis_validation(lib):
+    a = _lib.DealiasAxisArgs()
+    a.src, a.dst = 0x1000, 0x2000
+    a.batch, a.channels, a.axis, a.patch, a.taps = 1, 3, 1, 3, 5
+    a.grid[:] = [4, 8, 8]
+    assert lib.strata_hip_dealias_axis(ctypes.byref(a), None) == _lib.EINVAL  # 3 does not divide 8
+    assert "divide" in lib.strata_hip_last_error().decode()
+    a.patch, a.taps = 2, 17
+    assert lib.strata_hip_dealias_axis(ctypes.byref(a), None) == _lib.EINVAL
+    assert "taps" in lib.strata_hip_last_error().decode()
+    a.taps, a.axis = 5, 3
+    assert lib.strata_hip_dealias_axis(ctypes.byref(a), None) == _lib.EINVAL
+    assert "axis" in lib.strata_hip_last_error().decode()
+    a.axis, a.dst = 1, 0x1000
+    assert lib.strata_hip_dealias_axis(ctypes.byref(a), None) == _lib.EINVAL
+    assert "alias" in lib.strata_hip_last_error().decode()
+    a.dst, a.mean = 0x2000, 0x3000
+    assert lib.strata_hip_dealias_axis(ctypes.byref(a), None) == _lib.EINVAL
+    assert "both" in lib.strata_hip_last_error().decode()
+    a.mean, a.batch = None, 0
+    assert lib.strata_hip_dealias_axis(ctypes.byref(a), None) == _lib.OK

@@ -1,6 +1,7 @@
 """The rollout step's HIP kernels (state normalise + patchify, state update)
-and the patch embedding against the CPU oracle: bit-exact for the data
-movement and the fp32/bf16 element math, through the C ABI."""
+and the patch embeddings (plain and dealiased) against the CPU oracle:
+bit-exact for the data movement and the fp32/bf16 element math, through the C
+ABI; relative L2 <= 1e-2 for the bf16 embedding GEMMs."""
 
 import ctypes
 
@@ -9,7 +10,7 @@ import torch
 
 from oracle import pipeline as O
 from strata_amd import _lib, ops
-from strata_amd.pipeline import PatchEmbed3D, StepNorms
+from strata_amd.pipeline import DealiasedPatchEmbed3D, PatchEmbed3D, StepNorms
 
 from .conftest import rel_l2
 
@@ -115,3 +116,65 @@ def test_step_norms_from_running_norm_buffers(gpu):
     assert n.src_channel.dtype == torch.int32 and n.src_channel.tolist() == [0, 1, -1, 3]
     n2 = n.to(gpu)
     assert n2.tgt_std.is_cuda and torch.equal(n2.tgt_mean.cpu(), (mean * 2).reshape(-1))
+
+
+DEALIAS_CASES = [  # (B, C, grid, patch, resample_filter)
+    (2, 5, (4, 16, 12), (1, 2, 2), (1, 4, 6, 4, 1)),
+    (1, 3, (4, 8, 8), (2, 2, 2), (1, 1)),
+    (1, 4, (2, 16, 8), (1, 4, 2), (1, 3, 3, 1)),
+    (2, 80, (2, 8, 8), (1, 2, 2), (1, 4, 6, 4, 1)),
+]
+
+
+@pytest.mark.parametrize("case", DEALIAS_CASES, ids=str)
+@pytest.mark.parametrize("normed", [False, True])
+def test_dealiased_patch_embed_vs_oracle(gpu, case, normed):
+    """DealiasedPatchEmbed3D (filter passes + patchify + GEMM) against the
+    reference's stride-1 conv -> replicate pad -> strided low-pass
+    (screamcast/dealias.py:111-143) in float64, on the normalised state
+    rounded as the GPU path rounds its weights (bf16)."""
+    B, C, grid, patch, filt = case
+    torch.manual_seed(0)
+    emb = DealiasedPatchEmbed3D(*grid, patch_size=patch, in_chans=C, embed_dim=48, resample_filter=filt)
+    g = torch.Generator().manual_seed(8)
+    x = torch.randn(B, C, *grid, generator=g) * 2 + 0.5
+    mean, std = (torch.randn(C, generator=g), torch.rand(C, generator=g) + 0.5) if normed else (None, None)
+    if normed:
+        x[0, 0, 0, 0, 0] = float("nan")  # normalised to 0, as RunningNorm2d does
+    w = emb.proj.weight.detach().bfloat16().double()
+    b = emb.proj.bias.detach().bfloat16().double()
+    ref = O.dealiased_patch_embed(O.normalize(x, mean, std), w, b, patch, filt)
+    with torch.no_grad():
+        got = emb.to(gpu)(x.to(gpu), None if mean is None else mean.to(gpu), None if std is None else std.to(gpu))
+    assert got.shape == ref.shape
+    assert torch.isfinite(got.float()).all()
+    assert rel_l2(got.float().cpu(), ref.float()) <= 1e-2
+
+
+def test_dealias_axis_pass_vs_fp64(gpu):
+    """One filter pass per axis against the clamped-tap sum in float64."""
+    g = torch.Generator().manual_seed(12)
+    x = torch.randn(2, 3, 6, 10, 12, generator=g)
+    taps = [0.0625, 0.25, 0.375, 0.25, 0.0625]
+    for axis, p in ((0, 2), (1, 2), (2, 4), (2, 1)):
+        got = ops.dealias_axis(x.to(gpu), None, None, axis, p, taps).cpu()
+        S = x.shape[2 + axis]
+        i = torch.arange(S)
+        ref = torch.zeros_like(x, dtype=torch.float64)
+        for t, f in enumerate(taps):
+            src = (p * (i // p) - 2 + t).clamp(0, S - p) + i % p
+            ref += f * x.double().index_select(2 + axis, src)
+        assert (got.double() - ref).abs().max() <= 1e-6 * ref.abs().max(), (axis, p)
+
+
+def test_dealiased_embed_is_state_dict_compatible(gpu):
+    """The dealiased embedding loads a PatchEmbed3D checkpoint under strict=True
+    (proj.weight / proj.bias; the filter buffer is not persistent), and a
+    one-tap filter makes it the plain embedding."""
+    plain = PatchEmbed3D((1, 2, 2), 4, 32)
+    deal = DealiasedPatchEmbed3D(2, 8, 8, patch_size=(1, 2, 2), in_chans=4, embed_dim=32, resample_filter=(5.0,))
+    deal.load_state_dict(plain.state_dict(), strict=True)
+    assert "dealias_filter" not in deal.state_dict()
+    x = torch.randn(1, 4, 2, 8, 8, generator=torch.Generator().manual_seed(13)).to(gpu)
+    with torch.no_grad():
+        assert torch.equal(deal.to(gpu)(x), plain.to(gpu)(x))
