@@ -276,8 +276,10 @@ def bench_step_io(device, reps, warmup):
 def bench_backward(device, reps, warmup):
     """Training kernels: the NA3D backward at the configs[1] shape ([2, 8, 64, 64] tokens,
     8 x 64 heads, W=(3,7,7), bf16; FLOPs = 2.5 x the forward's 4*N*|W|*D, the usual
-    attention-backward count) and the GEMM-GELU backward's fused epilogue GEMM
-    (gelu'(x @ w.T + b) * dout) at the configs[3] fc1 shape."""
+    attention-backward count) as training runs it (given the forward's log-sum-exp,
+    ``na3d_bwd``) and with the statistic recomputed (``na3d_bwd_recompute``), and the
+    GEMM-GELU backward's fused epilogue GEMM (gelu'(x @ w.T + b) * dout) at the
+    configs[3] fc1 shape."""
     import torch
 
     from strata_amd import _lib, ops
@@ -285,7 +287,7 @@ def bench_backward(device, reps, warmup):
     g = torch.Generator(device=device).manual_seed(0)
     shape, ker = (2, 8, 64, 64, 8, 64), [3, 7, 7]
     q, k, v, do = (torch.randn(shape, generator=g, device=device).bfloat16() for _ in range(4))
-    out = torch.ops.strata_hip.na3d_fwd(q, k, v, ker, [1, 1, 1], None, [0, 0, 0], list(shape[1:4]))
+    out, lse = torch.ops.strata_hip.na3d_fwd_lse(q, k, v, ker, [1, 1, 1], None)
     M, N, K = 131072, 4096, 1024
     x = torch.randn(M, K, generator=g, device=device).bfloat16()
     w = (torch.randn(N, K, generator=g, device=device) * K**-0.5).bfloat16()
@@ -293,7 +295,9 @@ def bench_backward(device, reps, warmup):
     dy = torch.randn(M, N, generator=g, device=device).bfloat16()
     B, Z, Y, X, H, D = shape
     fns = (
-        ("na3d_bwd", lambda: ops.na3d_bwd(q, k, v, out, do, ker, [1, 1, 1], None),
+        ("na3d_bwd", lambda: ops.na3d_bwd(q, k, v, out, do, ker, [1, 1, 1], None, lse),
+         2.5 * 4.0 * B * Z * Y * X * H * 147 * D),
+        ("na3d_bwd_recompute", lambda: ops.na3d_bwd(q, k, v, out, do, ker, [1, 1, 1], None),
          2.5 * 4.0 * B * Z * Y * X * H * 147 * D),
         ("gelu_grad_gemm", lambda: ops.gemm_bias_act(x, w, b, dy, _lib.ACT_GELU_TANH_GRAD, _lib.RES_MUL),
          2.0 * M * N * K),

@@ -26,7 +26,7 @@
 extern "C" {
 #endif
 
-#define STRATA_HIP_ABI_VERSION 5
+#define STRATA_HIP_ABI_VERSION 6
 
 enum strata_hip_status {
   STRATA_HIP_OK = 0,
@@ -91,6 +91,10 @@ typedef struct strata_hip_na3d_args {
   int64_t k_stride[5];
   int64_t v_stride[5];
   int64_t o_stride[5]; /* strides of `out` over (b, z', y', x', h) */
+  float* lse;          /* fp32 [B, Z', Y', X', H] contiguous, or NULL: each query's
+                          log2-sum-exp over its window of the log2-unit scores
+                          scale*log2(e)*q.k (q rounded to bf16 after the scaling on
+                          the bf16 path), the statistic strata_hip_na3d_bwd needs */
 } strata_hip_na3d_args;
 
 int strata_hip_na3d_fwd(const strata_hip_na3d_args* args, void* stream);
@@ -102,7 +106,10 @@ int strata_hip_na3d_fwd(const strata_hip_na3d_args* args, void* stream);
  * forward.  q, k, v, out, dout, dq, dk, dv: contiguous heads-last
  * [B, Z, Y, X, H, D], one dtype (f32 or bf16; fp32 math), 16-byte aligned;
  * head_dim 32, 64 or 128.  workspace: 2 * B*Z*Y*X*H floats of caller memory
- * (per-query log-sum-exp and rowsum(dout * out)), overwritten.
+ * (per-query log-sum-exp and rowsum(dout * out)), overwritten.  lse: the
+ * forward's lse output for the same q, k (strata_hip_na3d_fwd over the whole
+ * grid), or NULL; given, the log-sum-exp is not recomputed (only the rowsum
+ * half of the workspace is written).
  * ------------------------------------------------------------------------- */
 typedef struct strata_hip_na3d_bwd_args {
   const void* q;
@@ -122,6 +129,7 @@ typedef struct strata_hip_na3d_bwd_args {
   int32_t kernel[3];
   int32_t dilation[3];
   float scale;
+  const float* lse; /* [B, Z, Y, X, H] from the forward, or NULL */
 } strata_hip_na3d_bwd_args;
 
 int strata_hip_na3d_bwd(const strata_hip_na3d_bwd_args* args, void* stream);

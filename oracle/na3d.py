@@ -61,11 +61,15 @@ def na3d(
     q_extent: Sequence[int] | None = None,
     compute_dtype: torch.dtype = torch.float32,
     max_chunk_bytes: int = 1 << 28,
-) -> Tensor:
+    return_lse: bool = False,
+):
     """NA3D forward on the CPU; returns ``[B, *q_extent, H, D]`` in ``compute_dtype``.
 
     Chunked over (batch, head, query z-slice, query y-rows) so the gathered
-    window stays below ``max_chunk_bytes``.
+    window stays below ``max_chunk_bytes``.  ``return_lse``: also return each
+    query's log2-sum-exp over its window of the log2-unit scores
+    ``scale * log2(e) * q.k``, ``[B, *q_extent, H]`` (the statistic the HIP
+    forward emits for the backward; NATTEN keeps the natural-log one).
     """
     B, Z, Y, X, H, D = q.shape
     kz, ky, kx = _triple(kernel_size)
@@ -81,6 +85,7 @@ def na3d(
     kc = k.to(compute_dtype)
     vc = v.to(compute_dtype)
     out = torch.empty((B, ez, ey, ex, H, D), dtype=compute_dtype)
+    lse = torch.empty((B, ez, ey, ex, H), dtype=compute_dtype) if return_lse else None
     elem = torch.finfo(compute_dtype).bits // 8
     rows = max(1, min(ey, max_chunk_bytes // max(1, ex * W * D * elem)))
     for b in range(B):
@@ -102,7 +107,9 @@ def na3d(
                     s = torch.einsum("yxd,yxwd->yxw", qq, kw) * scale
                     p = torch.softmax(s, dim=-1)
                     out[b, zi, y0 : y0 + r, :, h, :] = torch.einsum("yxw,yxwd->yxd", p, vw)
-    return out
+                    if return_lse:
+                        lse[b, zi, y0 : y0 + r, :, h] = torch.logsumexp(s, dim=-1) / math.log(2.0)
+    return (out, lse) if return_lse else out
 
 
 def _window_by_search(i: int, length: int, kernel: int, dilation: int) -> list[int]:

@@ -14,7 +14,7 @@ from pathlib import Path
 
 LIB_PATH = Path(__file__).resolve().parent / "libstrata_hip.so"
 
-ABI_VERSION = 5
+ABI_VERSION = 6
 
 OK = 0
 EINVAL = -1
@@ -63,6 +63,7 @@ class Na3dArgs(ctypes.Structure):
         ("k_stride", _i64x5),
         ("v_stride", _i64x5),
         ("o_stride", _i64x5),
+        ("lse", ctypes.c_void_p),
     ]
 
 
@@ -164,6 +165,7 @@ class Na3dBwdArgs(ctypes.Structure):
         ("kernel", ctypes.c_int32 * 3),
         ("dilation", ctypes.c_int32 * 3),
         ("scale", ctypes.c_float),
+        ("lse", ctypes.c_void_p),
     ]
 
 

@@ -38,7 +38,13 @@ struct Na3dParams {
   int dil[3];
   float scale;
   int64_t qs[5], ks[5], vs[5], os[5];
+  float* lse;  // [B, ext0, ext1, ext2, H] log2-sum-exp of the log2-unit scores, or null
 };
+
+// Index of query (box coordinates ez, ey, ex) in the lse output.
+__device__ __forceinline__ int64_t lse_index(const Na3dParams& p, int b, int ez, int ey, int ex, int h) {
+  return ((((int64_t)b * p.ext[0] + ez) * p.ext[1] + ey) * p.ext[2] + ex) * p.H + h;
+}
 
 // ---------------------------------------------------------------------------
 // Scalar kernel
@@ -108,6 +114,7 @@ __global__ __launch_bounds__(256) void na3d_scalar_kernel(Na3dParams p, int64_t 
   T* op = (T*)p.o + b * p.os[0] + ez * p.os[1] + ey * p.os[2] + ex * p.os[3] + h * p.os[4];
 #pragma unroll
   for (int d = 0; d < D; ++d) op[d] = (T)(acc[d] * inv);
+  if (p.lse) p.lse[idx] = (m + logf(l)) * 1.4426950408889634f;  // idx enumerates (b, ez, ey, ex, h)
 }
 
 // ---------------------------------------------------------------------------
@@ -510,6 +517,7 @@ __device__ __forceinline__ void na3d_mfma_body(const Na3dParams p, const Na3dTil
 #pragma unroll
         for (int db = 0; db < DB; ++db) oacc[tt][db] *= alpha;
         lacc[tt] *= alpha;
+        mref[tt] += d;
 #pragma unroll
         for (int i = 0; i < 4; ++i) nb[tt][i] -= d;
 #pragma unroll
@@ -551,6 +559,7 @@ __device__ __forceinline__ void na3d_mfma_body(const Na3dParams p, const Na3dTil
     const int oz = rz - p.org[0];
     const int oy = gy + dy * qy - p.org[1];
     const int ox = gx + dx * qx - p.org[2];
+    if (p.lse && g == 0) p.lse[lse_index(p, b, oz, oy, ox, h)] = mref[tt] + __log2f(lacc[tt][0]);
     bf16* op = (bf16*)p.o + (int64_t)b * p.os[0] + (int64_t)oz * p.os[1] + (int64_t)oy * p.os[2] +
                (int64_t)ox * p.os[3] + (int64_t)h * p.os[4];
 #pragma unroll
@@ -845,6 +854,7 @@ __device__ __forceinline__ void na3d_strip_body(const Na3dParams p, const Na3dSt
   f32x4 lacc[NS];
   f32x4 nb[NS];  // x bias - reference: the C operand of the QK MFMA
   int syl[NS];   // first window row of this lane's query row (relative to the segment)
+  float mslot[NS];  // the slot's softmax reference (log2 units), for the lse output
   // Uniform slot state: tile index (-1: empty) and packed groups
   // [ylo | yhi << 10 | end << 20]: groups below ylo or from yhi on have rows
   // outside some query's window; `end` is the tile's last group.
@@ -873,6 +883,7 @@ __device__ __forceinline__ void na3d_strip_body(const Na3dParams p, const Na3dSt
         d = fmaf((float)qreg[k][ks][e], (float)kself[ks][e], d);
       }
     const float mref = colsum(d);
+    mslot[k] = mref;
 #pragma unroll
     for (int i = 0; i < 4; ++i) nb[k][i] = ((xmask >> i) & 1) ? -INFINITY : -mref;
 #pragma unroll
@@ -889,6 +900,9 @@ __device__ __forceinline__ void na3d_strip_body(const Na3dParams p, const Na3dSt
     s_tile[k] = -1;
     if (qy >= ye || qx >= qx1) return;
     const float inv = 1.f / lacc[k][0];
+    if (p.lse && g == 0)
+      p.lse[lse_index(p, b, rz - p.org[0], gy + dy * qy - p.org[1], gx + dx * qx - p.org[2], h)] =
+          mslot[k] + __log2f(lacc[k][0]);
     char* op = obase + ooff + (int64_t)qy * orow;
 #pragma unroll
     for (int db = 0; db < DB; ++db) {
@@ -1053,6 +1067,7 @@ __device__ __forceinline__ void na3d_strip_body(const Na3dParams p, const Na3dSt
 #pragma unroll
           for (int db = 0; db < DB; ++db) oacc[k][db] *= alpha;
           lacc[k] *= alpha;
+          mslot[k] += d;
 #pragma unroll
           for (int i = 0; i < 4; ++i) nb[k][i] -= d;
 #pragma unroll
@@ -1693,6 +1708,8 @@ extern "C" int strata_hip_na3d_fwd(const strata_hip_na3d_args* a, void* stream) 
     p.os[i] = a->o_stride[i];
   }
   p.scale = a->scale;
+  p.lse = a->lse;
+  if (p.lse && ((uintptr_t)p.lse & 3u)) return fail(STRATA_HIP_EINVAL, "na3d: lse must be 4-byte aligned");
   if ((int64_t)p.B * p.ext[0] * p.ext[1] * p.ext[2] == 0) return STRATA_HIP_OK;
   hipStream_t st = (hipStream_t)stream;
 
@@ -1730,7 +1747,9 @@ extern "C" int strata_hip_na3d_fwd(const strata_hip_na3d_args* a, void* stream) 
       return launch_mfma_d<32>(p, st);
     case 64:
       if (strip_fits(p))
-        return strip_regular(p) ? launch_strip<64, 4, 4, 2, true>(p, st) : launch_strip<64, 4, 4, 2, false>(p, st);
+        // the regular-strip kernel keeps no softmax reference: no lse output
+        return strip_regular(p) && !p.lse ? launch_strip<64, 4, 4, 2, true>(p, st)
+                                          : launch_strip<64, 4, 4, 2, false>(p, st);
       return launch_mfma_d<64>(p, st);
     default:
       return launch_mfma_d<128>(p, st);

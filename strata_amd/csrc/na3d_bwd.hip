@@ -12,8 +12,9 @@
 // and dilation 1 (the training shapes) runs MFMA versions (below); the general
 // VALU versions (4 lanes per token, D/4 head dims per lane, dot products closed
 // by two xor shuffles) take everything else:
-//   prep: per query, log2-sum-exp of its scores (recomputed: the forward keeps
-//         no statistics) and D_i, into a caller-provided fp32 workspace;
+//   prep: per query, log2-sum-exp of its scores (recomputed, unless the caller
+//         passes the forward's, strata_hip_na3d_fwd's lse output: then only
+//         D_i) and D_i, into a caller-provided fp32 workspace;
 //   dq:   per query, a walk over its window;
 //   dkv:  per key, a walk over its inverse window {i : j in W(i)}, which per
 //         axis is an interval (window starts are non-decreasing in i):
@@ -37,6 +38,7 @@ struct Na3dBwdParams {
   int ker[3], dil[3];
   float scale;
   int nyt, nxt;  // 4-row tiles along y, 16-column workgroup boxes along x
+  int lse_given; // lse holds the forward's statistics: prep computes D_i only
 };
 
 template <typename T, int DPL>
@@ -606,6 +608,27 @@ __global__ __launch_bounds__(256) void na3d_bwd_dkv_mfma_kernel(Na3dBwdParams p)
 #endif
 }
 
+// D_i = dO_i . O_i alone, for a backward given the forward's log-sum-exp:
+// LPR lanes per (token, head) row, 16 bytes of dO and of O each, closed by
+// xor shuffles.
+template <typename T, int D>
+__global__ __launch_bounds__(256) void na3d_bwd_dsum_kernel(Na3dBwdParams p, int64_t rows) {
+  constexpr int EPL = 16 / (int)sizeof(T), LPR = D / EPL;
+  const int64_t idx = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  const int64_t row = idx / LPR;
+  const int c = (int)(idx % LPR);
+  float s = 0.f;
+  if (row < rows) {
+    float a[EPL], o[EPL];
+    load_dims<T, EPL>((const T*)p.dout + row * D + c * EPL, a);
+    load_dims<T, EPL>((const T*)p.o + row * D + c * EPL, o);
+#pragma unroll
+    for (int e = 0; e < EPL; ++e) s = fmaf(a[e], o[e], s);
+  }
+  for (int sh = 1; sh < LPR; sh <<= 1) s += __shfl_xor(s, sh);
+  if (row < rows && c == 0) p.dsum[row] = s;
+}
+
 // The MFMA kernels: dilation 1, kx <= 13 (a 4-column tile's x union fits one 16-key block).
 static bool mfma_ok(const Na3dBwdParams& p) {
   return p.dil[0] == 1 && p.dil[1] == 1 && p.dil[2] == 1 && p.ker[2] <= 13 && !std::getenv("STRATA_HIP_NA3D_BWD_VALU");
@@ -617,10 +640,16 @@ static int launch_bwd(const Na3dBwdParams& p, hipStream_t st) {
   if (blocks == 0) return STRATA_HIP_OK;
   if (blocks > 0x7fffffff) return fail(STRATA_HIP_EUNSUPPORTED, "na3d_bwd: problem too large for one launch");
   const dim3 grid((unsigned)blocks), block(256);
-  if (sizeof(T) == 2 && D == 64 && mfma_ok(p))
+  if (p.lse_given) {
+    constexpr int LPR = D * (int)sizeof(T) / 16;
+    const int64_t rows = (int64_t)p.B * p.Z * p.Y * p.X * p.H;
+    hipLaunchKernelGGL((na3d_bwd_dsum_kernel<T, D>), dim3((unsigned)((rows * LPR + 255) / 256)), block, 0, st, p,
+                       rows);
+  } else if (sizeof(T) == 2 && D == 64 && mfma_ok(p)) {
     hipLaunchKernelGGL(na3d_bwd_prep_mfma_kernel, grid, block, 0, st, p);
-  else
+  } else {
     hipLaunchKernelGGL((na3d_bwd_prep_kernel<T, D>), grid, block, 0, st, p);
+  }
   if (sizeof(T) == 2 && D == 64 && mfma_ok(p))
     hipLaunchKernelGGL(na3d_bwd_dq_mfma_kernel, grid, block, 0, st, p);
   else
@@ -692,6 +721,13 @@ extern "C" int strata_hip_na3d_bwd(const strata_hip_na3d_bwd_args* a, void* stre
   const int64_t tokens = (int64_t)p.B * p.Z * p.Y * p.X * p.H;
   p.lse = a->workspace;
   p.dsum = a->workspace + tokens;
+  if (a->lse) {  // the forward's statistics: prep reduces to D_i
+    if ((uintptr_t)a->lse & 3u) return fail(STRATA_HIP_EINVAL, "na3d_bwd: lse must be 4-byte aligned");
+    if (tokens * (a->head_dim * (a->dtype == STRATA_HIP_BF16 ? 2 : 4) / 16) / 256 + 1 > 0x7fffffff)
+      return fail(STRATA_HIP_EUNSUPPORTED, "na3d_bwd: problem too large for one launch");
+    p.lse = const_cast<float*>(a->lse);
+    p.lse_given = 1;
+  }
   p.nyt = (p.Y + 3) / 4;
   p.nxt = (p.X + 15) / 16;
   hipStream_t st = (hipStream_t)stream;

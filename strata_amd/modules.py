@@ -118,7 +118,7 @@ class FusedNA3DAttention(nn.Module):
         else:
             qkv6 = qkv.view(B, Z, Y, X, 3, H, D)
             q, k, v = qkv6[..., 0, :, :], qkv6[..., 1, :, :], qkv6[..., 2, :, :]
-        a = ops.na3d_fwd(q, k, v, self.kernel_size, self.dilation, self.scale, [0, 0, 0], [Z, Y, X])
+        a = ops.na3d(q, k, v, self.kernel_size, self.dilation, self.scale)
         a = a.view(B, Z, Y, X, C)
         if self.gate_proj is not None:  # a * sigmoid(x @ Wg^T + bg) in one GEMM
             a = ops.gemm_bias_act(x, self.gate_proj.weight, self.gate_proj.bias, a, _lib.ACT_SIGMOID, _lib.RES_MUL)

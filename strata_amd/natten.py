@@ -5,7 +5,8 @@ dilation=..., backend=...)`` with heads-last ``[B, Z, Y, X, H, D]`` tensors
 (backend string from screamcast/config.py:99 -> train.py:143 ->
 screamcast/strata_wrappers.py:331,490,582).  Installing this module under the
 name ``natten`` (see :func:`install_as_natten`) routes that call to
-``torch.ops.strata_hip.na3d_fwd`` without touching the caller.
+``torch.ops.strata_hip.na3d_fwd`` (``na3d_fwd_lse`` when gradients are wanted,
+so that the backward reuses the forward's log-sum-exp) without touching the caller.
 
 Supported: odd kernel sizes, any dilation with kernel*dilation <= size,
 non-causal, stride 1, default or explicit scale.  Everything else raises
@@ -83,7 +84,8 @@ def na3d(
             raise ValueError(
                 f"na3d: kernel_size * dilation ({k}*{d}) exceeds the input size {L} along axis {ax}"
             )
-    return torch.ops.strata_hip.na3d_fwd(query, key, value, list(ks), list(dil), scale, [0, 0, 0], list(grid))
+    # with gradients wanted, the forward keeps its log-sum-exp for the backward
+    return ops.na3d(query, key, value, list(ks), list(dil), scale)
 
 
 def install_as_natten() -> types.ModuleType:

@@ -23,6 +23,8 @@ from . import _lib
 __all__ = [
     "na3d_fwd",
     "na3d_bwd",
+    "na3d_fwd_lse",
+    "na3d",
     "rope_qkv_pack",
     "gemm_bias_act",
     "layer_norm",
@@ -108,7 +110,10 @@ def na3d_fwd(
     Makefile:11; call routed by screamcast/config.py:99 -> train.py:143 ->
     screamcast/strata_wrappers.py:331,490,582).
     """
-    name = "na3d_fwd"
+    return _na3d_launch("na3d_fwd", q, k, v, kernel, dilation, scale, q_origin, q_extent, None)
+
+
+def _na3d_launch(name, q, k, v, kernel, dilation, scale, q_origin, q_extent, lse: Optional[Tensor]) -> Tensor:
     _require_gpu(name, q, k, v)
     if not (q.shape == k.shape == v.shape):
         raise ValueError(f"{name}: q, k, v must share one shape, got {tuple(q.shape)}, {tuple(k.shape)}, {tuple(v.shape)}")
@@ -136,6 +141,7 @@ def na3d_fwd(
     a.k_stride[:] = ks
     a.v_stride[:] = vs
     a.o_stride[:] = [out.stride(i) for i in range(5)]
+    a.lse = lse.data_ptr() if lse is not None else None
     with torch.cuda.device(q.device):
         _lib.call("strata_hip_na3d_fwd", a, _stream(q))
     return out
@@ -145,6 +151,25 @@ def na3d_fwd(
 def _(q, k, v, kernel, dilation, scale, q_origin, q_extent):
     B, H, D = q.shape[0], q.shape[4], q.shape[5]
     return q.new_empty((B, *[int(e) for e in q_extent], H, D))
+
+
+@torch.library.custom_op("strata_hip::na3d_fwd_lse", mutates_args=())
+def na3d_fwd_lse(
+    q: Tensor, k: Tensor, v: Tensor, kernel: Sequence[int], dilation: Sequence[int], scale: Optional[float]
+) -> tuple[Tensor, Tensor]:
+    """``na3d_fwd`` over the whole grid that also returns each query's log2-sum-exp
+    ``[B, Z, Y, X, H]`` fp32 (of the log2-unit scores ``scale*log2(e)*q.k``), the
+    statistic the backward needs; its autograd passes it on so the backward does
+    not recompute it.  ``na3d`` below picks this op when gradients are wanted."""
+    B, Z, Y, X, H, D = q.shape
+    lse = torch.empty((B, Z, Y, X, H), dtype=torch.float32, device=q.device)
+    out = _na3d_launch("na3d_fwd_lse", q, k, v, kernel, dilation, scale, [0, 0, 0], [Z, Y, X], lse)
+    return out, lse
+
+
+@na3d_fwd_lse.register_fake
+def _(q, k, v, kernel, dilation, scale):
+    return q.new_empty(q.shape), q.new_empty(q.shape[:5], dtype=torch.float32)
 
 
 @torch.library.custom_op("strata_hip::na3d_bwd", mutates_args=())
@@ -157,10 +182,12 @@ def na3d_bwd(
     kernel: Sequence[int],
     dilation: Sequence[int],
     scale: Optional[float],
+    lse: Optional[Tensor] = None,
 ) -> tuple[Tensor, Tensor, Tensor]:
     """``(dq, dk, dv)`` of ``out = na3d(q, k, v)`` over the whole grid, given ``dout``
     (NATTEN 0.21.5's na3d backward, reached in training through train.py:1161).
-    Heads-last ``[B, Z, Y, X, H, D]``, bf16 or fp32 (fp32 math), D in {32, 64, 128}."""
+    Heads-last ``[B, Z, Y, X, H, D]``, bf16 or fp32 (fp32 math), D in {32, 64, 128}.
+    ``lse``: the forward's statistics from ``na3d_fwd_lse`` (else recomputed)."""
     name = "na3d_bwd"
     _require_gpu(name, q, k, v, out, dout)
     shape = q.shape
@@ -186,13 +213,18 @@ def na3d_bwd(
     a.kernel[:] = kernel
     a.dilation[:] = dilation
     a.scale = float(D**-0.5 if scale is None else scale)
+    if lse is not None:
+        if lse.shape != shape[:5] or lse.dtype != torch.float32 or lse.device != q.device:
+            raise ValueError(f"{name}: lse must be float32 {tuple(shape[:5])} on {q.device}")
+        lse = lse.contiguous()
+        a.lse = lse.data_ptr()
     with torch.cuda.device(q.device):
         _lib.call("strata_hip_na3d_bwd", a, _stream(q))
     return dq, dk, dv
 
 
 @na3d_bwd.register_fake
-def _(q, k, v, out, dout, kernel, dilation, scale):
+def _(q, k, v, out, dout, kernel, dilation, scale, lse=None):
     return torch.empty_like(q), torch.empty_like(k), torch.empty_like(v)
 
 
@@ -215,6 +247,33 @@ def _na3d_backward(ctx, dout):
 
 
 na3d_fwd.register_autograd(_na3d_backward, setup_context=_na3d_setup_context)
+
+
+def _na3d_lse_setup_context(ctx, inputs, output):
+    q, k, v, kernel, dilation, scale = inputs
+    out, lse = output
+    ctx.kernel, ctx.dilation, ctx.scale = kernel, dilation, scale
+    ctx.mark_non_differentiable(lse)
+    ctx.save_for_backward(q, k, v, out, lse)
+
+
+def _na3d_lse_backward(ctx, dout, dlse):
+    q, k, v, out, lse = ctx.saved_tensors
+    dq, dk, dv = na3d_bwd(q, k, v, out, dout.contiguous(), ctx.kernel, ctx.dilation, ctx.scale, lse)
+    return dq, dk, dv, None, None, None
+
+
+na3d_fwd_lse.register_autograd(_na3d_lse_backward, setup_context=_na3d_lse_setup_context)
+
+
+def na3d(q: Tensor, k: Tensor, v: Tensor, kernel: Sequence[int], dilation: Sequence[int],
+         scale: Optional[float] = None) -> Tensor:
+    """Full-grid NA3D for modules: ``na3d_fwd_lse`` (forward statistics kept for
+    the backward) when autograd will need them, else ``na3d_fwd``."""
+    if torch.is_grad_enabled() and (q.requires_grad or k.requires_grad or v.requires_grad):
+        return na3d_fwd_lse(q, k, v, kernel, dilation, scale)[0]
+    Z, Y, X = q.shape[1:4]
+    return na3d_fwd(q, k, v, kernel, dilation, scale, [0, 0, 0], [Z, Y, X])
 
 
 # ---------------------------------------------------------------------------

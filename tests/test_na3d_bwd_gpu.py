@@ -63,7 +63,10 @@ def test_autograd_through_the_forward_op_and_natten_shim(gpu):
     leaves = [t.clone().requires_grad_(True) for t in (qg, kg, vg)]
     out = natten_na3d(*leaves, kernel_size=kernel)
     out.backward(dg)
-    direct = torch.ops.strata_hip.na3d_bwd(qg, kg, vg, out.detach(), dg, list(kernel), [1, 1, 1], None)
+    # with gradients wanted the shim runs na3d_fwd_lse: the backward gets its lse
+    out2, lse = torch.ops.strata_hip.na3d_fwd_lse(qg, kg, vg, list(kernel), [1, 1, 1], None)
+    assert torch.equal(out.detach(), out2)
+    direct = torch.ops.strata_hip.na3d_bwd(qg, kg, vg, out2, dg, list(kernel), [1, 1, 1], None, lse)
     for leaf, d in zip(leaves, direct):
         assert torch.equal(leaf.grad, d)
     ref = O.na3d_backward(q, k, v, dout, kernel)
@@ -90,3 +93,55 @@ def test_bwd_mfma_matches_valu_path(gpu, case, monkeypatch):
     slow = torch.ops.strata_hip.na3d_bwd(qg, kg, vg, out, dg, list(kernel), list(dil), None)
     for a, b in zip(fast, slow):
         assert rel_l2(a.float(), b.float()) <= 1e-2
+
+
+@pytest.mark.parametrize("case", CASES, ids=str)
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16], ids=["f32", "bf16"])
+def test_forward_lse_vs_oracle(gpu, case, dtype):
+    """The forward's log2-sum-exp (scalar, general MFMA and strip kernels) against
+    the oracle's, and the output unchanged by asking for it."""
+    shape, kernel, dil = case
+    (q, k, v, _), (qg, kg, vg, _) = _inputs(shape, 5, dtype, gpu)
+    out, lse = torch.ops.strata_hip.na3d_fwd_lse(qg, kg, vg, list(kernel), list(dil), None)
+    assert torch.equal(out, _fwd(qg, kg, vg, kernel, dil))
+    _, ref = O.na3d(q, k, v, kernel, dil, compute_dtype=torch.float64, return_lse=True)
+    # bf16: the kernels score bf16(scale*log2(e)*q) against k, a 2^-9 relative rounding of q
+    tol = 1e-4 if dtype == torch.float32 else 3e-2
+    assert (lse.double().cpu() - ref).abs().max().item() <= tol
+
+
+def test_forward_lse_of_a_query_box_on_the_regular_strip_shape(gpu):
+    """A halo-interior box that would take the reference-free strip kernel takes
+    the strip kernel with a softmax reference when the lse is asked for."""
+    from strata_amd import _lib
+
+    shape, kernel, org, ext = (1, 3, 24, 30, 2, 64), (3, 13, 13), (0, 6, 7), (3, 10, 13)
+    (q, k, v, _), (qg, kg, vg, _) = _inputs(shape, 6, torch.bfloat16, gpu)
+    out = torch.empty((1, *ext, 2, 64), dtype=torch.bfloat16, device=gpu)
+    lse = torch.empty((1, *ext, 2), dtype=torch.float32, device=gpu)
+    a = _lib.Na3dArgs()
+    a.q, a.k, a.v, a.out, a.lse = qg.data_ptr(), kg.data_ptr(), vg.data_ptr(), out.data_ptr(), lse.data_ptr()
+    a.dtype, a.batch, a.heads, a.head_dim, a.scale = _lib.BF16, 1, 2, 64, 64**-0.5
+    a.grid[:], a.q_origin[:], a.q_extent[:] = shape[1:4], org, ext
+    a.kernel[:], a.dilation[:] = kernel, [1, 1, 1]
+    a.q_stride[:], a.k_stride[:], a.v_stride[:] = ([qg.stride(i) for i in range(5)],) * 3
+    a.o_stride[:] = [out.stride(i) for i in range(5)]
+    _lib.call("strata_hip_na3d_fwd", a, torch.cuda.current_stream().cuda_stream)
+    ref_o, ref_l = O.na3d(q, k, v, kernel, q_origin=org, q_extent=ext, compute_dtype=torch.float64, return_lse=True)
+    assert rel_l2(out.float().cpu(), ref_o.float()) <= 1e-2
+    assert (lse.double().cpu() - ref_l).abs().max().item() <= 3e-2
+
+
+@pytest.mark.parametrize("case", CASES, ids=str)
+def test_bwd_with_forward_lse_matches_recompute(gpu, case):
+    """The backward given the forward's lse (prep reduced to rowsum(dO*O)) agrees
+    with the backward that recomputes it, and with the oracle."""
+    shape, kernel, dil = case
+    (q, k, v, dout), (qg, kg, vg, dg) = _inputs(shape, 7, torch.bfloat16, gpu)
+    out, lse = torch.ops.strata_hip.na3d_fwd_lse(qg, kg, vg, list(kernel), list(dil), None)
+    given = torch.ops.strata_hip.na3d_bwd(qg, kg, vg, out, dg, list(kernel), list(dil), None, lse)
+    recomputed = torch.ops.strata_hip.na3d_bwd(qg, kg, vg, out, dg, list(kernel), list(dil), None)
+    ref = O.na3d_backward(q, k, v, dout, kernel, dil)
+    for name, a, b, r in zip(("dq", "dk", "dv"), given, recomputed, ref):
+        assert rel_l2(a.float(), b.float()) <= 2e-3, name
+        assert rel_l2(a.float().cpu(), r) <= 1e-2, name

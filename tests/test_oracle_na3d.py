@@ -171,3 +171,27 @@ def test_backward_dv_is_transposed_attention():
     # total weight is conserved: every query distributes exactly 1
     assert torch.allclose(dv[..., 0].sum(), torch.tensor(2 * 5 * 5, dtype=torch.float64))
     assert torch.all(dv[..., 1:] == 0)
+
+
+def test_lse_is_the_dense_logsumexp_when_the_window_is_the_grid():
+    """With the window the whole (odd) grid, each query's lse is the base-2
+    logsumexp of its dense scores; on a real window it matches a per-query
+    loop over the keys that the brute-force oracle visits."""
+    import math
+
+    g = torch.Generator().manual_seed(31)
+    B, Z, Y, X, H, D = 1, 3, 5, 7, 2, 16
+    q, k, v = (torch.randn(B, Z, Y, X, H, D, generator=g, dtype=torch.float64) for _ in range(3))
+    scale = 0.3
+    _, lse = O.na3d(q, k, v, (Z, Y, X), scale=scale, compute_dtype=torch.float64, return_lse=True)
+    qf = q.reshape(B, -1, H, D)
+    kf = k.reshape(B, -1, H, D)
+    s = torch.einsum("bqhd,bkhd->bhqk", qf, kf) * scale
+    ref = (torch.logsumexp(s, dim=-1) / math.log(2.0)).permute(0, 2, 1).reshape(B, Z, Y, X, H)
+    assert torch.allclose(lse, ref, atol=1e-12)
+    # a clamped 3x3x5 window, one query near a corner, from the window definition
+    _, lse = O.na3d(q, k, v, (3, 3, 5), scale=scale, compute_dtype=torch.float64, return_lse=True)
+    z, y, x, h = 0, 4, 1, 1
+    keys = [(a, b_, c) for a in range(0, 3) for b_ in range(2, 5) for c in range(0, 5)]
+    sc = torch.stack([(q[0, z, y, x, h] * k[0, a, b_, c, h]).sum() * scale for a, b_, c in keys])
+    assert abs(lse[0, z, y, x, h].item() - (torch.logsumexp(sc, 0) / math.log(2.0)).item()) < 1e-12
