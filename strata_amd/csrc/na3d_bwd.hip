@@ -483,7 +483,7 @@ __global__ __launch_bounds__(256) void na3d_bwd_prep_mfma_kernel(Na3dBwdParams p
 // of the S MFMA.  Q is staged pre-scaled by scale * log2 e, so dK carries a
 // factor ln 2 at the end.
 // ---------------------------------------------------------------------------
-__global__ __launch_bounds__(256) void na3d_bwd_dkv_mfma_kernel(Na3dBwdParams p) {
+__global__ __launch_bounds__(256, 2) void na3d_bwd_dkv_mfma_kernel(Na3dBwdParams p) {
 #if defined(__HIP_DEVICE_COMPILE__)
   constexpr int D = 64, KS = 2, DB = 4, RBW = 16 * D * 2;
   __shared__ __attribute__((aligned(16))) char lds[4 * 4 * RBW];  // per wave: Q rows 0, 1; dO rows 0, 1
