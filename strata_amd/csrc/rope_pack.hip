@@ -79,13 +79,14 @@ __device__ __forceinline__ void rot8(const float* a, const float* b, const float
   }
 }
 
-// One head's q or k run of the half layout: optional RMSNorm, then rotation.
-__device__ __forceinline__ void half_run(const RopeParams& p, const bf16* src, bf16* dst, const float* cs,
-                                         const float* sn, int c, int cph, const bf16* w) {
+// One head's q or k run of the half layout (already loaded: lo = d in [8c, 8c + 8),
+// hi = the same + D/2): optional RMSNorm, then rotation.
+__device__ __forceinline__ void half_run(const RopeParams& p, const u32x4& lo, const u32x4& hi, bf16* dst,
+                                         const float* cs, const float* sn, int c, int cph, const bf16* w) {
   const int half = p.D / 2;
   float f[16];  // f[0..7]: d = 8c + j, f[8..15]: d = 8c + j + D/2
-  unpack8(*(const u32x4*)(src), f);
-  unpack8(*(const u32x4*)(src + half), f + 8);
+  unpack8(lo, f);
+  unpack8(hi, f + 8);
   if (p.qk_norm) {
     int dof[16];
 #pragma unroll
@@ -101,31 +102,55 @@ __device__ __forceinline__ void half_run(const RopeParams& p, const bf16* src, b
   *(u32x4*)(dst + half) = ob;
 }
 
-// Half layout: pair p = (d = p, d = p + D/2).
-__global__ __launch_bounds__(256) void rope_pack_half_kernel(RopeParams p, int64_t total) {
-  const int64_t idx = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-  if (idx >= total) return;
+// Half layout: pair p = (d = p, d = p + D/2).  A thread takes ROPE_R runs,
+// `slice` apart, and issues all their loads before any math (the pass is
+// latency-bound: one run per thread leaves too few bytes in flight).  slice
+// is a multiple of 64, so the D/16 lanes of a head share one validity and
+// their qk_norm shuffles stay within live lanes.
+constexpr int ROPE_R = 2;
+
+__global__ __launch_bounds__(256) void rope_pack_half_kernel(RopeParams p, int64_t total, int64_t slice) {
+  const int64_t idx0 = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (idx0 >= slice) return;
   const int cph = p.D / 16;
-  const int c = (int)(idx % cph);
-  const int64_t th = idx / cph;
-  const int h = (int)(th % p.H);
-  const int64_t tok = th / p.H;
   const int half = p.D / 2;
   const int64_t C = (int64_t)p.H * p.D;
-
-  const bf16* src = p.qkv + tok * p.ld + (int64_t)h * p.D + 8 * c;
-  const int64_t trow = table_row(p, tok) * half + 8 * c;
-  float cs[8], sn[8];
-  *(f32x4*)&cs[0] = *(const f32x4*)(p.cos + trow);
-  *(f32x4*)&cs[4] = *(const f32x4*)(p.cos + trow + 4);
-  *(f32x4*)&sn[0] = *(const f32x4*)(p.sin + trow);
-  *(f32x4*)&sn[4] = *(const f32x4*)(p.sin + trow + 4);
-
-  const int64_t dst = tok * C + (int64_t)h * p.D + 8 * c;
-  half_run(p, src, p.q + dst, cs, sn, c, cph, p.qw);
-  half_run(p, src + C, p.k + dst, cs, sn, c, cph, p.kw);
-  *(u32x4*)(p.v + dst) = *(const u32x4*)(src + 2 * C);
-  *(u32x4*)(p.v + dst + half) = *(const u32x4*)(src + 2 * C + half);
+  u32x4 raw[ROPE_R][6];
+  float cs[ROPE_R][8], sn[ROPE_R][8];
+  int64_t dst[ROPE_R];
+  int cc[ROPE_R];
+  bool ok[ROPE_R];
+#pragma unroll
+  for (int r = 0; r < ROPE_R; ++r) {
+    const int64_t idx = idx0 + r * slice;
+    ok[r] = idx < total;
+    const int64_t i = ok[r] ? idx : total - 1;  // a dead run reads a live one and stores nothing
+    const int c = (int)(i % cph);
+    const int64_t th = i / cph;
+    const int h = (int)(th % p.H);
+    const int64_t tok = th / p.H;
+    const bf16* src = p.qkv + tok * p.ld + (int64_t)h * p.D + 8 * c;
+#pragma unroll
+    for (int t = 0; t < 3; ++t) {
+      raw[r][2 * t] = *(const u32x4*)(src + t * C);
+      raw[r][2 * t + 1] = *(const u32x4*)(src + t * C + half);
+    }
+    const int64_t trow = table_row(p, tok) * half + 8 * c;
+    *(f32x4*)&cs[r][0] = *(const f32x4*)(p.cos + trow);
+    *(f32x4*)&cs[r][4] = *(const f32x4*)(p.cos + trow + 4);
+    *(f32x4*)&sn[r][0] = *(const f32x4*)(p.sin + trow);
+    *(f32x4*)&sn[r][4] = *(const f32x4*)(p.sin + trow + 4);
+    dst[r] = tok * C + (int64_t)h * p.D + 8 * c;
+    cc[r] = c;
+  }
+#pragma unroll
+  for (int r = 0; r < ROPE_R; ++r) {
+    if (!ok[r]) continue;  // uniform over the lanes of a head
+    half_run(p, raw[r][0], raw[r][1], p.q + dst[r], cs[r], sn[r], cc[r], cph, p.qw);
+    half_run(p, raw[r][2], raw[r][3], p.k + dst[r], cs[r], sn[r], cc[r], cph, p.kw);
+    *(u32x4*)(p.v + dst[r]) = raw[r][4];
+    *(u32x4*)(p.v + dst[r] + half) = raw[r][5];
+  }
 }
 
 // Interleaved layout: pair p = (d = 2p, d = 2p + 1).
@@ -497,9 +522,11 @@ extern "C" int strata_hip_rope_qkv_pack(const strata_hip_rope_pack_args* a, void
   const int threads = 256;
   const int64_t blocks = (total + threads - 1) / threads;
   if (blocks > 0x7fffffff) return fail(STRATA_HIP_EUNSUPPORTED, "rope_qkv_pack: too many tokens");
-  if (a->layout == STRATA_HIP_ROPE_HALF)
-    hipLaunchKernelGGL(rope_pack_half_kernel, dim3((unsigned)blocks), dim3(threads), 0, (hipStream_t)stream, p, total);
-  else
+  if (a->layout == STRATA_HIP_ROPE_HALF) {
+    const int64_t slice = ((total + ROPE_R - 1) / ROPE_R + 63) / 64 * 64;
+    hipLaunchKernelGGL(rope_pack_half_kernel, dim3((unsigned)((slice + threads - 1) / threads)), dim3(threads), 0,
+                       (hipStream_t)stream, p, total, slice);
+  } else
     hipLaunchKernelGGL(rope_pack_inter_kernel, dim3((unsigned)blocks), dim3(threads), 0, (hipStream_t)stream, p, total);
   return check_launch("rope_pack_kernel");
 }
