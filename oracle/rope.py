@@ -12,6 +12,13 @@ not installable here, so the formulas are the textbook ones:
     theta = coord * base^(-j/(P/2)) per axis.
 Conventions (pair split x | y, half pair layout, spherical-centroid centre,
 tables broadcast over z) are the build's, recorded with the fixtures.
+
+Level index in z: with ``level_pairs = L > 0`` the P = D/2
+pairs split into three axis groups, x | y | level: pairs [0, n) rotate by x,
+[n, 2n) by y and [2n, P) by the token's vertical level index z (0, 1, ...,
+Z-1, in level units), n = (P - L)/2; inside each group of size m the angular
+frequencies are base^(-j/m), j = 0..m-1.  configs[1] uses P = 32, L = 8
+(12 | 12 | 8).  ``level_pairs = 0`` is the 2D table broadcast over z.
 """
 
 from __future__ import annotations
@@ -52,20 +59,43 @@ def stereographic(lat: Tensor, lon: Tensor, lat0: Tensor, lon0: Tensor) -> tuple
     return x, y
 
 
-def rope_angles(cx: Tensor, cy: Tensor, head_dim: int, base: float) -> Tensor:
-    """Angles ``[..., D/2]``: pairs [0, P/2) rotate by cx, [P/2, P) by cy."""
-    half = head_dim // 4
-    j = torch.arange(half, dtype=torch.float64)
-    omega = torch.pow(torch.tensor(float(base), dtype=torch.float64), -j / half)
-    return torch.cat([cx.double()[..., None] * omega, cy.double()[..., None] * omega], dim=-1)
+def _omega(m: int, base: float) -> Tensor:
+    j = torch.arange(m, dtype=torch.float64)
+    return torch.pow(torch.tensor(float(base), dtype=torch.float64), -j / m)
 
 
-def tables(lat: Tensor, lon: Tensor, head_dim: int, base: float, length_scale: float) -> tuple[Tensor, Tensor]:
-    """cos/sin ``[B, 1, Y, X, D/2]`` (float64) for token lat/lon ``[B, Y, X]``."""
+def rope_angles(cx: Tensor, cy: Tensor, head_dim: int, base: float, cz: Tensor | None = None,
+                level_pairs: int = 0) -> Tensor:
+    """Angles ``[..., D/2]``: pairs [0, n) rotate by cx, [n, 2n) by cy and, with
+    ``level_pairs`` = L > 0, [2n, P) by cz (n = (P - L)/2; n = P/2 without levels)."""
+    P = head_dim // 2
+    n = (P - level_pairs) // 2
+    if level_pairs < 0 or 2 * n + level_pairs != P or n < 1:
+        raise ValueError(f"cannot split {P} pairs into x | y | {level_pairs} level pairs")
+    om = _omega(n, base)
+    parts = [cx.double()[..., None] * om, cy.double()[..., None] * om]
+    if level_pairs:
+        if cz is None:
+            raise ValueError("level pairs need level coordinates cz")
+        parts.append(cz.double()[..., None] * _omega(level_pairs, base))
+    return torch.cat(parts, dim=-1)
+
+
+def tables(lat: Tensor, lon: Tensor, head_dim: int, base: float, length_scale: float, levels: int = 0,
+           level_pairs: int = 0) -> tuple[Tensor, Tensor]:
+    """cos/sin (float64) for token lat/lon ``[B, Y, X]``: ``[B, 1, Y, X, D/2]``, or with
+    ``levels`` = Z > 0 and ``level_pairs`` > 0 ``[B, Z, Y, X, D/2]`` (level index z)."""
     lat0, lon0 = spherical_centroid(lat, lon)
     x, y = stereographic(lat, lon, lat0, lon0)
-    ang = rope_angles(x / length_scale, y / length_scale, head_dim, base)
-    return torch.cos(ang).unsqueeze(1), torch.sin(ang).unsqueeze(1)
+    x, y = x / length_scale, y / length_scale
+    if not level_pairs:
+        ang = rope_angles(x, y, head_dim, base)
+        return torch.cos(ang).unsqueeze(1), torch.sin(ang).unsqueeze(1)
+    B, Y, X = lat.shape
+    z = torch.arange(levels, dtype=torch.float64).view(1, levels, 1, 1).expand(B, levels, Y, X)
+    ang = rope_angles(x.unsqueeze(1).expand(B, levels, Y, X), y.unsqueeze(1).expand(B, levels, Y, X), head_dim,
+                      base, z, level_pairs)
+    return torch.cos(ang), torch.sin(ang)
 
 
 def apply_rope(t: Tensor, cos: Tensor, sin: Tensor, layout: str = "half") -> Tensor:

@@ -591,7 +591,14 @@ extern "C" int strata_hip_gemm_bias_act(const strata_hip_gemm_args* a, void* str
   hipStream_t st = (hipStream_t)stream;
   // Plain GEMMs (no activation; bias and an added residual at most) go to
   // hipBLASLt; the fused epilogues, and anything it declines, run here.
-  if (gemm_lt_enabled() && gemm_lt(p, st) == STRATA_HIP_OK) return STRATA_HIP_OK;
+  if (gemm_lt_enabled()) {
+    const int lt = gemm_lt(p, st);
+    if (lt == STRATA_HIP_OK) return STRATA_HIP_OK;
+    if (lt == GEMM_LT_FAILED)
+      return fail(STRATA_HIP_ELAUNCH,
+                  "gemm: hipblasLtCreate failed on this device (plain GEMMs run on hipBLASLt; "
+                  "STRATA_HIP_GEMM=native selects the hand-written kernels)");
+  }
   // The large-tile kernels stream 64-wide K steps with 32-bit lane offsets
   // inside a 256-row block: K a multiple of 64, row strides small enough.
   const bool big = p.K % 64 == 0 && 256 * p.ldx * 2 + 4096 < (int64_t)OOB && 256 * p.ldw * 2 + 4096 < (int64_t)OOB;

@@ -14,10 +14,14 @@
 // rounding to bf16).  No workspace: the library allocates nothing per call.
 //
 // State: one hipBLASLt handle per device (created on first use with that
-// device current) and a host-side plan cache (descriptors + the heuristic's
-// first algorithm) keyed by device, shape, strides and epilogue.  A plan's
-// bias pointer is set under the cache mutex right before the asynchronous
-// launch, so concurrent callers on different threads stay correct.
+// device current; creating it allocates) and a host-side plan cache
+// (descriptors + the heuristic's first algorithm) keyed by device, shape,
+// strides and epilogue.  A plan's bias pointer is set under the cache mutex
+// right before the asynchronous launch, so concurrent callers on different
+// threads stay correct.  A failed handle creation is an error of that call
+// (GEMM_LT_FAILED), not remembered: the next call tries again.  A shape for
+// which the heuristic offers no algorithm is declined and runs on the
+// hand-written kernels.
 #include <hip/hip_runtime.h>
 #include <hipblaslt/hipblaslt.h>
 
@@ -44,7 +48,6 @@ using LtKey = std::tuple<int, int64_t, int64_t, int64_t, int64_t, int64_t, int64
 
 std::mutex g_mu;
 hipblasLtHandle_t g_handle[64] = {};
-bool g_handle_failed[64] = {};
 std::map<LtKey, LtPlan> g_plans;
 
 bool build_plan(hipblasLtHandle_t h, const GemmParams& p, bool has_bias, bool has_res, LtPlan& pl) {
@@ -95,11 +98,9 @@ int gemm_lt(const GemmParams& p, hipStream_t stream) {
   if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return GEMM_LT_DECLINED;
 
   std::lock_guard<std::mutex> lock(g_mu);
-  if (g_handle_failed[dev]) return GEMM_LT_DECLINED;
   if (!g_handle[dev] && hipblasLtCreate(&g_handle[dev]) != HIPBLAS_STATUS_SUCCESS) {
     g_handle[dev] = nullptr;
-    g_handle_failed[dev] = true;
-    return GEMM_LT_DECLINED;
+    return GEMM_LT_FAILED;
   }
   const LtKey key{dev, p.M, p.N, p.K, p.ldx, p.ldw, has_res ? p.ldr : 0, p.ldo, has_bias, has_res};
   auto it = g_plans.find(key);

@@ -102,6 +102,50 @@ class FusedNA3DAttention(nn.Module):
         else:
             self.q_norm = self.k_norm = None
 
+    # Children an attention module of the reference may own, besides parameter-free ones.
+    _KNOWN_CHILDREN = ("qkv", "proj", "gate_proj", "q_norm", "k_norm")
+
+    @classmethod
+    def from_attention(cls, attn: nn.Module, num_heads: int, kernel_size, dilation=1, qk_norm: bool = False,
+                       qk_norm_eps: float = 1e-6, rope_layout: int = _lib.ROPE_HALF,
+                       scale: Optional[float] = None) -> "FusedNA3DAttention":
+        """Wrap an existing attention module, sharing its Linear (and RMSNorm) children.
+
+        The children are re-registered in the module's own order, so the state-dict
+        keys (``qkv``, ``proj``, ``gate_proj``, ``q_norm``, ``k_norm``) and the
+        ``named_parameters()`` order are unchanged.  A child that holds parameters
+        under any other name raises ``TypeError`` (its role would be unknown)."""
+        qkv, proj = getattr(attn, "qkv", None), getattr(attn, "proj", None)
+        if not (isinstance(qkv, nn.Linear) and isinstance(proj, nn.Linear)):
+            raise TypeError("expected an attention module with nn.Linear children qkv and proj")
+        dim = qkv.in_features
+        if qkv.out_features != 3 * dim or proj.in_features != dim or dim % num_heads:
+            raise TypeError(f"qkv {tuple(qkv.weight.shape)} / proj {tuple(proj.weight.shape)} do not fit "
+                            f"a {num_heads}-head attention")
+        for name, child in attn.named_children():
+            if name not in cls._KNOWN_CHILDREN and any(True for _ in child.parameters()):
+                raise TypeError(f"attention child {name!r} holds parameters this drop-in does not use")
+        new = cls.__new__(cls)
+        nn.Module.__init__(new)
+        new.gate_proj = new.q_norm = new.k_norm = None
+        for name, child in attn.named_children():
+            setattr(new, name, child)
+        gate = getattr(attn, "gate_proj", None)
+        if gate is not None and not isinstance(gate, nn.Linear):
+            raise TypeError("gate_proj must be an nn.Linear")
+        for nname in ("q_norm", "k_norm"):
+            norm = getattr(attn, nname, None)
+            w = getattr(norm, "weight", None) if norm is not None else None
+            setattr(new, nname, norm if isinstance(w, torch.Tensor) else None)
+        new.dim, new.num_heads = dim, num_heads
+        new.head_dim = dim // num_heads
+        new.kernel_size = _triple(kernel_size)
+        new.dilation = _triple(dilation)
+        new.rope_layout = rope_layout
+        new.scale = scale
+        new.qk_norm, new.qk_norm_eps = qk_norm, qk_norm_eps
+        return new
+
     def attention(self, x: Tensor, rope: Optional[tuple[Tensor, Tensor]] = None) -> Tensor:
         """Attention output before the projection, ``[B, Z, Y, X, C]``."""
         B, Z, Y, X, C = x.shape
@@ -176,6 +220,54 @@ def swap_mlps(model: nn.Module) -> int:
                 setattr(parent, name, GemmGeluMlp.from_mlp(child))
                 n += 1
     return n
+
+
+def _is_attention(m: nn.Module) -> bool:
+    qkv, proj = getattr(m, "qkv", None), getattr(m, "proj", None)
+    return (isinstance(qkv, nn.Linear) and isinstance(proj, nn.Linear) and qkv.out_features == 3 * qkv.in_features
+            and proj.in_features == qkv.in_features)
+
+
+def swap_attention(model: nn.Module, num_heads, kernel_size, dilation=1, qk_norm=False, qk_norm_eps: float = 1e-6,
+                   rope_layout: int = _lib.ROPE_HALF, scale: Optional[float] = None) -> int:
+    """Replace every attention-shaped child (``nn.Linear`` children ``qkv`` [3C, C] and
+    ``proj`` [C, C], optionally ``gate_proj`` and RMSNorms ``q_norm`` / ``k_norm``) by a
+    :class:`FusedNA3DAttention` sharing those modules: the qkv GEMM, the (qk-norm +)
+    RoPE + pack kernel, NA3D, the gate GEMM and the proj GEMM on the HIP library.
+
+    The pattern is the reference's post-construction ``_use_tanh_gelu`` swap
+    (screamcast/strata_wrappers.py:76-100, applied at :342 and :509): modules are
+    found by structure, parameters are shared, and state-dict keys and
+    ``named_parameters()`` order stay as they were (tests/test_param_order.py:87-119).
+    ``num_heads``, ``kernel_size``, ``dilation`` and ``qk_norm`` are either one value
+    for every swapped module or a sequence with one entry per module, in
+    ``model.modules()`` order (a per-block dilation schedule, for instance).
+    Returns the number of modules swapped; raises ``RuntimeError`` if there were
+    none (as ``_use_tanh_gelu`` does)."""
+    targets = [(parent, name, child) for parent in list(model.modules())
+               for name, child in list(parent.named_children())
+               if not isinstance(child, FusedNA3DAttention) and _is_attention(child)]
+    if not targets:
+        raise RuntimeError("swap_attention found no module with qkv [3C, C] and proj [C, C] Linear children")
+
+    def pick(v, i, is_scalar):
+        if is_scalar(v):
+            return v
+        v = list(v)
+        if len(v) != len(targets):
+            raise ValueError(f"{len(v)} per-module values for {len(targets)} attention modules")
+        return v[i]
+
+    for i, (parent, name, child) in enumerate(targets):
+        new = FusedNA3DAttention.from_attention(
+            child,
+            pick(num_heads, i, lambda v: isinstance(v, int)),
+            pick(kernel_size, i, lambda v: isinstance(v, int) or (len(v) == 3 and all(isinstance(t, int) for t in v))),
+            pick(dilation, i, lambda v: isinstance(v, int) or (len(v) == 3 and all(isinstance(t, int) for t in v))),
+            pick(qk_norm, i, lambda v: isinstance(v, bool)),
+            qk_norm_eps, rope_layout, scale)
+        setattr(parent, name, new)
+    return len(targets)
 
 
 def init_xavier_(module: nn.Module, generator: torch.Generator) -> None:

@@ -16,7 +16,11 @@ this build fixes (the reference leaves them to physicsnemo):
   y, with angular frequency ``base ** (-j / (P/2))`` for j in [0, P/2)
   (axial 2D RoPE; RoFormer frequency schedule per axis).
 * Tables are ``[B, 1, Y, X, P]`` (one table per tile, broadcast over the
-  vertical level index z), float32.
+  vertical level index z), float32.  With ``level_pairs`` = L > 0 (BASELINE
+  configs[1]'s level index in z) the pairs split x | y | level instead: [0, n)
+  rotate by x, [n, 2n) by y, [2n, P) by the level index z = 0..Z-1, n = (P-L)/2,
+  each group with frequencies base^(-j/m) over its own size m; the tables are
+  then ``[B, Z, Y, X, P]``.
 * Pair layout of the rotated vector: "half" (pair p = (p, p + D/2)).
 
 Tables cost O(B*Y*X*P) and are built with torch ops on the tokens' device;
@@ -58,27 +62,45 @@ def stereographic_projection(lat: Tensor, lon: Tensor, lat0: Tensor, lon0: Tenso
     return kk * c * torch.sin(dl), kk * (c0 * s - s0 * c * torch.cos(dl))
 
 
-def axial_rope_cos_sin(cx: Tensor, cy: Tensor, head_dim: int, base: float) -> tuple[Tensor, Tensor]:
-    """cos/sin ``[..., D/2]`` for per-token coordinates cx, cy ``[...]``."""
+def axial_rope_cos_sin(cx: Tensor, cy: Tensor, head_dim: int, base: float, cz: Tensor | None = None,
+                       level_pairs: int = 0) -> tuple[Tensor, Tensor]:
+    """cos/sin ``[..., D/2]`` for per-token coordinates cx, cy (and level cz) ``[...]``."""
     P = head_dim // 2
-    if head_dim % 4:
-        raise ValueError("axial 2D RoPE needs head_dim divisible by 4")
-    half = P // 2
-    j = torch.arange(half, dtype=torch.float64, device=cx.device)
-    omega = base ** (-j / half)
-    ang = torch.cat([cx.double()[..., None] * omega, cy.double()[..., None] * omega], dim=-1)
+    n, rem = divmod(P - level_pairs, 2)
+    if head_dim % 2 or level_pairs < 0 or rem or n < 1:
+        raise ValueError(f"cannot split {P} RoPE pairs into x | y | {level_pairs} level pairs")
+
+    def freqs(m: int) -> Tensor:
+        return base ** (-torch.arange(m, dtype=torch.float64, device=cx.device) / m)
+
+    parts = [cx.double()[..., None] * freqs(n), cy.double()[..., None] * freqs(n)]
+    if level_pairs:
+        if cz is None:
+            raise ValueError("level pairs need level coordinates")
+        parts.append(cz.double()[..., None] * freqs(level_pairs))
+    ang = torch.cat(parts, dim=-1)
     return torch.cos(ang).float(), torch.sin(ang).float()
 
 
 def stereographic_rope_tables(
-    lat: Tensor, lon: Tensor, head_dim: int, base: float, length_scale: float
+    lat: Tensor, lon: Tensor, head_dim: int, base: float, length_scale: float, levels: int = 0,
+    level_pairs: int = 0,
 ) -> tuple[Tensor, Tensor]:
-    """Tables ``[B, 1, Y, X, D/2]`` from token lat/lon ``[B, Y, X]`` (radians)."""
+    """Tables ``[B, 1, Y, X, D/2]`` from token lat/lon ``[B, Y, X]`` (radians); with
+    ``level_pairs`` > 0, ``[B, levels, Y, X, D/2]`` whose last ``level_pairs`` pairs
+    rotate by the level index z."""
     lat64, lon64 = lat.double(), lon.double()
     lat0, lon0 = spherical_centroid(lat64, lon64)
     x, y = stereographic_projection(lat64, lon64, lat0, lon0)
-    cos, sin = axial_rope_cos_sin(x / length_scale, y / length_scale, head_dim, base)
-    return cos.unsqueeze(1).contiguous(), sin.unsqueeze(1).contiguous()
+    x, y = x / length_scale, y / length_scale
+    if not level_pairs:
+        cos, sin = axial_rope_cos_sin(x, y, head_dim, base)
+        return cos.unsqueeze(1).contiguous(), sin.unsqueeze(1).contiguous()
+    B, Y, X = lat.shape
+    z = torch.arange(levels, dtype=torch.float64, device=lat.device).view(1, levels, 1, 1).expand(B, levels, Y, X)
+    cos, sin = axial_rope_cos_sin(x.unsqueeze(1).expand(B, levels, Y, X), y.unsqueeze(1).expand(B, levels, Y, X),
+                                  head_dim, base, z, level_pairs)
+    return cos.contiguous(), sin.contiguous()
 
 
 def synthetic_tile_latlon(

@@ -196,7 +196,8 @@ def test_rope_pack_qk_norm_vs_oracle(gpu, layout, affine):
 
 def test_rope_pack_stereographic_tables(gpu):
     """configs[1]-style tables (64x64 tile, 32 pairs, base 1e4) built by the
-    product helper agree with the float64 oracle and drive the pack kernel."""
+    product helper agree with the float64 oracle and drive the pack kernel
+    (the level-index tables of configs[1] run in tests/test_configs_gpu.py)."""
     g = torch.Generator().manual_seed(0)
     lat, lon = P.synthetic_tile_latlon(2, 64, 64, g)
     ls = P.default_rope_length_scale(1)
@@ -204,6 +205,15 @@ def test_rope_pack_stereographic_tables(gpu):
     c2, s2 = R.tables(lat, lon, 64, 10000.0, ls)
     assert (cos.double().cpu() - c2).abs().max() < 1e-5
     assert (sin.double().cpu() - s2).abs().max() < 1e-5
+    # ... and drive the pack kernel: [2, 2, 64, 64] tokens x 4 heads (tables broadcast over z)
+    B, Z, H, D = 2, 2, 4, 64
+    qkv = _randn((B, Z, 64, 64, 3 * H * D), g)
+    q, k, v = torch.ops.strata_hip.rope_qkv_pack(qkv.to(gpu), cos, sin, H, _lib.ROPE_HALF, False, 1e-6, None, None)
+    t = qkv.double().view(B, Z, 64, 64, 3, H, D)
+    for got, ref in ((q, R.apply_rope(t[..., 0, :, :], c2, s2)), (k, R.apply_rope(t[..., 1, :, :], c2, s2))):
+        d = (got.double().cpu() - ref).abs()
+        assert (d <= ref.abs() * 2**-7 + 1e-6).all(), d.max()
+    assert torch.equal(v.cpu(), qkv.view(B, Z, 64, 64, 3, H, D)[..., 2, :, :])
 
 
 @pytest.mark.parametrize("C", [64, 768, 1024, 4096])

@@ -88,3 +88,62 @@ def test_product_tables_match_oracle():
     x, y = R.stereographic(lat, lon, *R.spherical_centroid(lat, lon))
     dx = (x[:, :, 1:] - x[:, :, :-1]) / ls
     assert torch.allclose(dx, torch.ones_like(dx), atol=3e-2)
+
+
+def test_level_index_convention_closed_forms():
+    """configs[1]'s level index in z: pairs x | y | level = 12 | 12 | 8 for D = 64.
+    Closed forms: the level pair j at level z has angle z * base^(-j/8) (pair 24:
+    exactly z radians); level 0 is the identity on the level pairs; the x | y groups
+    are the 2D table of a 48-wide head (12 frequencies per axis); the x | y part does
+    not depend on z."""
+    g = torch.Generator().manual_seed(0)
+    lat, lon = P.synthetic_tile_latlon(2, 8, 8, g)
+    ls = R.default_rope_length_scale(1)
+    Z, base = 5, 10000.0
+    c, s = R.tables(lat, lon, 64, base, ls, levels=Z, level_pairs=8)
+    assert c.shape == (2, Z, 8, 8, 32)
+    ang = torch.atan2(s, c)
+    for z in range(Z):
+        for j in range(8):
+            want = z * base ** (-j / 8)
+            got = ang[:, z, :, :, 24 + j]
+            d = torch.remainder(got - want + math.pi, 2 * math.pi) - math.pi  # angle mod 2 pi
+            assert d.abs().max() < 1e-12, (z, j)
+    assert torch.equal(c[:, 0, ..., 24:], torch.ones_like(c[:, 0, ..., 24:]))
+    assert torch.equal(s[:, 0, ..., 24:], torch.zeros_like(s[:, 0, ..., 24:]))
+    c2, s2 = R.tables(lat, lon, 48, base, ls)  # 2D table of 24 pairs: 12 per axis
+    for z in range(Z):
+        assert torch.allclose(c[:, z, ..., :24], c2[:, 0], atol=1e-15)
+        assert torch.allclose(s[:, z, ..., :24], s2[:, 0], atol=1e-15)
+
+
+def test_level_rotation_is_relative_in_z():
+    """<R(z1) q, R(z2) k> over the level pairs depends only on z1 - z2."""
+    g = torch.Generator().manual_seed(1)
+    lat, lon = P.synthetic_tile_latlon(1, 2, 2, g)
+    c, s = R.tables(lat, lon, 64, 10000.0, R.default_rope_length_scale(1), levels=8, level_pairs=8)
+    q = torch.zeros(1, 8, 2, 2, 1, 64, dtype=torch.float64)
+    k = torch.zeros_like(q)
+    qv = torch.randn(64, generator=g, dtype=torch.float64)
+    kv = torch.randn(64, generator=g, dtype=torch.float64)
+    lvl = [d for p in range(24, 32) for d in (p, p + 32)]  # half layout: pair p = (p, p + 32)
+    q[..., lvl] = qv[lvl]
+    k[..., lvl] = kv[lvl]
+    rq, rk = R.apply_rope(q, c, s), R.apply_rope(k, c, s)
+    dot = lambda z1, z2: (rq[0, z1, 0, 0, 0] * rk[0, z2, 0, 0, 0]).sum()  # noqa: E731
+    assert abs(dot(5, 2) - dot(4, 1)) < 1e-12 and abs(dot(3, 3) - dot(0, 0)) < 1e-12
+    assert abs(dot(5, 2) - dot(2, 5)) > 1e-6  # and it is not symmetric in the offset
+
+
+def test_product_level_tables_match_oracle():
+    g = torch.Generator().manual_seed(2)
+    lat, lon = P.synthetic_tile_latlon(2, 16, 16, g)
+    ls = P.default_rope_length_scale(1)
+    cp, sp = P.stereographic_rope_tables(lat, lon, 64, 10000.0, ls, levels=8, level_pairs=8)
+    co, so = R.tables(lat, lon, 64, 10000.0, ls, levels=8, level_pairs=8)
+    assert cp.shape == (2, 8, 16, 16, 32) and cp.dtype == torch.float32
+    assert (cp.double() - co).abs().max() < 1e-6 and (sp.double() - so).abs().max() < 1e-6
+    import pytest
+
+    with pytest.raises(ValueError):
+        P.stereographic_rope_tables(lat, lon, 64, 10000.0, ls, levels=8, level_pairs=7)
