@@ -117,10 +117,13 @@ def test_cfg4_stage_blocks_full_shape(gpu):
     _block_vs_oracle(gpu, 6, (8, 32, 32), 1024, 16, (3, 9, 9), ls_patch=2, entries=(0, 5))
 
 
-def test_cfg4_full_model_step_properties(gpu):
+def test_cfg4_full_model_step_properties(gpu, monkeypatch):
     """Full configs[4] model (12 + 12 blocks, batch 6 face tiles, 80 channels):
-    finite step; permuting the faces (with their tables) permutes the output bit for
-    bit; a zero head makes the step the identity; 2 steps of rollout stay finite."""
+    finite step; permuting the faces (with their tables) permutes the output -- bit
+    for bit, and run to run, with every GEMM on the hand-written kernels; within
+    1e-2 with the plain GEMMs on hipBLASLt, whose results vary in the last bits
+    from run to run (seen: 0 to 2.8e-3 rel-L2 of the tendency after 24 blocks);
+    a zero head makes the step the identity; 2 steps of rollout stay finite."""
     torch.manual_seed(0)
     model = TwoStageStrata()
     init_xavier_(model, torch.Generator().manual_seed(1))
@@ -130,18 +133,32 @@ def test_cfg4_full_model_step_properties(gpu):
     lat, lon = P.synthetic_tile_latlon(6, 64, 64, g)
     r1, r2 = model.rope_tables(lat.to(gpu), lon.to(gpu))
     xg = x.to(gpu)
+    perm = torch.tensor([3, 0, 5, 1, 4, 2], device=gpu)
+    pr1 = tuple(t[perm] for t in r1)
+    pr2 = tuple(t[perm] for t in r2)
     print("cfg4 full step", flush=True)
     y = model.step(xg, r1, r2)
     torch.cuda.synchronize()
     assert torch.isfinite(y).all()
     assert (y - xg).abs().max() > 0
-    perm = torch.tensor([3, 0, 5, 1, 4, 2], device=gpu)
-    pr1 = tuple(t[perm] for t in r1)
-    pr2 = tuple(t[perm] for t in r2)
     print("cfg4 permuted faces", flush=True)
     yp = model.step(xg[perm], pr1, pr2)
-    d = (yp - y[perm]).abs().max().item()
-    assert torch.equal(yp, y[perm]), f"face permutation changed the output by {d}"
+    err = rel_l2(yp - xg[perm], y[perm] - xg[perm])
+    print(f"  permuted vs permuted output: rel-L2 of the tendency {err:.3e}", flush=True)
+    assert err <= 1e-2
+    monkeypatch.setenv("STRATA_HIP_GEMM", "native")
+    print("cfg4 permuted faces, hand-written GEMMs", flush=True)
+    yn = model.step(xg, r1, r2)
+    assert torch.equal(model.step(xg, r1, r2), yn)  # deterministic run to run
+    ynp = model.step(xg[perm], pr1, pr2)
+    d = (ynp - yn[perm]).abs().max().item()
+    assert torch.equal(ynp, yn[perm]), f"face permutation changed the output by {d}"
+    # Two bf16 evaluations that differ only in the plain GEMMs' rounding, carried
+    # through 24 blocks: the tendencies agree to a few percent.
+    err = rel_l2(yn - xg, y - xg)
+    print(f"  hand-written vs hipBLASLt plain GEMMs: rel-L2 of the tendency {err:.3e}", flush=True)
+    assert err <= 5e-2
+    monkeypatch.delenv("STRATA_HIP_GEMM")
     print("cfg4 rollout 2 steps", flush=True)
     yr = model.rollout(xg, 2, r1, r2)
     assert torch.isfinite(yr).all()
