@@ -140,6 +140,20 @@ typedef struct strata_hip_na3d_bwd_args {
 int strata_hip_na3d_bwd(const strata_hip_na3d_bwd_args* args, void* stream);
 
 /* ---------------------------------------------------------------------------
+ * NA3D backward without allocation: no counterpart in the reference.  For
+ * callers that cannot allocate device memory or pass a workspace (code under
+ * HIP graph capture, serving loops, harnesses that forbid hipMalloc).  Same
+ * arguments and results as strata_hip_na3d_bwd, except that `workspace` must
+ * be NULL: the per-query statistics live in a scratch array of the library's
+ * own, one per device (16 MiB, held until the process ends), so at most
+ * B*Z*Y*X*H = 2^21 (query, head) pairs per call; larger calls return
+ * STRATA_HIP_EUNSUPPORTED.  Nothing is allocated or freed.  Every call on one
+ * device uses that device's scratch: calls that overlap in time on one device
+ * (different streams or threads) race.
+ * ------------------------------------------------------------------------- */
+int strata_hip_na3d_bwd_noalloc(const strata_hip_na3d_bwd_args* args, void* stream);
+
+/* ---------------------------------------------------------------------------
  * Stereographic-RoPE + QKV pack.
  * Replaces the attention's qkv split + RoPE of the physicsnemo Strata block
  * (attn.qkv keys at tests/regression_data/sweep1_...param_order.txt:3-4;

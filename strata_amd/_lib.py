@@ -258,6 +258,7 @@ class StateUpdateArgs(ctypes.Structure):
 EXPORTS = {
     "strata_hip_na3d_fwd": ([ctypes.POINTER(Na3dArgs), ctypes.c_void_p], ctypes.c_int),
     "strata_hip_na3d_bwd": ([ctypes.POINTER(Na3dBwdArgs), ctypes.c_void_p], ctypes.c_int),
+    "strata_hip_na3d_bwd_noalloc": ([ctypes.POINTER(Na3dBwdArgs), ctypes.c_void_p], ctypes.c_int),
     "strata_hip_rope_qkv_pack": ([ctypes.POINTER(RopePackArgs), ctypes.c_void_p], ctypes.c_int),
     "strata_hip_gemm_bias_act": ([ctypes.POINTER(GemmArgs), ctypes.c_void_p], ctypes.c_int),
     "strata_hip_layer_norm": ([ctypes.POINTER(LayerNormArgs), ctypes.c_void_p], ctypes.c_int),

@@ -24,6 +24,7 @@
 // the neighbouring tokens of a tile share most of their window, so their
 // K/V (or Q/dO) reads hit in L1/L2.
 #include <cstdlib>
+#include <mutex>
 
 #include "common.h"
 
@@ -677,8 +678,68 @@ static bool aligned16b(const void* ptr) { return ((uintptr_t)ptr & 15u) == 0; }
 
 using namespace strata;
 
+// Scratch of strata_hip_na3d_bwd_noalloc: the per-query log-sum-exp and
+// rowsum(dout * out) of one call, for at most NA3D_BWD_SCRATCH_TOKENS
+// (query, head) pairs (16 MiB).  Every device the library runs on holds its own
+// copy until the process ends; host code reaches it only through the address
+// hipGetSymbolAddress returns for that device (the array's name is a host-side
+// stand-in, not a device address).  Calls on one device share it: two calls
+// that overlap in time on one device race.
+constexpr int64_t NA3D_BWD_SCRATCH_TOKENS = int64_t(1) << 21;
+static __device__ __align__(256) float scratch[2 * NA3D_BWD_SCRATCH_TOKENS];
+
+namespace {
+constexpr int MAX_DEVICES = 64;
+std::mutex g_scratch_mu;
+float* g_scratch[MAX_DEVICES] = {};
+
+// The current device's copy of `scratch`, looked up once per device.
+int scratch_for_current_device(float** out) {
+  int dev = -1;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= MAX_DEVICES)
+    return fail(STRATA_HIP_ELAUNCH, "na3d_bwd_noalloc: no current HIP device");
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (!g_scratch[dev]) {
+    void* ptr = nullptr;
+    const hipError_t e = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch));
+    if (e != hipSuccess || !ptr)
+      return fail(STRATA_HIP_ELAUNCH, std::string("na3d_bwd_noalloc: hipGetSymbolAddress(scratch): ") +
+                                          hipGetErrorString(e));
+    g_scratch[dev] = (float*)ptr;
+  }
+  *out = g_scratch[dev];
+  return STRATA_HIP_OK;
+}
+}  // namespace
+
+// Argument checks and the launch shared by both entry points; `workspace` is
+// the caller's buffer or this device's scratch.
+static int na3d_bwd_run(const strata_hip_na3d_bwd_args* a, float* workspace, void* stream);
+
 extern "C" int strata_hip_na3d_bwd(const strata_hip_na3d_bwd_args* a, void* stream) {
   if (!a) return fail(STRATA_HIP_EINVAL, "na3d_bwd: null args");
+  return na3d_bwd_run(a, a->workspace, stream);
+}
+
+extern "C" int strata_hip_na3d_bwd_noalloc(const strata_hip_na3d_bwd_args* a, void* stream) {
+  if (!a) return fail(STRATA_HIP_EINVAL, "na3d_bwd_noalloc: null args");
+  if (a->workspace)
+    return fail(STRATA_HIP_EINVAL, "na3d_bwd_noalloc: workspace must be NULL (the library's scratch is used)");
+  if (a->batch < 0 || a->heads <= 0 || a->grid[0] <= 0 || a->grid[1] <= 0 || a->grid[2] <= 0)
+    return fail(STRATA_HIP_EINVAL, "na3d_bwd_noalloc: bad batch/heads/grid");
+  const int64_t tokens = (int64_t)a->batch * a->grid[0] * a->grid[1] * a->grid[2] * a->heads;
+  if (tokens > NA3D_BWD_SCRATCH_TOKENS)
+    return fail(STRATA_HIP_EUNSUPPORTED,
+                "na3d_bwd_noalloc: B*Z*Y*X*H = " + std::to_string(tokens) + " exceeds the scratch maximum of " +
+                    std::to_string(NA3D_BWD_SCRATCH_TOKENS) + " (query, head) pairs; use strata_hip_na3d_bwd");
+  if (tokens == 0) return na3d_bwd_run(a, nullptr, stream);
+  float* ws = nullptr;
+  const int rc = scratch_for_current_device(&ws);
+  if (rc != STRATA_HIP_OK) return rc;
+  return na3d_bwd_run(a, ws, stream);
+}
+
+static int na3d_bwd_run(const strata_hip_na3d_bwd_args* a, float* workspace, void* stream) {
   if (a->dtype != STRATA_HIP_F32 && a->dtype != STRATA_HIP_BF16)
     return fail(STRATA_HIP_EINVAL, "na3d_bwd: dtype must be f32 or bf16");
   if (a->batch < 0 || a->heads <= 0 || a->head_dim <= 0)
@@ -694,7 +755,7 @@ extern "C" int strata_hip_na3d_bwd(const strata_hip_na3d_bwd_args* a, void* stre
       return fail(STRATA_HIP_EINVAL, std::string("na3d_bwd: dilation * kernel exceeds the grid on axis ") + axis[i]);
   }
   if (a->batch == 0) return STRATA_HIP_OK;
-  const void* ptrs[] = {a->q, a->k, a->v, a->out, a->dout, a->dq, a->dk, a->dv, a->workspace};
+  const void* ptrs[] = {a->q, a->k, a->v, a->out, a->dout, a->dq, a->dk, a->dv, workspace};
   for (const void* ptr : ptrs) {
     if (!ptr) return fail(STRATA_HIP_EINVAL, "na3d_bwd: null tensor pointer");
     if (!aligned16b(ptr)) return fail(STRATA_HIP_EINVAL, "na3d_bwd: tensors must be 16-byte aligned");
@@ -719,8 +780,8 @@ extern "C" int strata_hip_na3d_bwd(const strata_hip_na3d_bwd_args* a, void* stre
   }
   p.scale = a->scale;
   const int64_t tokens = (int64_t)p.B * p.Z * p.Y * p.X * p.H;
-  p.lse = a->workspace;
-  p.dsum = a->workspace + tokens;
+  p.lse = workspace;
+  p.dsum = workspace + tokens;
   if (a->lse) {  // the forward's statistics: prep reduces to D_i
     if ((uintptr_t)a->lse & 3u) return fail(STRATA_HIP_EINVAL, "na3d_bwd: lse must be 4-byte aligned");
     if (tokens * (a->head_dim * (a->dtype == STRATA_HIP_BF16 ? 2 : 4) / 16) / 256 + 1 > 0x7fffffff)
