@@ -1342,52 +1342,96 @@ __device__ __forceinline__ void na3d_strip_fast_body(const Na3dParams p, const N
     return __builtin_amdgcn_ballot_w64(valid && !ok) != 0;
   };
 
+  // QK scores of slot k against the stage's RPS key rows, from the x bias.
+  auto scores = [&](int k, const bf16x8 (&ak)[RPS][KS], f32x4 (&sacc)[RPS]) {
+#pragma unroll
+    for (int r = 0; r < RPS; ++r) {
+      sacc[r] = xbias;
+#pragma unroll
+      for (int ks = 0; ks < KS; ++ks)
+        sacc[r] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ak[r][ks], qreg[k][ks], sacc[r], 0, 0, 0);
+    }
+  };
+  // Row sums and O^T += V^T P^T of slot k for the stage's row pairs.
+  auto accumulate = [&](int k, const bf16x8 (&pb)[NRP], const bf16x8 (&av)[NRP][DB]) {
+#pragma unroll
+    for (int rp = 0; rp < NRP; ++rp) {
+      lacc[k] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ones, pb[rp], lacc[k], 0, 0, 0);
+#pragma unroll
+      for (int db = 0; db < DB; ++db)
+        oacc[k][db] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(av[rp][db], pb[rp], oacc[k][db], 0, 0, 0);
+    }
+  };
+  auto exp_pack = [&](const f32x4& sv) {
+    return (u32x2){pack_bf16x2(__builtin_amdgcn_exp2f(sv[0]), __builtin_amdgcn_exp2f(sv[1])),
+                   pack_bf16x2(__builtin_amdgcn_exp2f(sv[2]), __builtin_amdgcn_exp2f(sv[3]))};
+  };
+  auto rows_to_b = [](const u32x2& a, const u32x2& b) {
+    return __builtin_bit_cast(bf16x8, (u32x4){a[0], a[1], b[0], b[1]});
+  };
+
   // One stage's tile math for every slot.  C: slot of the tile in its first group.
   // ACT: bit k set if slot k holds a live tile (ramp groups at a strip's ends skip the others).
+  //
+  // The tile in its first group (slot C) sees group row r only from query rows
+  // t <= r, the tile in its last group (slot C + 1) sees row r only from t >= r:
+  // slot C's row r and slot C + 1's row r + 1 are live on disjoint lanes (r < 3).
+  // When both slots hold tiles their scores on those rows are merged lane by lane
+  // before the exponential (one v_exp_f32 per merged value instead of two) and
+  // split again by the same masks: 20 exponentials for the two tiles instead of 32.
   auto stage_math = [&](auto cst, auto act, const bf16x8 (&ak)[RPS][KS], const bf16x8 (&av)[NRP][DB]) {
     constexpr int C = decltype(cst)::value;
     constexpr int ACT = decltype(act)::value;
+    constexpr int C1 = (C + 1) & (NS - 1);
+    constexpr bool MERGE = ((ACT >> C) & 1) && ((ACT >> C1) & 1);
+    if constexpr (MERGE) {
+      f32x4 s0[RPS], s1[RPS];
+      scores(C, ak, s0);
+      scores(C1, ak, s1);
+      u32x2 pm[3];
 #pragma unroll
-    for (int tt = 0; tt < NS; ++tt) {
+      for (int r = 0; r < 3; ++r) {
+        f32x4 m;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) m[i] = ylo[r] ? s1[r + 1][i] : s0[r][i];  // t > r: slot C + 1's row r + 1
+        pm[r] = exp_pack(m);
+      }
+      const u32x2 c3 = exp_pack(s0[3]), d0 = exp_pack(s1[0]);
+      const u32x2 zero = {0u, 0u};
+      u32x2 cr[3], dr[3];
+#pragma unroll
+      for (int r = 0; r < 3; ++r) {
+        cr[r] = ylo[r] ? zero : pm[r];  // slot C, row r: t <= r
+        dr[r] = yhi[r] ? zero : pm[r];  // slot C + 1, row r + 1: t >= r + 1
+      }
+      const bf16x8 pc[NRP] = {rows_to_b(cr[0], cr[1]), rows_to_b(cr[2], c3)};
+      const bf16x8 pd[NRP] = {rows_to_b(d0, dr[0]), rows_to_b(dr[1], dr[2])};
+      accumulate(C, pc, av);
+      accumulate(C1, pd, av);
+    }
+#pragma unroll
+    for (int tt = MERGE ? 2 : 0; tt < NS; ++tt) {
       const int k = (C + tt) & (NS - 1);  // tt = 0: the tile's first group, tt = 1: its last
       if (!((ACT >> k) & 1)) continue;
       f32x4 sacc[RPS];
-#pragma unroll
-      for (int r = 0; r < RPS; ++r) {
-        sacc[r] = xbias;
-#pragma unroll
-        for (int ks = 0; ks < KS; ++ks)
-          sacc[r] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ak[r][ks], qreg[k][ks], sacc[r], 0, 0, 0);
-      }
+      scores(k, ak, sacc);
       bf16x8 pb[NRP];
 #pragma unroll
       for (int rp = 0; rp < NRP; ++rp) {
-        float pv[8];
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          pv[i] = __builtin_amdgcn_exp2f(sacc[2 * rp][i]);
-          pv[4 + i] = __builtin_amdgcn_exp2f(sacc[2 * rp + 1][i]);
-        }
-        u32x4 pw = {pack_bf16x2(pv[0], pv[1]), pack_bf16x2(pv[2], pv[3]), pack_bf16x2(pv[4], pv[5]),
-                    pack_bf16x2(pv[6], pv[7])};
+        u32x2 ra = exp_pack(sacc[2 * rp]), rb = exp_pack(sacc[2 * rp + 1]);
+        u32x2* rw[2] = {&ra, &rb};
 #pragma unroll
         for (int h2 = 0; h2 < 2; ++h2) {
-          const int r = 2 * rp + h2;  // key row of the group: dwords 2*h2, 2*h2+1 hold its 4 keys
+          const int r = 2 * rp + h2;  // key row of the group
           if ((tt == 0 && r <= 2) || (tt == 1 && r >= 1)) {
             const bool zero = tt == 0 ? ylo[r < 3 ? r : 2] : yhi[r >= 1 ? r - 1 : 0];
-            pw[2 * h2] = zero ? 0u : pw[2 * h2];
-            pw[2 * h2 + 1] = zero ? 0u : pw[2 * h2 + 1];
+            (*rw[h2])[0] = zero ? 0u : (*rw[h2])[0];
+            (*rw[h2])[1] = zero ? 0u : (*rw[h2])[1];
           }
         }
-        pb[rp] = __builtin_bit_cast(bf16x8, pw);
+        pb[rp] = rows_to_b(ra, rb);
       }
-#pragma unroll
-      for (int rp = 0; rp < NRP; ++rp) {
-        lacc[k] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ones, pb[rp], lacc[k], 0, 0, 0);
-#pragma unroll
-        for (int db = 0; db < DB; ++db)
-          oacc[k][db] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(av[rp][db], pb[rp], oacc[k][db], 0, 0, 0);
-      }
+      accumulate(k, pb, av);
     }
   };
 
@@ -1477,7 +1521,8 @@ __device__ __forceinline__ void na3d_strip_fast_body(const Na3dParams p, const N
   using ALL = std::integral_constant<int, 15>;
   // Ramp-up: tile g starts in group g (slot g), so groups 0-2 compute only
   // the slots already holding a tile.  From group 3 on every slot computes
-  // (the ramp-down's emptied slots too: their masks would depend on NT mod 4).
+  // (the ramp-down's emptied slots too: separate instances for the ramp-down
+  // groups make the register allocator spill).
   group(I0{}, std::integral_constant<int, 1>{}, 0);
   group(I1{}, std::integral_constant<int, 3>{}, 1);
   group(I2{}, std::integral_constant<int, 7>{}, 2);
