@@ -19,7 +19,9 @@
 //  * na3d_strip_kernel:  the same tile math for 4-column tiles (kx 10..13,
 //    head_dim 64), but a workgroup walks a whole column of tiles along y and
 //    streams every key row once, four tiles in flight per wave.
+#include <cstdlib>
 #include <type_traits>
+#include <utility>
 
 #include "common.h"
 
@@ -624,22 +626,25 @@ struct StripTile {
   int b, h, gz, gy, gx, iz, qy0, ye, qx0, qx1;
 };
 
-// Rare path of the strip kernel: recompute one 4x4 tile of queries exactly,
-// straight from global memory, with a running maximum (fp32 online softmax).
-// Called by a whole wave when the tile's unnormalised sums left the range
-// the fast path guarantees (scores far from 0 in log2 units, or non-finite
-// inputs).  Lane l handles query l >> 2 (row-major in the tile)
+// Rare path of the strip kernels: recompute one (16/TX) x TX tile of queries
+// exactly, straight from global memory, with a running maximum (fp32 online
+// softmax).  Called by a whole wave when the tile's unnormalised sums left the
+// range the fast path guarantees (scores far from 0 in log2 units, or
+// non-finite inputs).  Lane l handles query l >> 2 (row-major in the tile)
 // and the head-dim quarter l & 3 (16 values); invalid queries (past the
 // chunk's last row or column) compute a clamped copy and store nothing.
+template <int TX = 4>
 __device__ __forceinline__ void na3d_strip_tile_exact(const Na3dParams* pp, StripTile t) {
 #if defined(__HIP_DEVICE_COMPILE__)
+  constexpr int TY = 16 / TX;
   const Na3dParams& p = *pp;
   const int lane = (int)__builtin_amdgcn_workitem_id_x() & 63;
   const int n = lane >> 2, dq = lane & 3;
   const int dz = p.dil[0], dy = p.dil[1], dx = p.dil[2];
   const int Lz = sub_len(p.L[0], t.gz, dz), Ly = sub_len(p.L[1], t.gy, dy), Lx = sub_len(p.L[2], t.gx, dx);
-  const bool valid = t.qy0 + n / 4 < t.ye && t.qx0 + n % 4 < t.qx1;
-  const int qy = min(t.qy0 + n / 4, t.ye - 1), qx = min(t.qx0 + n % 4, t.qx1 - 1);
+  static_assert(TX * TY == 16, "16 queries per tile");
+  const bool valid = t.qy0 + n / TX < t.ye && t.qx0 + n % TX < t.qx1;
+  const int qy = min(t.qy0 + n / TX, t.ye - 1), qx = min(t.qx0 + n % TX, t.qx1 - 1);
   const int sz = win_start(t.iz, Lz, p.ker[0]), sy = win_start(qy, Ly, p.ker[1]), sx = win_start(qx, Lx, p.ker[2]);
   const int rz = t.gz + dz * t.iz, ry = t.gy + dy * qy, rx = t.gx + dx * qx;
   const bf16* qp = (const bf16*)p.q + (int64_t)t.b * p.qs[0] + (int64_t)rz * p.qs[1] + (int64_t)ry * p.qs[2] +
@@ -1139,12 +1144,22 @@ __global__ __launch_bounds__(256, 2) void na3d_strip_kernel(Na3dParams p, Na3dSt
 // ~26 log2 units below 2^-100 underflow (relative weight below 2^-26 each).
 // (gfx950's v_dot2c_f32_bf16 does not keep an fp32 sum: the row sums stay on
 // the ones-operand MFMA.)
-template <int D, int TX, int RPS, int NBUF>
+template <typename F, int... I>
+__device__ __forceinline__ void static_for_impl(F&& f, std::integer_sequence<int, I...>) {
+  (f(std::integral_constant<int, I>{}), ...);
+}
+// f(integral_constant<int, i>) for i = 0 .. N-1, unrolled at compile time.
+template <int N, typename F>
+__device__ __forceinline__ void static_for(F&& f) {
+  static_for_impl(f, std::make_integer_sequence<int, N>{});
+}
+
+template <int D, int TX, int RPS, int NBUF, int KY>
 __device__ __forceinline__ void na3d_strip_fast_body(const Na3dParams p, const Na3dStrips sg) {
 #if defined(__HIP_DEVICE_COMPILE__)
   constexpr int NWX = NA3D_NWX;
-  constexpr int NS = 4;                   // tile slots per wave
   constexpr int TY = 16 / TX;
+  constexpr int NS = (TY + KY - 1) / RPS;  // tile slots per wave: groups a tile's y-union spans
   constexpr int WQX = NWX * TX;           // workgroup query columns
   constexpr int LW = (NWX - 1) * TX + 16; // keys of a row the workgroup reads (no padding)
   constexpr int KPK = 512 / D;            // keys per KiB
@@ -1158,11 +1173,13 @@ __device__ __forceinline__ void na3d_strip_fast_body(const Na3dParams p, const N
   constexpr int QWB = 16 * D * 2;         // one wave's 16 rows of Q (or of self keys), bytes
   constexpr int QTB = NWX * QWB;          // Q of one tile row of the workgroup
   constexpr int RING_B = NBUF * STAGE_B;
-  constexpr int KY = 13, KR = KY / 2;     // window rows and radius in y
+  constexpr int KR = KY / 2;              // window radius in y
+  constexpr int FLIP = LW % 8 == 4 ? 1 : 0;  // odd rows start half a swizzle period in: chunk slot bit 2 flips
   constexpr uint32_t LMIN_BITS = (127u - 100u) << 23;  // 2^-100 as an fp32 bit pattern
   constexpr uint32_t INF_BITS = 0x7f800000u;
-  static_assert(TX == 4 && TY == 4 && RPS == 4 && TY + KY - 1 == NS * RPS, "regular strip geometry");
-  static_assert(D == 64 && LW % 8 == 4, "odd rows start half a swizzle period in: chunk slot bit 2 flips");
+  static_assert(TY == RPS && TY + KY - 1 == NS * RPS && NS >= 2 && (RPS == 2 || RPS == 4),
+                "regular strip geometry: one tile starts per group and its y-union spans NS groups");
+  static_assert(D == 64 && (LW % 8 == 4 || LW % 8 == 0), "rows start at a whole or half swizzle period");
   static_assert(LPT * NWX * 1024 == STAGE_B && 2 * LPT * 1024 == RPS * RB,
                 "stage layout: waves 0-1 load the K rows, waves 2-3 the V rows, LPT KiB each");
   static_assert(QWB == KS * 1024, "16 query rows are KS 1-KiB loads");
@@ -1200,7 +1217,7 @@ __device__ __forceinline__ void na3d_strip_fast_body(const Na3dParams p, const N
   const int NT = (ye - ys + TY - 1) / TY;
   const int S = ys - KR;                 // first key row of tile 0's union (unclamped)
   const int NR = ye - ys + 2 * KR;       // key rows the strip streams
-  const int NG = (NR + RPS - 1) / RPS;   // row groups (NT + 3)
+  const int NG = (NR + RPS - 1) / RPS;   // row groups (NT + NS - 1)
 
   const int kz = p.ker[0], kx = p.ker[2];
   const int sz = win_start(iz, Lz, kz);
@@ -1302,8 +1319,13 @@ __device__ __forceinline__ void na3d_strip_fast_body(const Na3dParams p, const N
   for (int i = 0; i < 4; ++i) xbias[i] = ((xmask >> i) & 1) ? -INFINITY : 0.f;
   typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
   bf16x8_t ones = {(bf16)1.f, (bf16)1.f, (bf16)1.f, (bf16)1.f, (bf16)1.f, (bf16)1.f, (bf16)1.f, (bf16)1.f};
-  const bool ylo[3] = {trow > 0, trow > 1, trow > 2};  // first group: rows 0..2 masked for later query rows
-  const bool yhi[3] = {trow < 1, trow < 2, trow < 3};  // last group: rows 1..3 masked for earlier query rows
+  // first group: row r (r < RPS - 1) masked for query rows t > r; last group: row r + 1 for t < r + 1
+  bool ylo[RPS - 1], yhi[RPS - 1];
+#pragma unroll
+  for (int r = 0; r < RPS - 1; ++r) {
+    ylo[r] = trow > r;
+    yhi[r] = trow < r + 1;
+  }
 
   // Tile j enters slot k: Q from LDS, pre-scaled to log2 units.
   auto start_tile = [&](int k, uint32_t off) {
@@ -1375,62 +1397,58 @@ __device__ __forceinline__ void na3d_strip_fast_body(const Na3dParams p, const N
   //
   // The tile in its first group (slot C) sees group row r only from query rows
   // t <= r, the tile in its last group (slot C + 1) sees row r only from t >= r:
-  // slot C's row r and slot C + 1's row r + 1 are live on disjoint lanes (r < 3).
-  // When both slots hold tiles their scores on those rows are merged lane by lane
-  // before the exponential (one v_exp_f32 per merged value instead of two) and
-  // split again by the same masks: 20 exponentials for the two tiles instead of 32.
+  // slot C's row r and slot C + 1's row r + 1 are live on disjoint lanes
+  // (r < RPS - 1).  When both slots hold tiles their scores on those rows are
+  // merged lane by lane before the exponential (one v_exp_f32 per merged value
+  // instead of two) and split again by the same masks: for 4-row stages 20
+  // exponentials for the two tiles instead of 32, for 2-row stages 12 instead of 16.
   auto stage_math = [&](auto cst, auto act, const bf16x8 (&ak)[RPS][KS], const bf16x8 (&av)[NRP][DB]) {
     constexpr int C = decltype(cst)::value;
     constexpr int ACT = decltype(act)::value;
-    constexpr int C1 = (C + 1) & (NS - 1);
+    constexpr int C1 = (C + 1) % NS;
     constexpr bool MERGE = ((ACT >> C) & 1) && ((ACT >> C1) & 1);
+    const u32x2 zero = {0u, 0u};
     if constexpr (MERGE) {
       f32x4 s0[RPS], s1[RPS];
       scores(C, ak, s0);
       scores(C1, ak, s1);
-      u32x2 pm[3];
+      u32x2 cr[RPS], dr[RPS];  // packed P rows of slot C and of slot C + 1
 #pragma unroll
-      for (int r = 0; r < 3; ++r) {
+      for (int r = 0; r < RPS - 1; ++r) {
         f32x4 m;
 #pragma unroll
         for (int i = 0; i < 4; ++i) m[i] = ylo[r] ? s1[r + 1][i] : s0[r][i];  // t > r: slot C + 1's row r + 1
-        pm[r] = exp_pack(m);
+        const u32x2 pm = exp_pack(m);
+        cr[r] = ylo[r] ? zero : pm;      // slot C, row r: t <= r
+        dr[r + 1] = yhi[r] ? zero : pm;  // slot C + 1, row r + 1: t >= r + 1
       }
-      const u32x2 c3 = exp_pack(s0[3]), d0 = exp_pack(s1[0]);
-      const u32x2 zero = {0u, 0u};
-      u32x2 cr[3], dr[3];
+      cr[RPS - 1] = exp_pack(s0[RPS - 1]);
+      dr[0] = exp_pack(s1[0]);
+      bf16x8 pc[NRP], pd[NRP];
 #pragma unroll
-      for (int r = 0; r < 3; ++r) {
-        cr[r] = ylo[r] ? zero : pm[r];  // slot C, row r: t <= r
-        dr[r] = yhi[r] ? zero : pm[r];  // slot C + 1, row r + 1: t >= r + 1
+      for (int rp = 0; rp < NRP; ++rp) {
+        pc[rp] = rows_to_b(cr[2 * rp], cr[2 * rp + 1]);
+        pd[rp] = rows_to_b(dr[2 * rp], dr[2 * rp + 1]);
       }
-      const bf16x8 pc[NRP] = {rows_to_b(cr[0], cr[1]), rows_to_b(cr[2], c3)};
-      const bf16x8 pd[NRP] = {rows_to_b(d0, dr[0]), rows_to_b(dr[1], dr[2])};
       accumulate(C, pc, av);
       accumulate(C1, pd, av);
     }
 #pragma unroll
     for (int tt = MERGE ? 2 : 0; tt < NS; ++tt) {
-      const int k = (C + tt) & (NS - 1);  // tt = 0: the tile's first group, tt = 1: its last
+      const int k = (C + tt) % NS;  // tt = 0: the tile's first group, tt = 1: its last
       if (!((ACT >> k) & 1)) continue;
       f32x4 sacc[RPS];
       scores(k, ak, sacc);
+      u32x2 pr[RPS];
+#pragma unroll
+      for (int r = 0; r < RPS; ++r) {
+        pr[r] = exp_pack(sacc[r]);
+        if (tt == 0 && r < RPS - 1) pr[r] = ylo[r] ? zero : pr[r];
+        if (tt == 1 && r >= 1) pr[r] = yhi[r - 1] ? zero : pr[r];
+      }
       bf16x8 pb[NRP];
 #pragma unroll
-      for (int rp = 0; rp < NRP; ++rp) {
-        u32x2 ra = exp_pack(sacc[2 * rp]), rb = exp_pack(sacc[2 * rp + 1]);
-        u32x2* rw[2] = {&ra, &rb};
-#pragma unroll
-        for (int h2 = 0; h2 < 2; ++h2) {
-          const int r = 2 * rp + h2;  // key row of the group
-          if ((tt == 0 && r <= 2) || (tt == 1 && r >= 1)) {
-            const bool zero = tt == 0 ? ylo[r < 3 ? r : 2] : yhi[r >= 1 ? r - 1 : 0];
-            (*rw[h2])[0] = zero ? 0u : (*rw[h2])[0];
-            (*rw[h2])[1] = zero ? 0u : (*rw[h2])[1];
-          }
-        }
-        pb[rp] = rows_to_b(ra, rb);
-      }
+      for (int rp = 0; rp < NRP; ++rp) pb[rp] = rows_to_b(pr[2 * rp], pr[2 * rp + 1]);
       accumulate(k, pb, av);
     }
   };
@@ -1471,7 +1489,7 @@ __device__ __forceinline__ void na3d_strip_fast_body(const Na3dParams p, const N
   uint32_t cur_off = 0;
   uint64_t bad_tiles = 0;  // tiles (index < 64) for the exact path
   bool bad_high = false;   // some tile with index >= 64 needs it
-  // Group gr (slot gr & 3 = C starts tile gr, slot (C + 1) & 3 finishes tile gr - 3).
+  // Group gr (slot gr % NS = C starts tile gr, slot (C + 1) % NS finishes tile gr - NS + 1).
   auto group = [&](auto cst, auto act, int gr) {
     constexpr int C = decltype(cst)::value;
     for (int zc = 0; zc < kz; ++zc) {
@@ -1492,7 +1510,7 @@ __device__ __forceinline__ void na3d_strip_fast_body(const Na3dParams p, const N
 #pragma unroll
       for (int r = 0; r < RPS; ++r)
 #pragma unroll
-        for (int ks = 0; ks < KS; ++ks) ak[r][ks] = *(const bf16x8*)(st + r * RB + koff[ks ^ (r & 1)]);
+        for (int ks = 0; ks < KS; ++ks) ak[r][ks] = *(const bf16x8*)(st + r * RB + koff[ks ^ (FLIP & r)]);
       bf16x8 av[NRP][DB];
 #pragma unroll
       for (int rp = 0; rp < NRP; ++rp)
@@ -1500,41 +1518,39 @@ __device__ __forceinline__ void na3d_strip_fast_body(const Na3dParams p, const N
         for (int db = 0; db < DB; ++db) {
           const bf16x4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4bf16(LDS_PTR(bf16x4, st + voffs[db] + 2 * rp * RB));
           const bf16x4 hi =
-              __builtin_amdgcn_ds_read_tr16_b64_v4bf16(LDS_PTR(bf16x4, st + voffs[db ^ 2] + (2 * rp + 1) * RB));
+              __builtin_amdgcn_ds_read_tr16_b64_v4bf16(LDS_PTR(bf16x4, st + voffs[db ^ (2 * FLIP)] + (2 * rp + 1) * RB));
           av[rp][db] = __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7);
         }
       stage_math(cst, act, ak, av);
       cur_off = cur_off + STAGE_B == RING_B ? 0 : cur_off + STAGE_B;
     }
     const int jf = gr - (NS - 1);
-    if (jf >= 0 && jf < NT && finish_tile((C + 1) & (NS - 1), jf)) {
+    if (jf >= 0 && jf < NT && finish_tile((C + 1) % NS, jf)) {
       if (jf < 64)
         bad_tiles |= 1ull << jf;
       else
         bad_high = true;
     }
   };
-  using I0 = std::integral_constant<int, 0>;
-  using I1 = std::integral_constant<int, 1>;
-  using I2 = std::integral_constant<int, 2>;
-  using I3 = std::integral_constant<int, 3>;
-  using ALL = std::integral_constant<int, 15>;
-  // Ramp-up: tile g starts in group g (slot g), so groups 0-2 compute only
-  // the slots already holding a tile.  From group 3 on every slot computes
-  // (the ramp-down's emptied slots too: separate instances for the ramp-down
-  // groups make the register allocator spill).
-  group(I0{}, std::integral_constant<int, 1>{}, 0);
-  group(I1{}, std::integral_constant<int, 3>{}, 1);
-  group(I2{}, std::integral_constant<int, 7>{}, 2);
-  for (int gr = 3;; gr += NS) {  // NG = NT + 3 >= 4
-    group(I3{}, ALL{}, gr);
-    if (gr + 1 >= NG) break;
-    group(I0{}, ALL{}, gr + 1);
-    if (gr + 2 >= NG) break;
-    group(I1{}, ALL{}, gr + 2);
-    if (gr + 3 >= NG) break;
-    group(I2{}, ALL{}, gr + 3);
-    if (gr + 4 >= NG) break;
+  using ALL = std::integral_constant<int, (1 << NS) - 1>;
+  // Ramp-up: tile g starts in group g (slot g), so groups 0 .. NS-2 compute
+  // only the slots already holding a tile.  From group NS-1 on every slot
+  // computes (the ramp-down's emptied slots too: separate instances for the
+  // ramp-down groups make the register allocator spill).
+  static_for<NS - 1>([&](auto ig) {
+    constexpr int G = decltype(ig)::value;
+    group(std::integral_constant<int, G>{}, std::integral_constant<int, (1 << (G + 1)) - 1>{}, G);
+  });
+  for (int gr = NS - 1;; gr += NS) {  // NG = NT + NS - 1 >= NS
+    bool done = false;
+    static_for<NS>([&](auto ii) {
+      constexpr int I = decltype(ii)::value;
+      if (!done) {
+        group(std::integral_constant<int, (NS - 1 + I) % NS>{}, ALL{}, gr + I);
+        done = gr + I + 1 >= NG;
+      }
+    });
+    if (done) break;
   }
   wait_vmcnt(0);  // the ring's trailing (empty) stages
 
@@ -1544,14 +1560,16 @@ __device__ __forceinline__ void na3d_strip_fast_body(const Na3dParams p, const N
     __builtin_amdgcn_s_waitcnt(0);
     for (int j = 0; j < NT; ++j)
       if (j < 64 ? ((bad_tiles >> j) & 1) : bad_high)
-        na3d_strip_tile_exact(&p, StripTile{b, h, gz, gy, gx, iz, ys + TY * j, ye, xw0, qx1});
+        na3d_strip_tile_exact<TX>(&p, StripTile{b, h, gz, gy, gx, iz, ys + TY * j, ye, xw0, qx1});
   }
 #endif
 }
 
-template <int D, int TX, int RPS, int NBUF>
-__global__ __launch_bounds__(256, 2) void na3d_strip_fast_kernel(Na3dParams p, Na3dStrips sg) {
-  na3d_strip_fast_body<D, TX, RPS, NBUF>(p, sg);
+// Two workgroups per CU (the 13-row window: 64 KiB of LDS each, ~230 VGPRs);
+// three for 5-row windows (48 KiB of LDS, 163 VGPRs; wider windows would spill).
+template <int D, int TX, int RPS, int NBUF, int KY>
+__global__ __launch_bounds__(256, TX == 8 && KY <= 5 ? 3 : 2) void na3d_strip_fast_kernel(Na3dParams p, Na3dStrips sg) {
+  na3d_strip_fast_body<D, TX, RPS, NBUF, KY>(p, sg);
 }
 
 
@@ -1635,7 +1653,7 @@ static int launch_mfma_tx(const Na3dParams& p, hipStream_t st) {
 // Strip kernel launch.  Work units are (batch, head, residue, z, column box)
 // strips over the whole y range; the y range is cut into chunks only when the
 // strips alone would not fill the GPU several times over.
-template <int D, int TX, int RPS, int NBUF, bool FAST>
+template <int D, int TX, int RPS, int NBUF, bool FAST, int KY = 13>
 static int launch_strip(const Na3dParams& p, hipStream_t st) {
   constexpr int TY = 16 / TX;
   Na3dStrips sg;
@@ -1652,19 +1670,25 @@ static int launch_strip(const Na3dParams& p, hipStream_t st) {
   const int64_t strips = (int64_t)sg.nxt * sg.nzt * sg.nres * p.H * p.B;
   if (strips == 0 || nty == 0) return STRATA_HIP_OK;
   int nch = 1;
-  while (strips * nch < 2048 && nch < nty) ++nch;
+  // Cut the y range into chunks only when the strips alone would leave the GPU
+  // short of work: 4-column tiles aim at 2048 workgroups; the 2 x 8 tiles of
+  // the small windows (one ramp of NS - 1 groups per chunk, short strips) at
+  // one round of two workgroups per CU.
+  const int target = TX == 8 ? 512 : 2048;
+  while (strips * nch < target && nch < nty) ++nch;
   sg.cty = (nty + nch - 1) / nch;
   sg.nch = (nty + sg.cty - 1) / sg.cty;
   const int64_t total = strips * sg.nch;
   if (total > 0x7fffffff) return fail(STRATA_HIP_EUNSUPPORTED, "na3d: problem too large for one launch");
   sg.total = (int)total;
-  if (FAST) {
-    hipLaunchKernelGGL((na3d_strip_fast_kernel<D, TX, RPS, NBUF>), dim3((unsigned)total), dim3(64 * NA3D_NWX), 0, st,
+  if constexpr (FAST) {
+    hipLaunchKernelGGL((na3d_strip_fast_kernel<D, TX, RPS, NBUF, KY>), dim3((unsigned)total), dim3(64 * NA3D_NWX), 0, st,
                        p, sg);
     return check_launch("na3d_strip_fast_kernel");
+  } else {
+    hipLaunchKernelGGL((na3d_strip_kernel<D, TX, RPS, NBUF>), dim3((unsigned)total), dim3(64 * NA3D_NWX), 0, st, p, sg);
+    return check_launch("na3d_strip_kernel");
   }
-  hipLaunchKernelGGL((na3d_strip_kernel<D, TX, RPS, NBUF>), dim3((unsigned)total), dim3(64 * NA3D_NWX), 0, st, p, sg);
-  return check_launch("na3d_strip_kernel");
 }
 
 // The strip kernel covers 4-column tiles (kx 10..13, ky <= 13) of head_dim 64
@@ -1694,6 +1718,49 @@ static bool strip_regular(const Na3dParams& p) {
     if (y0 - r < 0 || y1 - 1 + r > sub_len(p.L[1], g, dy) - 1) return false;
   }
   return true;
+}
+
+// Small windows on regular strips (na3d_strip_fast_kernel with 2 x 8 tiles and
+// two rows per stage): head_dim 64, kx <= 9 (an 8-column tile's x-union fits one
+// 16-key block), ky in {5, 7, 9}, kz >= 2, no y dilation, and no lse output.
+// Only query rows whose y window is not clamped form regular strips; the host
+// splits the query box in y and gives the clamped edge rows to the general kernel.
+static bool small_strip_fits(const Na3dParams& p) {
+  if (p.D != 64 || p.lse || p.ker[0] < 2 || p.ker[2] > 9 || p.dil[1] != 1) return false;
+  if (p.ker[1] != 5 && p.ker[1] != 7 && p.ker[1] != 9) return false;
+  if (p.L[1] >= 4096) return false;
+  const int64_t* sd[2] = {p.qs, p.ks};
+  for (int t = 0; t < 2; ++t)
+    if (((int64_t)(p.L[1] - 1) * sd[t][2] + (int64_t)(p.L[2] - 1) * sd[t][3] + p.D) * 2 >= 0x7fffffffLL) return false;
+  return true;
+}
+
+template <int D>
+static int launch_mfma_d(const Na3dParams& p, hipStream_t st);
+
+// The query box restricted to rows [y0, y1) of itself (output pointer shifted).
+static Na3dParams y_sub_box(const Na3dParams& p, int y0, int y1) {
+  Na3dParams s = p;
+  s.o = (char*)p.o + 2 * (int64_t)(y0 - p.org[1]) * p.os[2];
+  s.org[1] = y0;
+  s.ext[1] = y1 - y0;
+  return s;
+}
+
+static int launch_small_strips(const Na3dParams& p, hipStream_t st) {
+  const int kr = p.ker[1] / 2;
+  const int y0 = p.org[1], y1 = p.org[1] + p.ext[1];
+  const int r0 = y0 > kr ? y0 : kr, r1 = y1 < p.L[1] - kr ? y1 : p.L[1] - kr;
+  if (r1 - r0 < 2) return launch_mfma_d<64>(p, st);
+  int rc = STRATA_HIP_OK;
+  if (r0 > y0 && (rc = launch_mfma_d<64>(y_sub_box(p, y0, r0), st)) != STRATA_HIP_OK) return rc;
+  if (r1 < y1 && (rc = launch_mfma_d<64>(y_sub_box(p, r1, y1), st)) != STRATA_HIP_OK) return rc;
+  const Na3dParams mid = y_sub_box(p, r0, r1);
+  switch (p.ker[1]) {
+    case 5: return launch_strip<64, 8, 2, 2, true, 5>(mid, st);
+    case 7: return launch_strip<64, 8, 2, 2, true, 7>(mid, st);
+    default: return launch_strip<64, 8, 2, 2, true, 9>(mid, st);
+  }
 }
 
 template <int D>
@@ -1795,6 +1862,7 @@ extern "C" int strata_hip_na3d_fwd(const strata_hip_na3d_args* a, void* stream) 
         // the regular-strip kernel keeps no softmax reference: no lse output
         return strip_regular(p) && !p.lse ? launch_strip<64, 4, 4, 2, true>(p, st)
                                           : launch_strip<64, 4, 4, 2, false>(p, st);
+      if (small_strip_fits(p) && !std::getenv("STRATA_HIP_NA3D_NO_SMALL_STRIPS")) return launch_small_strips(p, st);
       return launch_mfma_d<64>(p, st);
     default:
       return launch_mfma_d<128>(p, st);

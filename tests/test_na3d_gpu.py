@@ -270,3 +270,63 @@ def test_regular_strip_large_scores_in_range(gpu):
     assert torch.isfinite(out.float()).all()
     assert rel_l2(out.float(), ref) <= BF16_TOL
     assert rel_l2(out[0, 1, 3, 4, 1].float().cpu(), ref[0, 1, 3, 4, 1]) <= BF16_TOL
+
+
+# Small windows on regular strips (2 x 8 tiles, two rows per stage, ky in {5, 7, 9},
+# kx <= 9): the rows with unclamped y windows take the strip kernel, the clamped
+# edge rows the general kernel, one output.  Cases: whole grids with every edge,
+# ragged x, a query box reaching into the clamped rows, dilation in z and x, an
+# anisotropic window, a grid with fewer regular rows than a tile pair, batches of heads.
+SMALL_CASES = [
+    # shape (B, Z, Y, X, H, D), kernel, dilation, origin, extent
+    ((1, 4, 20, 24, 2, 64), (3, 7, 7), (1, 1, 1), (0, 0, 0), None),
+    ((1, 5, 30, 33, 1, 64), (3, 5, 5), (1, 1, 1), (0, 0, 0), None),
+    ((2, 6, 27, 40, 2, 64), (3, 9, 9), (1, 1, 1), (1, 3, 5), (4, 20, 30)),
+    ((1, 6, 24, 24, 1, 64), (3, 7, 7), (2, 1, 2), (0, 0, 0), None),
+    ((1, 3, 16, 16, 2, 64), (3, 7, 9), (1, 1, 1), (0, 2, 0), (3, 12, 16)),
+    ((1, 4, 9, 16, 1, 64), (3, 7, 7), (1, 1, 1), (0, 0, 0), None),
+    ((1, 3, 40, 36, 3, 64), (3, 9, 7), (1, 1, 1), (0, 0, 0), None),
+]
+
+
+@pytest.mark.parametrize("case", SMALL_CASES, ids=[f"{c[0]}-k{c[1]}-d{c[2]}-box{c[3]}" for c in SMALL_CASES])
+def test_small_window_strips_vs_oracle(gpu, case):
+    shape, kernel, dil, origin, extent = case
+    print(f"small strip {shape} k{kernel} d{dil} o{origin} e{extent}", flush=True)
+    q, k, v = _rand(shape, 31, torch.bfloat16, gpu)
+    out = _run(q, k, v, kernel, dil, origin, extent)
+    ref = O.na3d(q.cpu(), k.cpu(), v.cpu(), kernel, dil, q_origin=origin, q_extent=extent)
+    assert torch.isfinite(out.float()).all()
+    assert rel_l2(out.float(), ref) <= BF16_TOL
+
+
+def test_small_window_strip_score_out_of_range(gpu):
+    """A 7x7 query whose best key scores ~160 (log2 units) and one whose keys all
+    score ~-160 leave the reference-free range of the small-window strip kernel:
+    their 2 x 8 tiles are recomputed exactly."""
+    shape = (1, 3, 20, 24, 1, 64)
+    q, k, v = (t.float() for t in _rand(shape, 12, torch.bfloat16, "cpu"))
+    u = torch.zeros(64)
+    u[:32] = 1.0 / 32**0.5
+    q[0, 1, 9, 10, 0] = 30.0 * u
+    k[0, 2, 11, 12, 0] = 30.0 * u
+    q[0, 1, 12, 5, 0] = -30.0 * u
+    k[0, :, 9:16, 2:9, 0] = 0.1 * k[0, :, 9:16, 2:9, 0] + 30.0 * u
+    q, k, v = (t.bfloat16() for t in (q, k, v))
+    out = _run(q.to(gpu), k.to(gpu), v.to(gpu), (3, 7, 7))
+    ref = O.na3d(q, k, v, (3, 7, 7))
+    assert torch.isfinite(out.float()).all()
+    assert rel_l2(out.float(), ref) <= BF16_TOL
+    for idx in ((0, 1, 9, 10, 0), (0, 1, 12, 5, 0)):
+        assert rel_l2(out[idx].float().cpu(), ref[idx]) <= BF16_TOL, idx
+
+
+def test_small_window_strips_match_general_kernel(gpu, monkeypatch):
+    """The same configs[3]-like launch through the strip path and, with it
+    switched off, through the general kernel: both within bf16 rounding."""
+    g = torch.Generator(device=gpu).manual_seed(5)
+    q, k, v = (torch.randn((1, 8, 64, 64, 4, 64), generator=g, device=gpu).bfloat16() for _ in range(3))
+    a = _run(q, k, v, (3, 7, 7))
+    monkeypatch.setenv("STRATA_HIP_NA3D_NO_SMALL_STRIPS", "1")
+    b = _run(q, k, v, (3, 7, 7))
+    assert rel_l2(a.float(), b.float()) <= 5e-3
