@@ -6,12 +6,15 @@ padded cube-face tiles (16,144,144), outputs for the interior (16,128,128),
 One step = one NA3D launch over the whole batch; inputs are resident in HBM.
 FLOPs = 4 * N_q(interior) * |W| * D per head.
 
-Also reported: the full Strata block tokens/s with a per-kernel
-breakdown and the RoPE+QKV-pack prologue's HBM GB/s, the configs[4] two-stage
-4-step rollout, the roofline of the dominant kernel, and the CPU oracle timed
-on a bounded sample on this host.
+Also reported: configs[1] (RoPE pack + NA3D (3,7,7)), the full Strata block
+(configs[3]) tokens/s with a per-kernel breakdown and the RoPE+QKV-pack
+prologue's HBM GB/s, the configs[4] two-stage 4-step rollout, the roofline of
+the dominant kernel (HBM-bound: its algorithmic bytes need longer at 8 TB/s than
+its FLOPs at the bf16 peak), and the CPU oracle on this host's cores for
+configs[0]-[4] (bounded; ``--cpu-full`` times configs[3] in full, median of 5).
 
-    python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-block] [--no-rollout] [--no-halo] [--no-backward] [--no-cpu]
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cfg1] [--no-block] [--no-rollout] [--no-halo]
+                    [--no-backward] [--no-cpu] [--cpu-full]
 """
 
 from __future__ import annotations
@@ -151,6 +154,74 @@ def bench_block(device, steps, warmup):
         "kernel_tflops": {k: round(v, 1) for k, v in tflops.items()},
         "prologue_GBps": rope_bytes / (t_rope * 1e-3) / 1e9,
         "prologue_pct_hbm": 100.0 * rope_bytes / (t_rope * 1e-3) / 1e9 / PEAK_HBM_GBPS,
+    }
+
+
+def cfg1_inputs(device):
+    """configs[1] inputs: q, k, v ~ N(0,1) [2,8,64,64,8,64] (seed 0, in that order), the
+    stereographic tables of 64x64 tiles with the level index in z (pairs x | y | level =
+    12 | 12 | 8, base 1e4), and the packed qkv [2,8,64,64,3*8*64] the pack kernel reads."""
+    import torch
+
+    from strata_amd import rope as P
+
+    B, Z, Y, X, H, D = 2, 8, 64, 64, 8, 64
+    g = torch.Generator().manual_seed(0)
+    q, k, v = (torch.randn(B, Z, Y, X, H, D, generator=g).bfloat16() for _ in range(3))
+    lat, lon = P.synthetic_tile_latlon(B, Y, X, g)
+    cos, sin = P.stereographic_rope_tables(lat, lon, D, 10000.0, P.default_rope_length_scale(1), levels=Z,
+                                           level_pairs=8)
+    qkv = torch.stack([q, k, v], dim=4).reshape(B, Z, Y, X, 3 * H * D)
+    return q, k, v, qkv, cos, sin, lat, lon
+
+
+def bench_cfg1(device, steps, warmup):
+    """stereographic RoPE (+ QKV pack) then NA3D (3,7,7) on [2,8,64,64,8,64] bf16."""
+    import torch
+
+    B, Z, Y, X, H, D = 2, 8, 64, 64, 8, 64
+    _, _, _, qkv, cos, sin, _, _ = cfg1_inputs(torch.device("cpu"))
+    qkv, cos, sin = qkv.to(device), cos.to(device), sin.to(device)
+    pack = torch.ops.strata_hip.rope_qkv_pack
+    na = torch.ops.strata_hip.na3d_fwd
+
+    def run_pack():
+        return pack(qkv, cos, sin, H, 0, False, 1e-6, None, None)
+
+    q, k, v = run_pack()
+
+    def run_na():
+        return na(q, k, v, [3, 7, 7], [1, 1, 1], None, [0, 0, 0], [Z, Y, X])
+
+    def timed(fn):
+        for _ in range(warmup):
+            fn()
+        torch.cuda.synchronize()
+        a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        a.record()
+        for _ in range(steps):
+            fn()
+        b.record()
+        torch.cuda.synchronize()
+        return a.elapsed_time(b) / steps
+
+    t_pack, t_na = timed(run_pack), timed(run_na)
+    M = B * Z * Y * X
+    flops = 4.0 * M * H * 147 * D
+    na_bytes = 4 * M * H * D * 2  # q, k, v read once, o written once
+    pack_bytes = M * 3 * H * D * 2 * 2 + cos.numel() * 4 * 2  # qkv read, q/k/v written, tables read
+    return {
+        "workload": "configs[1] stereographic RoPE (level index in z: pairs x|y|level = 12|12|8, base 1e4) + "
+        "QKV pack, then NA3D W=(3,7,7) on [2,8,64,64,8,64] bf16, q/k/v ~ N(0,1) seed 0",
+        "na3d_ms": round(t_na, 4),
+        "na3d_tflops": round(flops / (t_na * 1e-3) / 1e12, 1),
+        "na3d_pct_bf16_peak": round(100.0 * flops / (t_na * 1e-3) / 1e12 / PEAK_BF16_TFLOPS, 2),
+        "na3d_algorithmic_GBps": round(na_bytes / (t_na * 1e-3) / 1e9, 1),
+        "na3d_pct_hbm": round(100.0 * na_bytes / (t_na * 1e-3) / 1e9 / PEAK_HBM_GBPS, 1),
+        "rope_pack_ms": round(t_pack, 4),
+        "rope_pack_GBps": round(pack_bytes / (t_pack * 1e-3) / 1e9, 1),
+        "rope_pack_pct_hbm": round(100.0 * pack_bytes / (t_pack * 1e-3) / 1e9 / PEAK_HBM_GBPS, 1),
+        "total_ms": round(t_pack + t_na, 4),
     }
 
 
@@ -320,35 +391,138 @@ def bench_backward(device, reps, warmup):
     return res
 
 
-def cpu_baseline():
-    """The CPU oracle on a bounded sample of configs[2]: tile 0, head 0, 4 z-slices."""
+def _cpu_affinity() -> int:
+    try:
+        return len(os.sched_getaffinity(0))
+    except (AttributeError, OSError):
+        return os.cpu_count() or 1
+
+
+def _cpu_threads() -> int:
+    """Host threads for the CPU baseline: the process's share of the host, i.e. its
+    CPU affinity mask, capped by OMP_NUM_THREADS where the host sets one (the GPU
+    boxes set 16 per GPU)."""
+    n = _cpu_affinity()
+    env = os.environ.get("OMP_NUM_THREADS", "")
+    return min(n, int(env)) if env.isdigit() and int(env) > 0 else n
+
+
+def _cpu_model() -> str:
+    try:
+        for line in Path("/proc/cpuinfo").read_text().splitlines():
+            if line.startswith("model name"):
+                return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
+
+
+def _median_time(fn, reps: int, warmup: int = 1) -> tuple[float, list[float]]:
+    for _ in range(warmup):
+        fn()
+    times = []
+    for _ in range(reps):
+        t0 = time.perf_counter()
+        fn()
+        times.append(time.perf_counter() - t0)
+    return statistics.median(times), times
+
+
+def _cpu_block_case(B, grid, C, H, kernel, ls_patch=1):
+    """Inputs of one oracle block run: x ~ N(0,1) seed 0, Xavier seed 1 weights, tables."""
     import torch
 
-    from oracle import na3d as O
+    from oracle import rope as R
+    from strata_amd import rope as P
+    from strata_amd.modules import StrataBlock, init_xavier_
 
-    threads = min(16, os.cpu_count() or 1)
+    blk = StrataBlock(C, H, kernel)
+    init_xavier_(blk, torch.Generator().manual_seed(1))
+    params = {k: v.detach().float() for k, v in blk.state_dict().items()}
+    g = torch.Generator().manual_seed(0)
+    x = torch.randn(B, *grid, C, generator=g)
+    lat, lon = P.synthetic_tile_latlon(B, grid[1], grid[2], g)
+    c, s = R.tables(lat, lon, C // H, 10000.0, R.default_rope_length_scale(ls_patch))
+    return x, params, c.float(), s.float()
+
+
+def cpu_baselines(full: bool):
+    """The torch-CPU oracle (fp32) on this host, all its threads, beside the GPU figures.
+
+    Headline (``cpu_baseline``): a bounded sample of configs[2] (tile 0, head 0,
+    z 0-3 of the interior: 4.25 GFLOP), warm-up + median of 5.  ``cpu_configs``:
+    configs[0] and configs[1] in full (median of 5 / of 3), configs[3] on batch entry
+    0 (x4, labelled extrapolated; in full with ``full``), configs[2] from the
+    sample (x FLOP ratio) and configs[4] from one block per stage at batch 1
+    (x tokens x blocks x tiles x steps), both labelled extrapolated."""
+    import torch
+
+    from oracle import block as OB
+    from oracle import na3d as O
+    from oracle import rope as R
+
+    threads = _cpu_threads()
     torch.set_num_threads(threads)
+    reps = 5 if full else 3
+    out = {}
+    # configs[2] sample (the headline cpu_baseline)
     g = torch.Generator().manual_seed(0)
     shape = (1, 16, 144, 144, 1, 64)
     q, k, v = (torch.randn(shape, generator=g) for _ in range(3))
     box_o, box_e = (0, 8, 8), (4, 128, 128)
-    nq = box_e[0] * box_e[1] * box_e[2]
-    flops = O.na3d_flops(1, 1, 64, nq, (3, 13, 13))
-    O.na3d(q, k, v, (3, 13, 13), q_origin=box_o, q_extent=(1, 16, 128))  # warm-up
-    times = []
-    for _ in range(3):
-        t0 = time.perf_counter()
-        O.na3d(q, k, v, (3, 13, 13), q_origin=box_o, q_extent=box_e)
-        times.append(time.perf_counter() - t0)
-    t = statistics.median(times)
-    return {
-        "value": flops / t / 1e12,
+    f_sample = O.na3d_flops(1, 1, 64, box_e[0] * box_e[1] * box_e[2], (3, 13, 13))
+    t2, _ = _median_time(lambda: O.na3d(q, k, v, (3, 13, 13), q_origin=box_o, q_extent=box_e), 5)
+    f2 = 4.0 * 6 * 16 * (16 * 128 * 128) * 507 * 64
+    headline = {
+        "value": f_sample / t2 / 1e12,
         "unit": "TFLOP/s",
         "cores": threads,
         "kind": "port",
-        "sample": "configs[2] NA3D, tile 0, head 0, query box z 0-3 x interior 128x128 (4.25 GFLOP), "
-        f"fp32 torch-CPU oracle, median of 3 = {t:.2f} s",
+        "sample": "configs[2] NA3D, tile 0, head 0, query box z 0-3 x interior 128x128 (4.25 GFLOP), fp32 "
+        f"torch-CPU oracle, warm-up + median of 5 = {t2:.2f} s, {threads} threads",
+        "host": {"os_cpu_count": os.cpu_count(), "affinity_cpus": _cpu_affinity(),
+                 "omp_num_threads": os.environ.get("OMP_NUM_THREADS"),
+                 "torch_threads": torch.get_num_threads(), "cpu_model": _cpu_model()},
     }
+    out["configs[2]"] = {"seconds": round(t2 * f2 / f_sample, 1), "extrapolated": True,
+                         "from": "the sample above x FLOP ratio (x768)"}
+    # configs[0]: fp32 NA3D [1,4,16,16,4,32], W=(3,5,5), vs nothing (plumbing)
+    g = torch.Generator().manual_seed(0)
+    s0 = (1, 4, 16, 16, 4, 32)
+    q0, k0, v0 = (torch.randn(s0, generator=g) for _ in range(3))
+    t0, _ = _median_time(lambda: O.na3d(q0, k0, v0, (3, 5, 5)), 5)
+    out["configs[0]"] = {"seconds": round(t0, 5), "gflops": round(O.na3d_flops(1, 4, 32, 4 * 16 * 16, (3, 5, 5)) / t0 / 1e9, 2)}
+    # configs[1]: RoPE (level tables) + NA3D in full
+    q1, k1, v1, _, c1, s1, _, _ = cfg1_inputs(torch.device("cpu"))
+    q1, k1, v1, c1, s1 = q1.float(), k1.float(), v1.float(), c1.float(), s1.float()
+
+    def run1():
+        return O.na3d(R.apply_rope(q1, c1, s1), R.apply_rope(k1, c1, s1), v1, (3, 7, 7))
+
+    t1, _ = _median_time(run1, 5 if full else 3, 1 if full else 0)
+    out["configs[1]"] = {"seconds": round(t1, 3), "gflops": round(4.0 * 2 * 8 * 64 * 64 * 8 * 147 * 64 / t1 / 1e9, 2)}
+    # configs[3]: the block
+    B3 = 4 if full else 1
+    x, prm, c, s = _cpu_block_case(4, (8, 64, 64), 1024, 16, (3, 7, 7))
+    x, c, s = x[:B3], c[:B3], s[:B3]
+    t3, _ = _median_time(lambda: OB.block_forward(x, prm, 16, (3, 7, 7), c, s), reps if full else 1, 1 if full else 0)
+    out["configs[3]"] = {"seconds": round(t3 * 4 / B3, 2), "extrapolated": not full,
+                         "tokens_per_s": round(4 * 8 * 64 * 64 / (t3 * 4 / B3), 1),
+                         "from": "in full" if full else "batch entry 0 (one run) x4"}
+    # configs[4]: one block per stage at batch 1 (stage 1 on a quarter of its z range
+    # unless full), scaled by tokens x 12 blocks x 6 tiles x 4 steps
+    za = 16 if full else 4
+    xa, pa, ca, sa = _cpu_block_case(1, (za, 64, 64), 768, 12, (3, 7, 7))
+    xb, pb, cb, sb = _cpu_block_case(1, (8, 32, 32), 1024, 16, (3, 9, 9), ls_patch=2)
+    ta, _ = _median_time(lambda: OB.block_forward(xa, pa, 12, (3, 7, 7), ca, sa), 1, 0)
+    tb, _ = _median_time(lambda: OB.block_forward(xb, pb, 16, (3, 9, 9), cb, sb), 1, 0)
+    ta *= 16 / za
+    t4 = (ta * 12 + tb * 12) * 6 * 4
+    out["configs[4]"] = {"seconds": round(t4, 1), "extrapolated": True,
+                         "from": f"one stage-1 block ({ta:.2f} s, run on z 0-{za - 1} and scaled) and one stage-2 "
+                                 f"block ({tb:.2f} s) at batch 1, x12 blocks x6 tiles x4 steps (embed/merge/head "
+                                 "not included)"}
+    return headline, out
 
 
 def load_traffic():
@@ -372,6 +546,9 @@ def main():
     ap.add_argument("--no-rollout", action="store_true")
     ap.add_argument("--no-halo", action="store_true")
     ap.add_argument("--no-backward", action="store_true")
+    ap.add_argument("--no-cfg1", action="store_true")
+    ap.add_argument("--cpu-full", action="store_true",
+                    help="CPU baseline in full: configs[3] over its whole batch, warm-up + median of 5 everywhere")
     ap.add_argument(
         "--copy-calibration",
         action="store_true",
@@ -437,17 +614,23 @@ def main():
         },
         "pct_bf16_peak": round(100.0 * tflops / PEAK_BF16_TFLOPS, 2),
         "wall_ms_per_step": round(wall_ms, 4),
+        # Binding roofline: the algorithmic bytes (14.60 GB) take 1.825 ms at 8 TB/s, the
+        # algorithmic FLOPs (3.266 TF) 1.298 ms at 2516.6 TFLOP/s, so HBM bounds the kernel.
         "roofline": {
-            "bound": "mfma",
-            "achieved": round(tflops, 2),
-            "peak": PEAK_BF16_TFLOPS,
-            "unit": "TFLOP/s",
-            "frac": round(tflops / PEAK_BF16_TFLOPS, 4),
+            "bound": "hbm",
+            "achieved": round(alg_bytes / (ms * 1e-3) / 1e9, 1),
+            "peak": PEAK_HBM_GBPS,
+            "unit": "GB/s",
+            "frac": round(alg_bytes / (ms * 1e-3) / 1e9 / PEAK_HBM_GBPS, 4),
             "traffic": load_traffic(),
             "algorithmic_bytes": alg_bytes,
-            "algorithmic_GBps": round(alg_bytes / (ms * 1e-3) / 1e9, 1),
+            "mfma": {"achieved": round(tflops, 2), "peak": PEAK_BF16_TFLOPS, "unit": "TFLOP/s",
+                     "frac": round(tflops / PEAK_BF16_TFLOPS, 4)},
         },
     }
+    if not args.no_cfg1:
+        log("bench: timing configs[1] (RoPE pack + NA3D)")
+        result["cfg1"] = bench_cfg1(dev, args.steps, args.warmup)
     if not args.no_block:
         log("bench: timing the configs[3] block")
         result["block"] = bench_block(dev, max(3, args.steps // 2), 2)
@@ -463,8 +646,8 @@ def main():
         log("bench: timing the backward kernels")
         result["backward"] = bench_backward(dev, 5, 1)
     if not args.no_cpu:
-        log("bench: timing the CPU oracle sample")
-        result["cpu_baseline"] = cpu_baseline()
+        log("bench: timing the CPU oracle (configs[0]-[4], bounded)" + (" in full" if args.cpu_full else ""))
+        result["cpu_baseline"], result["cpu_configs"] = cpu_baselines(args.cpu_full)
     print(json.dumps(result), flush=True)
 
 

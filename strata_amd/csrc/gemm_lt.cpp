@@ -23,12 +23,15 @@
 // which the heuristic offers no algorithm is declined and runs on the
 // hand-written kernels.
 #include <hip/hip_runtime.h>
+#include <hipblaslt/hipblaslt-ext.hpp>
 #include <hipblaslt/hipblaslt.h>
 
+#include <cstdio>
 #include <cstdlib>
 #include <cstring>
 #include <map>
 #include <mutex>
+#include <string>
 #include <tuple>
 
 #include "gemm.h"
@@ -72,13 +75,32 @@ bool build_plan(hipblasLtHandle_t h, const GemmParams& p, bool has_bias, bool ha
   if (hipblasLtMatmulPreferenceCreate(&pref) != HIPBLAS_STATUS_SUCCESS) return false;
   uint64_t ws = 0;
   hipblasLtMatmulPreferenceSetAttribute(pref, HIPBLASLT_MATMUL_PREF_MAX_WORKSPACE_BYTES, &ws, sizeof(ws));
-  hipblasLtMatmulHeuristicResult_t res[1];
+  constexpr int NREQ = 32;
+  hipblasLtMatmulHeuristicResult_t res[NREQ];
   int nres = 0;
   const hipblasStatus_t st =
-      hipblasLtMatmulAlgoGetHeuristic(h, pl.desc, pl.la, pl.lb, pl.lc, pl.ld, pref, 1, res, &nres);
+      hipblasLtMatmulAlgoGetHeuristic(h, pl.desc, pl.la, pl.lb, pl.lc, pl.ld, pref, NREQ, res, &nres);
   hipblasLtMatmulPreferenceDestroy(pref);
   if (st != HIPBLAS_STATUS_SUCCESS || nres < 1) return false;
-  pl.algo = res[0].algo;
+  // The heuristic's first choice is often a stream-K kernel ("_SK<n>_" with
+  // n > 0 in its name): work units are split across workgroups and their
+  // partial sums combined in a schedule that varies from run to run, so the
+  // result's last bits do too.  Take the best-ranked data-parallel kernel
+  // instead (results then repeat bit for bit); stream-K only if there is none.
+  int pick = 0;
+  for (int i = 0; i < nres; ++i) {
+    const std::string name = hipblaslt_ext::getKernelNameFromAlgo(h, res[i].algo);
+    const size_t sk = name.find("_SK");
+    if (sk == std::string::npos || sk + 3 >= name.size() || name[sk + 3] == '0') {
+      pick = i;
+      break;
+    }
+  }
+  pl.algo = res[pick].algo;
+  if (std::getenv("STRATA_HIP_GEMM_LT_VERBOSE"))
+    std::fprintf(stderr, "strata_hip gemm_lt M=%lld N=%lld K=%lld: candidate %d of %d: %s\n", (long long)p.M,
+                 (long long)p.N, (long long)p.K, pick, nres,
+                 hipblaslt_ext::getKernelNameFromAlgo(h, res[pick].algo).c_str());
   return true;
 }
 
