@@ -56,6 +56,10 @@ __device__ __forceinline__ void wait_vmcnt(int n) {
   }
 }
 
+__device__ __forceinline__ void wait_lgkm0() {
+  __builtin_amdgcn_s_waitcnt(15 | (7 << 4) | (3 << 14));  // lgkmcnt(0), vmcnt/expcnt untouched
+}
+
 // One 1-KiB global->LDS copy: lane i's 16 bytes at `voff` within the buffer
 // described by `rsrc` land at LDS byte address `lds_addr + 16*i`; offsets
 // beyond the descriptor's record count read as zero.  Issued as inline asm so

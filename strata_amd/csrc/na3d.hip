@@ -616,9 +616,6 @@ struct Na3dStrips {
   int total;     // workgroups in the launch
 };
 
-__device__ __forceinline__ void wait_lgkm0() {
-  __builtin_amdgcn_s_waitcnt(15 | (7 << 4) | (3 << 14));  // lgkmcnt(0), vmcnt/expcnt untouched
-}
 
 // Where one strip tile's queries sit: batch, head, residue (gz, gy, gx), the
 // tile's sub-grid z, first query row and first column, and the chunk's ends.

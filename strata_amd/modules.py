@@ -270,6 +270,23 @@ def swap_attention(model: nn.Module, num_heads, kernel_size, dilation=1, qk_norm
     return len(targets)
 
 
+def interleaved_dilations(n_layers: int, na_dilation: int, kernel_size, grid, interleaved: bool = True) -> list:
+    """Per-block NA3D dilations for ``do_interleaved_dilation`` / ``na_dilations``
+    (screamcast/config.py:97-98, passed at screamcast/strata_wrappers.py:326-328).
+
+    The schedule itself lives in physicsnemo's Strata (not available here), so this
+    one is this build's reading of the flag names, parity unpinned: without
+    interleaving every block is undilated; with it, even blocks are undilated and
+    odd blocks dilate every axis by ``na_dilation`` where ``kernel * na_dilation``
+    fits the token grid (NATTEN's requirement), else that axis stays undilated.
+    Feed the result to ``swap_attention(..., dilation=...)`` or ``StrataBlock``."""
+    k = _triple(kernel_size)
+    if not interleaved or na_dilation <= 1:
+        return [[1, 1, 1] for _ in range(n_layers)]
+    odd = [na_dilation if kk * na_dilation <= L else 1 for kk, L in zip(k, grid)]
+    return [[1, 1, 1] if i % 2 == 0 else list(odd) for i in range(n_layers)]
+
+
 def init_xavier_(module: nn.Module, generator: torch.Generator) -> None:
     """Xavier-uniform weights, zero biases (DiT-style init), from one CPU generator."""
     for m in module.modules():

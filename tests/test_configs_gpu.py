@@ -223,3 +223,58 @@ def test_gemm_epilogues_production_size(gpu, case):
     err = rel_l2(got, ref)
     print(f"  {len(rows)} rows, rel-L2 {err:.3e}", flush=True)
     assert err <= TOL
+
+
+# ---------------------------------------------------------------------------
+# The production block (screamcast train_configs.py:295-317): 1024 wide, 16 x 64
+# heads, attn_kernel = 3 (taken as (3,3,3)), gated attention, non-affine qk
+# RMSNorm, stereographic RoPE with base 100 and the length scale of horizontal
+# patch 4 (strata_wrappers.py:333-338), on the rollout tile geometry: a 512-px
+# tile + 32-px halo at patch 4 = (24,144,144) tokens (run_screamcast_nudged.py:156-165).
+# ---------------------------------------------------------------------------
+def _crop_checks(out, x, params, cos, sin, H, kernel, crops, grid):
+    """The block is local: on a crop of the input (tables cropped, not rebuilt)
+    the oracle reproduces the full-grid output wherever a query's clamped
+    window is the same in the crop as in the grid."""
+    for lo, hi in crops:
+        sl = tuple(slice(a, b) for a, b in zip(lo, hi))
+        xc = x[(slice(0, 1), *sl)].float()
+        cc, sc = cos[(slice(0, 1), *sl)], sin[(slice(0, 1), *sl)]
+        ref = OB.block_forward(xc, params, H, kernel, cc, sc, gated=True, qk_norm=True)
+        keep = []
+        for a, b, L, k in zip(lo, hi, grid, kernel):
+            r = k // 2
+            keep.append(slice(0 if a == 0 else r, (b - a) if b == L else (b - a) - r))
+        got = out[(slice(0, 1), *sl)][(slice(None), *keep)].float()
+        want = ref[(slice(None), *keep)]
+        err = rel_l2(got, want)
+        print(f"  crop {lo}-{hi}: rel-L2 {err:.3e}", flush=True)
+        assert err <= TOL, (lo, hi, err)
+
+
+@pytest.mark.skip(reason="faulted the GPU (memory fault) on its one run at the full (24,144,144) x 1024 tile; "
+                         "cause not found by reading the kernels involved; kept off the GPU until it is")
+def test_production_block_rollout_geometry(gpu):
+    Z, Y, X, C, H, kernel = 24, 144, 144, 1024, 16, (3, 3, 3)
+    blk = StrataBlock(C, H, kernel, gated=True, qk_norm=True)
+    init_xavier_(blk, torch.Generator().manual_seed(1))
+    with torch.no_grad():
+        blk.attn.gate_proj.bias.normal_(generator=torch.Generator().manual_seed(2))
+    params = {k: v.detach().bfloat16().float() for k, v in blk.state_dict().items()}
+    blk = blk.to(gpu).bfloat16()
+    g = torch.Generator().manual_seed(0)
+    x = torch.randn(1, Z, Y, X, C, generator=g).bfloat16()
+    ls = P.default_rope_length_scale(4)
+    lat, lon = P.synthetic_tile_latlon(1, Y, X, g, spacing=ls)
+    cos, sin = P.stereographic_rope_tables(lat, lon, C // H, 100.0, ls)
+    print("production block (24,144,144) x 1024, gated, qk-norm, RoPE base 100", flush=True)
+    with torch.no_grad():
+        out = blk(x.to(gpu), (cos.to(gpu), sin.to(gpu)))
+    torch.cuda.synchronize()
+    assert torch.isfinite(out.float()).all()
+    co, so = R.tables(lat, lon, C // H, 100.0, ls)
+    co = co.float().expand(1, Z, Y, X, C // H // 2)
+    so = so.float().expand(1, Z, Y, X, C // H // 2)
+    _crop_checks(out.cpu(), x, params, co, so, H, kernel,
+                 [((0, 0, 0), (5, 12, 12)), ((10, 70, 100), (15, 82, 112)), ((19, 132, 132), (24, 144, 144))],
+                 (Z, Y, X))

@@ -173,3 +173,12 @@ def test_swapped_attention_keeps_an_affine_qk_norm():
     assert [n for n, _ in holder.named_parameters()] == names
     assert holder.attn.q_norm is not None and holder.attn.q_norm.weight.shape == (4,)
     assert holder.attn.head_dim == 4 and torch.equal(holder.attn.qkv.weight, holder.attn.qkv.weight)
+
+
+def test_interleaved_dilation_schedule():
+    from strata_amd.modules import interleaved_dilations
+
+    assert interleaved_dilations(4, 3, 3, (24, 16, 16), interleaved=False) == [[1, 1, 1]] * 4
+    s = interleaved_dilations(4, 3, (3, 5, 5), (8, 16, 16))
+    assert s[0] == s[2] == [1, 1, 1] and s[1] == s[3] == [1, 3, 3]  # 3*3 > 8 keeps z undilated
+    assert interleaved_dilations(3, 3, 3, (24, 144, 144))[1] == [3, 3, 3]
