@@ -75,6 +75,16 @@ __device__ __forceinline__ void dma_row16(u32x4 rsrc, uint32_t lds_addr, uint32_
       : "memory", "m0");
 }
 
+// One dword per lane into LDS at lds_addr + 4 * lane (as dma_row16).
+__device__ __forceinline__ void dma_dword(u32x4 rsrc, uint32_t lds_addr, uint32_t voff) {
+  asm volatile(
+      "s_mov_b32 m0, %0\n\t"
+      "s_nop 0\n\t"
+      "buffer_load_dword %1, %2, 0 offen lds" ::"s"(lds_addr),
+      "v"(voff), "s"(rsrc)
+      : "memory", "m0");
+}
+
 __device__ __forceinline__ u32x4 make_rsrc(const void* base, uint32_t num_records) {
   const uint64_t a = (uint64_t)base;
   // dword1 holds base[47:32] with stride 0; dword3 = gfx9 data/num format for raw buffers.

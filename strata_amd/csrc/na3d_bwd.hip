@@ -8,10 +8,12 @@
 //   dQ_i  = scale * sum_{j in W(i)} dS_ij k_j
 //   dK_j  = scale * sum_{i : j in W(i)} dS_ij q_i,   dV_j = sum_{i : j in W(i)} p_ij dO_i
 //
-// Three kernels, each a wave per 4 x 4 tile of tokens.  bf16 with head_dim 64
-// and dilation 1 (the training shapes) runs MFMA versions (below); the general
-// VALU versions (4 lanes per token, D/4 head dims per lane, dot products closed
-// by two xor shuffles) take everything else:
+// Three kernels, each a wave per 4 x 4 tile of tokens, four waves side by side
+// along x per workgroup.  bf16 with head_dim 64, dilation 1 and kx <= 13 (the
+// training shapes) runs MFMA versions (below: dq and dk/dv stage the
+// workgroup's shared K/V or Q/dO rows in LDS); the general VALU versions (4
+// lanes per token, D/4 head dims per lane, dot products closed by two xor
+// shuffles) take everything else:
 //   prep: per query, log2-sum-exp of its scores (recomputed, unless the caller
 //         passes the forward's, strata_hip_na3d_fwd's lse output: then only
 //         D_i) and D_i, into a caller-provided fp32 workspace;
@@ -20,9 +22,8 @@
 //         axis is an interval (window starts are non-decreasing in i):
 //         lo = 0 if j <= k - 1 else j - k + 1 + k/2,  hi = Lg - 1 if j >= Lg - k else j + k/2
 //         (sub-grid coordinates of the dilation residue class).
-// Scores run in log2 units (q pre-scaled by scale * log2 e), fp32 throughout;
-// the neighbouring tokens of a tile share most of their window, so their
-// K/V (or Q/dO) reads hit in L1/L2.
+// Scores run in log2 units (q, or in dk/dv k, pre-scaled by scale * log2 e),
+// fp32 throughout.
 #include <cstdlib>
 #include <mutex>
 
@@ -267,137 +268,12 @@ __global__ __launch_bounds__(256) void na3d_bwd_dkv_kernel(Na3dBwdParams p) {
 }
 
 // ---------------------------------------------------------------------------
-// MFMA dq for bf16, head_dim 64, dilation 1 (the training shapes): a wave per
-// 4 x 4 query tile walks its window union a (z, row pair) at a time.  Per row
-// pair (32 keys of one 16-key x block): S^T = K Q^T and dP^T = V dO^T on
-// v_mfma_f32_16x16x32_bf16 (keys on M, queries on N, both straight from
-// global memory), dS^T = P^T (dP^T - D) in registers, and dQ^T += K^T dS^T
-// with K^T read back transposed (ds_read_b64_tr_b16) from the two K rows the
-// wave has just written to its own 4 KiB of LDS.  Masks: a per-lane bias of
-// 0 / -inf per key for the x window and per row for the y window (the z
-// window is the wave's for every query).
-// ---------------------------------------------------------------------------
-__global__ __launch_bounds__(256) void na3d_bwd_dq_mfma_kernel(Na3dBwdParams p) {
-#if defined(__HIP_DEVICE_COMPILE__)
-  constexpr int D = 64, KS = 2, DB = 4, RBW = 16 * D * 2;  // bytes of one 16-key row in LDS
-  __shared__ __attribute__((aligned(16))) char lds[4 * 2 * RBW];
-  const int tid = (int)threadIdx.x;
-  const int wave = tid >> 6, lane = tid & 63, n16 = lane & 15, g = lane >> 4;
-  const Tok t = token_at(p, n16);  // MFMA column n16 = the lane's query
-  char* wl = lds + wave * 2 * RBW;
-  const float c2 = p.scale * 1.4426950408889634f;
-  const int kz = p.ker[0], ky = p.ker[1], kx = p.ker[2];
-
-  // this lane's query: n16 = (row, column) of the wave's 4 x 4 tile (as token_of)
-  const int64_t qi = tok_index(p, t.b, t.z, t.y, t.x, t.h);
-  bf16x8 qreg[KS], doreg[KS];
-#pragma unroll
-  for (int ks = 0; ks < KS; ++ks) {
-    qreg[ks] = *(const bf16x8*)((const bf16*)p.q + qi * D + 8 * (4 * ks + g));
-    doreg[ks] = *(const bf16x8*)((const bf16*)p.dout + qi * D + 8 * (4 * ks + g));
-#pragma unroll
-    for (int e = 0; e < 8; ++e) qreg[ks][e] = (bf16)((float)qreg[ks][e] * c2);
-  }
-  const float lse = p.lse[qi], dsum = p.dsum[qi];
-
-  // the wave's key block: 16 keys from the window start of its first column
-  const int xw0 = min(((int)blockIdx.x % p.nxt) * 16 + wave * 4, p.X - 1);
-  const int X0 = win_start(xw0, p.X, kx);
-  const int sx = win_start(t.x, p.X, kx);
-  f32x4 xb, ninf = {-INFINITY, -INFINITY, -INFINITY, -INFINITY};
-#pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    const int key = X0 + 4 * g + i;
-    xb[i] = (key >= sx && key < sx + kx) ? 0.f : -INFINITY;
-  }
-  const int kxl = min(X0 + n16, p.X - 1);  // key column this lane loads (clamped)
-  // rows: the union of the tile rows' windows
-  const int ty0 = ((int)(blockIdx.x / p.nxt) % p.nyt) * 4;
-  const int Yu0 = win_start(min(ty0, p.Y - 1), p.Y, ky);
-  const int NR = win_start(min(ty0 + 3, p.Y - 1), p.Y, ky) + ky - Yu0;
-  const int sy = win_start(t.y, p.Y, ky);
-  const int sz = win_start(t.z, p.Z, kz);
-  // V^T-style transposed read offsets within a row (as the forward's PV operand)
-  uint32_t toff[DB];
-  {
-    const int keyv = 4 * g + (n16 >> 2), dq = n16 & 3;
-#pragma unroll
-    for (int db = 0; db < DB; ++db)
-      toff[db] = (uint32_t)((keyv * D + 8 * ((2 * db + (dq >> 1)) ^ (keyv & 7)) + 4 * (dq & 1)) * 2);
-  }
-  f32x4 acc[DB];
-#pragma unroll
-  for (int db = 0; db < DB; ++db) acc[db] = (f32x4){0.f, 0.f, 0.f, 0.f};
-
-  for (int a0 = 0; a0 < kz; ++a0) {
-    const int zk = sz + a0;
-    for (int r0 = 0; r0 < NR; r0 += 2) {
-      bf16x8 ak[2][KS], avn[2][KS];
-#pragma unroll
-      for (int rr = 0; rr < 2; ++rr) {
-        const int yk = min(Yu0 + r0 + rr, p.Y - 1);
-        const int64_t kj = tok_index(p, t.b, zk, yk, kxl, t.h);
-#pragma unroll
-        for (int ks = 0; ks < KS; ++ks) {
-          ak[rr][ks] = *(const bf16x8*)((const bf16*)p.k + kj * D + 8 * (4 * ks + g));
-          avn[rr][ks] = *(const bf16x8*)((const bf16*)p.v + kj * D + 8 * (4 * ks + g));
-        }
-      }
-      // K rows into this wave's LDS (swizzled 16-byte chunks) for the transposed read
-#pragma unroll
-      for (int rr = 0; rr < 2; ++rr)
-#pragma unroll
-        for (int ks = 0; ks < KS; ++ks)
-          *(bf16x8*)(wl + rr * RBW + n16 * D * 2 + 16 * ((4 * ks + g) ^ (n16 & 7))) = ak[rr][ks];
-      f32x4 sc[2], dp[2];
-#pragma unroll
-      for (int rr = 0; rr < 2; ++rr) {
-        const int yk = Yu0 + r0 + rr;
-        const bool rowin = r0 + rr < NR && yk >= sy && yk < sy + ky;
-        sc[rr] = rowin ? xb : ninf;
-        dp[rr] = (f32x4){0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-        for (int ks = 0; ks < KS; ++ks) {
-          sc[rr] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ak[rr][ks], qreg[ks], sc[rr], 0, 0, 0);
-          dp[rr] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(avn[rr][ks], doreg[ks], dp[rr], 0, 0, 0);
-        }
-      }
-      float ds[8];
-#pragma unroll
-      for (int rr = 0; rr < 2; ++rr)
-#pragma unroll
-        for (int i = 0; i < 4; ++i) ds[4 * rr + i] = exp2f(sc[rr][i] - lse) * (dp[rr][i] - dsum);
-      const u32x4 pw = {pack_bf16x2(ds[0], ds[1]), pack_bf16x2(ds[2], ds[3]), pack_bf16x2(ds[4], ds[5]),
-                        pack_bf16x2(ds[6], ds[7])};
-      const bf16x8 pb = __builtin_bit_cast(bf16x8, pw);
-      wait_lds();  // this wave's K rows are in LDS
-#pragma unroll
-      for (int db = 0; db < DB; ++db) {
-        const bf16x4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4bf16(LDS_PTR(bf16x4, wl + toff[db]));
-        const bf16x4 hi = __builtin_amdgcn_ds_read_tr16_b64_v4bf16(LDS_PTR(bf16x4, wl + RBW + toff[db]));
-        acc[db] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7), pb,
-                                                          acc[db], 0, 0, 0);
-      }
-      wait_lds();  // the transposed reads are done before the next pair overwrites the rows
-    }
-  }
-  if (t.valid) {
-    char* op = (char*)p.dq + 2 * (qi * D) + 8 * g;
-#pragma unroll
-    for (int db = 0; db < DB; ++db) {
-      const u32x2 w = {pack_bf16x2(acc[db][0] * p.scale, acc[db][1] * p.scale),
-                       pack_bf16x2(acc[db][2] * p.scale, acc[db][3] * p.scale)};
-      *(u32x2*)(op + 32 * db) = w;
-    }
-  }
-#endif
-}
-
-// ---------------------------------------------------------------------------
-// MFMA prep for bf16, head_dim 64, dilation 1: the dq kernel's walk with the
-// score MFMA only.  Each lane keeps a running maximum and sum over the 8 keys
-// of its query it sees per row pair; the four lanes of a query (g = 0..3)
-// merge them at the end.  D_i = dO_i . O_i on the same lanes.
+// MFMA prep for bf16, head_dim 64, dilation 1 (a backward without the
+// forward's lse): a wave per 4 x 4 query tile walks its window union a key row
+// at a time with the score MFMA only (S^T = K Q^T, keys on M straight from
+// global memory).  Each lane keeps a running maximum and sum over the 4 keys
+// of its query it sees per row; the four lanes of a query (g = 0..3) merge
+// them at the end.  D_i = dO_i . O_i on the same lanes.
 // ---------------------------------------------------------------------------
 __global__ __launch_bounds__(256) void na3d_bwd_prep_mfma_kernel(Na3dBwdParams p) {
 #if defined(__HIP_DEVICE_COMPILE__)
@@ -473,27 +349,41 @@ __global__ __launch_bounds__(256) void na3d_bwd_prep_mfma_kernel(Na3dBwdParams p
 }
 
 // ---------------------------------------------------------------------------
-// MFMA dk / dv for bf16, head_dim 64, dilation 1: a wave per 4 x 4 key tile
-// walks the union of its keys' inverse windows in blocks of 16 queries (one
-// (z, y) row, 16 consecutive x), two blocks at a time.  Per block: S = Q K^T
-// and dP = dO V^T (queries on M straight from global memory, the tile's K / V
-// held in registers as the N operand), P = 2^(S - lse), dS = P (dP - D); per
-// pair: dV^T += dO^T P and dK^T += Q^T dS (K = the pair's 32 queries) with
-// dO^T and Q^T read back transposed from the wave's own 8 KiB of LDS.  The
-// membership mask (key j in the window of query i, per axis) is the C operand
-// of the S MFMA.  Q is staged pre-scaled by scale * log2 e, so dK carries a
-// factor ln 2 at the end.
+// LDS-staged dk / dv for bf16, head_dim 64, dilation 1, kx <= 13.  The
+// workgroup's four 4 x 4 key tiles (16 key columns of one (b, h, z), 4 rows)
+// share their queries: the union of the tiles' inverse windows is walked two
+// query (z, y) rows at a time, each row's Q and dO over the workgroup's
+// inverse-window columns (at most 16 + kx - 1 <= 28, staged as 32) copied into
+// LDS once per workgroup by `buffer_load ... lds` (a ring of three stages),
+// with the rows' log2-sum-exp and D_i beside them.  A wave takes its keys'
+// 16-query block(s) of each staged row: S = Q K^T and dP = dO V^T with the
+// tile's K (pre-scaled by scale * log2 e) and V as the register operand, the
+// membership mask (key j in W(i) per axis, exact at clamped edges) as the C
+// operand of S, P = 2^(S - lse), dS = P (dP - D); then dV^T += dO^T P and
+// dK^T += Q^T dS over the row pair, with dO^T and Q^T read transposed
+// (ds_read_b64_tr_b16).  A wave's keys near a grid edge can need up to 22
+// queries along x: a second 16-query block then starts at most 16 columns
+// before the stage's end and skips the columns the first one covered.
 // ---------------------------------------------------------------------------
-__global__ __launch_bounds__(256, 2) void na3d_bwd_dkv_mfma_kernel(Na3dBwdParams p) {
+namespace dkvl {
+constexpr int SW = 32;                     // staged query columns per row
+constexpr int RB = SW * 64 * 2;            // bytes of one staged row of Q (or dO)
+constexpr int NBUF = 3;                    // ring stages
+constexpr int STAGE = 4 * RB + 4 * SW * 4;  // Q r0, Q r1, dO r0, dO r1, lse r0, r1, D r0, r1
+}  // namespace dkvl
+
+__global__ __launch_bounds__(256, 3) void na3d_bwd_dkv_lds_kernel(Na3dBwdParams p) {
 #if defined(__HIP_DEVICE_COMPILE__)
-  constexpr int D = 64, KS = 2, DB = 4, RBW = 16 * D * 2;
-  __shared__ __attribute__((aligned(16))) char lds[4 * 4 * RBW];  // per wave: Q rows 0, 1; dO rows 0, 1
+  using namespace dkvl;
+  constexpr int D = 64, KS = 2, DB = 4;
+  __shared__ __attribute__((aligned(1024))) char lds[NBUF * STAGE];
   const int tid = (int)threadIdx.x;
-  const int wave = tid >> 6, lane = tid & 63, n16 = lane & 15, g = lane >> 4;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int lane = tid & 63, n16 = lane & 15, g = lane >> 4;
   const Tok t = token_at(p, n16);  // MFMA column n16 = the lane's key
-  char* wl = lds + wave * 4 * RBW;
   const float c2 = p.scale * 1.4426950408889634f;
   const int kz = p.ker[0], ky = p.ker[1], kx = p.ker[2];
+  const uint32_t lds_base = (uint32_t)(uintptr_t)(__attribute__((address_space(3))) char*)lds;
 
   const int64_t kj = tok_index(p, t.b, t.z, t.y, t.x, t.h);
   bf16x8 kreg[KS], vreg[KS];
@@ -501,109 +391,337 @@ __global__ __launch_bounds__(256, 2) void na3d_bwd_dkv_mfma_kernel(Na3dBwdParams
   for (int ks = 0; ks < KS; ++ks) {
     kreg[ks] = *(const bf16x8*)((const bf16*)p.k + kj * D + 8 * (4 * ks + g));
     vreg[ks] = *(const bf16x8*)((const bf16*)p.v + kj * D + 8 * (4 * ks + g));
+#pragma unroll
+    for (int e = 0; e < 8; ++e) kreg[ks][e] = (bf16)((float)kreg[ks][e] * c2);
   }
-  // the tile's keys: columns [kx0, kx1], rows [ky0, ky1] (clamped to the grid)
-  const int kx0 = min(((int)blockIdx.x % p.nxt) * 16 + wave * 4, p.X - 1), kx1 = min(kx0 + 3, p.X - 1);
-  const int ky0 = min(((int)(blockIdx.x / p.nxt) % p.nyt) * 4, p.Y - 1), ky1 = min(ky0 + 3, p.Y - 1);
+
+  // ---- x: the workgroup's query columns [SX0, SX0 + SW) and this wave's blocks ----
+  const int KX0 = ((int)blockIdx.x % p.nxt) * 16;
   int f, n;
+  axis_inv(min(KX0, p.X - 1), p.X, kx, 1, f, n);
+  const int SX0 = f;
+  const int kx0 = min(KX0 + wave * 4, p.X - 1), kx1 = min(kx0 + 3, p.X - 1);
   axis_inv(kx0, p.X, kx, 1, f, n);
-  const int QX0 = f;
+  const int wlo = f;
   axis_inv(kx1, p.X, kx, 1, f, n);
-  const int NXB = (f + n - QX0 + 15) / 16;  // 16-query blocks along x
+  const int whi = f + n;                 // one past the wave's last query column
+  const int bs0 = wlo - SX0;             // <= 12
+  const int nxb = whi - wlo > 16 ? 2 : 1;
+  const int bs1 = min(bs0 + 16, SW - 16);
+  int bs[2] = {bs0, bs1};
+  // x membership of the lane's key in the windows of the block's columns 4g..4g+3
+  uint32_t xm[2];
+#pragma unroll
+  for (int xb = 0; xb < 2; ++xb) {
+    xm[xb] = 0;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      const int cl = bs[xb] + 4 * g + e;  // column within the stage
+      const int qx = SX0 + cl;
+      const int sx = win_start(min(qx, p.X - 1), p.X, kx);
+      const bool in = qx < p.X && (xb == 0 || cl >= bs0 + 16) && t.x >= sx && t.x < sx + kx;
+      xm[xb] |= in ? (1u << e) : 0u;
+    }
+  }
+  // LDS offsets: Q / dO A-operand rows (column bs + n16) and transposed reads
+  uint32_t aoff[2][KS], toff[2][DB];
+#pragma unroll
+  for (int xb = 0; xb < 2; ++xb) {
+    const int col = bs[xb] + n16;
+#pragma unroll
+    for (int ks = 0; ks < KS; ++ks) aoff[xb][ks] = (uint32_t)((col * D + 8 * ((4 * ks + g) ^ (col & 7))) * 2);
+    const int colv = bs[xb] + 4 * g + (n16 >> 2), dq = n16 & 3;
+#pragma unroll
+    for (int db = 0; db < DB; ++db)
+      toff[xb][db] = (uint32_t)((colv * D + 8 * ((2 * db + (dq >> 1)) ^ (colv & 7)) + 4 * (dq & 1)) * 2);
+  }
+
+  // ---- y, z: the query rows of the workgroup's keys ----
+  const int ky0 = min(((int)(blockIdx.x / p.nxt) % p.nyt) * 4, p.Y - 1), ky1 = min(ky0 + 3, p.Y - 1);
   axis_inv(ky0, p.Y, ky, 1, f, n);
   const int QY0 = f;
   axis_inv(ky1, p.Y, ky, 1, f, n);
   const int NY = f + n - QY0;
   int QZ0, NZ;
   axis_inv(t.z, p.Z, kz, 1, QZ0, NZ);
-  const int nb = NZ * NY * NXB;
+  const int nrows = NZ * NY;
+  const int nst = (nrows + 1) / 2;
 
-  uint32_t toff[DB];  // transposed-read offsets within a 16-row block (as the forward's V^T)
+  // ---- copies: wave w stages query columns 8w .. 8w+7 of both rows of Q and dO;
+  // waves 0 / 1 also the rows' lse / D (one dword per lane) ----
+  const int64_t rowb = (int64_t)p.H * D * 2;  // bytes between neighbouring x tokens
+  const uint32_t rec = (uint32_t)((int64_t)(p.X - 1) * rowb + D * 2);
+  uint32_t voff;
   {
-    const int keyv = 4 * g + (n16 >> 2), dq = n16 & 3;
-#pragma unroll
-    for (int db = 0; db < DB; ++db)
-      toff[db] = (uint32_t)((keyv * D + 8 * ((2 * db + (dq >> 1)) ^ (keyv & 7)) + 4 * (dq & 1)) * 2);
+    const int cl = 8 * wave + (lane >> 3);
+    const int qx = SX0 + cl;
+    const int chunk = (lane & 7) ^ (cl & 7);
+    voff = qx < p.X ? (uint32_t)(qx * rowb + 16 * chunk) : OOB;
   }
+  const int scol = lane & 31;  // lse / D copies: lane -> (row lane >> 5, column lane & 31)
+  const bool scol_in = SX0 + scol < p.X;
+  const char* qbase = (const char*)p.q + 2 * (int64_t)t.h * D;
+  const char* obase = (const char*)p.dout + 2 * (int64_t)t.h * D;
+  const float* sbase = wave == 0 ? p.lse : p.dsum;
+  auto row_tok = [&](int sr) {  // token index of (row sr, x = 0, head 0)
+    const int zq = QZ0 + sr / NY, yq = QY0 + sr % NY;
+    return (((int64_t)t.b * p.Z + zq) * p.Y + yq) * p.X * p.H;
+  };
+  const int nload = wave < 2 ? 5 : 4;
+  auto issue = [&](int s) {
+    const uint32_t st = lds_base + (uint32_t)((s % NBUF) * STAGE);
+    const int r0 = 2 * s, r1 = 2 * s + 1;
+    const bool l0 = r0 < nrows, l1 = r1 < nrows;
+    const int64_t t0 = l0 ? row_tok(r0) : 0, t1 = l1 ? row_tok(r1) : 0;
+    dma_row16(make_rsrc(qbase + t0 * D * 2, l0 ? rec : 0u), st + 0 * RB + wave * 1024, voff);
+    dma_row16(make_rsrc(qbase + t1 * D * 2, l1 ? rec : 0u), st + 1 * RB + wave * 1024, voff);
+    dma_row16(make_rsrc(obase + t0 * D * 2, l0 ? rec : 0u), st + 2 * RB + wave * 1024, voff);
+    dma_row16(make_rsrc(obase + t1 * D * 2, l1 ? rec : 0u), st + 3 * RB + wave * 1024, voff);
+    if (wave < 2) {
+      // row 1 sits (t1 - t0) tokens after row 0 in the [B, Z, Y, X, H] statistics
+      const int64_t dt = l1 ? t1 - t0 : 0;
+      const uint32_t so = (lane < 32 ? (l0 && scol_in) : (l1 && scol_in))
+                              ? (uint32_t)(((lane < 32 ? 0 : dt) + (int64_t)(SX0 + scol) * p.H + t.h) * 4)
+                              : OOB;
+      const uint32_t srec = l0 ? (uint32_t)((dt + (int64_t)p.X * p.H) * 4) : 0u;
+      dma_dword(make_rsrc(sbase + t0, srec), st + 4 * RB + wave * 2 * SW * 4, so);
+    }
+  };
+
   f32x4 dk[DB], dv[DB];
 #pragma unroll
   for (int db = 0; db < DB; ++db) dk[db] = dv[db] = (f32x4){0.f, 0.f, 0.f, 0.f};
+  const f32x4 ninf = {-INFINITY, -INFINITY, -INFINITY, -INFINITY};
 
-  for (int bi = 0; bi < nb; bi += 2) {
-    float pv[2][4], sv[2][4];
 #pragma unroll
-    for (int hb = 0; hb < 2; ++hb) {
-      const int bj = bi + hb;
-      const bool live = bj < nb;
-      const int bjc = live ? bj : bi;
-      const int xb = bjc % NXB, r = bjc / NXB;
-      const int qy = QY0 + r % NY, qz = QZ0 + r / NY;
-      const int qx = QX0 + 16 * xb + n16;  // the query this lane loads (A operand row n16)
-      const int64_t qi = tok_index(p, t.b, qz, qy, min(qx, p.X - 1), t.h);
-      bf16x8 qa[KS], da[KS];
+  for (int s = 0; s < NBUF - 1; ++s) issue(s);
+  for (int s = 0; s < nst; ++s) {
+    if (wave < 2)
+      wait_vmcnt((NBUF - 2) * 5);
+    else
+      wait_vmcnt((NBUF - 2) * 4);
+    lds_barrier();
+    issue(s + NBUF - 1);
+    const char* st = lds + (s % NBUF) * STAGE;
+    const float* sl = (const float*)(st + 4 * RB);  // lse r0, lse r1, D r0, D r1
+    // y / z membership of the lane's key for the two rows
+    bool yz[2];
 #pragma unroll
-      for (int ks = 0; ks < KS; ++ks) {
-        qa[ks] = *(const bf16x8*)((const bf16*)p.q + qi * D + 8 * (4 * ks + g));
-        da[ks] = *(const bf16x8*)((const bf16*)p.dout + qi * D + 8 * (4 * ks + g));
+    for (int r = 0; r < 2; ++r) {
+      const int sr = 2 * s + r;
+      const int zq = QZ0 + sr / NY, yq = QY0 + sr % NY;
+      const int wy = win_start(min(yq, p.Y - 1), p.Y, ky), wz = win_start(min(zq, p.Z - 1), p.Z, kz);
+      yz[r] = sr < nrows && t.y >= wy && t.y < wy + ky && t.z >= wz && t.z < wz + kz;
+    }
 #pragma unroll
-        for (int e = 0; e < 8; ++e) qa[ks][e] = (bf16)((float)qa[ks][e] * c2);
-        *(bf16x8*)(wl + hb * RBW + n16 * D * 2 + 16 * ((4 * ks + g) ^ (n16 & 7))) = qa[ks];
-        *(bf16x8*)(wl + (2 + hb) * RBW + n16 * D * 2 + 16 * ((4 * ks + g) ^ (n16 & 7))) = da[ks];
+    for (int xb = 0; xb < 2; ++xb) {
+      if (xb >= nxb) break;  // wave-uniform
+      float pv[2][4], sv[2][4];
+#pragma unroll
+      for (int r = 0; r < 2; ++r) {
+        f32x4 sc, dp = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int e = 0; e < 4; ++e) sc[e] = (yz[r] && ((xm[xb] >> e) & 1)) ? 0.f : -INFINITY;
+#pragma unroll
+        for (int ks = 0; ks < KS; ++ks) {
+          const bf16x8 qa = *(const bf16x8*)(st + r * RB + aoff[xb][ks]);
+          const bf16x8 da = *(const bf16x8*)(st + (2 + r) * RB + aoff[xb][ks]);
+          sc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(qa, kreg[ks], sc, 0, 0, 0);
+          dp = __builtin_amdgcn_mfma_f32_16x16x32_bf16(da, vreg[ks], dp, 0, 0, 0);
+        }
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          const int cl = bs[xb] + 4 * g + e;
+          const float lse = sl[r * SW + cl], dsm = sl[(2 + r) * SW + cl];
+          pv[r][e] = __builtin_amdgcn_exp2f(sc[e] - lse);
+          sv[r][e] = pv[r][e] * (dp[e] - dsm);
+        }
       }
-      // mask: query rows 4g..4g+3 of the block against this lane's key
-      const bool yz = live && t.y >= win_start(qy, p.Y, ky) && t.y < win_start(qy, p.Y, ky) + ky &&
-                      t.z >= win_start(qz, p.Z, kz) && t.z < win_start(qz, p.Z, kz) + kz;
-      f32x4 sc, dp = {0.f, 0.f, 0.f, 0.f};
-      float lse[4], dsm[4];
+      const bf16x8 pbp = __builtin_bit_cast(
+          bf16x8, ((u32x4){pack_bf16x2(pv[0][0], pv[0][1]), pack_bf16x2(pv[0][2], pv[0][3]),
+                           pack_bf16x2(pv[1][0], pv[1][1]), pack_bf16x2(pv[1][2], pv[1][3])}));
+      const bf16x8 pbs = __builtin_bit_cast(
+          bf16x8, ((u32x4){pack_bf16x2(sv[0][0], sv[0][1]), pack_bf16x2(sv[0][2], sv[0][3]),
+                           pack_bf16x2(sv[1][0], sv[1][1]), pack_bf16x2(sv[1][2], sv[1][3])}));
 #pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const int qxi = QX0 + 16 * xb + 4 * g + i;
-        const int sx = win_start(min(qxi, p.X - 1), p.X, kx);
-        sc[i] = (yz && qxi < p.X && t.x >= sx && t.x < sx + kx) ? 0.f : -INFINITY;
-        const int64_t qr = tok_index(p, t.b, qz, qy, min(qxi, p.X - 1), t.h);
-        lse[i] = p.lse[qr];
-        dsm[i] = p.dsum[qr];
-      }
-#pragma unroll
-      for (int ks = 0; ks < KS; ++ks) {
-        sc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(qa[ks], kreg[ks], sc, 0, 0, 0);
-        dp = __builtin_amdgcn_mfma_f32_16x16x32_bf16(da[ks], vreg[ks], dp, 0, 0, 0);
-      }
-#pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        pv[hb][i] = exp2f(sc[i] - lse[i]);
-        sv[hb][i] = pv[hb][i] * (dp[i] - dsm[i]);
+      for (int db = 0; db < DB; ++db) {
+        const bf16x4 q0 = __builtin_amdgcn_ds_read_tr16_b64_v4bf16(LDS_PTR(bf16x4, st + toff[xb][db]));
+        const bf16x4 q1 = __builtin_amdgcn_ds_read_tr16_b64_v4bf16(LDS_PTR(bf16x4, st + RB + toff[xb][db]));
+        const bf16x4 o0 = __builtin_amdgcn_ds_read_tr16_b64_v4bf16(LDS_PTR(bf16x4, st + 2 * RB + toff[xb][db]));
+        const bf16x4 o1 = __builtin_amdgcn_ds_read_tr16_b64_v4bf16(LDS_PTR(bf16x4, st + 3 * RB + toff[xb][db]));
+        dk[db] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_shufflevector(q0, q1, 0, 1, 2, 3, 4, 5, 6, 7), pbs,
+                                                         dk[db], 0, 0, 0);
+        dv[db] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_shufflevector(o0, o1, 0, 1, 2, 3, 4, 5, 6, 7), pbp,
+                                                         dv[db], 0, 0, 0);
       }
     }
-    const bf16x8 pbp = __builtin_bit_cast(
-        bf16x8, ((u32x4){pack_bf16x2(pv[0][0], pv[0][1]), pack_bf16x2(pv[0][2], pv[0][3]),
-                         pack_bf16x2(pv[1][0], pv[1][1]), pack_bf16x2(pv[1][2], pv[1][3])}));
-    const bf16x8 pbs = __builtin_bit_cast(
-        bf16x8, ((u32x4){pack_bf16x2(sv[0][0], sv[0][1]), pack_bf16x2(sv[0][2], sv[0][3]),
-                         pack_bf16x2(sv[1][0], sv[1][1]), pack_bf16x2(sv[1][2], sv[1][3])}));
-    wait_lds();  // this wave's Q / dO rows are in LDS
-#pragma unroll
-    for (int db = 0; db < DB; ++db) {
-      const bf16x4 q0 = __builtin_amdgcn_ds_read_tr16_b64_v4bf16(LDS_PTR(bf16x4, wl + toff[db]));
-      const bf16x4 q1 = __builtin_amdgcn_ds_read_tr16_b64_v4bf16(LDS_PTR(bf16x4, wl + RBW + toff[db]));
-      const bf16x4 o0 = __builtin_amdgcn_ds_read_tr16_b64_v4bf16(LDS_PTR(bf16x4, wl + 2 * RBW + toff[db]));
-      const bf16x4 o1 = __builtin_amdgcn_ds_read_tr16_b64_v4bf16(LDS_PTR(bf16x4, wl + 3 * RBW + toff[db]));
-      dk[db] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_shufflevector(q0, q1, 0, 1, 2, 3, 4, 5, 6, 7), pbs,
-                                                       dk[db], 0, 0, 0);
-      dv[db] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_shufflevector(o0, o1, 0, 1, 2, 3, 4, 5, 6, 7), pbp,
-                                                       dv[db], 0, 0, 0);
-    }
-    wait_lds();  // the transposed reads are done before the next pair overwrites the rows
   }
+  wait_vmcnt(0);  // the ring's trailing (empty) stages
   if (t.valid) {
-    constexpr float LN2 = 0.6931471805599453f;  // Q was staged as scale * log2(e) * q
     char* kp = (char*)p.dk + 2 * (kj * D) + 8 * g;
     char* vp = (char*)p.dv + 2 * (kj * D) + 8 * g;
 #pragma unroll
     for (int db = 0; db < DB; ++db) {
-      *(u32x2*)(kp + 32 * db) = (u32x2){pack_bf16x2(dk[db][0] * LN2, dk[db][1] * LN2),
-                                        pack_bf16x2(dk[db][2] * LN2, dk[db][3] * LN2)};
+      *(u32x2*)(kp + 32 * db) = (u32x2){pack_bf16x2(dk[db][0] * p.scale, dk[db][1] * p.scale),
+                                        pack_bf16x2(dk[db][2] * p.scale, dk[db][3] * p.scale)};
       *(u32x2*)(vp + 32 * db) = (u32x2){pack_bf16x2(dv[db][0], dv[db][1]), pack_bf16x2(dv[db][2], dv[db][3])};
+    }
+  }
+#endif
+}
+
+// ---------------------------------------------------------------------------
+// LDS-staged dq for bf16, head_dim 64, dilation 1, kx <= 13: the forward's
+// walk for the workgroup's four 4 x 4 query tiles (16 query columns of one
+// (b, h, z), 4 rows).  The union of their windows is walked two key (z, y)
+// rows at a time, each row's K and V over the workgroup's window columns (at
+// most 16 + kx - 1 <= 28, staged as 32) copied into LDS once per workgroup
+// (`buffer_load ... lds`, a ring of three stages).  A wave takes its tile's
+// 16-key block of each row (4 + kx - 1 <= 16 keys): S^T = K Q^T and dP^T =
+// V dO^T with Q (pre-scaled by scale * log2 e) and dO as the register operand,
+// the membership mask as the C operand of S^T, P^T = 2^(S^T - lse),
+// dS^T = P^T (dP^T - D); then dQ^T += K^T dS^T over the row pair with K^T
+// read transposed (ds_read_b64_tr_b16).
+// ---------------------------------------------------------------------------
+namespace dql {
+constexpr int SW = 32;          // staged key columns per row
+constexpr int RB = SW * 64 * 2;  // bytes of one staged row of K (or V)
+constexpr int NBUF = 3;
+constexpr int STAGE = 4 * RB;    // K r0, K r1, V r0, V r1
+}  // namespace dql
+
+__global__ __launch_bounds__(256, 3) void na3d_bwd_dq_lds_kernel(Na3dBwdParams p) {
+#if defined(__HIP_DEVICE_COMPILE__)
+  using namespace dql;
+  constexpr int D = 64, KS = 2, DB = 4;
+  __shared__ __attribute__((aligned(1024))) char lds[NBUF * STAGE];
+  const int tid = (int)threadIdx.x;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int lane = tid & 63, n16 = lane & 15, g = lane >> 4;
+  const Tok t = token_at(p, n16);  // MFMA column n16 = the lane's query
+  const float c2 = p.scale * 1.4426950408889634f;
+  const int kz = p.ker[0], ky = p.ker[1], kx = p.ker[2];
+  const uint32_t lds_base = (uint32_t)(uintptr_t)(__attribute__((address_space(3))) char*)lds;
+
+  const int64_t qi = tok_index(p, t.b, t.z, t.y, t.x, t.h);
+  bf16x8 qreg[KS], doreg[KS];
+#pragma unroll
+  for (int ks = 0; ks < KS; ++ks) {
+    qreg[ks] = *(const bf16x8*)((const bf16*)p.q + qi * D + 8 * (4 * ks + g));
+    doreg[ks] = *(const bf16x8*)((const bf16*)p.dout + qi * D + 8 * (4 * ks + g));
+#pragma unroll
+    for (int e = 0; e < 8; ++e) qreg[ks][e] = (bf16)((float)qreg[ks][e] * c2);
+  }
+  const float lse = p.lse[qi], dsum = p.dsum[qi];
+
+  // ---- x: the workgroup's key columns [SX0, SX0 + SW) and this wave's block ----
+  const int QX0 = ((int)blockIdx.x % p.nxt) * 16;
+  const int SX0 = win_start(min(QX0, p.X - 1), p.X, kx);
+  const int qx0 = min(QX0 + wave * 4, p.X - 1);
+  const int bs = win_start(qx0, p.X, kx) - SX0;  // <= 12
+  const int sx = win_start(t.x, p.X, kx);
+  uint32_t xm = 0;  // bit e: key column bs + 4g + e is in the lane's query window
+#pragma unroll
+  for (int e = 0; e < 4; ++e) {
+    const int kc = SX0 + bs + 4 * g + e;
+    xm |= (kc >= sx && kc < sx + kx) ? (1u << e) : 0u;
+  }
+  uint32_t aoff[KS], toff[DB];
+  {
+    const int col = bs + n16;
+#pragma unroll
+    for (int ks = 0; ks < KS; ++ks) aoff[ks] = (uint32_t)((col * D + 8 * ((4 * ks + g) ^ (col & 7))) * 2);
+    const int colv = bs + 4 * g + (n16 >> 2), dq = n16 & 3;
+#pragma unroll
+    for (int db = 0; db < DB; ++db)
+      toff[db] = (uint32_t)((colv * D + 8 * ((2 * db + (dq >> 1)) ^ (colv & 7)) + 4 * (dq & 1)) * 2);
+  }
+
+  // ---- y, z: the key rows of the workgroup's queries ----
+  const int ty0 = ((int)(blockIdx.x / p.nxt) % p.nyt) * 4;
+  const int KY0 = win_start(min(ty0, p.Y - 1), p.Y, ky);
+  const int NY = win_start(min(ty0 + 3, p.Y - 1), p.Y, ky) + ky - KY0;
+  const int KZ0 = win_start(t.z, p.Z, kz);
+  const int nrows = kz * NY;
+  const int nst = (nrows + 1) / 2;
+  const int sy = win_start(t.y, p.Y, ky);
+
+  // ---- copies: wave w stages key columns 8w .. 8w+7 of both rows of K and V ----
+  const int64_t rowb = (int64_t)p.H * D * 2;
+  const uint32_t rec = (uint32_t)((int64_t)(p.X - 1) * rowb + D * 2);
+  uint32_t voff;
+  {
+    const int cl = 8 * wave + (lane >> 3);
+    const int kc = SX0 + cl;
+    const int chunk = (lane & 7) ^ (cl & 7);
+    voff = kc < p.X ? (uint32_t)(kc * rowb + 16 * chunk) : OOB;
+  }
+  const char* kbase = (const char*)p.k + 2 * (int64_t)t.h * D;
+  const char* vbase = (const char*)p.v + 2 * (int64_t)t.h * D;
+  auto row_tok = [&](int sr) {
+    const int zk = KZ0 + sr / NY, yk = KY0 + sr % NY;
+    return (((int64_t)t.b * p.Z + zk) * p.Y + yk) * p.X * p.H;
+  };
+  auto issue = [&](int s) {
+    const uint32_t st = lds_base + (uint32_t)((s % NBUF) * STAGE);
+    const int r0 = 2 * s, r1 = 2 * s + 1;
+    const bool l0 = r0 < nrows, l1 = r1 < nrows;
+    const int64_t t0 = l0 ? row_tok(r0) : 0, t1 = l1 ? row_tok(r1) : 0;
+    dma_row16(make_rsrc(kbase + t0 * D * 2, l0 ? rec : 0u), st + 0 * RB + wave * 1024, voff);
+    dma_row16(make_rsrc(kbase + t1 * D * 2, l1 ? rec : 0u), st + 1 * RB + wave * 1024, voff);
+    dma_row16(make_rsrc(vbase + t0 * D * 2, l0 ? rec : 0u), st + 2 * RB + wave * 1024, voff);
+    dma_row16(make_rsrc(vbase + t1 * D * 2, l1 ? rec : 0u), st + 3 * RB + wave * 1024, voff);
+  };
+
+  f32x4 acc[DB];
+#pragma unroll
+  for (int db = 0; db < DB; ++db) acc[db] = (f32x4){0.f, 0.f, 0.f, 0.f};
+
+#pragma unroll
+  for (int s = 0; s < NBUF - 1; ++s) issue(s);
+  for (int s = 0; s < nst; ++s) {
+    wait_vmcnt((NBUF - 2) * 4);
+    lds_barrier();
+    issue(s + NBUF - 1);
+    const char* st = lds + (s % NBUF) * STAGE;
+    float ds[2][4];
+#pragma unroll
+    for (int r = 0; r < 2; ++r) {
+      const int sr = 2 * s + r;
+      const int yk = KY0 + sr % NY;
+      const bool yin = sr < nrows && yk >= sy && yk < sy + ky;  // z: every staged plane is in the window
+      f32x4 sc, dp = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int e = 0; e < 4; ++e) sc[e] = (yin && ((xm >> e) & 1)) ? 0.f : -INFINITY;
+#pragma unroll
+      for (int ks = 0; ks < KS; ++ks) {
+        const bf16x8 ka = *(const bf16x8*)(st + r * RB + aoff[ks]);
+        const bf16x8 va = *(const bf16x8*)(st + (2 + r) * RB + aoff[ks]);
+        sc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ka, qreg[ks], sc, 0, 0, 0);
+        dp = __builtin_amdgcn_mfma_f32_16x16x32_bf16(va, doreg[ks], dp, 0, 0, 0);
+      }
+#pragma unroll
+      for (int e = 0; e < 4; ++e) ds[r][e] = __builtin_amdgcn_exp2f(sc[e] - lse) * (dp[e] - dsum);
+    }
+    const bf16x8 pb = __builtin_bit_cast(
+        bf16x8, ((u32x4){pack_bf16x2(ds[0][0], ds[0][1]), pack_bf16x2(ds[0][2], ds[0][3]),
+                         pack_bf16x2(ds[1][0], ds[1][1]), pack_bf16x2(ds[1][2], ds[1][3])}));
+#pragma unroll
+    for (int db = 0; db < DB; ++db) {
+      const bf16x4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4bf16(LDS_PTR(bf16x4, st + toff[db]));
+      const bf16x4 hi = __builtin_amdgcn_ds_read_tr16_b64_v4bf16(LDS_PTR(bf16x4, st + RB + toff[db]));
+      acc[db] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7), pb,
+                                                        acc[db], 0, 0, 0);
+    }
+  }
+  wait_vmcnt(0);  // the ring's trailing (empty) stages
+  if (t.valid) {
+    char* op = (char*)p.dq + 2 * (qi * D) + 8 * g;
+#pragma unroll
+    for (int db = 0; db < DB; ++db) {
+      const u32x2 w = {pack_bf16x2(acc[db][0] * p.scale, acc[db][1] * p.scale),
+                       pack_bf16x2(acc[db][2] * p.scale, acc[db][3] * p.scale)};
+      *(u32x2*)(op + 32 * db) = w;
     }
   }
 #endif
@@ -631,8 +749,12 @@ __global__ __launch_bounds__(256) void na3d_bwd_dsum_kernel(Na3dBwdParams p, int
 }
 
 // The MFMA kernels: dilation 1, kx <= 13 (a 4-column tile's x union fits one 16-key block).
+// The LDS kernels' copies address one (b, z, y) row of a tensor with 32-bit
+// offsets (X * H * D bf16), the statistics two rows apart (one z-slice).
 static bool mfma_ok(const Na3dBwdParams& p) {
-  return p.dil[0] == 1 && p.dil[1] == 1 && p.dil[2] == 1 && p.ker[2] <= 13 && !std::getenv("STRATA_HIP_NA3D_BWD_VALU");
+  const int64_t row = (int64_t)p.X * p.H;
+  return p.dil[0] == 1 && p.dil[1] == 1 && p.dil[2] == 1 && p.ker[2] <= 13 && row * 64 * 2 < (int64_t)OOB &&
+         ((int64_t)p.Y + 1) * row * 4 < (int64_t)OOB && !std::getenv("STRATA_HIP_NA3D_BWD_VALU");
 }
 
 template <typename T, int D>
@@ -652,11 +774,11 @@ static int launch_bwd(const Na3dBwdParams& p, hipStream_t st) {
     hipLaunchKernelGGL((na3d_bwd_prep_kernel<T, D>), grid, block, 0, st, p);
   }
   if (sizeof(T) == 2 && D == 64 && mfma_ok(p))
-    hipLaunchKernelGGL(na3d_bwd_dq_mfma_kernel, grid, block, 0, st, p);
+    hipLaunchKernelGGL(na3d_bwd_dq_lds_kernel, grid, block, 0, st, p);
   else
     hipLaunchKernelGGL((na3d_bwd_dq_kernel<T, D>), grid, block, 0, st, p);
   if (sizeof(T) == 2 && D == 64 && mfma_ok(p))
-    hipLaunchKernelGGL(na3d_bwd_dkv_mfma_kernel, grid, block, 0, st, p);
+    hipLaunchKernelGGL(na3d_bwd_dkv_lds_kernel, grid, block, 0, st, p);
   else
     hipLaunchKernelGGL((na3d_bwd_dkv_kernel<T, D>), grid, block, 0, st, p);
   return check_launch("na3d_bwd kernels");

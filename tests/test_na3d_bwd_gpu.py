@@ -21,6 +21,9 @@ CASES = [  # shape [B, Z, Y, X, H, D], kernel, dilation
     ((1, 5, 7, 9, 2, 64), (5, 7, 9), (1, 1, 1)),
     ((1, 3, 21, 30, 2, 64), (3, 13, 13), (1, 1, 1)),  # MFMA dq: x union of 16 keys, ragged tiles
     ((2, 4, 6, 37, 1, 64), (3, 5, 11), (1, 1, 1)),
+    # LDS dq / dk/dv: three workgroup columns (the last ragged), keys at both x edges
+    # needing two 16-query blocks, clamped y windows, a multi-stage ring
+    ((1, 4, 13, 45, 2, 64), (3, 9, 13), (1, 1, 1)),
 ]
 
 
@@ -95,15 +98,30 @@ def test_bwd_mfma_matches_valu_path(gpu, case, monkeypatch):
         assert rel_l2(a.float(), b.float()) <= 1e-2
 
 
+def _plain_takes_small_strips(shape, kernel, dil, dtype):
+    """Whether a whole-grid forward without lse runs the reference-free small-window
+    strip kernel (bf16, head_dim 64, kz >= 2, kx <= 9, ky in {5, 7, 9}, no y dilation,
+    at least two query rows whose y window is not clamped); the lse request cannot."""
+    Y, D = shape[2], shape[5]
+    return (dtype == torch.bfloat16 and D == 64 and kernel[0] >= 2 and kernel[2] <= 9 and kernel[1] in (5, 7, 9)
+            and dil[1] == 1 and Y - 2 * (kernel[1] // 2) >= 2)
+
+
 @pytest.mark.parametrize("case", CASES, ids=str)
 @pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16], ids=["f32", "bf16"])
 def test_forward_lse_vs_oracle(gpu, case, dtype):
     """The forward's log2-sum-exp (scalar, general MFMA and strip kernels) against
-    the oracle's, and the output unchanged by asking for it."""
+    the oracle's, and the output unchanged by asking for it: bit for bit when one
+    kernel serves both requests, within bf16 rounding when the plain request runs
+    the reference-free small-window strips."""
     shape, kernel, dil = case
     (q, k, v, _), (qg, kg, vg, _) = _inputs(shape, 5, dtype, gpu)
     out, lse = torch.ops.strata_hip.na3d_fwd_lse(qg, kg, vg, list(kernel), list(dil), None)
-    assert torch.equal(out, _fwd(qg, kg, vg, kernel, dil))
+    plain = _fwd(qg, kg, vg, kernel, dil)
+    if _plain_takes_small_strips(shape, kernel, dil, dtype):
+        assert rel_l2(out.float(), plain.float()) <= 4e-3
+    else:
+        assert torch.equal(out, plain)
     _, ref = O.na3d(q, k, v, kernel, dil, compute_dtype=torch.float64, return_lse=True)
     # bf16: the kernels score bf16(scale*log2(e)*q) against k, a 2^-9 relative rounding of q
     tol = 1e-4 if dtype == torch.float32 else 3e-2
