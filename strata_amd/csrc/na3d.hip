@@ -1749,9 +1749,15 @@ static int launch_small_strips(const Na3dParams& p, hipStream_t st) {
   const int y0 = p.org[1], y1 = p.org[1] + p.ext[1];
   const int r0 = y0 > kr ? y0 : kr, r1 = y1 < p.L[1] - kr ? y1 : p.L[1] - kr;
   if (r1 - r0 < 2) return launch_mfma_d<64>(p, st);
+  // The clamped edge rows (at most kr = ky / 2 <= 4 at each end) on the general
+  // kernel with workgroups as tall as the edge: 2 rows for ky = 5, else 4.
+  auto edge = [&](int e0, int e1) {
+    const Na3dParams e = y_sub_box(p, e0, e1);
+    return e1 - e0 <= 2 ? launch_mfma_tx<64, 8, 1>(e, st) : launch_mfma_tx<64, 8, 2>(e, st);
+  };
   int rc = STRATA_HIP_OK;
-  if (r0 > y0 && (rc = launch_mfma_d<64>(y_sub_box(p, y0, r0), st)) != STRATA_HIP_OK) return rc;
-  if (r1 < y1 && (rc = launch_mfma_d<64>(y_sub_box(p, r1, y1), st)) != STRATA_HIP_OK) return rc;
+  if (r0 > y0 && (rc = edge(y0, r0)) != STRATA_HIP_OK) return rc;
+  if (r1 < y1 && (rc = edge(r1, y1)) != STRATA_HIP_OK) return rc;
   const Na3dParams mid = y_sub_box(p, r0, r1);
   switch (p.ker[1]) {
     case 5: return launch_strip<64, 8, 2, 2, true, 5>(mid, st);
