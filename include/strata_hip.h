@@ -166,6 +166,8 @@ int strata_hip_na3d_bwd_noalloc(const strata_hip_na3d_bwd_args* args, void* stre
  * broadcasts one table over all levels).
  * q, k, v: [M, H, D] bf16 contiguous (heads-last token layout).  RoPE rotates
  * the pairs of q and k; v is copied.  Any of q/k/v may alias nothing else.
+ * v may be NULL: then only q and k are written (a caller that reads v straight
+ * out of qkv, as a view with token stride qkv_row_stride, saves the copy).
  *
  * qk_norm = 1 applies RMSNorm over D to every (token, head) of q and k before
  * the rotation, x * rsqrt(mean(x^2) + qk_norm_eps) * weight (fp32 math;
@@ -198,7 +200,9 @@ int strata_hip_rope_qkv_pack(const strata_hip_rope_pack_args* args, void* stream
 
 /* Backward of the pack: dqkv [M, (3, H, D)] (row stride dqkv_row_stride) =
  * (R(-theta) dq, R(-theta) dk, dv) for dq, dk, dv [M, H, D] contiguous bf16
- * and the forward's cos/sin tables and layout.  With qk_norm = 1 the q and k
+ * and the forward's cos/sin tables and layout.  dv may be NULL: v's columns of
+ * dqkv are then written as zeros (a v read as a view of qkv adds its gradient
+ * there itself).  With qk_norm = 1 the q and k
  * columns are further taken through the RMSNorm backward, recomputed from the
  * forward's input qkv (row stride qkv_row_stride):
  *   g = R(-theta) dout * w,  r = 1/sqrt(mean(x^2) + eps),

@@ -1690,15 +1690,16 @@ static int launch_strip(const Na3dParams& p, hipStream_t st) {
 
 // The strip kernel covers 4-column tiles (kx 10..13, ky <= 13) of head_dim 64
 // with a window at least two slices deep (the next tile's Q is copied while the
-// second slice of a group runs); its Q and self-key descriptors address one
-// (batch, z, head) slice with 31-bit byte offsets.
+// second slice of a group runs); its Q, K and V rows of one (batch, z, head)
+// slice must fit 31-bit byte offsets (V may be a strided view of the qkv GEMM's
+// output, three times the stride of a packed tensor).
 static bool strip_fits(const Na3dParams& p) {
   if (p.D != 64 || p.ker[0] < 2 || p.ker[2] < 10 || p.ker[2] > 13) return false;
   // Taller windows keep more than four tiles alive per row group (the walk
   // would split into many short segments); row groups are packed in 10 bits.
   if (p.ker[1] > 13 || p.L[1] >= 4096) return false;
-  const int64_t* sd[2] = {p.qs, p.ks};
-  for (int t = 0; t < 2; ++t)
+  const int64_t* sd[3] = {p.qs, p.ks, p.vs};
+  for (int t = 0; t < 3; ++t)
     if (((int64_t)(p.L[1] - 1) * sd[t][2] + (int64_t)(p.L[2] - 1) * sd[t][3] + p.D) * 2 >= 0x7fffffffLL) return false;
   return true;
 }
@@ -1726,8 +1727,8 @@ static bool small_strip_fits(const Na3dParams& p) {
   if (p.D != 64 || p.lse || p.ker[0] < 2 || p.ker[2] > 9 || p.dil[1] != 1) return false;
   if (p.ker[1] != 5 && p.ker[1] != 7 && p.ker[1] != 9) return false;
   if (p.L[1] >= 4096) return false;
-  const int64_t* sd[2] = {p.qs, p.ks};
-  for (int t = 0; t < 2; ++t)
+  const int64_t* sd[3] = {p.qs, p.ks, p.vs};
+  for (int t = 0; t < 3; ++t)
     if (((int64_t)(p.L[1] - 1) * sd[t][2] + (int64_t)(p.L[2] - 1) * sd[t][3] + p.D) * 2 >= 0x7fffffffLL) return false;
   return true;
 }

@@ -131,9 +131,13 @@ __global__ __launch_bounds__(256) void rope_pack_half_kernel(RopeParams p, int64
     const int64_t tok = th / p.H;
     const bf16* src = p.qkv + tok * p.ld + (int64_t)h * p.D + 8 * c;
 #pragma unroll
-    for (int t = 0; t < 3; ++t) {
+    for (int t = 0; t < 2; ++t) {
       raw[r][2 * t] = *(const u32x4*)(src + t * C);
       raw[r][2 * t + 1] = *(const u32x4*)(src + t * C + half);
+    }
+    if (p.v) {  // uniform: v is copied only when asked for
+      raw[r][4] = *(const u32x4*)(src + 2 * C);
+      raw[r][5] = *(const u32x4*)(src + 2 * C + half);
     }
     const int64_t trow = table_row(p, tok) * half + 8 * c;
     *(f32x4*)&cs[r][0] = *(const f32x4*)(p.cos + trow);
@@ -148,8 +152,10 @@ __global__ __launch_bounds__(256) void rope_pack_half_kernel(RopeParams p, int64
     if (!ok[r]) continue;  // uniform over the lanes of a head
     half_run(p, raw[r][0], raw[r][1], p.q + dst[r], cs[r], sn[r], cc[r], cph, p.qw);
     half_run(p, raw[r][2], raw[r][3], p.k + dst[r], cs[r], sn[r], cc[r], cph, p.kw);
-    *(u32x4*)(p.v + dst[r]) = raw[r][4];
-    *(u32x4*)(p.v + dst[r] + half) = raw[r][5];
+    if (p.v) {
+      *(u32x4*)(p.v + dst[r]) = raw[r][4];
+      *(u32x4*)(p.v + dst[r] + half) = raw[r][5];
+    }
   }
 }
 
@@ -193,7 +199,7 @@ __global__ __launch_bounds__(256) void rope_pack_inter_kernel(RopeParams p, int6
   const int64_t dst = tok * C + (int64_t)h * p.D + 8 * c;
   *(u32x4*)(p.q + dst) = rot_inter(p, *(const u32x4*)(src), cs, sn, c, cph, p.qw);
   *(u32x4*)(p.k + dst) = rot_inter(p, *(const u32x4*)(src + C), cs, sn, c, cph, p.kw);
-  *(u32x4*)(p.v + dst) = *(const u32x4*)(src + 2 * C);
+  if (p.v) *(u32x4*)(p.v + dst) = *(const u32x4*)(src + 2 * C);
 }
 
 // Backward of the pack without qk_norm: the gradient of a rotation by theta is
@@ -231,8 +237,8 @@ __global__ __launch_bounds__(256) void rope_unpack_half_kernel(RopeParams p, int
     *(u32x4*)(dst + t * C) = oa;
     *(u32x4*)(dst + t * C + half) = ob;
   }
-  *(u32x4*)(dst + 2 * C) = *(const u32x4*)(p.v + src);
-  *(u32x4*)(dst + 2 * C + half) = *(const u32x4*)(p.v + src + half);
+  *(u32x4*)(dst + 2 * C) = p.v ? *(const u32x4*)(p.v + src) : (u32x4){0u, 0u, 0u, 0u};  // no dv: v's columns are zero
+  *(u32x4*)(dst + 2 * C + half) = p.v ? *(const u32x4*)(p.v + src + half) : (u32x4){0u, 0u, 0u, 0u};
 }
 
 __global__ __launch_bounds__(256) void rope_unpack_inter_kernel(RopeParams p, int64_t total) {
@@ -264,7 +270,7 @@ __global__ __launch_bounds__(256) void rope_unpack_inter_kernel(RopeParams p, in
     }
     *(u32x4*)(dst + t * C) = o;
   }
-  *(u32x4*)(dst + 2 * C) = *(const u32x4*)(p.v + src);
+  *(u32x4*)(dst + 2 * C) = p.v ? *(const u32x4*)(p.v + src) : (u32x4){0u, 0u, 0u, 0u};
 }
 
 // Backward with qk_norm: each of q and k goes back through the rotation,
@@ -373,8 +379,8 @@ __global__ __launch_bounds__(256) void rope_unpack_norm_kernel(RopeParams p, int
       *(u32x4*)(dst + t * C) = lo;
       if constexpr (HALF) *(u32x4*)(dst + t * C + half) = hi;
     }
-    *(u32x4*)(dst + 2 * C) = *(const u32x4*)(p.v + src);
-    if constexpr (HALF) *(u32x4*)(dst + 2 * C + half) = *(const u32x4*)(p.v + src + half);
+    *(u32x4*)(dst + 2 * C) = p.v ? *(const u32x4*)(p.v + src) : (u32x4){0u, 0u, 0u, 0u};
+    if constexpr (HALF) *(u32x4*)(dst + 2 * C + half) = p.v ? *(const u32x4*)(p.v + src + half) : (u32x4){0u, 0u, 0u, 0u};
   }
 
   if (!p.dqw && !p.dkw) return;  // uniform: no weight gradients wanted
@@ -396,7 +402,7 @@ using namespace strata;
 
 extern "C" int strata_hip_rope_qkv_pack_bwd(const strata_hip_rope_pack_bwd_args* a, void* stream) {
   if (!a) return fail(STRATA_HIP_EINVAL, "rope_qkv_pack_bwd: null args");
-  if (!a->dq || !a->dk || !a->dv || !a->cos || !a->sin || !a->dqkv)
+  if (!a->dq || !a->dk || !a->cos || !a->sin || !a->dqkv)
     return fail(STRATA_HIP_EINVAL, "rope_qkv_pack_bwd: null pointer");
   if (a->batch < 0 || a->grid[0] <= 0 || a->grid[1] <= 0 || a->grid[2] <= 0 || a->heads <= 0)
     return fail(STRATA_HIP_EINVAL, "rope_qkv_pack_bwd: bad batch/grid/heads");
@@ -472,7 +478,7 @@ extern "C" int strata_hip_rope_qkv_pack_bwd(const strata_hip_rope_pack_bwd_args*
 
 extern "C" int strata_hip_rope_qkv_pack(const strata_hip_rope_pack_args* a, void* stream) {
   if (!a) return fail(STRATA_HIP_EINVAL, "rope_qkv_pack: null args");
-  if (!a->qkv || !a->cos || !a->sin || !a->q || !a->k || !a->v)
+  if (!a->qkv || !a->cos || !a->sin || !a->q || !a->k)
     return fail(STRATA_HIP_EINVAL, "rope_qkv_pack: null pointer");
   if (a->batch < 0 || a->grid[0] <= 0 || a->grid[1] <= 0 || a->grid[2] <= 0 || a->heads <= 0)
     return fail(STRATA_HIP_EINVAL, "rope_qkv_pack: bad batch/grid/heads");

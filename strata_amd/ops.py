@@ -282,7 +282,7 @@ def na3d(q: Tensor, k: Tensor, v: Tensor, kernel: Sequence[int], dilation: Seque
 @torch.library.custom_op("strata_hip::rope_qkv_pack", mutates_args=())
 def rope_qkv_pack(qkv: Tensor, cos: Tensor, sin: Tensor, heads: int, rope_layout: int, qk_norm: bool = False,
                   qk_norm_eps: float = 1e-6, q_norm_weight: Optional[Tensor] = None,
-                  k_norm_weight: Optional[Tensor] = None) -> tuple[Tensor, Tensor, Tensor]:
+                  k_norm_weight: Optional[Tensor] = None, pack_v: bool = True) -> tuple[Tensor, Tensor, Tensor]:
     """Split ``attn.qkv``'s output into heads-last q, k, v and rotate q, k.
 
     qkv: ``[B, Z, Y, X, 3*H*D]`` bf16 (column order (3, H, D), last dim
@@ -291,7 +291,10 @@ def rope_qkv_pack(qkv: Tensor, cos: Tensor, sin: Tensor, heads: int, rope_layout
     1 = interleaved (pair p = (2p, 2p+1)).  qk_norm: RMSNorm over D of each
     (token, head) of q and k before the rotation, ``x * rsqrt(mean(x^2) + eps)
     * weight`` (weights bf16 ``[D]`` or None; screamcast/config.py:91-93).
-    Returns q, k, v ``[B, Z, Y, X, H, D]``.
+    Returns q, k, v ``[B, Z, Y, X, H, D]``.  pack_v=False leaves v out (an empty
+    tensor is returned in its place): the caller reads v straight out of qkv as
+    the strided view ``qkv.view(B, Z, Y, X, 3, H, D)[..., 2, :, :]``, which the
+    NA3D op takes as it is, and the pack moves a third fewer bytes.
     """
     name = "rope_qkv_pack"
     _require_gpu(name, qkv, cos, sin)
@@ -325,12 +328,12 @@ def rope_qkv_pack(qkv: Tensor, cos: Tensor, sin: Tensor, heads: int, rope_layout
     shape = (B, Z, Y, X, heads, D)
     q = torch.empty(shape, dtype=qkv.dtype, device=qkv.device)
     k = torch.empty_like(q)
-    v = torch.empty_like(q)
+    v = torch.empty_like(q) if pack_v else q.new_empty(0)
     if q.numel() == 0:
         return q, k, v
     a = _lib.RopePackArgs()
     a.qkv, a.cos, a.sin = flat.data_ptr(), cos_c.data_ptr(), sin_c.data_ptr()
-    a.q, a.k, a.v = q.data_ptr(), k.data_ptr(), v.data_ptr()
+    a.q, a.k, a.v = q.data_ptr(), k.data_ptr(), (v.data_ptr() if pack_v else None)
     a.batch = B
     a.grid[:] = [Z, Y, X]
     a.table_z = cos.shape[1]
@@ -346,16 +349,17 @@ def rope_qkv_pack(qkv: Tensor, cos: Tensor, sin: Tensor, heads: int, rope_layout
 
 
 @rope_qkv_pack.register_fake
-def _(qkv, cos, sin, heads, rope_layout, qk_norm=False, qk_norm_eps=1e-6, q_norm_weight=None, k_norm_weight=None):
+def _(qkv, cos, sin, heads, rope_layout, qk_norm=False, qk_norm_eps=1e-6, q_norm_weight=None, k_norm_weight=None,
+      pack_v=True):
     B, Z, Y, X, C3 = qkv.shape
     D = C3 // (3 * heads)
     shape = (B, Z, Y, X, heads, D)
-    return qkv.new_empty(shape), qkv.new_empty(shape), qkv.new_empty(shape)
+    return qkv.new_empty(shape), qkv.new_empty(shape), qkv.new_empty(shape if pack_v else (0,))
 
 
 def _rope_setup_context(ctx, inputs, output):
-    qkv, cos, sin, heads, rope_layout, qk_norm, qk_norm_eps, q_norm_weight, k_norm_weight = inputs
-    ctx.qk_norm, ctx.heads, ctx.layout = bool(qk_norm), int(heads), int(rope_layout)
+    qkv, cos, sin, heads, rope_layout, qk_norm, qk_norm_eps, q_norm_weight, k_norm_weight, pack_v = inputs
+    ctx.qk_norm, ctx.heads, ctx.layout, ctx.pack_v = bool(qk_norm), int(heads), int(rope_layout), bool(pack_v)
     ctx.qk_norm_eps = float(qk_norm_eps)
     ctx.qkv_shape = tuple(qkv.shape)
     if ctx.qk_norm:  # the RMSNorm backward recomputes the norms from the input
@@ -367,15 +371,19 @@ def _rope_setup_context(ctx, inputs, output):
 def _rope_backward(ctx, dq, dk, dv):
     """d(qkv) = (R(-theta) dq, R(-theta) dk, dv) in qkv's (3, H, D) column layout;
     with qk_norm, q and k further through the RMSNorm backward (and the norm
-    weights' gradients, summed over tokens and heads in fp32)."""
+    weights' gradients, summed over tokens and heads in fp32).  Without a dv
+    (pack_v=False, or no gradient reached v) v's columns are zero: a v read as a
+    view of qkv adds its own gradient there."""
     cos, sin = ctx.saved_tensors[:2]
     B, Z, Y, X, C3 = ctx.qkv_shape
     D = C3 // (3 * ctx.heads)
     grads = [g.contiguous() if g is not None else torch.zeros((B, Z, Y, X, ctx.heads, D), dtype=torch.bfloat16,
-                                                                 device=cos.device) for g in (dq, dk, dv)]
+                                                                 device=cos.device) for g in (dq, dk)]
+    dv = dv.contiguous() if (ctx.pack_v and dv is not None) else None
     dqkv = torch.empty(ctx.qkv_shape, dtype=torch.bfloat16, device=cos.device)
     a = _lib.RopePackBwdArgs()
-    a.dq, a.dk, a.dv = (g.data_ptr() for g in grads)
+    a.dq, a.dk = (g.data_ptr() for g in grads)
+    a.dv = dv.data_ptr() if dv is not None else None
     cos_c, sin_c = cos.contiguous(), sin.contiguous()
     a.cos, a.sin, a.dqkv = cos_c.data_ptr(), sin_c.data_ptr(), dqkv.data_ptr()
     a.batch = B
@@ -401,7 +409,7 @@ def _rope_backward(ctx, dq, dk, dv):
             _lib.call("strata_hip_rope_qkv_pack_bwd", a, _stream(dqkv))
     if ctx.qk_norm:
         dws = [d.to(w.dtype) if d is not None else None for d, w in zip(dws, ctx.saved_tensors[3:])]
-    return dqkv, None, None, None, None, None, None, dws[0], dws[1]
+    return dqkv, None, None, None, None, None, None, dws[0], dws[1], None
 
 
 rope_qkv_pack.register_autograd(_rope_backward, setup_context=_rope_setup_context)

@@ -194,6 +194,34 @@ def test_rope_pack_qk_norm_vs_oracle(gpu, layout, affine):
         assert (rms - 1).abs().max() < 1e-2
 
 
+@pytest.mark.parametrize("layout", [_lib.ROPE_HALF, _lib.ROPE_INTERLEAVED])
+@pytest.mark.parametrize("qk_norm", [False, True])
+def test_rope_pack_without_v(gpu, layout, qk_norm):
+    """pack_v=False (the block's path: v read out of qkv as a strided view) writes the
+    same q and k bit for bit, returns no v, and the gradient reaching qkv through the
+    pack and the view equals the one through the full pack."""
+    B, Z, Y, X, H, D = 1, 3, 6, 10, 4, 64
+    g = torch.Generator().manual_seed(21 + layout + 2 * qk_norm)
+    qkv = _randn((B, Z, Y, X, 3 * H * D), g).to(gpu)
+    ang = torch.rand(B, 1, Y, X, D // 2, generator=g) * 20 - 10
+    cos, sin = torch.cos(ang).to(gpu), torch.sin(ang).to(gpu)
+    wq = (1 + 0.3 * torch.randn(D, generator=g)).bfloat16().to(gpu) if qk_norm else None
+    args = (cos, sin, H, layout, qk_norm, 1e-6, wq, None)
+    q, k, v = ops.rope_qkv_pack(qkv, *args)
+    q2, k2, v2 = ops.rope_qkv_pack(qkv, *args, pack_v=False)
+    assert torch.equal(q, q2) and torch.equal(k, k2) and v2.numel() == 0
+    w = [torch.randn(q.shape, generator=g).to(gpu) for _ in range(3)]
+    grads = []
+    for pack_v in (True, False):
+        x = qkv.detach().clone().requires_grad_()
+        a, b, c = ops.rope_qkv_pack(x, *args, pack_v=pack_v)
+        if not pack_v:
+            c = x.view(B, Z, Y, X, 3, H, D)[..., 2, :, :]
+        ((a.float() * w[0]).sum() + (b.float() * w[1]).sum() + (c.float() * w[2]).sum()).backward()
+        grads.append(x.grad)
+    assert torch.equal(grads[0], grads[1])
+
+
 def test_rope_pack_stereographic_tables(gpu):
     """configs[1]-style tables (64x64 tile, 32 pairs, base 1e4) built by the
     product helper agree with the float64 oracle and drive the pack kernel
