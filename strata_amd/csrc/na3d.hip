@@ -134,8 +134,7 @@ struct Na3dTiles {
 // ids k, k+8, ...; map those to the k-th contiguous block of tiles.
 // (__builtin_amdgcn_workgroup_id_x keeps the id visibly uniform to the
 // compiler, unlike blockIdx.x's out-of-line library call.)
-__device__ __forceinline__ int xcd_tile_order(int n) {
-  const int id = (int)__builtin_amdgcn_workgroup_id_x();
+__device__ __forceinline__ int xcd_tile_order(int n, int id) {
   const int xcd = id & 7, local = id >> 3;
   const int q = n >> 3, rem = n & 7;
   return xcd < rem ? xcd * (q + 1) + local : rem * (q + 1) + (xcd - rem) * q + local;
@@ -225,8 +224,17 @@ __device__ __forceinline__ uint32_t bit_range(int lo, int hi) {
 // the QK MFMA starts from C = bias - m (bias in {0, -inf} per key for the x
 // mask), so the MFMA itself returns u and no VALU work sits between the scores
 // and the exponentials outside the boundary rows of the y mask.
+// LDS bytes of one workgroup of the general kernel: a ring of NBUF stages.
+template <int D, int TX, int RPS, int NBUF>
+constexpr int mfma_lds_bytes() {
+  return NBUF * 2 * RPS * (((NA3D_NWX - 1) * TX + 16 + 512 / D - 1) / (512 / D) * (512 / D)) * D * 2;
+}
+
+// `lds`: the workgroup's LDS (mfma_lds_bytes), 1 KiB aligned; `id`: its tile
+// index in [0, tg.total) (the kernels pass their workgroup id; the fused
+// small-window kernel an offset one, in a block of ids starting at a multiple of 8).
 template <int D, int TX, int NTY, int RPS, int NBUF>
-__device__ __forceinline__ void na3d_mfma_body(const Na3dParams p, const Na3dTiles tg) {
+__device__ __forceinline__ void na3d_mfma_body(const Na3dParams p, const Na3dTiles tg, char* lds, int id) {
 #if defined(__HIP_DEVICE_COMPILE__)  // the body is device code only; the host pass needs just the signature
   constexpr int NWX = NA3D_NWX;
   constexpr int TY = 16 / TX;
@@ -249,9 +257,9 @@ __device__ __forceinline__ void na3d_mfma_body(const Na3dParams p, const Na3dTil
   constexpr float TAU = 64.f;
   static_assert(RB % 1024 == 0 && (2 * RPS * RKB) % NWX == 0 && (RPS == 2 || RPS == 4), "stage layout");
 
-  __shared__ __attribute__((aligned(1024))) char lds[NBUF * STAGE_B];
+  static_assert(NBUF * STAGE_B == mfma_lds_bytes<D, TX, RPS, NBUF>(), "LDS size");
 
-  const int wg = xcd_tile_order(tg.total);
+  const int wg = xcd_tile_order(tg.total, id);
   const int per = tg.nxt * tg.nyt * tg.nzt;
   int t = wg / per;
   int zt, yt, xt;
@@ -577,11 +585,13 @@ __device__ __forceinline__ void na3d_mfma_body(const Na3dParams p, const Na3dTil
 // Two workgroups per CU for head_dim <= 64; head_dim 128 needs the full register file.
 template <int D, int TX, int NTY, int RPS, int NBUF>
 __global__ __launch_bounds__(256, 2) void na3d_mfma_kernel(Na3dParams p, Na3dTiles tg) {
-  na3d_mfma_body<D, TX, NTY, RPS, NBUF>(p, tg);
+  __shared__ __attribute__((aligned(1024))) char lds[mfma_lds_bytes<D, TX, RPS, NBUF>()];
+  na3d_mfma_body<D, TX, NTY, RPS, NBUF>(p, tg, lds, (int)__builtin_amdgcn_workgroup_id_x());
 }
 template <int D, int TX, int NTY, int RPS, int NBUF>
 __global__ __launch_bounds__(256, 1) void na3d_mfma_wide_kernel(Na3dParams p, Na3dTiles tg) {
-  na3d_mfma_body<D, TX, NTY, RPS, NBUF>(p, tg);
+  __shared__ __attribute__((aligned(1024))) char lds[mfma_lds_bytes<D, TX, RPS, NBUF>()];
+  na3d_mfma_body<D, TX, NTY, RPS, NBUF>(p, tg, lds, (int)__builtin_amdgcn_workgroup_id_x());
 }
 
 // ---------------------------------------------------------------------------
@@ -723,7 +733,7 @@ __device__ __forceinline__ void na3d_strip_body(const Na3dParams p, const Na3dSt
   __shared__ __attribute__((aligned(1024))) char lds[RING_B + QTB];
 
   // ---- work unit ----
-  int t = xcd_tile_order(sg.total);
+  int t = xcd_tile_order(sg.total, (int)__builtin_amdgcn_workgroup_id_x());
   const int xb = t % sg.nxt;
   t /= sg.nxt;
   const int zt = t % sg.nzt;
@@ -1151,8 +1161,17 @@ __device__ __forceinline__ void static_for(F&& f) {
   static_for_impl(f, std::make_integer_sequence<int, N>{});
 }
 
+// LDS bytes of one workgroup of the regular-strip kernel: the K/V ring and the
+// staged Q of the next tile.
+template <int D, int TX, int RPS, int NBUF>
+constexpr int strip_fast_lds_bytes() {
+  return NBUF * 2 * RPS * ((NA3D_NWX - 1) * TX + 16) * D * 2 + NA3D_NWX * 16 * D * 2;
+}
+
+// `lds`: the workgroup's LDS (strip_fast_lds_bytes), 1 KiB aligned; `id`: its
+// work-unit index in [0, sg.total) (as na3d_mfma_body).
 template <int D, int TX, int RPS, int NBUF, int KY>
-__device__ __forceinline__ void na3d_strip_fast_body(const Na3dParams p, const Na3dStrips sg) {
+__device__ __forceinline__ void na3d_strip_fast_body(const Na3dParams p, const Na3dStrips sg, char* lds, int id) {
 #if defined(__HIP_DEVICE_COMPILE__)
   constexpr int NWX = NA3D_NWX;
   constexpr int TY = 16 / TX;
@@ -1182,10 +1201,10 @@ __device__ __forceinline__ void na3d_strip_fast_body(const Na3dParams p, const N
   static_assert(QWB == KS * 1024, "16 query rows are KS 1-KiB loads");
   static_assert(QTB <= RING_B, "tile 0's Q is staged through the ring");
 
-  __shared__ __attribute__((aligned(1024))) char lds[RING_B + QTB];
+  static_assert(RING_B + QTB == strip_fast_lds_bytes<D, TX, RPS, NBUF>(), "LDS size");
 
   // ---- work unit (as na3d_strip_body) ----
-  int t = xcd_tile_order(sg.total);
+  int t = xcd_tile_order(sg.total, id);
   const int xb = t % sg.nxt;
   t /= sg.nxt;
   const int zt = t % sg.nzt;
@@ -1566,7 +1585,32 @@ __device__ __forceinline__ void na3d_strip_fast_body(const Na3dParams p, const N
 // three for 5-row windows (48 KiB of LDS, 163 VGPRs; wider windows would spill).
 template <int D, int TX, int RPS, int NBUF, int KY>
 __global__ __launch_bounds__(256, TX == 8 && KY <= 5 ? 3 : 2) void na3d_strip_fast_kernel(Na3dParams p, Na3dStrips sg) {
-  na3d_strip_fast_body<D, TX, RPS, NBUF, KY>(p, sg);
+  __shared__ __attribute__((aligned(1024))) char lds[strip_fast_lds_bytes<D, TX, RPS, NBUF>()];
+  na3d_strip_fast_body<D, TX, RPS, NBUF, KY>(p, sg, lds, (int)__builtin_amdgcn_workgroup_id_x());
+}
+
+// Small windows in one launch: the regular strips of the rows whose y window is
+// not clamped, and the general kernel (a 2-stage ring, workgroups as tall as an
+// edge: 2 rows for ky = 5, else 4) over the clamped rows at each end, so the short
+// edge workgroups fill the strips' tail instead of running after them.  Workgroup
+// ids [0, n0) take the strips, [n0, n0 + n1) the top edge, the rest the bottom
+// edge; n0 and n1 are multiples of 8, so each part keeps its XCD-aware tile order.
+template <int KY>
+__global__ __launch_bounds__(256, KY <= 5 ? 3 : 2) void na3d_small_fused_kernel(Na3dParams mid, Na3dStrips sg,
+                                                                               Na3dParams e0, Na3dTiles t0,
+                                                                               Na3dParams e1, Na3dTiles t1, int n0,
+                                                                               int n1) {
+  constexpr int NTYE = KY <= 5 ? 1 : 2;
+  constexpr int LS = strip_fast_lds_bytes<64, 8, 2, 2>(), LE = mfma_lds_bytes<64, 8, 2, 2>();
+  __shared__ __attribute__((aligned(1024))) char lds[LS > LE ? LS : LE];
+  const int id = (int)__builtin_amdgcn_workgroup_id_x();
+  if (id < n0) {
+    if (id < sg.total) na3d_strip_fast_body<64, 8, 2, 2, KY>(mid, sg, lds, id);
+  } else if (id < n0 + n1) {
+    if (id - n0 < t0.total) na3d_mfma_body<64, 8, NTYE, 2, 2>(e0, t0, lds, id - n0);
+  } else if (id - n0 - n1 < t1.total) {
+    na3d_mfma_body<64, 8, NTYE, 2, 2>(e1, t1, lds, id - n0 - n1);
+  }
 }
 
 
@@ -1596,24 +1640,39 @@ static int launch_scalar(const Na3dParams& p, hipStream_t st) {
   return check_launch("na3d_scalar_kernel");
 }
 
-template <int D, int TX, int NTY, int RPS, int NBUF>
-static int launch_mfma_cfg(const Na3dParams& p, hipStream_t st) {
-  Na3dTiles tg;
-  int nq[3] = {0, 0, 0};
-  for (int a = 0; a < 3; ++a)
+// Query counts per axis of the box (largest over the dilation residue classes).
+static void box_queries(const Na3dParams& p, int (&nq)[3]) {
+  for (int a = 0; a < 3; ++a) {
+    nq[a] = 0;
     for (int g = 0; g < p.dil[a]; ++g) {
       const int n = sub_end(p.org[a], p.ext[a], g, p.dil[a]) - sub_first(p.org[a], g, p.dil[a]);
       nq[a] = n > nq[a] ? n : nq[a];
     }
+  }
+}
+
+// Workgroup tiles of the general kernel over the query box; false if the grid
+// would not fit one launch.
+template <int TX, int NTY>
+static bool make_tiles(const Na3dParams& p, Na3dTiles& tg) {
+  int nq[3];
+  box_queries(p, nq);
   constexpr int TY = 16 / TX;
   tg.nzt = nq[0];
   tg.nyt = (nq[1] + NTY * TY - 1) / (NTY * TY);
   tg.nxt = (nq[2] + NA3D_NWX * TX - 1) / (NA3D_NWX * TX);
   tg.nres = p.dil[0] * p.dil[1] * p.dil[2];
   const int64_t total = (int64_t)tg.nxt * tg.nyt * tg.nzt * tg.nres * p.H * p.B;
+  tg.total = total > 0x7fffffff ? 0 : (int)total;
+  return total <= 0x7fffffff;
+}
+
+template <int D, int TX, int NTY, int RPS, int NBUF>
+static int launch_mfma_cfg(const Na3dParams& p, hipStream_t st) {
+  Na3dTiles tg;
+  if (!make_tiles<TX, NTY>(p, tg)) return fail(STRATA_HIP_EUNSUPPORTED, "na3d: problem too large for one launch");
+  const int total = tg.total;
   if (total == 0) return STRATA_HIP_OK;
-  if (total > 0x7fffffff) return fail(STRATA_HIP_EUNSUPPORTED, "na3d: problem too large for one launch");
-  tg.total = (int)total;
   if (D >= 128)
     hipLaunchKernelGGL((na3d_mfma_wide_kernel<D, TX, NTY, RPS, NBUF>), dim3((unsigned)total), dim3(64 * NA3D_NWX), 0,
                        st, p, tg);
@@ -1650,22 +1709,20 @@ static int launch_mfma_tx(const Na3dParams& p, hipStream_t st) {
 // Strip kernel launch.  Work units are (batch, head, residue, z, column box)
 // strips over the whole y range; the y range is cut into chunks only when the
 // strips alone would not fill the GPU several times over.
-template <int D, int TX, int RPS, int NBUF, bool FAST, int KY = 13>
-static int launch_strip(const Na3dParams& p, hipStream_t st) {
+// Strip work units over the query box; false if they would not fit one launch.
+template <int TX>
+static bool make_strips(const Na3dParams& p, Na3dStrips& sg) {
   constexpr int TY = 16 / TX;
-  Na3dStrips sg;
-  int nq[3] = {0, 0, 0};
-  for (int a = 0; a < 3; ++a)
-    for (int g = 0; g < p.dil[a]; ++g) {
-      const int n = sub_end(p.org[a], p.ext[a], g, p.dil[a]) - sub_first(p.org[a], g, p.dil[a]);
-      nq[a] = n > nq[a] ? n : nq[a];
-    }
+  int nq[3];
+  box_queries(p, nq);
   sg.nzt = nq[0];
   sg.nxt = (nq[2] + NA3D_NWX * TX - 1) / (NA3D_NWX * TX);
   sg.nres = p.dil[0] * p.dil[1] * p.dil[2];
   const int nty = (nq[1] + TY - 1) / TY;
   const int64_t strips = (int64_t)sg.nxt * sg.nzt * sg.nres * p.H * p.B;
-  if (strips == 0 || nty == 0) return STRATA_HIP_OK;
+  sg.nch = sg.cty = 1;
+  sg.total = 0;
+  if (strips == 0 || nty == 0) return true;
   int nch = 1;
   // Cut the y range into chunks only when the strips alone would leave the GPU
   // short of work: 4-column tiles aim at 2048 workgroups; the 2 x 8 tiles of
@@ -1676,8 +1733,17 @@ static int launch_strip(const Na3dParams& p, hipStream_t st) {
   sg.cty = (nty + nch - 1) / nch;
   sg.nch = (nty + sg.cty - 1) / sg.cty;
   const int64_t total = strips * sg.nch;
-  if (total > 0x7fffffff) return fail(STRATA_HIP_EUNSUPPORTED, "na3d: problem too large for one launch");
+  if (total > 0x7fffffff) return false;
   sg.total = (int)total;
+  return true;
+}
+
+template <int D, int TX, int RPS, int NBUF, bool FAST, int KY = 13>
+static int launch_strip(const Na3dParams& p, hipStream_t st) {
+  Na3dStrips sg;
+  if (!make_strips<TX>(p, sg)) return fail(STRATA_HIP_EUNSUPPORTED, "na3d: problem too large for one launch");
+  const int total = sg.total;
+  if (total == 0) return STRATA_HIP_OK;
   if constexpr (FAST) {
     hipLaunchKernelGGL((na3d_strip_fast_kernel<D, TX, RPS, NBUF, KY>), dim3((unsigned)total), dim3(64 * NA3D_NWX), 0, st,
                        p, sg);
@@ -1750,21 +1816,28 @@ static int launch_small_strips(const Na3dParams& p, hipStream_t st) {
   const int y0 = p.org[1], y1 = p.org[1] + p.ext[1];
   const int r0 = y0 > kr ? y0 : kr, r1 = y1 < p.L[1] - kr ? y1 : p.L[1] - kr;
   if (r1 - r0 < 2) return launch_mfma_d<64>(p, st);
-  // The clamped edge rows (at most kr = ky / 2 <= 4 at each end) on the general
-  // kernel with workgroups as tall as the edge: 2 rows for ky = 5, else 4.
-  auto edge = [&](int e0, int e1) {
-    const Na3dParams e = y_sub_box(p, e0, e1);
-    return e1 - e0 <= 2 ? launch_mfma_tx<64, 8, 1>(e, st) : launch_mfma_tx<64, 8, 2>(e, st);
-  };
-  int rc = STRATA_HIP_OK;
-  if (r0 > y0 && (rc = edge(y0, r0)) != STRATA_HIP_OK) return rc;
-  if (r1 < y1 && (rc = edge(r1, y1)) != STRATA_HIP_OK) return rc;
-  const Na3dParams mid = y_sub_box(p, r0, r1);
+  // the clamped edge rows: at most kr = ky / 2 <= 4 at each end
+  const Na3dParams mid = y_sub_box(p, r0, r1), e0 = y_sub_box(p, y0, r0), e1 = y_sub_box(p, r1, y1);
+  Na3dStrips sg;
+  Na3dTiles t0, t1;
+  const bool ok = make_strips<8>(mid, sg) && (p.ker[1] <= 5 ? make_tiles<8, 1>(e0, t0) && make_tiles<8, 1>(e1, t1)
+                                                            : make_tiles<8, 2>(e0, t0) && make_tiles<8, 2>(e1, t1));
+  const int64_t n0 = (sg.total + 7) / 8 * 8, n1 = (t0.total + 7) / 8 * 8, total = n0 + n1 + t1.total;
+  if (!ok || total > 0x7fffffff) return fail(STRATA_HIP_EUNSUPPORTED, "na3d: problem too large for one launch");
+  if (total == 0) return STRATA_HIP_OK;
+  const dim3 grid((unsigned)total), block(64 * NA3D_NWX);
   switch (p.ker[1]) {
-    case 5: return launch_strip<64, 8, 2, 2, true, 5>(mid, st);
-    case 7: return launch_strip<64, 8, 2, 2, true, 7>(mid, st);
-    default: return launch_strip<64, 8, 2, 2, true, 9>(mid, st);
+    case 5:
+      hipLaunchKernelGGL(na3d_small_fused_kernel<5>, grid, block, 0, st, mid, sg, e0, t0, e1, t1, (int)n0, (int)n1);
+      break;
+    case 7:
+      hipLaunchKernelGGL(na3d_small_fused_kernel<7>, grid, block, 0, st, mid, sg, e0, t0, e1, t1, (int)n0, (int)n1);
+      break;
+    default:
+      hipLaunchKernelGGL(na3d_small_fused_kernel<9>, grid, block, 0, st, mid, sg, e0, t0, e1, t1, (int)n0, (int)n1);
+      break;
   }
+  return check_launch("na3d_small_fused_kernel");
 }
 
 template <int D>
