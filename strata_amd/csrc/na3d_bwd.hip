@@ -102,13 +102,14 @@ struct Tok {
   bool valid;
 };
 
-// The token of in-tile index t (row t >> 2, column t & 3) of this lane's wave.
-__device__ __forceinline__ Tok token_at(const Na3dBwdParams& p, int t) {
+// The token of in-tile index t (row r0 + (t >> 2), column t & 3) of this lane's
+// wave, for workgroups of `rows` rows (nyt of them along y).
+__device__ __forceinline__ Tok token_rows(const Na3dBwdParams& p, int nyt, int rows, int r0, int t) {
   int w = (int)blockIdx.x;
   const int xb = w % p.nxt;
   w /= p.nxt;
-  const int yt = w % p.nyt;
-  w /= p.nyt;
+  const int yt = w % nyt;
+  w /= nyt;
   const int z = w % p.Z;
   w /= p.Z;
   const int h = w % p.H;
@@ -118,7 +119,7 @@ __device__ __forceinline__ Tok token_at(const Na3dBwdParams& p, int t) {
   k.b = b;
   k.h = h;
   k.z = z;
-  k.y = yt * 4 + (t >> 2);
+  k.y = yt * rows + r0 + (t >> 2);
   k.x = xb * 16 + wave * 4 + (t & 3);
   k.valid = k.y < p.Y && k.x < p.X;
   if (!k.valid) {  // clamp so every address stays in range; nothing is stored
@@ -127,6 +128,9 @@ __device__ __forceinline__ Tok token_at(const Na3dBwdParams& p, int t) {
   }
   return k;
 }
+
+// The token of in-tile index t (row t >> 2, column t & 3) of this lane's wave.
+__device__ __forceinline__ Tok token_at(const Na3dBwdParams& p, int t) { return token_rows(p, p.nyt, 4, 0, t); }
 
 // VALU kernels: 4 lanes per token, lane l on token l >> 2.
 __device__ __forceinline__ Tok token_of(const Na3dBwdParams& p) { return token_at(p, ((int)threadIdx.x & 63) >> 2); }
@@ -350,8 +354,9 @@ __global__ __launch_bounds__(256) void na3d_bwd_prep_mfma_kernel(Na3dBwdParams p
 
 // ---------------------------------------------------------------------------
 // LDS-staged dk / dv for bf16, head_dim 64, dilation 1, kx <= 13.  The
-// workgroup's four 4 x 4 key tiles (16 key columns of one (b, h, z), 4 rows)
-// share their queries: the union of the tiles' inverse windows is walked two
+// workgroup's 4 x 4 key tiles (four waves side by side along x, NT tiles per
+// wave stacked along y: 16 key columns of one (b, h, z), 4 NT rows) share their
+// queries: the union of the tiles' inverse windows is walked two
 // query (z, y) rows at a time, each row's Q and dO over the workgroup's
 // inverse-window columns (at most 16 + kx - 1 <= 28, staged as 32) copied into
 // LDS once per workgroup by `buffer_load ... lds` (a ring of three stages),
@@ -363,8 +368,14 @@ __global__ __launch_bounds__(256) void na3d_bwd_prep_mfma_kernel(Na3dBwdParams p
 // dK^T += Q^T dS over the row pair, with dO^T and Q^T read transposed
 // (ds_read_b64_tr_b16).  A wave's keys near a grid edge can need up to 22
 // queries along x: a second 16-query block then starts at most 16 columns
-// before the stage's end and skips the columns the first one covered.
+// before the stage's end and skips the columns the first one covered.  A tile
+// none of whose keys lies in either staged row's windows skips the stage.
 // ---------------------------------------------------------------------------
+// 4x4 tiles per wave of the LDS kernels, stacked along y: two share each staged
+// row pair between a wave's tiles (configs[1] 0.65 -> 0.62 ms, the configs[3]
+// shape 2.31 -> 2.15 ms against one tile per wave).
+constexpr int NA3D_BWD_NT = 2;
+
 namespace dkvl {
 constexpr int SW = 32;                     // staged query columns per row
 constexpr int RB = SW * 64 * 2;            // bytes of one staged row of Q (or dO)
@@ -372,7 +383,8 @@ constexpr int NBUF = 3;                    // ring stages
 constexpr int STAGE = 4 * RB + 4 * SW * 4;  // Q r0, Q r1, dO r0, dO r1, lse r0, r1, D r0, r1
 }  // namespace dkvl
 
-__global__ __launch_bounds__(256, 3) void na3d_bwd_dkv_lds_kernel(Na3dBwdParams p) {
+template <int NT>
+__global__ __launch_bounds__(256, NT == 1 ? 3 : 2) void na3d_bwd_dkv_lds_kernel(Na3dBwdParams p, int nyt) {
 #if defined(__HIP_DEVICE_COMPILE__)
   using namespace dkvl;
   constexpr int D = 64, KS = 2, DB = 4;
@@ -380,20 +392,27 @@ __global__ __launch_bounds__(256, 3) void na3d_bwd_dkv_lds_kernel(Na3dBwdParams 
   const int tid = (int)threadIdx.x;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int lane = tid & 63, n16 = lane & 15, g = lane >> 4;
-  const Tok t = token_at(p, n16);  // MFMA column n16 = the lane's key
+  Tok t[NT];  // MFMA column n16 of tile tt = the lane's key in rows 4 tt .. 4 tt + 3 of the workgroup
+#pragma unroll
+  for (int tt = 0; tt < NT; ++tt) t[tt] = token_rows(p, nyt, 4 * NT, 4 * tt, n16);
   const float c2 = p.scale * 1.4426950408889634f;
   const int kz = p.ker[0], ky = p.ker[1], kx = p.ker[2];
   const uint32_t lds_base = (uint32_t)(uintptr_t)(__attribute__((address_space(3))) char*)lds;
 
-  const int64_t kj = tok_index(p, t.b, t.z, t.y, t.x, t.h);
-  bf16x8 kreg[KS], vreg[KS];
+  int64_t kj[NT];
+  bf16x8 kreg[NT][KS], vreg[NT][KS];
 #pragma unroll
-  for (int ks = 0; ks < KS; ++ks) {
-    kreg[ks] = *(const bf16x8*)((const bf16*)p.k + kj * D + 8 * (4 * ks + g));
-    vreg[ks] = *(const bf16x8*)((const bf16*)p.v + kj * D + 8 * (4 * ks + g));
+  for (int tt = 0; tt < NT; ++tt) {
+    kj[tt] = tok_index(p, t[tt].b, t[tt].z, t[tt].y, t[tt].x, t[tt].h);
 #pragma unroll
-    for (int e = 0; e < 8; ++e) kreg[ks][e] = (bf16)((float)kreg[ks][e] * c2);
+    for (int ks = 0; ks < KS; ++ks) {
+      kreg[tt][ks] = *(const bf16x8*)((const bf16*)p.k + kj[tt] * D + 8 * (4 * ks + g));
+      vreg[tt][ks] = *(const bf16x8*)((const bf16*)p.v + kj[tt] * D + 8 * (4 * ks + g));
+#pragma unroll
+      for (int e = 0; e < 8; ++e) kreg[tt][ks][e] = (bf16)((float)kreg[tt][ks][e] * c2);
+    }
   }
+  const Tok& t0 = t[0];  // b, h, z and the key column are the same for every tile
 
   // ---- x: the workgroup's query columns [SX0, SX0 + SW) and this wave's blocks ----
   const int KX0 = ((int)blockIdx.x % p.nxt) * 16;
@@ -419,7 +438,7 @@ __global__ __launch_bounds__(256, 3) void na3d_bwd_dkv_lds_kernel(Na3dBwdParams 
       const int cl = bs[xb] + 4 * g + e;  // column within the stage
       const int qx = SX0 + cl;
       const int sx = win_start(min(qx, p.X - 1), p.X, kx);
-      const bool in = qx < p.X && (xb == 0 || cl >= bs0 + 16) && t.x >= sx && t.x < sx + kx;
+      const bool in = qx < p.X && (xb == 0 || cl >= bs0 + 16) && t0.x >= sx && t0.x < sx + kx;
       xm[xb] |= in ? (1u << e) : 0u;
     }
   }
@@ -437,13 +456,13 @@ __global__ __launch_bounds__(256, 3) void na3d_bwd_dkv_lds_kernel(Na3dBwdParams 
   }
 
   // ---- y, z: the query rows of the workgroup's keys ----
-  const int ky0 = min(((int)(blockIdx.x / p.nxt) % p.nyt) * 4, p.Y - 1), ky1 = min(ky0 + 3, p.Y - 1);
+  const int ky0 = min(((int)(blockIdx.x / p.nxt) % nyt) * 4 * NT, p.Y - 1), ky1 = min(ky0 + 4 * NT - 1, p.Y - 1);
   axis_inv(ky0, p.Y, ky, 1, f, n);
   const int QY0 = f;
   axis_inv(ky1, p.Y, ky, 1, f, n);
   const int NY = f + n - QY0;
   int QZ0, NZ;
-  axis_inv(t.z, p.Z, kz, 1, QZ0, NZ);
+  axis_inv(t0.z, p.Z, kz, 1, QZ0, NZ);
   const int nrows = NZ * NY;
   const int nst = (nrows + 1) / 2;
 
@@ -460,38 +479,38 @@ __global__ __launch_bounds__(256, 3) void na3d_bwd_dkv_lds_kernel(Na3dBwdParams 
   }
   const int scol = lane & 31;  // lse / D copies: lane -> (row lane >> 5, column lane & 31)
   const bool scol_in = SX0 + scol < p.X;
-  const char* qbase = (const char*)p.q + 2 * (int64_t)t.h * D;
-  const char* obase = (const char*)p.dout + 2 * (int64_t)t.h * D;
+  const char* qbase = (const char*)p.q + 2 * (int64_t)t0.h * D;
+  const char* obase = (const char*)p.dout + 2 * (int64_t)t0.h * D;
   const float* sbase = wave == 0 ? p.lse : p.dsum;
   auto row_tok = [&](int sr) {  // token index of (row sr, x = 0, head 0)
     const int zq = QZ0 + sr / NY, yq = QY0 + sr % NY;
-    return (((int64_t)t.b * p.Z + zq) * p.Y + yq) * p.X * p.H;
+    return (((int64_t)t0.b * p.Z + zq) * p.Y + yq) * p.X * p.H;
   };
-  const int nload = wave < 2 ? 5 : 4;
   auto issue = [&](int s) {
     const uint32_t st = lds_base + (uint32_t)((s % NBUF) * STAGE);
     const int r0 = 2 * s, r1 = 2 * s + 1;
     const bool l0 = r0 < nrows, l1 = r1 < nrows;
-    const int64_t t0 = l0 ? row_tok(r0) : 0, t1 = l1 ? row_tok(r1) : 0;
-    dma_row16(make_rsrc(qbase + t0 * D * 2, l0 ? rec : 0u), st + 0 * RB + wave * 1024, voff);
-    dma_row16(make_rsrc(qbase + t1 * D * 2, l1 ? rec : 0u), st + 1 * RB + wave * 1024, voff);
-    dma_row16(make_rsrc(obase + t0 * D * 2, l0 ? rec : 0u), st + 2 * RB + wave * 1024, voff);
-    dma_row16(make_rsrc(obase + t1 * D * 2, l1 ? rec : 0u), st + 3 * RB + wave * 1024, voff);
+    const int64_t w0 = l0 ? row_tok(r0) : 0, w1 = l1 ? row_tok(r1) : 0;
+    dma_row16(make_rsrc(qbase + w0 * D * 2, l0 ? rec : 0u), st + 0 * RB + wave * 1024, voff);
+    dma_row16(make_rsrc(qbase + w1 * D * 2, l1 ? rec : 0u), st + 1 * RB + wave * 1024, voff);
+    dma_row16(make_rsrc(obase + w0 * D * 2, l0 ? rec : 0u), st + 2 * RB + wave * 1024, voff);
+    dma_row16(make_rsrc(obase + w1 * D * 2, l1 ? rec : 0u), st + 3 * RB + wave * 1024, voff);
     if (wave < 2) {
-      // row 1 sits (t1 - t0) tokens after row 0 in the [B, Z, Y, X, H] statistics
-      const int64_t dt = l1 ? t1 - t0 : 0;
+      // row 1 sits (w1 - w0) tokens after row 0 in the [B, Z, Y, X, H] statistics
+      const int64_t dt = l1 ? w1 - w0 : 0;
       const uint32_t so = (lane < 32 ? (l0 && scol_in) : (l1 && scol_in))
-                              ? (uint32_t)(((lane < 32 ? 0 : dt) + (int64_t)(SX0 + scol) * p.H + t.h) * 4)
+                              ? (uint32_t)(((lane < 32 ? 0 : dt) + (int64_t)(SX0 + scol) * p.H + t0.h) * 4)
                               : OOB;
       const uint32_t srec = l0 ? (uint32_t)((dt + (int64_t)p.X * p.H) * 4) : 0u;
-      dma_dword(make_rsrc(sbase + t0, srec), st + 4 * RB + wave * 2 * SW * 4, so);
+      dma_dword(make_rsrc(sbase + w0, srec), st + 4 * RB + wave * 2 * SW * 4, so);
     }
   };
 
-  f32x4 dk[DB], dv[DB];
+  f32x4 dk[NT][DB], dv[NT][DB];
 #pragma unroll
-  for (int db = 0; db < DB; ++db) dk[db] = dv[db] = (f32x4){0.f, 0.f, 0.f, 0.f};
-  const f32x4 ninf = {-INFINITY, -INFINITY, -INFINITY, -INFINITY};
+  for (int tt = 0; tt < NT; ++tt)
+#pragma unroll
+    for (int db = 0; db < DB; ++db) dk[tt][db] = dv[tt][db] = (f32x4){0.f, 0.f, 0.f, 0.f};
 
 #pragma unroll
   for (int s = 0; s < NBUF - 1; ++s) issue(s);
@@ -504,67 +523,96 @@ __global__ __launch_bounds__(256, 3) void na3d_bwd_dkv_lds_kernel(Na3dBwdParams 
     issue(s + NBUF - 1);
     const char* st = lds + (s % NBUF) * STAGE;
     const float* sl = (const float*)(st + 4 * RB);  // lse r0, lse r1, D r0, D r1
-    // y / z membership of the lane's key for the two rows
-    bool yz[2];
+    // y / z membership of the lane's key (each tile) for the two rows; a tile none of
+    // whose keys is in either row's windows skips the stage (wave-uniform)
+    bool yz[NT][2], act[NT];
 #pragma unroll
     for (int r = 0; r < 2; ++r) {
       const int sr = 2 * s + r;
       const int zq = QZ0 + sr / NY, yq = QY0 + sr % NY;
       const int wy = win_start(min(yq, p.Y - 1), p.Y, ky), wz = win_start(min(zq, p.Z - 1), p.Z, kz);
-      yz[r] = sr < nrows && t.y >= wy && t.y < wy + ky && t.z >= wz && t.z < wz + kz;
+      const bool zin = sr < nrows && t0.z >= wz && t0.z < wz + kz;
+#pragma unroll
+      for (int tt = 0; tt < NT; ++tt) yz[tt][r] = zin && t[tt].y >= wy && t[tt].y < wy + ky;
     }
+#pragma unroll
+    for (int tt = 0; tt < NT; ++tt) act[tt] = __builtin_amdgcn_ballot_w64(yz[tt][0] || yz[tt][1]) != 0;
 #pragma unroll
     for (int xb = 0; xb < 2; ++xb) {
       if (xb >= nxb) break;  // wave-uniform
-      float pv[2][4], sv[2][4];
+      bf16x8 qa[2][KS], da[2][KS];
+      float lse[2][4], dsm[2][4];
 #pragma unroll
       for (int r = 0; r < 2; ++r) {
-        f32x4 sc, dp = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-        for (int e = 0; e < 4; ++e) sc[e] = (yz[r] && ((xm[xb] >> e) & 1)) ? 0.f : -INFINITY;
 #pragma unroll
         for (int ks = 0; ks < KS; ++ks) {
-          const bf16x8 qa = *(const bf16x8*)(st + r * RB + aoff[xb][ks]);
-          const bf16x8 da = *(const bf16x8*)(st + (2 + r) * RB + aoff[xb][ks]);
-          sc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(qa, kreg[ks], sc, 0, 0, 0);
-          dp = __builtin_amdgcn_mfma_f32_16x16x32_bf16(da, vreg[ks], dp, 0, 0, 0);
+          qa[r][ks] = *(const bf16x8*)(st + r * RB + aoff[xb][ks]);
+          da[r][ks] = *(const bf16x8*)(st + (2 + r) * RB + aoff[xb][ks]);
         }
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
           const int cl = bs[xb] + 4 * g + e;
-          const float lse = sl[r * SW + cl], dsm = sl[(2 + r) * SW + cl];
-          pv[r][e] = __builtin_amdgcn_exp2f(sc[e] - lse);
-          sv[r][e] = pv[r][e] * (dp[e] - dsm);
+          lse[r][e] = sl[r * SW + cl];
+          dsm[r][e] = sl[(2 + r) * SW + cl];
         }
       }
-      const bf16x8 pbp = __builtin_bit_cast(
-          bf16x8, ((u32x4){pack_bf16x2(pv[0][0], pv[0][1]), pack_bf16x2(pv[0][2], pv[0][3]),
-                           pack_bf16x2(pv[1][0], pv[1][1]), pack_bf16x2(pv[1][2], pv[1][3])}));
-      const bf16x8 pbs = __builtin_bit_cast(
-          bf16x8, ((u32x4){pack_bf16x2(sv[0][0], sv[0][1]), pack_bf16x2(sv[0][2], sv[0][3]),
-                           pack_bf16x2(sv[1][0], sv[1][1]), pack_bf16x2(sv[1][2], sv[1][3])}));
+      bf16x8 pbp[NT], pbs[NT];
+#pragma unroll
+      for (int tt = 0; tt < NT; ++tt) {
+        if (!act[tt]) continue;
+        float pv[2][4], sv[2][4];
+#pragma unroll
+        for (int r = 0; r < 2; ++r) {
+          f32x4 sc, dp = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+          for (int e = 0; e < 4; ++e) sc[e] = (yz[tt][r] && ((xm[xb] >> e) & 1)) ? 0.f : -INFINITY;
+#pragma unroll
+          for (int ks = 0; ks < KS; ++ks) {
+            sc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(qa[r][ks], kreg[tt][ks], sc, 0, 0, 0);
+            dp = __builtin_amdgcn_mfma_f32_16x16x32_bf16(da[r][ks], vreg[tt][ks], dp, 0, 0, 0);
+          }
+#pragma unroll
+          for (int e = 0; e < 4; ++e) {
+            pv[r][e] = __builtin_amdgcn_exp2f(sc[e] - lse[r][e]);
+            sv[r][e] = pv[r][e] * (dp[e] - dsm[r][e]);
+          }
+        }
+        pbp[tt] = __builtin_bit_cast(
+            bf16x8, ((u32x4){pack_bf16x2(pv[0][0], pv[0][1]), pack_bf16x2(pv[0][2], pv[0][3]),
+                             pack_bf16x2(pv[1][0], pv[1][1]), pack_bf16x2(pv[1][2], pv[1][3])}));
+        pbs[tt] = __builtin_bit_cast(
+            bf16x8, ((u32x4){pack_bf16x2(sv[0][0], sv[0][1]), pack_bf16x2(sv[0][2], sv[0][3]),
+                             pack_bf16x2(sv[1][0], sv[1][1]), pack_bf16x2(sv[1][2], sv[1][3])}));
+      }
 #pragma unroll
       for (int db = 0; db < DB; ++db) {
         const bf16x4 q0 = __builtin_amdgcn_ds_read_tr16_b64_v4bf16(LDS_PTR(bf16x4, st + toff[xb][db]));
         const bf16x4 q1 = __builtin_amdgcn_ds_read_tr16_b64_v4bf16(LDS_PTR(bf16x4, st + RB + toff[xb][db]));
         const bf16x4 o0 = __builtin_amdgcn_ds_read_tr16_b64_v4bf16(LDS_PTR(bf16x4, st + 2 * RB + toff[xb][db]));
         const bf16x4 o1 = __builtin_amdgcn_ds_read_tr16_b64_v4bf16(LDS_PTR(bf16x4, st + 3 * RB + toff[xb][db]));
-        dk[db] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_shufflevector(q0, q1, 0, 1, 2, 3, 4, 5, 6, 7), pbs,
-                                                         dk[db], 0, 0, 0);
-        dv[db] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_shufflevector(o0, o1, 0, 1, 2, 3, 4, 5, 6, 7), pbp,
-                                                         dv[db], 0, 0, 0);
+        const bf16x8 qt = __builtin_shufflevector(q0, q1, 0, 1, 2, 3, 4, 5, 6, 7);
+        const bf16x8 ot = __builtin_shufflevector(o0, o1, 0, 1, 2, 3, 4, 5, 6, 7);
+#pragma unroll
+        for (int tt = 0; tt < NT; ++tt) {
+          if (!act[tt]) continue;
+          dk[tt][db] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(qt, pbs[tt], dk[tt][db], 0, 0, 0);
+          dv[tt][db] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ot, pbp[tt], dv[tt][db], 0, 0, 0);
+        }
       }
     }
   }
   wait_vmcnt(0);  // the ring's trailing (empty) stages
-  if (t.valid) {
-    char* kp = (char*)p.dk + 2 * (kj * D) + 8 * g;
-    char* vp = (char*)p.dv + 2 * (kj * D) + 8 * g;
+#pragma unroll
+  for (int tt = 0; tt < NT; ++tt) {
+    if (!t[tt].valid) continue;
+    char* kp = (char*)p.dk + 2 * (kj[tt] * D) + 8 * g;
+    char* vp = (char*)p.dv + 2 * (kj[tt] * D) + 8 * g;
 #pragma unroll
     for (int db = 0; db < DB; ++db) {
-      *(u32x2*)(kp + 32 * db) = (u32x2){pack_bf16x2(dk[db][0] * p.scale, dk[db][1] * p.scale),
-                                        pack_bf16x2(dk[db][2] * p.scale, dk[db][3] * p.scale)};
-      *(u32x2*)(vp + 32 * db) = (u32x2){pack_bf16x2(dv[db][0], dv[db][1]), pack_bf16x2(dv[db][2], dv[db][3])};
+      *(u32x2*)(kp + 32 * db) = (u32x2){pack_bf16x2(dk[tt][db][0] * p.scale, dk[tt][db][1] * p.scale),
+                                        pack_bf16x2(dk[tt][db][2] * p.scale, dk[tt][db][3] * p.scale)};
+      *(u32x2*)(vp + 32 * db) =
+          (u32x2){pack_bf16x2(dv[tt][db][0], dv[tt][db][1]), pack_bf16x2(dv[tt][db][2], dv[tt][db][3])};
     }
   }
 #endif
@@ -572,8 +620,9 @@ __global__ __launch_bounds__(256, 3) void na3d_bwd_dkv_lds_kernel(Na3dBwdParams 
 
 // ---------------------------------------------------------------------------
 // LDS-staged dq for bf16, head_dim 64, dilation 1, kx <= 13: the forward's
-// walk for the workgroup's four 4 x 4 query tiles (16 query columns of one
-// (b, h, z), 4 rows).  The union of their windows is walked two key (z, y)
+// walk for the workgroup's 4 x 4 query tiles (four waves along x, NT per wave
+// along y: 16 query columns of one (b, h, z), 4 NT rows).  The union of their
+// windows is walked two key (z, y)
 // rows at a time, each row's K and V over the workgroup's window columns (at
 // most 16 + kx - 1 <= 28, staged as 32) copied into LDS once per workgroup
 // (`buffer_load ... lds`, a ring of three stages).  A wave takes its tile's
@@ -581,7 +630,8 @@ __global__ __launch_bounds__(256, 3) void na3d_bwd_dkv_lds_kernel(Na3dBwdParams 
 // V dO^T with Q (pre-scaled by scale * log2 e) and dO as the register operand,
 // the membership mask as the C operand of S^T, P^T = 2^(S^T - lse),
 // dS^T = P^T (dP^T - D); then dQ^T += K^T dS^T over the row pair with K^T
-// read transposed (ds_read_b64_tr_b16).
+// read transposed (ds_read_b64_tr_b16).  A tile whose queries see neither
+// staged row skips the stage.
 // ---------------------------------------------------------------------------
 namespace dql {
 constexpr int SW = 32;          // staged key columns per row
@@ -590,7 +640,8 @@ constexpr int NBUF = 3;
 constexpr int STAGE = 4 * RB;    // K r0, K r1, V r0, V r1
 }  // namespace dql
 
-__global__ __launch_bounds__(256, 3) void na3d_bwd_dq_lds_kernel(Na3dBwdParams p) {
+template <int NT>
+__global__ __launch_bounds__(256, NT == 1 ? 3 : 2) void na3d_bwd_dq_lds_kernel(Na3dBwdParams p, int nyt) {
 #if defined(__HIP_DEVICE_COMPILE__)
   using namespace dql;
   constexpr int D = 64, KS = 2, DB = 4;
@@ -598,28 +649,39 @@ __global__ __launch_bounds__(256, 3) void na3d_bwd_dq_lds_kernel(Na3dBwdParams p
   const int tid = (int)threadIdx.x;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int lane = tid & 63, n16 = lane & 15, g = lane >> 4;
-  const Tok t = token_at(p, n16);  // MFMA column n16 = the lane's query
+  Tok t[NT];  // MFMA column n16 of tile tt = the lane's query in rows 4 tt .. 4 tt + 3 of the workgroup
+#pragma unroll
+  for (int tt = 0; tt < NT; ++tt) t[tt] = token_rows(p, nyt, 4 * NT, 4 * tt, n16);
   const float c2 = p.scale * 1.4426950408889634f;
   const int kz = p.ker[0], ky = p.ker[1], kx = p.ker[2];
   const uint32_t lds_base = (uint32_t)(uintptr_t)(__attribute__((address_space(3))) char*)lds;
 
-  const int64_t qi = tok_index(p, t.b, t.z, t.y, t.x, t.h);
-  bf16x8 qreg[KS], doreg[KS];
+  int64_t qi[NT];
+  bf16x8 qreg[NT][KS], doreg[NT][KS];
+  float lse[NT], dsum[NT];
+  int sy[NT];
 #pragma unroll
-  for (int ks = 0; ks < KS; ++ks) {
-    qreg[ks] = *(const bf16x8*)((const bf16*)p.q + qi * D + 8 * (4 * ks + g));
-    doreg[ks] = *(const bf16x8*)((const bf16*)p.dout + qi * D + 8 * (4 * ks + g));
+  for (int tt = 0; tt < NT; ++tt) {
+    qi[tt] = tok_index(p, t[tt].b, t[tt].z, t[tt].y, t[tt].x, t[tt].h);
 #pragma unroll
-    for (int e = 0; e < 8; ++e) qreg[ks][e] = (bf16)((float)qreg[ks][e] * c2);
+    for (int ks = 0; ks < KS; ++ks) {
+      qreg[tt][ks] = *(const bf16x8*)((const bf16*)p.q + qi[tt] * D + 8 * (4 * ks + g));
+      doreg[tt][ks] = *(const bf16x8*)((const bf16*)p.dout + qi[tt] * D + 8 * (4 * ks + g));
+#pragma unroll
+      for (int e = 0; e < 8; ++e) qreg[tt][ks][e] = (bf16)((float)qreg[tt][ks][e] * c2);
+    }
+    lse[tt] = p.lse[qi[tt]];
+    dsum[tt] = p.dsum[qi[tt]];
+    sy[tt] = win_start(t[tt].y, p.Y, ky);
   }
-  const float lse = p.lse[qi], dsum = p.dsum[qi];
+  const Tok& t0 = t[0];  // b, h, z and the query column are the same for every tile
 
   // ---- x: the workgroup's key columns [SX0, SX0 + SW) and this wave's block ----
   const int QX0 = ((int)blockIdx.x % p.nxt) * 16;
   const int SX0 = win_start(min(QX0, p.X - 1), p.X, kx);
   const int qx0 = min(QX0 + wave * 4, p.X - 1);
   const int bs = win_start(qx0, p.X, kx) - SX0;  // <= 12
-  const int sx = win_start(t.x, p.X, kx);
+  const int sx = win_start(t0.x, p.X, kx);
   uint32_t xm = 0;  // bit e: key column bs + 4g + e is in the lane's query window
 #pragma unroll
   for (int e = 0; e < 4; ++e) {
@@ -638,13 +700,12 @@ __global__ __launch_bounds__(256, 3) void na3d_bwd_dq_lds_kernel(Na3dBwdParams p
   }
 
   // ---- y, z: the key rows of the workgroup's queries ----
-  const int ty0 = ((int)(blockIdx.x / p.nxt) % p.nyt) * 4;
+  const int ty0 = ((int)(blockIdx.x / p.nxt) % nyt) * 4 * NT;
   const int KY0 = win_start(min(ty0, p.Y - 1), p.Y, ky);
-  const int NY = win_start(min(ty0 + 3, p.Y - 1), p.Y, ky) + ky - KY0;
-  const int KZ0 = win_start(t.z, p.Z, kz);
+  const int NY = win_start(min(ty0 + 4 * NT - 1, p.Y - 1), p.Y, ky) + ky - KY0;
+  const int KZ0 = win_start(t0.z, p.Z, kz);
   const int nrows = kz * NY;
   const int nst = (nrows + 1) / 2;
-  const int sy = win_start(t.y, p.Y, ky);
 
   // ---- copies: wave w stages key columns 8w .. 8w+7 of both rows of K and V ----
   const int64_t rowb = (int64_t)p.H * D * 2;
@@ -656,26 +717,28 @@ __global__ __launch_bounds__(256, 3) void na3d_bwd_dq_lds_kernel(Na3dBwdParams p
     const int chunk = (lane & 7) ^ (cl & 7);
     voff = kc < p.X ? (uint32_t)(kc * rowb + 16 * chunk) : OOB;
   }
-  const char* kbase = (const char*)p.k + 2 * (int64_t)t.h * D;
-  const char* vbase = (const char*)p.v + 2 * (int64_t)t.h * D;
+  const char* kbase = (const char*)p.k + 2 * (int64_t)t0.h * D;
+  const char* vbase = (const char*)p.v + 2 * (int64_t)t0.h * D;
   auto row_tok = [&](int sr) {
     const int zk = KZ0 + sr / NY, yk = KY0 + sr % NY;
-    return (((int64_t)t.b * p.Z + zk) * p.Y + yk) * p.X * p.H;
+    return (((int64_t)t0.b * p.Z + zk) * p.Y + yk) * p.X * p.H;
   };
   auto issue = [&](int s) {
     const uint32_t st = lds_base + (uint32_t)((s % NBUF) * STAGE);
     const int r0 = 2 * s, r1 = 2 * s + 1;
     const bool l0 = r0 < nrows, l1 = r1 < nrows;
-    const int64_t t0 = l0 ? row_tok(r0) : 0, t1 = l1 ? row_tok(r1) : 0;
-    dma_row16(make_rsrc(kbase + t0 * D * 2, l0 ? rec : 0u), st + 0 * RB + wave * 1024, voff);
-    dma_row16(make_rsrc(kbase + t1 * D * 2, l1 ? rec : 0u), st + 1 * RB + wave * 1024, voff);
-    dma_row16(make_rsrc(vbase + t0 * D * 2, l0 ? rec : 0u), st + 2 * RB + wave * 1024, voff);
-    dma_row16(make_rsrc(vbase + t1 * D * 2, l1 ? rec : 0u), st + 3 * RB + wave * 1024, voff);
+    const int64_t w0 = l0 ? row_tok(r0) : 0, w1 = l1 ? row_tok(r1) : 0;
+    dma_row16(make_rsrc(kbase + w0 * D * 2, l0 ? rec : 0u), st + 0 * RB + wave * 1024, voff);
+    dma_row16(make_rsrc(kbase + w1 * D * 2, l1 ? rec : 0u), st + 1 * RB + wave * 1024, voff);
+    dma_row16(make_rsrc(vbase + w0 * D * 2, l0 ? rec : 0u), st + 2 * RB + wave * 1024, voff);
+    dma_row16(make_rsrc(vbase + w1 * D * 2, l1 ? rec : 0u), st + 3 * RB + wave * 1024, voff);
   };
 
-  f32x4 acc[DB];
+  f32x4 acc[NT][DB];
 #pragma unroll
-  for (int db = 0; db < DB; ++db) acc[db] = (f32x4){0.f, 0.f, 0.f, 0.f};
+  for (int tt = 0; tt < NT; ++tt)
+#pragma unroll
+    for (int db = 0; db < DB; ++db) acc[tt][db] = (f32x4){0.f, 0.f, 0.f, 0.f};
 
 #pragma unroll
   for (int s = 0; s < NBUF - 1; ++s) issue(s);
@@ -684,43 +747,67 @@ __global__ __launch_bounds__(256, 3) void na3d_bwd_dq_lds_kernel(Na3dBwdParams p
     lds_barrier();
     issue(s + NBUF - 1);
     const char* st = lds + (s % NBUF) * STAGE;
-    float ds[2][4];
+    // y membership of the two key rows in each tile's query windows (z: every staged
+    // plane is in the window); a tile with neither row in any window skips the stage
+    bool yin[NT][2], act[NT];
 #pragma unroll
     for (int r = 0; r < 2; ++r) {
       const int sr = 2 * s + r;
       const int yk = KY0 + sr % NY;
-      const bool yin = sr < nrows && yk >= sy && yk < sy + ky;  // z: every staged plane is in the window
-      f32x4 sc, dp = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-      for (int e = 0; e < 4; ++e) sc[e] = (yin && ((xm >> e) & 1)) ? 0.f : -INFINITY;
+      for (int tt = 0; tt < NT; ++tt) yin[tt][r] = sr < nrows && yk >= sy[tt] && yk < sy[tt] + ky;
+    }
+#pragma unroll
+    for (int tt = 0; tt < NT; ++tt) act[tt] = __builtin_amdgcn_ballot_w64(yin[tt][0] || yin[tt][1]) != 0;
+    bf16x8 ka[2][KS], va[2][KS];
+#pragma unroll
+    for (int r = 0; r < 2; ++r)
 #pragma unroll
       for (int ks = 0; ks < KS; ++ks) {
-        const bf16x8 ka = *(const bf16x8*)(st + r * RB + aoff[ks]);
-        const bf16x8 va = *(const bf16x8*)(st + (2 + r) * RB + aoff[ks]);
-        sc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ka, qreg[ks], sc, 0, 0, 0);
-        dp = __builtin_amdgcn_mfma_f32_16x16x32_bf16(va, doreg[ks], dp, 0, 0, 0);
+        ka[r][ks] = *(const bf16x8*)(st + r * RB + aoff[ks]);
+        va[r][ks] = *(const bf16x8*)(st + (2 + r) * RB + aoff[ks]);
       }
+    bf16x8 pb[NT];
 #pragma unroll
-      for (int e = 0; e < 4; ++e) ds[r][e] = __builtin_amdgcn_exp2f(sc[e] - lse) * (dp[e] - dsum);
+    for (int tt = 0; tt < NT; ++tt) {
+      if (!act[tt]) continue;
+      float ds[2][4];
+#pragma unroll
+      for (int r = 0; r < 2; ++r) {
+        f32x4 sc, dp = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int e = 0; e < 4; ++e) sc[e] = (yin[tt][r] && ((xm >> e) & 1)) ? 0.f : -INFINITY;
+#pragma unroll
+        for (int ks = 0; ks < KS; ++ks) {
+          sc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ka[r][ks], qreg[tt][ks], sc, 0, 0, 0);
+          dp = __builtin_amdgcn_mfma_f32_16x16x32_bf16(va[r][ks], doreg[tt][ks], dp, 0, 0, 0);
+        }
+#pragma unroll
+        for (int e = 0; e < 4; ++e) ds[r][e] = __builtin_amdgcn_exp2f(sc[e] - lse[tt]) * (dp[e] - dsum[tt]);
+      }
+      pb[tt] = __builtin_bit_cast(
+          bf16x8, ((u32x4){pack_bf16x2(ds[0][0], ds[0][1]), pack_bf16x2(ds[0][2], ds[0][3]),
+                           pack_bf16x2(ds[1][0], ds[1][1]), pack_bf16x2(ds[1][2], ds[1][3])}));
     }
-    const bf16x8 pb = __builtin_bit_cast(
-        bf16x8, ((u32x4){pack_bf16x2(ds[0][0], ds[0][1]), pack_bf16x2(ds[0][2], ds[0][3]),
-                         pack_bf16x2(ds[1][0], ds[1][1]), pack_bf16x2(ds[1][2], ds[1][3])}));
 #pragma unroll
     for (int db = 0; db < DB; ++db) {
       const bf16x4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4bf16(LDS_PTR(bf16x4, st + toff[db]));
       const bf16x4 hi = __builtin_amdgcn_ds_read_tr16_b64_v4bf16(LDS_PTR(bf16x4, st + RB + toff[db]));
-      acc[db] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7), pb,
-                                                        acc[db], 0, 0, 0);
+      const bf16x8 kt = __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7);
+#pragma unroll
+      for (int tt = 0; tt < NT; ++tt)
+        if (act[tt]) acc[tt][db] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kt, pb[tt], acc[tt][db], 0, 0, 0);
     }
   }
   wait_vmcnt(0);  // the ring's trailing (empty) stages
-  if (t.valid) {
-    char* op = (char*)p.dq + 2 * (qi * D) + 8 * g;
+#pragma unroll
+  for (int tt = 0; tt < NT; ++tt) {
+    if (!t[tt].valid) continue;
+    char* op = (char*)p.dq + 2 * (qi[tt] * D) + 8 * g;
 #pragma unroll
     for (int db = 0; db < DB; ++db) {
-      const u32x2 w = {pack_bf16x2(acc[db][0] * p.scale, acc[db][1] * p.scale),
-                       pack_bf16x2(acc[db][2] * p.scale, acc[db][3] * p.scale)};
+      const u32x2 w = {pack_bf16x2(acc[tt][db][0] * p.scale, acc[tt][db][1] * p.scale),
+                       pack_bf16x2(acc[tt][db][2] * p.scale, acc[tt][db][3] * p.scale)};
       *(u32x2*)(op + 32 * db) = w;
     }
   }
@@ -773,12 +860,16 @@ static int launch_bwd(const Na3dBwdParams& p, hipStream_t st) {
   } else {
     hipLaunchKernelGGL((na3d_bwd_prep_kernel<T, D>), grid, block, 0, st, p);
   }
+  // LDS kernels: workgroups of 4 * NT rows
+  constexpr int NT = NA3D_BWD_NT;
+  const int nyt_lds = (p.Y + 4 * NT - 1) / (4 * NT);
+  const dim3 grid_lds((unsigned)((int64_t)p.B * p.H * p.Z * nyt_lds * p.nxt));
   if (sizeof(T) == 2 && D == 64 && mfma_ok(p))
-    hipLaunchKernelGGL(na3d_bwd_dq_lds_kernel, grid, block, 0, st, p);
+    hipLaunchKernelGGL(na3d_bwd_dq_lds_kernel<NT>, grid_lds, block, 0, st, p, nyt_lds);
   else
     hipLaunchKernelGGL((na3d_bwd_dq_kernel<T, D>), grid, block, 0, st, p);
   if (sizeof(T) == 2 && D == 64 && mfma_ok(p))
-    hipLaunchKernelGGL(na3d_bwd_dkv_lds_kernel, grid, block, 0, st, p);
+    hipLaunchKernelGGL(na3d_bwd_dkv_lds_kernel<NT>, grid_lds, block, 0, st, p, nyt_lds);
   else
     hipLaunchKernelGGL((na3d_bwd_dkv_kernel<T, D>), grid, block, 0, st, p);
   return check_launch("na3d_bwd kernels");
