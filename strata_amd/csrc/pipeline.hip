@@ -37,6 +37,14 @@ struct PipeParams {
 
 constexpr int PIPE_LDS = 48 * 1024;
 constexpr int PIPE_THREADS = 256;
+constexpr int PIPE_U = 4;  // state-row passes per wave whose loads are in flight together
+
+// Lanes a state-row run of `run` floats takes: run rounded up to a power of two (<= 64).
+__device__ __forceinline__ int run_lanes(int run) {
+  int l = 1;
+  while (l < run) l <<= 1;
+  return l;
+}
 
 // Element index of (c, dz, dy, dx) within a token.
 __device__ __forceinline__ int token_elem(const PipeParams& p, int order, int c, int dz, int dy, int dx) {
@@ -88,20 +96,37 @@ __global__ __launch_bounds__(PIPE_THREADS) void state_patchify_kernel(PipeParams
   const int x0 = tx0 * p.px;
   const int tid = (int)threadIdx.x;
 
-  // state rows (c, dz, dy) -> tile[token][element], normalised, in bf16: a
-  // wave per row, a lane per x (run <= 64)
+  // state rows (c, dz, dy) -> tile[token][element], normalised, in bf16.  A
+  // row's run takes RP lanes (run rounded up to a power of two), so a wave pass
+  // covers 64 / RP rows, and a wave issues PIPE_U passes' loads before using them.
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6), lane = tid & 63;
-  const int t = lane / p.px, dx = lane - t * p.px;
-  for (int r = wave; r < rows; r += PIPE_THREADS / 64) {
-    const int dy = r % p.py, dz = (r / p.py) % p.pz, c = r / (p.py * p.pz);
-    if (lane < run) {
-      const int64_t src = (((int64_t)b * p.C + c) * p.Z + (tz * p.pz + dz)) * (int64_t)p.Y * p.X +
-                          (int64_t)(ty * p.py + dy) * p.X + x0 + lane;
-      const float v = p.state[src];
-      float n = v;
-      if (p.mean) n = (v - p.mean[c]) / p.std[c];
-      if (!__builtin_isfinite(v)) n = 0.f;
-      tile[t * K + token_elem(p, 0, c, dz, dy, dx)] = (bf16)n;
+  const int RP = run_lanes(run), sub = lane / RP, xi = lane - sub * RP;
+  const int t = xi / p.px, dx = xi - t * p.px;
+  const int step = (PIPE_THREADS / 64) * (64 / RP);  // rows per pass of the workgroup
+  for (int r0 = wave * (64 / RP) + sub; r0 < rows + step * (PIPE_U - 1); r0 += step * PIPE_U) {
+    float v[PIPE_U];
+    int cc[PIPE_U], el[PIPE_U];
+#pragma unroll
+    for (int u = 0; u < PIPE_U; ++u) {
+      const int r = r0 + u * step;
+      v[u] = 0.f;
+      cc[u] = -1;
+      if (r < rows && xi < run) {
+        const int dy = r % p.py, dz = (r / p.py) % p.pz, c = r / (p.py * p.pz);
+        cc[u] = c;
+        el[u] = t * K + token_elem(p, 0, c, dz, dy, dx);
+        v[u] = p.state[(((int64_t)b * p.C + c) * p.Z + (tz * p.pz + dz)) * (int64_t)p.Y * p.X +
+                       (int64_t)(ty * p.py + dy) * p.X + x0 + xi];
+      }
+    }
+#pragma unroll
+    for (int u = 0; u < PIPE_U; ++u) {
+      if (cc[u] >= 0) {
+        float n = v[u];
+        if (p.mean) n = (v[u] - p.mean[cc[u]]) / p.std[cc[u]];
+        if (!__builtin_isfinite(v[u])) n = 0.f;
+        tile[el[u]] = (bf16)n;
+      }
     }
   }
   __syncthreads();
@@ -133,27 +158,52 @@ __global__ __launch_bounds__(PIPE_THREADS) void state_update_kernel(PipeParams p
   bf16* src = (bf16*)p.tokens + ((((int64_t)b * p.Tz + tz) * p.Ty + ty) * p.Tx + tx0) * K;
   copy_run<true>(p, tile, src, nt * K, tid);
   __syncthreads();
-  // tile -> state rows (c, dz, dy): a wave per row, a lane per x (run <= 64)
+  // tile -> state rows (c, dz, dy), as state_patchify: RP lanes per row, 64 / RP
+  // rows per wave pass, PIPE_U passes' state loads issued before any store
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6), lane = tid & 63;
-  const int t = lane / p.px, dx = lane - t * p.px;
-  for (int r = wave; r < rows; r += PIPE_THREADS / 64) {
-    const int dy = r % p.py, dz = (r / p.py) % p.pz, c = r / (p.py * p.pz);
-    if (lane >= run) continue;
-    const int xi = lane;
-    const float pr = (float)tile[t * K + token_elem(p, p.order, c, dz, dy, dx)];
-    // denormalise in fp32 (a multiply, then an add, each rounded: the pragma
-    // above keeps them from contracting to an fma), round to bf16
-    float d = pr;
-    if (p.mean) d = pr * p.std[c] + p.mean[c];
-    d = (float)(bf16)d;
-    const int64_t sp = (int64_t)(tz * p.pz + dz) * p.Y * p.X + (int64_t)(ty * p.py + dy) * p.X + x0 + xi;
-    const int sc = p.src ? p.src[c] : c;  // entries outside [0, Cin) add nothing
-    if (sc >= 0 && sc < p.Cin) d += p.state[((int64_t)b * p.Cin + sc) * p.Z * (int64_t)p.Y * p.X + sp];
-    if (p.clamp) {
-      const float lo = p.clamp[c];
-      if (!__builtin_isnan(lo)) d = d < lo ? lo : d;  // clamp(min=lo): NaN stays NaN
+  const int RP = run_lanes(run), sub = lane / RP, xi = lane - sub * RP;
+  const int t = xi / p.px, dx = xi - t * p.px;
+  const int step = (PIPE_THREADS / 64) * (64 / RP);
+  const int64_t plane = (int64_t)p.Z * p.Y * p.X;
+  for (int r0 = wave * (64 / RP) + sub; r0 < rows + step * (PIPE_U - 1); r0 += step * PIPE_U) {
+    float prev[PIPE_U];
+    int cc[PIPE_U], el[PIPE_U];
+    bool add[PIPE_U];
+    int64_t sp[PIPE_U];
+#pragma unroll
+    for (int u = 0; u < PIPE_U; ++u) {
+      const int r = r0 + u * step;
+      prev[u] = 0.f;
+      cc[u] = -1;
+      add[u] = false;
+      if (r < rows && xi < run) {
+        const int dy = r % p.py, dz = (r / p.py) % p.pz, c = r / (p.py * p.pz);
+        cc[u] = c;
+        el[u] = t * K + token_elem(p, p.order, c, dz, dy, dx);
+        sp[u] = (int64_t)(tz * p.pz + dz) * p.Y * p.X + (int64_t)(ty * p.py + dy) * p.X + x0 + xi;
+        const int sc = p.src ? p.src[c] : c;  // entries outside [0, Cin) add nothing
+        add[u] = sc >= 0 && sc < p.Cin;
+        if (add[u]) prev[u] = p.state[((int64_t)b * p.Cin + sc) * plane + sp[u]];
+      }
     }
-    p.next[((int64_t)b * p.C + c) * p.Z * (int64_t)p.Y * p.X + sp] = d;
+#pragma unroll
+    for (int u = 0; u < PIPE_U; ++u) {
+      const int c = cc[u];
+      if (c >= 0) {
+        const float pr = (float)tile[el[u]];
+        // denormalise in fp32 (a multiply, then an add, each rounded: the pragma
+        // above keeps them from contracting to an fma), round to bf16
+        float d = pr;
+        if (p.mean) d = pr * p.std[c] + p.mean[c];
+        d = (float)(bf16)d;
+        if (add[u]) d += prev[u];
+        if (p.clamp) {
+          const float lo = p.clamp[c];
+          if (!__builtin_isnan(lo)) d = d < lo ? lo : d;  // clamp(min=lo): NaN stays NaN
+        }
+        p.next[((int64_t)b * p.C + c) * plane + sp[u]] = d;
+      }
+    }
   }
 }
 
