@@ -137,6 +137,12 @@ def test_gemm_and_layernorm_validation(lib):
     r.qk_norm, r.head_dim, r.qkv_row_stride = 1, 48, 288  # D/16 = 3 is not a power of two
     assert lib.strata_hip_rope_qkv_pack(ctypes.byref(r), None) == _lib.EINVAL
     assert "power of two" in lib.strata_hip_last_error().decode()
+    r.v = None  # v may be NULL (only q and k written): validation goes on to the next check
+    assert lib.strata_hip_rope_qkv_pack(ctypes.byref(r), None) == _lib.EINVAL
+    assert "power of two" in lib.strata_hip_last_error().decode()
+    r.q = None
+    assert lib.strata_hip_rope_qkv_pack(ctypes.byref(r), None) == _lib.EINVAL
+    assert "null pointer" in lib.strata_hip_last_error().decode()
     g.k = g.ldx = g.ldw = 16
     g.res_op = 5
     assert lib.strata_hip_gemm_bias_act(ctypes.byref(g), None) == _lib.EINVAL
