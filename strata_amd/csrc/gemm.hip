@@ -330,8 +330,15 @@ __device__ __forceinline__ void gemm_dma_body(const GemmParams& p) {
     const int xcd = t & 7, local = t >> 3, q = ntiles >> 3, rem = ntiles & 7;
     return xcd < rem ? xcd * (q + 1) + local : rem * (q + 1) + (xcd - rem) * q + local;
   }();
-  const int tn = wg % p.nt;
-  const int tm = wg / p.nt;
+  // Tiles in groups of GRP row panels x every column panel, row panel fastest:
+  // an XCD's 32 concurrent tiles share 4 panels of x and 8 of w (measured at
+  // the block's shapes with the stores below: 1-2% faster than one row panel
+  // x all columns).
+  constexpr int GRP = 4;
+  const int gi = wg / (GRP * p.nt), li = wg % (GRP * p.nt);
+  const int gmn = min(GRP, p.mt - gi * GRP);  // row panels in this (possibly last) group
+  const int tm = gi * GRP + li % gmn;
+  const int tn = li / gmn;
   const int64_t m0 = (int64_t)tm * BM;
   const int64_t n0 = (int64_t)tn * BN;
 
@@ -499,7 +506,10 @@ __device__ __forceinline__ void gemm_dma_body(const GemmParams& p) {
                            combine_t<RES>(bf16_hi(w4[e]), bf16_hi(r4[it][e])));
     }
     if (full || (gm < p.M && gn + 8 <= p.N)) {
-      *(u32x4*)(p.out + gm * p.ldo + gn) = o;
+      // Streaming store: the output is not read again here, and a tile-round's
+      // outputs (32 MB over the grid) would otherwise push the x and w panels
+      // out of L2 (M = 131072, N = 4096, K = 1024 with GELU: 1.32 -> 1.27 ms).
+      __builtin_nontemporal_store(o, (u32x4*)(p.out + gm * p.ldo + gn));
     } else if (gm < p.M && gn < p.N) {
       for (int e = 0; e < 8 && gn + e < p.N; ++e) {  // ragged last columns
         const uint32_t wd = w4[e >> 1];
