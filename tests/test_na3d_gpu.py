@@ -286,6 +286,12 @@ SMALL_CASES = [
     ((1, 3, 16, 16, 2, 64), (3, 7, 9), (1, 1, 1), (0, 2, 0), (3, 12, 16)),
     ((1, 4, 9, 16, 1, 64), (3, 7, 7), (1, 1, 1), (0, 0, 0), None),
     ((1, 3, 40, 36, 3, 64), (3, 9, 7), (1, 1, 1), (0, 0, 0), None),
+    # query box clear of both y edges: the launch holds strips only
+    ((2, 4, 40, 32, 2, 64), (3, 7, 7), (1, 1, 1), (1, 5, 3), (3, 25, 20)),
+    # only the bottom edge is clamped (two rows of the general body)
+    ((1, 4, 30, 20, 2, 64), (3, 5, 5), (1, 1, 1), (0, 10, 0), (4, 20, 20)),
+    # a single unclamped row: no regular strip, the general kernel alone
+    ((1, 3, 7, 16, 1, 64), (3, 7, 7), (1, 1, 1), (0, 0, 0), None),
 ]
 
 
