@@ -387,20 +387,42 @@ __device__ __forceinline__ void gemm_dma_body(const GemmParams& p) {
     for (int kk = 0; kk < 2; ++kk) boff[j][kk] = row * ROWB + gswz<CH>(2 * kk + hi, row) * 16;
   }
 
-  f32x16 acc[FN][FM];
+  // The bias enters as the C operand of each accumulator's first MFMA (no
+  // zero fill, no add in the epilogue): acc[i][j][4q + e] holds column
+  // 32i + 8q + 4hi + e of the wave tile.
+  const int64_t gn0 = n0 + wn * WTN, gm0 = m0 + wm * WTM;
+  const bool full = m0 + BM <= p.M && n0 + BN <= p.N;  // uniform
+  f32x16 binit[FN];
 #pragma unroll
   for (int i = 0; i < FN; ++i)
 #pragma unroll
-    for (int j = 0; j < FM; ++j)
+    for (int q = 0; q < 4; ++q) {
+      const int64_t gn = gn0 + 32 * i + 8 * q + 4 * hi;
+      float bv[4] = {0.f, 0.f, 0.f, 0.f};
+      if (p.bias) {
+        if (full || gn + 4 <= p.N) {
+          const u32x2 w2 = *(const u32x2*)(p.bias + gn);
+          bv[0] = bf16_lo(w2[0]);
+          bv[1] = bf16_hi(w2[0]);
+          bv[2] = bf16_lo(w2[1]);
+          bv[3] = bf16_hi(w2[1]);
+        } else {
+          for (int e = 0; e < 4; ++e) bv[e] = gn + e < p.N ? (float)p.bias[gn + e] : 0.f;  // ragged last columns
+        }
+      }
 #pragma unroll
-      for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.f;
+      for (int e = 0; e < 4; ++e) binit[i][4 * q + e] = bv[e];
+    }
 
+  f32x16 acc[FN][FM];
   const int nk = (int)(p.K / BK);
 #pragma unroll
   for (int s = 0; s < PD; ++s)
     if (s < nk) issue(s, s);
   int rd = 0, wr = PD;  // ring slots read by this stage / filled by the next issue
-  for (int kt = 0; kt < nk; ++kt) {
+  // One K step; FIRST: the step that starts every accumulator from the bias.
+  auto kstep = [&](int kt, auto first) {
+    constexpr bool FIRST = decltype(first)::value;
     // stage kt has landed once at most (stages issued after it) x LPW DMAs are pending
     const int later = min(PD - 1, nk - 1 - kt);
     wait_vmcnt(later * LPW);
@@ -430,36 +452,28 @@ __device__ __forceinline__ void gemm_dma_body(const GemmParams& p) {
       for (int i = 0; i < FN; ++i)
 #pragma unroll
         for (int j = 0; j < FM; ++j)
-          acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(af[cb][i], bfr[cb][j], acc[i][j], 0, 0, 0);
+          acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(af[cb][i], bfr[cb][j],
+                                                             FIRST && kk == 0 ? binit[i] : acc[i][j], 0, 0, 0);
     }
     // Let the scheduler interleave the LDS reads of the next sub-step with
     // the MFMAs of the current one (measured 1-3% faster than the default
     // order at the block's shapes; explicit sched_group_barrier groups gave
     // the default order back).
     __builtin_amdgcn_iglp_opt(1);
-  }
+  };
+  kstep(0, std::true_type{});
+  for (int kt = 1; kt < nk; ++kt) kstep(kt, std::false_type{});
 
   // ---- epilogue through LDS ----
-  // Phase 1: bias + activation on the accumulators, bf16 into this wave's
+  // Phase 1: activation on the accumulators (the bias is already in them), bf16 into this wave's
   // WTM x WTN slab of LDS (rows of SRB bytes, 16-byte chunks swizzled by row).
   // Phase 2: each lane reads 16 contiguous bytes of a row, combines the
   // residual read the same way, and writes 16 bytes: CPR lanes cover a row.
   // Loads and stores share vmcnt on gfx9 (a load issued after a store waits
-  // for it), so every bias and residual load is issued before the first
-  // store: the bias before the barrier, the residual rows into registers the
-  // accumulators have freed.  Tiles inside the matrix skip every bounds check.
+  // for it), so every residual load is issued before the first store, into
+  // registers the accumulators have freed.  Tiles inside the matrix skip
+  // every bounds check.
   constexpr int SRB = WTN * 2, CPR = WTN / 8, RPI = 64 / CPR, NIT = WTM / RPI;
-  const int64_t gn0 = n0 + wn * WTN, gm0 = m0 + wm * WTM;
-  const bool full = m0 + BM <= p.M && n0 + BN <= p.N;  // uniform
-  u32x2 bw[FN][4];
-#pragma unroll
-  for (int i = 0; i < FN; ++i)
-#pragma unroll
-    for (int q = 0; q < 4; ++q) {
-      const int64_t gn = gn0 + 32 * i + 8 * q + 4 * hi;
-      bw[i][q] = (u32x2){0u, 0u};
-      if (p.bias && (full || gn + 4 <= p.N)) bw[i][q] = *(const u32x2*)(p.bias + gn);
-    }
   lds_barrier();  // every wave is done reading the last stage
   char* slab = lds + wave * (WTM * WTN * 2);
 #pragma unroll
@@ -467,16 +481,11 @@ __device__ __forceinline__ void gemm_dma_body(const GemmParams& p) {
 #pragma unroll
     for (int q = 0; q < 4; ++q) {
       const int nl = 32 * i + 8 * q + 4 * hi;  // local column of this lane's quad
-      float bv[4] = {bf16_lo(bw[i][q][0]), bf16_hi(bw[i][q][0]), bf16_lo(bw[i][q][1]), bf16_hi(bw[i][q][1])};
-      if (!full && p.bias && gn0 + nl + 4 > p.N) {  // ragged last columns
-        const int64_t gn = gn0 + nl;
-        for (int e = 0; e < 4; ++e) bv[e] = gn + e < p.N ? (float)p.bias[gn + e] : 0.f;
-      }
 #pragma unroll
       for (int j = 0; j < FM; ++j) {
         float v[4];
 #pragma unroll
-        for (int e = 0; e < 4; ++e) v[e] = act_t<ACT>(acc[i][j][4 * q + e] + bv[e]);
+        for (int e = 0; e < 4; ++e) v[e] = act_t<ACT>(acc[i][j][4 * q + e]);
         const int ml = 32 * j + l32;
         const u32x2 w2 = {pack_bf16x2(v[0], v[1]), pack_bf16x2(v[2], v[3])};
         *(u32x2*)(slab + ml * SRB + (((nl >> 3) ^ (ml & 7)) << 4) + 8 * hi) = w2;
