@@ -6,6 +6,7 @@
 #include <stdint.h>
 
 #include <string>
+#include <utility>
 
 #include "../../include/strata_hip.h"
 
@@ -119,6 +120,28 @@ __host__ __device__ __forceinline__ int sub_first(int o, int g, int d) { return 
 __host__ __device__ __forceinline__ int sub_end(int o, int e, int g, int d) {
   int hi = o + e;
   return hi <= g ? 0 : (hi - g + d - 1) / d;
+}
+
+// ---- launch order and compile-time loops --------------------------------
+// Linear workgroup id remapped so that consecutive tiles run on one XCD:
+// the dispatcher deals workgroups round-robin over the 8 XCDs, so XCD k gets
+// ids k, k+8, ...; map those to the k-th contiguous block of tiles.
+// (__builtin_amdgcn_workgroup_id_x keeps the id visibly uniform to the
+// compiler, unlike blockIdx.x's out-of-line library call.)
+__device__ __forceinline__ int xcd_tile_order(int n, int id) {
+  const int xcd = id & 7, local = id >> 3;
+  const int q = n >> 3, rem = n & 7;
+  return xcd < rem ? xcd * (q + 1) + local : rem * (q + 1) + (xcd - rem) * q + local;
+}
+
+template <typename F, int... I>
+__device__ __forceinline__ void static_for_impl(F&& f, std::integer_sequence<int, I...>) {
+  (f(std::integral_constant<int, I>{}), ...);
+}
+// f(integral_constant<int, i>) for i = 0 .. N-1, unrolled at compile time.
+template <int N, typename F>
+__device__ __forceinline__ void static_for(F&& f) {
+  static_for_impl(f, std::make_integer_sequence<int, N>{});
 }
 
 }  // namespace strata

@@ -129,17 +129,6 @@ struct Na3dTiles {
   int total;          // workgroups in the launch
 };
 
-// Linear workgroup id remapped so that consecutive tiles run on one XCD:
-// the dispatcher deals workgroups round-robin over the 8 XCDs, so XCD k gets
-// ids k, k+8, ...; map those to the k-th contiguous block of tiles.
-// (__builtin_amdgcn_workgroup_id_x keeps the id visibly uniform to the
-// compiler, unlike blockIdx.x's out-of-line library call.)
-__device__ __forceinline__ int xcd_tile_order(int n, int id) {
-  const int xcd = id & 7, local = id >> 3;
-  const int q = n >> 3, rem = n & 7;
-  return xcd < rem ? xcd * (q + 1) + local : rem * (q + 1) + (xcd - rem) * q + local;
-}
-
 // Tile (z, y, x) of the w-th workgroup of one (batch, head, residue class):
 // 4 x 4 x 4 blocks of tiles (smaller at the grid's far edges), x fastest
 // inside a block.  The ~64 workgroups an XCD runs at once then cover one
@@ -1151,16 +1140,6 @@ __global__ __launch_bounds__(256, 2) void na3d_strip_kernel(Na3dParams p, Na3dSt
 // ~26 log2 units below 2^-100 underflow (relative weight below 2^-26 each).
 // (gfx950's v_dot2c_f32_bf16 does not keep an fp32 sum: the row sums stay on
 // the ones-operand MFMA.)
-template <typename F, int... I>
-__device__ __forceinline__ void static_for_impl(F&& f, std::integer_sequence<int, I...>) {
-  (f(std::integral_constant<int, I>{}), ...);
-}
-// f(integral_constant<int, i>) for i = 0 .. N-1, unrolled at compile time.
-template <int N, typename F>
-__device__ __forceinline__ void static_for(F&& f) {
-  static_for_impl(f, std::make_integer_sequence<int, N>{});
-}
-
 // LDS bytes of one workgroup of the regular-strip kernel: the K/V ring and the
 // staged Q of the next tile.
 template <int D, int TX, int RPS, int NBUF>

@@ -41,6 +41,7 @@ struct Na3dBwdParams {
   float scale;
   int nyt, nxt;  // 4-row tiles along y, 16-column workgroup boxes along x
   int lse_given; // lse holds the forward's statistics: prep computes D_i only
+  int qy0, qny;  // token rows [qy0, qy0 + qny) of the tile walks (0 and Y but for the dq edge rows)
 };
 
 template <typename T, int DPL>
@@ -119,9 +120,9 @@ __device__ __forceinline__ Tok token_rows(const Na3dBwdParams& p, int nyt, int r
   k.b = b;
   k.h = h;
   k.z = z;
-  k.y = yt * rows + r0 + (t >> 2);
+  k.y = p.qy0 + yt * rows + r0 + (t >> 2);
   k.x = xb * 16 + wave * 4 + (t & 3);
-  k.valid = k.y < p.Y && k.x < p.X;
+  k.valid = k.y < p.qy0 + p.qny && k.y < p.Y && k.x < p.X;
   if (!k.valid) {  // clamp so every address stays in range; nothing is stored
     k.y = min(k.y, p.Y - 1);
     k.x = min(k.x, p.X - 1);
@@ -700,7 +701,7 @@ __global__ __launch_bounds__(256, NT == 1 ? 3 : 2) void na3d_bwd_dq_lds_kernel(N
   }
 
   // ---- y, z: the key rows of the workgroup's queries ----
-  const int ty0 = ((int)(blockIdx.x / p.nxt) % nyt) * 4 * NT;
+  const int ty0 = p.qy0 + ((int)(blockIdx.x / p.nxt) % nyt) * 4 * NT;
   const int KY0 = win_start(min(ty0, p.Y - 1), p.Y, ky);
   const int NY = win_start(min(ty0 + 4 * NT - 1, p.Y - 1), p.Y, ky) + ky - KY0;
   const int KZ0 = win_start(t0.z, p.Z, kz);
@@ -814,6 +815,309 @@ __global__ __launch_bounds__(256, NT == 1 ? 3 : 2) void na3d_bwd_dq_lds_kernel(N
 #endif
 }
 
+// ---------------------------------------------------------------------------
+// dq on regular strips (bf16, head_dim 64, dilation 1, kx <= 9, ky in {5, 7},
+// kz >= 2): the forward's small-window strip walk.  A workgroup of four waves
+// side by side in x (8 query columns each) walks one (b, h, z) column of 2 x 8
+// query tiles down the query rows whose y window is not clamped; the key rows
+// of the windows stream once per workgroup through a two-stage LDS ring (two
+// 40-key rows of K, then of V, per stage; the kz slices of a row group back to
+// back), and each wave keeps NS = (ky + 1) / 2 tiles in flight, tile j in slot
+// j % NS: tile j's y-union is row groups j .. j + NS - 1, so in group gr the
+// tile in its first group is in slot gr % NS and the one in its last group in
+// slot (gr + 1) % NS, and the y masks are compile-time (query row t sees row r
+// of its first group for r >= t and of its last for r <= t).  Per slot and
+// stage: S^T = K Q^T (Q pre-scaled by scale * log2 e, the x window as the C
+// operand) and dP^T = V dO^T, P^T = 2^(S^T - lse), dS^T = P^T (dP^T - D), then
+// dQ^T += K^T dS^T with K^T read transposed.  P <= 1 (lse is the query's true
+// log-sum-exp), so no range check is needed.  Q, dO, lse and D of the next
+// tile are copied into LDS by `buffer_load ... lds` during the second slice of
+// a group.  The clamped rows at the y edges go to na3d_bwd_dq_lds_kernel.
+// ---------------------------------------------------------------------------
+struct BwdStrips {
+  int nxt;     // 32-column boxes along x
+  int nch;     // y chunks per (b, h, z) column
+  int cty;     // 2-row tiles per chunk
+  int y0, y1;  // the strip rows [y0, y1): windows not clamped in y
+  int total;   // workgroups
+};
+
+namespace dqs {
+constexpr int NWX = 4, TX = 8, TY = 2, RPS = 2, NBUF = 2, D = 64, KS = 2, DB = 4, CPK = 8, KPK = 8;
+constexpr int LW = (NWX - 1) * TX + 16;    // 40 keys of a staged row
+constexpr int RB = LW * D * 2;             // bytes of one (tensor, row) region
+constexpr int STAGE_B = 2 * RPS * RB;      // K rows 0..1, then V rows 0..1
+constexpr int LPT = STAGE_B / 1024 / NWX;  // 1-KiB copies per wave per stage
+constexpr int QWB = 16 * D * 2;            // one wave's 16 rows of Q (or dO)
+constexpr int TWB = 2 * QWB + 2 * 256;     // per wave: Q, dO, then lse and D (one dword row each)
+constexpr int QTB = NWX * TWB;
+constexpr int RING_B = NBUF * STAGE_B;
+constexpr int LDS_B = RING_B + QTB;
+static_assert(LPT * NWX * 1024 == STAGE_B && 2 * LPT * 1024 == RPS * RB, "waves 0-1 copy K, 2-3 copy V");
+static_assert(LW % 8 == 0, "rows start at whole swizzle periods");
+static_assert(QTB <= RING_B, "tile 0's operands are staged through the ring");
+}  // namespace dqs
+
+template <int KY>
+__global__ __launch_bounds__(256, 2) void na3d_bwd_dq_strip_kernel(Na3dBwdParams p, BwdStrips sg) {
+#if defined(__HIP_DEVICE_COMPILE__)
+  using namespace dqs;
+  constexpr int NS = (TY + KY - 1) / RPS;  // tile slots per wave
+  constexpr int KR = KY / 2;
+  static_assert(TY + KY - 1 == NS * RPS, "one tile starts per row group");
+  __shared__ __attribute__((aligned(1024))) char lds[LDS_B];
+
+  // ---- work unit: x box fastest, then z, chunk, head, batch ----
+  int t = xcd_tile_order(sg.total, (int)__builtin_amdgcn_workgroup_id_x());
+  const int xb = t % sg.nxt;
+  t /= sg.nxt;
+  const int z = t % p.Z;
+  t /= p.Z;
+  const int ch = t % sg.nch;
+  t /= sg.nch;
+  const int h = t % p.H;
+  const int b = t / p.H;
+  const int ys = sg.y0 + ch * sg.cty * TY;
+  const int ye = min(ys + sg.cty * TY, sg.y1);
+  const int x0 = xb * (NWX * TX);
+  if (ys >= ye) return;  // uniform over the workgroup
+  const int NT = (ye - ys + TY - 1) / TY;
+  const int S = ys - KR;            // first key row of tile 0's union
+  const int NR = ye - ys + 2 * KR;  // key rows the strip streams
+  const int NG = (NR + RPS - 1) / RPS;
+  const int kz = p.ker[0], kx = p.ker[2];
+  const int sz = win_start(z, p.Z, kz);
+  const int X0 = win_start(min(x0, p.X - 1), p.X, kx);
+
+  const int tid = (int)__builtin_amdgcn_workitem_id_x();
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int lane = tid & 63;
+  const int n16 = lane & 15;
+  const int g = lane >> 4;
+  const int trow = n16 / TX;
+  const uint32_t lds_base = (uint32_t)(uintptr_t)(__attribute__((address_space(3))) char*)lds;
+
+  // ---- x geometry of the wave and of this lane's query ----
+  const int xw0 = x0 + wave * TX;
+  const int off_w = win_start(min(xw0, p.X - 1), p.X, kx) - X0;  // the wave's 16-key block in the staged row
+  const int qx = xw0 + n16 % TX;
+  f32x4 xbias;  // 0 or -inf: key 4g + i of the block inside / outside this lane's x window
+  {
+    const int sx = win_start(min(qx, p.X - 1), p.X, kx);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int kc = X0 + off_w + 4 * g + i;
+      xbias[i] = kc >= sx && kc < sx + kx ? 0.f : -INFINITY;
+    }
+  }
+  const float c2 = p.scale * 1.4426950408889634f;
+
+  // ---- tensor geometry (contiguous [B, Z, Y, X, H, D]) ----
+  const int64_t colb = (int64_t)p.H * D * 2;  // bytes per x step
+  const int64_t rowb = (int64_t)p.X * colb;   // per y row
+  const int64_t zb = (int64_t)p.Y * rowb;     // per z slice
+  const int64_t slice = ((int64_t)b * p.Z + z) * zb + (int64_t)h * D * 2;  // (b, z, h) of the queries
+
+  // ---- K/V ring: stage-flat key f = row * LW + x, chunk slots swizzled by f & 7 ----
+  const bool vwave = wave >= 2;
+  uint32_t doff[LPT];
+#pragma unroll
+  for (int i = 0; i < LPT; ++i) {
+    const int f = ((wave & 1) * LPT + i) * KPK + lane / CPK;
+    const int row = f / LW, key = f % LW;
+    const int c = (lane % CPK) ^ (f & 7);
+    doff[i] = X0 + key < p.X ? (uint32_t)(row * rowb + (int64_t)(X0 + key) * colb + 16 * c) : OOB;
+  }
+  const char* kvseg = (const char*)(vwave ? p.v : p.k) + ((int64_t)b * p.Z + sz) * zb + (int64_t)h * D * 2 +
+                      (int64_t)S * rowb;
+  int cz = 0, cp = 0;
+  uint32_t issue_off = 0;
+  auto issue = [&]() {
+    const int nrow = min(max(NR - RPS * cp, 0), RPS);
+    const u32x4 rs = make_rsrc(kvseg + (int64_t)cp * RPS * rowb + (int64_t)cz * zb, (uint32_t)(nrow * rowb));
+    const uint32_t m0 = lds_base + issue_off + (uint32_t)wave * (LPT * 1024);
+#pragma unroll
+    for (int i = 0; i < LPT; ++i) dma_row16(rs, m0 + i * 1024, doff[i]);
+    issue_off = issue_off + STAGE_B == RING_B ? 0 : issue_off + STAGE_B;
+    if (++cz == kz) {
+      cz = 0;
+      ++cp;
+    }
+  };
+
+  // ---- Q, dO, lse and D of a tile: one (b, z, h) slice, 31-bit offsets ----
+  // (the record counts end at the slice, so the OOB offsets of idle lanes read zeros)
+  const uint32_t qrec = (uint32_t)(zb - (int64_t)h * D * 2);
+  const u32x4 rq = make_rsrc((const char*)p.q + slice, qrec);
+  const u32x4 rd = make_rsrc((const char*)p.dout + slice, qrec);
+  const int64_t sslice = ((int64_t)b * p.Z + z) * p.Y * p.X * p.H + h;  // (b, z, h) of the statistics
+  const uint32_t srec = (uint32_t)(((int64_t)p.Y * p.X * p.H - h) * 4);
+  const u32x4 rl = make_rsrc(p.lse + sslice, srec);
+  const u32x4 rs2 = make_rsrc(p.dsum + sslice, srec);
+  auto dma_tile = [&](int j, uint32_t off) {
+    const int yt0 = ys + TY * j;
+    const uint32_t m0 = lds_base + off + (uint32_t)wave * TWB;
+#pragma unroll
+    for (int i = 0; i < KS; ++i) {
+      const int n = lane / CPK + i * (64 / CPK);
+      const int qy = min(yt0 + n / TX, ye - 1), cx = min(xw0 + n % TX, p.X - 1);
+      const uint32_t o = (uint32_t)(qy * rowb + cx * colb) + 16 * (lane % CPK);
+      dma_row16(rq, m0 + i * 1024, o);
+      dma_row16(rd, m0 + QWB + i * 1024, o);
+    }
+    const int qy = min(yt0 + n16 / TX, ye - 1), cx = min(xw0 + n16 % TX, p.X - 1);
+    const uint32_t so = lane < 16 ? (uint32_t)(((int64_t)qy * p.X + cx) * p.H * 4) : OOB;
+    dma_dword(rl, m0 + 2 * QWB, so);
+    dma_dword(rs2, m0 + 2 * QWB + 256, so);
+  };
+
+  // ---- LDS read offsets within row 0 of a stage (row r adds r * RB) ----
+  uint32_t koff[KS], toff[DB];
+#pragma unroll
+  for (int ks = 0; ks < KS; ++ks) {
+    const int key = off_w + n16;
+    koff[ks] = (key * D + 8 * ((4 * ks + g) ^ (key & 7))) * 2;
+  }
+  {
+    const int keyv = off_w + 4 * g + (n16 >> 2), dq = n16 & 3;
+#pragma unroll
+    for (int db = 0; db < DB; ++db)
+      toff[db] = (keyv * D + 8 * ((2 * db + (dq >> 1)) ^ (keyv & 7)) + 4 * (dq & 1)) * 2;
+  }
+
+  // ---- tile slots ----
+  bf16x8 qreg[NS][KS], doreg[NS][KS];
+  float lsev[NS], dsv[NS];
+  f32x4 acc[NS][DB];
+  const bool ylo = trow > 0;  // first group: row 0 masked for query row 1
+  const bool yhi = trow < 1;  // last group: row 1 masked for query row 0
+
+  auto start_tile = [&](int k, uint32_t off) {
+    const char* qb = lds + off + wave * TWB;
+#pragma unroll
+    for (int ks = 0; ks < KS; ++ks) {
+      qreg[k][ks] = *(const bf16x8*)(qb + n16 * D * 2 + (4 * ks + g) * 16);
+      doreg[k][ks] = *(const bf16x8*)(qb + QWB + n16 * D * 2 + (4 * ks + g) * 16);
+#pragma unroll
+      for (int e = 0; e < 8; ++e) qreg[k][ks][e] = (bf16)((float)qreg[k][ks][e] * c2);
+    }
+    lsev[k] = *(const float*)(qb + 2 * QWB + 4 * n16);
+    dsv[k] = *(const float*)(qb + 2 * QWB + 256 + 4 * n16);
+#pragma unroll
+    for (int db = 0; db < DB; ++db) acc[k][db] = (f32x4){0.f, 0.f, 0.f, 0.f};
+  };
+  char* dqb = (char*)p.dq + slice + 8 * g;
+  auto finish_tile = [&](int k, int j) {
+    const int qy = ys + TY * j + trow;
+    if (qy < ye && qx < p.X) {
+      char* op = dqb + (int64_t)qy * rowb + (int64_t)qx * colb;
+#pragma unroll
+      for (int db = 0; db < DB; ++db) {
+        const u32x2 w = {pack_bf16x2(acc[k][db][0] * p.scale, acc[k][db][1] * p.scale),
+                         pack_bf16x2(acc[k][db][2] * p.scale, acc[k][db][3] * p.scale)};
+        *(u32x2*)(op + 32 * db) = w;
+      }
+    }
+  };
+
+  // One stage's math for every live slot.  C: slot of the tile in its first
+  // group; ACT: bit k set if slot k holds a tile.
+  auto stage_math = [&](auto cst, auto act, const bf16x8 (&ak)[RPS][KS], const bf16x8 (&vk)[RPS][KS],
+                        const bf16x8 (&kt)[DB]) {
+    constexpr int C = decltype(cst)::value;
+    constexpr int ACT = decltype(act)::value;
+    static_for<NS>([&](auto ttc) {
+      constexpr int tt = decltype(ttc)::value;  // 0: the tile's first group, 1: its last
+      constexpr int k = (C + tt) % NS;
+      if constexpr ((ACT >> k) & 1) {
+        float ds[RPS][4];
+#pragma unroll
+        for (int r = 0; r < RPS; ++r) {
+          f32x4 sc = xbias, dp = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+          for (int ks = 0; ks < KS; ++ks) {
+            sc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ak[r][ks], qreg[k][ks], sc, 0, 0, 0);
+            dp = __builtin_amdgcn_mfma_f32_16x16x32_bf16(vk[r][ks], doreg[k][ks], dp, 0, 0, 0);
+          }
+          const bool masked = (tt == 0 && r == 0 && ylo) || (tt == 1 && r == 1 && yhi);
+#pragma unroll
+          for (int e = 0; e < 4; ++e)
+            ds[r][e] = masked ? 0.f : __builtin_amdgcn_exp2f(sc[e] - lsev[k]) * (dp[e] - dsv[k]);
+        }
+        const bf16x8 pb = __builtin_bit_cast(
+            bf16x8, ((u32x4){pack_bf16x2(ds[0][0], ds[0][1]), pack_bf16x2(ds[0][2], ds[0][3]),
+                             pack_bf16x2(ds[1][0], ds[1][1]), pack_bf16x2(ds[1][2], ds[1][3])}));
+#pragma unroll
+        for (int db = 0; db < DB; ++db)
+          acc[k][db] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kt[db], pb, acc[k][db], 0, 0, 0);
+      }
+    });
+  };
+
+  // Tile 0's operands are staged through the ring before the ring starts.
+  dma_tile(0, 0);
+  wait_vmcnt(0);
+  start_tile(0, 0);
+  wait_lgkm0();
+  lds_barrier();  // tile 0's operands read before the ring overwrites them
+#pragma unroll
+  for (int s = 0; s < NBUF - 1; ++s) issue();
+
+  uint32_t cur_off = 0;
+  // Group gr: slot gr % NS starts tile gr, slot (gr + 1) % NS finishes tile gr - NS + 1.
+  auto group = [&](auto cst, auto act, int gr) {
+    constexpr int C = decltype(cst)::value;
+    for (int zc = 0; zc < kz; ++zc) {
+      const bool starting = zc == 0 && gr > 0 && gr < NT;
+      if (starting)
+        wait_vmcnt(0);  // the tile's operand copies as well
+      else
+        wait_vmcnt((NBUF - 2) * LPT);
+      lds_barrier();
+      issue();
+      if (starting) start_tile(C, (uint32_t)RING_B);
+      if (zc == 1 && gr + 1 < NT) dma_tile(gr + 1, (uint32_t)RING_B);
+      const char* st = lds + cur_off;
+      bf16x8 ak[RPS][KS], vk[RPS][KS], kt[DB];
+#pragma unroll
+      for (int r = 0; r < RPS; ++r)
+#pragma unroll
+        for (int ks = 0; ks < KS; ++ks) {
+          ak[r][ks] = *(const bf16x8*)(st + r * RB + koff[ks]);
+          vk[r][ks] = *(const bf16x8*)(st + (RPS + r) * RB + koff[ks]);
+        }
+#pragma unroll
+      for (int db = 0; db < DB; ++db) {
+        const bf16x4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4bf16(LDS_PTR(bf16x4, st + toff[db]));
+        const bf16x4 hi = __builtin_amdgcn_ds_read_tr16_b64_v4bf16(LDS_PTR(bf16x4, st + RB + toff[db]));
+        kt[db] = __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7);
+      }
+      stage_math(cst, act, ak, vk, kt);
+      cur_off = cur_off + STAGE_B == RING_B ? 0 : cur_off + STAGE_B;
+    }
+    const int jf = gr - (NS - 1);
+    if (jf >= 0 && jf < NT) finish_tile((C + 1) % NS, jf);
+  };
+  using ALL = std::integral_constant<int, (1 << NS) - 1>;
+  static_for<NS - 1>([&](auto ig) {  // ramp-up: only the slots already holding a tile
+    constexpr int G = decltype(ig)::value;
+    group(std::integral_constant<int, G>{}, std::integral_constant<int, (1 << (G + 1)) - 1>{}, G);
+  });
+  for (int gr = NS - 1;; gr += NS) {  // NG = NT + NS - 1 >= NS
+    bool done = false;
+    static_for<NS>([&](auto ii) {
+      constexpr int I = decltype(ii)::value;
+      if (!done) {
+        group(std::integral_constant<int, (NS - 1 + I) % NS>{}, ALL{}, gr + I);
+        done = gr + I + 1 >= NG;
+      }
+    });
+    if (done) break;
+  }
+  wait_vmcnt(0);  // the ring's trailing (empty) stages
+#endif
+}
+
 // D_i = dO_i . O_i alone, for a backward given the forward's log-sum-exp:
 // LPR lanes per (token, head) row, 16 bytes of dO and of O each, closed by
 // xor shuffles.
@@ -844,6 +1148,44 @@ static bool mfma_ok(const Na3dBwdParams& p) {
          ((int64_t)p.Y + 1) * row * 4 < (int64_t)OOB && !std::getenv("STRATA_HIP_NA3D_BWD_VALU");
 }
 
+// dq on strips (na3d_bwd_dq_strip_kernel): kx <= 9, ky in {5, 7}, kz >= 2, at
+// least two unclamped rows, and one (b, z) slice of Q / dO / statistics within
+// 31-bit offsets.  STRATA_HIP_NA3D_BWD_NO_STRIPS=1 switches the path off.
+static bool dq_strip_fits(const Na3dBwdParams& p) {
+  const int ky = p.ker[1];
+  if (p.ker[0] < 2 || p.ker[2] > 9 || (ky != 5 && ky != 7)) return false;  // ky = 9 would spill
+  if (p.Y - 2 * (ky / 2) < 2) return false;
+  if ((int64_t)p.Y * p.X * p.H * 64 * 2 >= 0x7fffffffLL) return false;
+  return !std::getenv("STRATA_HIP_NA3D_BWD_NO_STRIPS");
+}
+
+// Strip work units: (b, h, z, 32-column box), the strip rows cut into chunks
+// only while that leaves fewer than one round of two workgroups per CU.
+static bool make_bwd_strips(const Na3dBwdParams& p, BwdStrips& sg) {
+  const int kr = p.ker[1] / 2;
+  sg.y0 = kr;
+  sg.y1 = p.Y - kr;
+  sg.nxt = (p.X + 31) / 32;
+  const int nty = (sg.y1 - sg.y0 + 1) / 2;
+  const int64_t strips = (int64_t)p.B * p.H * p.Z * sg.nxt;
+  int nch = 1;
+  while (strips * nch < 512 && nch < nty) ++nch;
+  sg.cty = (nty + nch - 1) / nch;
+  sg.nch = (nty + sg.cty - 1) / sg.cty;
+  const int64_t total = strips * sg.nch;
+  if (total <= 0 || total > 0x7fffffff) return false;
+  sg.total = (int)total;
+  return true;
+}
+
+static void launch_dq_strips(const Na3dBwdParams& p, const BwdStrips& sg, hipStream_t st) {
+  const dim3 grid((unsigned)sg.total), block(256);
+  switch (p.ker[1]) {
+    case 5: hipLaunchKernelGGL(na3d_bwd_dq_strip_kernel<5>, grid, block, 0, st, p, sg); break;
+    default: hipLaunchKernelGGL(na3d_bwd_dq_strip_kernel<7>, grid, block, 0, st, p, sg); break;
+  }
+}
+
 template <typename T, int D>
 static int launch_bwd(const Na3dBwdParams& p, hipStream_t st) {
   const int64_t blocks = (int64_t)p.B * p.H * p.Z * p.nyt * p.nxt;
@@ -864,10 +1206,26 @@ static int launch_bwd(const Na3dBwdParams& p, hipStream_t st) {
   constexpr int NT = NA3D_BWD_NT;
   const int nyt_lds = (p.Y + 4 * NT - 1) / (4 * NT);
   const dim3 grid_lds((unsigned)((int64_t)p.B * p.H * p.Z * nyt_lds * p.nxt));
-  if (sizeof(T) == 2 && D == 64 && mfma_ok(p))
-    hipLaunchKernelGGL(na3d_bwd_dq_lds_kernel<NT>, grid_lds, block, 0, st, p, nyt_lds);
-  else
+  if (sizeof(T) == 2 && D == 64 && mfma_ok(p)) {
+    BwdStrips sg;
+    if (dq_strip_fits(p) && make_bwd_strips(p, sg)) {
+      // the unclamped rows on strips, the clamped ones at each y edge on the tile walk
+      static_assert(NT == 2, "edge rows: workgroups of 8 rows");
+      launch_dq_strips(p, sg, st);
+      Na3dBwdParams e = p;
+      for (int side = 0; side < 2; ++side) {
+        e.qy0 = side ? sg.y1 : 0;
+        e.qny = side ? p.Y - sg.y1 : sg.y0;
+        const int nyt_e = (e.qny + 4 * NT - 1) / (4 * NT);
+        const int64_t ge = (int64_t)p.B * p.H * p.Z * nyt_e * p.nxt;
+        if (ge > 0) hipLaunchKernelGGL(na3d_bwd_dq_lds_kernel<NT>, dim3((unsigned)ge), block, 0, st, e, nyt_e);
+      }
+    } else {
+      hipLaunchKernelGGL(na3d_bwd_dq_lds_kernel<NT>, grid_lds, block, 0, st, p, nyt_lds);
+    }
+  } else {
     hipLaunchKernelGGL((na3d_bwd_dq_kernel<T, D>), grid, block, 0, st, p);
+  }
   if (sizeof(T) == 2 && D == 64 && mfma_ok(p))
     hipLaunchKernelGGL(na3d_bwd_dkv_lds_kernel<NT>, grid_lds, block, 0, st, p, nyt_lds);
   else
@@ -1004,6 +1362,8 @@ static int na3d_bwd_run(const strata_hip_na3d_bwd_args* a, float* workspace, voi
   }
   p.nyt = (p.Y + 3) / 4;
   p.nxt = (p.X + 15) / 16;
+  p.qy0 = 0;
+  p.qny = p.Y;
   hipStream_t st = (hipStream_t)stream;
   return a->dtype == STRATA_HIP_BF16 ? launch_bwd_t<bf16>(p, a->head_dim, st) : launch_bwd_t<float>(p, a->head_dim, st);
 }

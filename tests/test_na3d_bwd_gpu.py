@@ -24,6 +24,11 @@ CASES = [  # shape [B, Z, Y, X, H, D], kernel, dilation
     # LDS dq / dk/dv: three workgroup columns (the last ragged), keys at both x edges
     # needing two 16-query blocks, clamped y windows, a multi-stage ring
     ((1, 4, 13, 45, 2, 64), (3, 9, 13), (1, 1, 1)),
+    # dq on strips (the unclamped rows) plus the tile walk on the clamped edge rows:
+    # two 32-column boxes (the second ragged), two batches; an odd strip row count
+    # cut into one-tile chunks
+    ((2, 4, 20, 40, 2, 64), (3, 7, 7), (1, 1, 1)),
+    ((1, 3, 33, 16, 3, 64), (3, 5, 5), (1, 1, 1)),
 ]
 
 
