@@ -24,6 +24,7 @@
 //         (sub-grid coordinates of the dilation residue class).
 // Scores run in log2 units (q, or in dk/dv k, pre-scaled by scale * log2 e),
 // fp32 throughout.
+#include <algorithm>
 #include <cstdlib>
 #include <mutex>
 
@@ -105,8 +106,8 @@ struct Tok {
 
 // The token of in-tile index t (row r0 + (t >> 2), column t & 3) of this lane's
 // wave, for workgroups of `rows` rows (nyt of them along y).
-__device__ __forceinline__ Tok token_rows(const Na3dBwdParams& p, int nyt, int rows, int r0, int t) {
-  int w = (int)blockIdx.x;
+__device__ __forceinline__ Tok token_rows(const Na3dBwdParams& p, int wid, int nyt, int rows, int r0, int t) {
+  int w = wid;
   const int xb = w % p.nxt;
   w /= p.nxt;
   const int yt = w % nyt;
@@ -131,7 +132,7 @@ __device__ __forceinline__ Tok token_rows(const Na3dBwdParams& p, int nyt, int r
 }
 
 // The token of in-tile index t (row t >> 2, column t & 3) of this lane's wave.
-__device__ __forceinline__ Tok token_at(const Na3dBwdParams& p, int t) { return token_rows(p, p.nyt, 4, 0, t); }
+__device__ __forceinline__ Tok token_at(const Na3dBwdParams& p, int t) { return token_rows(p, (int)blockIdx.x, p.nyt, 4, 0, t); }
 
 // VALU kernels: 4 lanes per token, lane l on token l >> 2.
 __device__ __forceinline__ Tok token_of(const Na3dBwdParams& p) { return token_at(p, ((int)threadIdx.x & 63) >> 2); }
@@ -152,7 +153,7 @@ __device__ __forceinline__ int axis_win_first(int c, int L, int k, int d) {
 }
 
 // Inverse window of key coordinate c on one axis: first query, query count (step d).
-__device__ __forceinline__ void axis_inv(int c, int L, int k, int d, int& first, int& count) {
+__host__ __device__ __forceinline__ void axis_inv(int c, int L, int k, int d, int& first, int& count) {
   const int g = c % d, j = c / d, Lg = sub_len(L, g, d), r = k / 2;
   const int lo = j - k + 1 <= 0 ? 0 : j - k + 1 + r;
   const int hi = j >= Lg - k ? Lg - 1 : j + r;
@@ -384,18 +385,18 @@ constexpr int NBUF = 3;                    // ring stages
 constexpr int STAGE = 4 * RB + 4 * SW * 4;  // Q r0, Q r1, dO r0, dO r1, lse r0, r1, D r0, r1
 }  // namespace dkvl
 
+// `lds`: NBUF * STAGE bytes, 1 KiB aligned; `id`: the work unit (key tile box).
 template <int NT>
-__global__ __launch_bounds__(256, NT == 1 ? 3 : 2) void na3d_bwd_dkv_lds_kernel(Na3dBwdParams p, int nyt) {
+__device__ __forceinline__ void na3d_bwd_dkv_lds_body(const Na3dBwdParams& p, int nyt, char* lds, int id) {
 #if defined(__HIP_DEVICE_COMPILE__)
   using namespace dkvl;
   constexpr int D = 64, KS = 2, DB = 4;
-  __shared__ __attribute__((aligned(1024))) char lds[NBUF * STAGE];
   const int tid = (int)threadIdx.x;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int lane = tid & 63, n16 = lane & 15, g = lane >> 4;
   Tok t[NT];  // MFMA column n16 of tile tt = the lane's key in rows 4 tt .. 4 tt + 3 of the workgroup
 #pragma unroll
-  for (int tt = 0; tt < NT; ++tt) t[tt] = token_rows(p, nyt, 4 * NT, 4 * tt, n16);
+  for (int tt = 0; tt < NT; ++tt) t[tt] = token_rows(p, id, nyt, 4 * NT, 4 * tt, n16);
   const float c2 = p.scale * 1.4426950408889634f;
   const int kz = p.ker[0], ky = p.ker[1], kx = p.ker[2];
   const uint32_t lds_base = (uint32_t)(uintptr_t)(__attribute__((address_space(3))) char*)lds;
@@ -416,7 +417,7 @@ __global__ __launch_bounds__(256, NT == 1 ? 3 : 2) void na3d_bwd_dkv_lds_kernel(
   const Tok& t0 = t[0];  // b, h, z and the key column are the same for every tile
 
   // ---- x: the workgroup's query columns [SX0, SX0 + SW) and this wave's blocks ----
-  const int KX0 = ((int)blockIdx.x % p.nxt) * 16;
+  const int KX0 = (id % p.nxt) * 16;
   int f, n;
   axis_inv(min(KX0, p.X - 1), p.X, kx, 1, f, n);
   const int SX0 = f;
@@ -457,7 +458,7 @@ __global__ __launch_bounds__(256, NT == 1 ? 3 : 2) void na3d_bwd_dkv_lds_kernel(
   }
 
   // ---- y, z: the query rows of the workgroup's keys ----
-  const int ky0 = min(((int)(blockIdx.x / p.nxt) % nyt) * 4 * NT, p.Y - 1), ky1 = min(ky0 + 4 * NT - 1, p.Y - 1);
+  const int ky0 = min(p.qy0 + (id / p.nxt % nyt) * 4 * NT, p.Y - 1), ky1 = min(ky0 + 4 * NT - 1, p.Y - 1);
   axis_inv(ky0, p.Y, ky, 1, f, n);
   const int QY0 = f;
   axis_inv(ky1, p.Y, ky, 1, f, n);
@@ -619,6 +620,12 @@ __global__ __launch_bounds__(256, NT == 1 ? 3 : 2) void na3d_bwd_dkv_lds_kernel(
 #endif
 }
 
+template <int NT>
+__global__ __launch_bounds__(256, NT == 1 ? 3 : 2) void na3d_bwd_dkv_lds_kernel(Na3dBwdParams p, int nyt) {
+  __shared__ __attribute__((aligned(1024))) char lds[dkvl::NBUF * dkvl::STAGE];
+  na3d_bwd_dkv_lds_body<NT>(p, nyt, lds, (int)__builtin_amdgcn_workgroup_id_x());
+}
+
 // ---------------------------------------------------------------------------
 // LDS-staged dq for bf16, head_dim 64, dilation 1, kx <= 13: the forward's
 // walk for the workgroup's 4 x 4 query tiles (four waves along x, NT per wave
@@ -641,18 +648,18 @@ constexpr int NBUF = 3;
 constexpr int STAGE = 4 * RB;    // K r0, K r1, V r0, V r1
 }  // namespace dql
 
+// `lds`: NBUF * STAGE bytes, 1 KiB aligned; `id`: the work unit (query tile box).
 template <int NT>
-__global__ __launch_bounds__(256, NT == 1 ? 3 : 2) void na3d_bwd_dq_lds_kernel(Na3dBwdParams p, int nyt) {
+__device__ __forceinline__ void na3d_bwd_dq_lds_body(const Na3dBwdParams& p, int nyt, char* lds, int id) {
 #if defined(__HIP_DEVICE_COMPILE__)
   using namespace dql;
   constexpr int D = 64, KS = 2, DB = 4;
-  __shared__ __attribute__((aligned(1024))) char lds[NBUF * STAGE];
   const int tid = (int)threadIdx.x;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int lane = tid & 63, n16 = lane & 15, g = lane >> 4;
   Tok t[NT];  // MFMA column n16 of tile tt = the lane's query in rows 4 tt .. 4 tt + 3 of the workgroup
 #pragma unroll
-  for (int tt = 0; tt < NT; ++tt) t[tt] = token_rows(p, nyt, 4 * NT, 4 * tt, n16);
+  for (int tt = 0; tt < NT; ++tt) t[tt] = token_rows(p, id, nyt, 4 * NT, 4 * tt, n16);
   const float c2 = p.scale * 1.4426950408889634f;
   const int kz = p.ker[0], ky = p.ker[1], kx = p.ker[2];
   const uint32_t lds_base = (uint32_t)(uintptr_t)(__attribute__((address_space(3))) char*)lds;
@@ -678,7 +685,7 @@ __global__ __launch_bounds__(256, NT == 1 ? 3 : 2) void na3d_bwd_dq_lds_kernel(N
   const Tok& t0 = t[0];  // b, h, z and the query column are the same for every tile
 
   // ---- x: the workgroup's key columns [SX0, SX0 + SW) and this wave's block ----
-  const int QX0 = ((int)blockIdx.x % p.nxt) * 16;
+  const int QX0 = (id % p.nxt) * 16;
   const int SX0 = win_start(min(QX0, p.X - 1), p.X, kx);
   const int qx0 = min(QX0 + wave * 4, p.X - 1);
   const int bs = win_start(qx0, p.X, kx) - SX0;  // <= 12
@@ -701,7 +708,7 @@ __global__ __launch_bounds__(256, NT == 1 ? 3 : 2) void na3d_bwd_dq_lds_kernel(N
   }
 
   // ---- y, z: the key rows of the workgroup's queries ----
-  const int ty0 = p.qy0 + ((int)(blockIdx.x / p.nxt) % nyt) * 4 * NT;
+  const int ty0 = p.qy0 + (id / p.nxt % nyt) * 4 * NT;
   const int KY0 = win_start(min(ty0, p.Y - 1), p.Y, ky);
   const int NY = win_start(min(ty0 + 4 * NT - 1, p.Y - 1), p.Y, ky) + ky - KY0;
   const int KZ0 = win_start(t0.z, p.Z, kz);
@@ -815,6 +822,12 @@ __global__ __launch_bounds__(256, NT == 1 ? 3 : 2) void na3d_bwd_dq_lds_kernel(N
 #endif
 }
 
+template <int NT>
+__global__ __launch_bounds__(256, NT == 1 ? 3 : 2) void na3d_bwd_dq_lds_kernel(Na3dBwdParams p, int nyt) {
+  __shared__ __attribute__((aligned(1024))) char lds[dql::NBUF * dql::STAGE];
+  na3d_bwd_dq_lds_body<NT>(p, nyt, lds, (int)__builtin_amdgcn_workgroup_id_x());
+}
+
 // ---------------------------------------------------------------------------
 // dq on regular strips (bf16, head_dim 64, dilation 1, kx <= 9, ky in {5, 7},
 // kz >= 2): the forward's small-window strip walk.  A workgroup of four waves
@@ -858,17 +871,17 @@ static_assert(LW % 8 == 0, "rows start at whole swizzle periods");
 static_assert(QTB <= RING_B, "tile 0's operands are staged through the ring");
 }  // namespace dqs
 
+// `lds`: dqs::LDS_B bytes, 1 KiB aligned; `id`: the work unit in [0, sg.total).
 template <int KY>
-__global__ __launch_bounds__(256, 2) void na3d_bwd_dq_strip_kernel(Na3dBwdParams p, BwdStrips sg) {
+__device__ __forceinline__ void na3d_bwd_dq_strip_body(const Na3dBwdParams& p, const BwdStrips& sg, char* lds, int id) {
 #if defined(__HIP_DEVICE_COMPILE__)
   using namespace dqs;
   constexpr int NS = (TY + KY - 1) / RPS;  // tile slots per wave
   constexpr int KR = KY / 2;
   static_assert(TY + KY - 1 == NS * RPS, "one tile starts per row group");
-  __shared__ __attribute__((aligned(1024))) char lds[LDS_B];
 
   // ---- work unit: x box fastest, then z, chunk, head, batch ----
-  int t = xcd_tile_order(sg.total, (int)__builtin_amdgcn_workgroup_id_x());
+  int t = xcd_tile_order(sg.total, id);
   const int xb = t % sg.nxt;
   t /= sg.nxt;
   const int z = t % p.Z;
@@ -1118,6 +1131,372 @@ __global__ __launch_bounds__(256, 2) void na3d_bwd_dq_strip_kernel(Na3dBwdParams
 #endif
 }
 
+// ---------------------------------------------------------------------------
+// dK or dV on regular strips (bf16, head_dim 64, dilation 1, kx <= 9,
+// ky in {5, 7}, kz >= 3): the strip walk with the roles of queries and keys
+// swapped.  A workgroup of four waves side by side in x (8 key columns each)
+// walks one (b, h, z) column of 2 x 8 key tiles down the key rows that no
+// clamped query window reaches (rows [2 r + 1, Y - 2 r - 1), r = ky / 2), so
+// that query row y sees key row y' exactly when |y - y'| <= r; the query rows
+// of their inverse windows stream once per workgroup through a two-stage LDS
+// ring (two 40-column rows of Q, then of dO, then the rows' lse and D), over
+// the query slices whose z windows hold the key slice.  Each wave keeps
+// NS = (ky + 1) / 2 tiles in flight with compile-time y masks, exactly as the
+// forward strip (key row t sees query row r of its first group for r >= t and
+// of its last for r <= t).  Per slot and stage, with the key tile as the
+// register operand (K pre-scaled by scale * log2 e): S = Q K^T, P = 2^(S - lse)
+// (x membership as the C operand), then
+//   DK = 0:  dV^T += dO^T P;
+//   DK = 1:  dP = dO V^T, dS = P (dP - D), dK^T += Q^T dS  (dK = scale * dK^T^T),
+// with dO^T and Q^T read transposed.  dK and dV are separate launches: one
+// kernel holding K, V and both accumulators for every slot would need more
+// registers than a wave has at two waves per SIMD.  A wave's query block is
+// the 16 columns from the first query whose window holds the wave's first key
+// column; the host checks that it covers the inverse windows of all 8 columns.
+// ---------------------------------------------------------------------------
+namespace dkvs {
+constexpr int NWX = 4, TX = 8, TY = 2, RPS = 2, NBUF = 2, D = 64, KS = 2, DB = 4, CPK = 8, KPK = 8;
+constexpr int LW = 40;                     // staged query columns per row
+constexpr int RB = LW * D * 2;             // bytes of one (tensor, row) region
+constexpr int SB = 256;                    // one row of lse (or D): 64 dwords, 40 used
+constexpr int STAGE_B = 2 * RPS * RB + 2 * RPS * SB;  // Q r0, r1, dO r0, r1, lse r0, r1, D r0, r1
+constexpr int LPT = 2 * RPS * RB / 1024 / NWX;         // 1-KiB copies per wave per stage
+constexpr int KWB = 16 * D * 2;            // one wave's 16 keys of K (or V)
+constexpr int TWB = 2 * KWB;               // per wave: K, V of the next tile
+constexpr int QTB = NWX * TWB;
+constexpr int RING_B = NBUF * STAGE_B;
+constexpr int LDS_B = RING_B + QTB;
+static_assert(LPT * NWX * 1024 == 2 * RPS * RB && 2 * LPT * 1024 == RPS * RB, "waves 0-1 copy Q, 2-3 copy dO");
+static_assert(QTB <= RING_B && STAGE_B % 1024 == 0, "stage layout");
+}  // namespace dkvs
+
+// `lds`: dkvs::LDS_B bytes, 1 KiB aligned; `id`: the work unit in [0, sg.total).
+template <int KY, int DKM>
+__device__ __forceinline__ void na3d_bwd_dkv_strip_body(const Na3dBwdParams& p, const BwdStrips& sg, char* lds, int id) {
+#if defined(__HIP_DEVICE_COMPILE__)
+  using namespace dkvs;
+  constexpr int NS = (TY + KY - 1) / RPS;
+  constexpr int KR = KY / 2;
+  static_assert(TY + KY - 1 == NS * RPS, "one tile starts per row group");
+
+  // ---- work unit: x box fastest, then key slice z, chunk, head, batch ----
+  int t = xcd_tile_order(sg.total, id);
+  const int xb = t % sg.nxt;
+  t /= sg.nxt;
+  const int z = t % p.Z;
+  t /= p.Z;
+  const int ch = t % sg.nch;
+  t /= sg.nch;
+  const int h = t % p.H;
+  const int b = t / p.H;
+  const int ys = sg.y0 + ch * sg.cty * TY;  // key rows [ys, ye)
+  const int ye = min(ys + sg.cty * TY, sg.y1);
+  const int x0 = xb * (NWX * TX);
+  if (ys >= ye) return;  // uniform over the workgroup
+  const int NT = (ye - ys + TY - 1) / TY;
+  const int S = ys - KR;            // first query row of tile 0's inverse window
+  const int NR = ye - ys + 2 * KR;  // query rows the strip streams
+  const int NG = (NR + RPS - 1) / RPS;
+  const int kz = p.ker[0], kx = p.ker[2];
+  int zq0, nzq, QX0, wq0, cnt;
+  axis_inv(z, p.Z, kz, 1, zq0, nzq);            // query slices whose windows hold slice z
+  axis_inv(min(x0, p.X - 1), p.X, kx, 1, QX0, cnt);  // first staged query column
+
+  const int tid = (int)__builtin_amdgcn_workitem_id_x();
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int lane = tid & 63;
+  const int n16 = lane & 15;
+  const int g = lane >> 4;
+  const int trow = n16 / TX;  // this lane's key row within a tile
+  const uint32_t lds_base = (uint32_t)(uintptr_t)(__attribute__((address_space(3))) char*)lds;
+
+  // ---- x geometry: the wave's 16-query block and this lane's key ----
+  const int xw0 = x0 + wave * TX;
+  axis_inv(min(xw0, p.X - 1), p.X, kx, 1, wq0, cnt);
+  const int qb = wq0 - QX0;  // the wave's block in the staged row (<= LW - 16, checked by the host)
+  const int kxl = xw0 + n16 % TX;
+  f32x4 xbias;  // 0 or -inf: query 4g + i of the block holds / misses the lane's key in its x window
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int qx = QX0 + qb + 4 * g + i;
+    const int sx = win_start(min(qx, p.X - 1), p.X, kx);
+    xbias[i] = qx < p.X && kxl >= sx && kxl < sx + kx ? 0.f : -INFINITY;
+  }
+  const float c2 = p.scale * 1.4426950408889634f;
+
+  // ---- tensor geometry (contiguous [B, Z, Y, X, H, D]) ----
+  const int64_t colb = (int64_t)p.H * D * 2;
+  const int64_t rowb = (int64_t)p.X * colb;
+  const int64_t zb = (int64_t)p.Y * rowb;
+  const int64_t slice = ((int64_t)b * p.Z + z) * zb + (int64_t)h * D * 2;  // (b, z, h) of the keys
+
+  // ---- ring: Q rows (waves 0-1) or dO rows (waves 2-3), then one statistics row per wave ----
+  const bool owave = wave >= 2;
+  uint32_t doff[LPT];
+#pragma unroll
+  for (int i = 0; i < LPT; ++i) {
+    const int f = ((wave & 1) * LPT + i) * KPK + lane / CPK;
+    const int row = f / LW, col = f % LW;
+    const int c = (lane % CPK) ^ (f & 7);
+    doff[i] = QX0 + col < p.X ? (uint32_t)(row * rowb + (int64_t)(QX0 + col) * colb + 16 * c) : OOB;
+  }
+  const char* qseg = (const char*)(owave ? p.dout : p.q) + ((int64_t)b * p.Z + zq0) * zb + (int64_t)h * D * 2 +
+                     (int64_t)S * rowb;
+  // statistics: wave w copies row (w & 1) of lse (w < 2) or of D (w >= 2)
+  const int64_t srow = (int64_t)p.X * p.H, sz = (int64_t)p.Y * srow;
+  const float* sseg = (owave ? p.dsum : p.lse) + ((int64_t)b * p.Z + zq0) * sz + (int64_t)S * srow + h;
+  const uint32_t soff = lane < LW && QX0 + lane < p.X ? (uint32_t)((QX0 + lane) * p.H * 4) : OOB;
+  int cz = 0, cp = 0;
+  uint32_t issue_off = 0;
+  auto issue = [&]() {
+    const int nrow = min(max(NR - RPS * cp, 0), RPS);
+    const u32x4 rs = make_rsrc(qseg + (int64_t)cp * RPS * rowb + (int64_t)cz * zb, (uint32_t)(nrow * rowb));
+    const uint32_t m0 = lds_base + issue_off + (uint32_t)wave * (LPT * 1024);
+#pragma unroll
+    for (int i = 0; i < LPT; ++i) dma_row16(rs, m0 + i * 1024, doff[i]);
+    if (DKM || !owave) {  // dV needs no D
+      const int r = wave & 1;
+      const u32x4 rst = make_rsrc(sseg + (int64_t)(cp * RPS + r) * srow + (int64_t)cz * sz,
+                                  r < nrow ? (uint32_t)(srow * 4) : 0u);
+      dma_dword(rst, lds_base + issue_off + 2 * RPS * RB + (uint32_t)wave * SB, soff);
+    }
+    issue_off = issue_off + STAGE_B == RING_B ? 0 : issue_off + STAGE_B;
+    if (++cz == nzq) {
+      cz = 0;
+      ++cp;
+    }
+  };
+
+  // ---- K (and V) of a key tile: one (b, z, h) slice ----
+  const uint32_t krec = (uint32_t)(zb - (int64_t)h * D * 2);
+  const u32x4 rk = make_rsrc((const char*)p.k + slice, krec);
+  const u32x4 rv = make_rsrc((const char*)p.v + slice, krec);
+  auto dma_tile = [&](int j, uint32_t off) {
+    const int yt0 = ys + TY * j;
+    const uint32_t m0 = lds_base + off + (uint32_t)wave * TWB;
+#pragma unroll
+    for (int i = 0; i < KS; ++i) {
+      const int n = lane / CPK + i * (64 / CPK);
+      const int ky = min(yt0 + n / TX, ye - 1), cx = min(xw0 + n % TX, p.X - 1);
+      const uint32_t o = (uint32_t)(ky * rowb + cx * colb) + 16 * (lane % CPK);
+      dma_row16(rk, m0 + i * 1024, o);
+      if (DKM) dma_row16(rv, m0 + KWB + i * 1024, o);
+    }
+  };
+
+  // ---- LDS read offsets within row 0 of a stage (row r adds r * RB) ----
+  uint32_t aoff[KS], toff[DB];
+#pragma unroll
+  for (int ks = 0; ks < KS; ++ks) {
+    const int col = qb + n16;
+    aoff[ks] = (col * D + 8 * ((4 * ks + g) ^ (col & 7))) * 2;
+  }
+  {
+    const int colv = qb + 4 * g + (n16 >> 2), dq = n16 & 3;
+#pragma unroll
+    for (int db = 0; db < DB; ++db)
+      toff[db] = (colv * D + 8 * ((2 * db + (dq >> 1)) ^ (colv & 7)) + 4 * (dq & 1)) * 2;
+  }
+  const uint32_t stoff = 2 * RPS * RB + 4 * (qb + 4 * g);  // this lane's 4 queries in a statistics row
+
+  // ---- tile slots ----
+  bf16x8 kreg[NS][KS], vreg[NS][KS];
+  f32x4 acc[NS][DB];
+  const bool ylo = trow > 0;  // first group: query row 0 masked for key row 1
+  const bool yhi = trow < 1;  // last group: query row 1 masked for key row 0
+
+  auto start_tile = [&](int k, uint32_t off) {
+    const char* kb = lds + off + wave * TWB;
+#pragma unroll
+    for (int ks = 0; ks < KS; ++ks) {
+      kreg[k][ks] = *(const bf16x8*)(kb + n16 * D * 2 + (4 * ks + g) * 16);
+#pragma unroll
+      for (int e = 0; e < 8; ++e) kreg[k][ks][e] = (bf16)((float)kreg[k][ks][e] * c2);
+      if (DKM) vreg[k][ks] = *(const bf16x8*)(kb + KWB + n16 * D * 2 + (4 * ks + g) * 16);
+    }
+#pragma unroll
+    for (int db = 0; db < DB; ++db) acc[k][db] = (f32x4){0.f, 0.f, 0.f, 0.f};
+  };
+  char* outb = (char*)(DKM ? p.dk : p.dv) + slice + 8 * g;
+  const float oscale = DKM ? p.scale : 1.f;
+  auto finish_tile = [&](int k, int j) {
+    const int ky = ys + TY * j + trow;
+    if (ky < ye && kxl < p.X) {
+      char* op = outb + (int64_t)ky * rowb + (int64_t)kxl * colb;
+#pragma unroll
+      for (int db = 0; db < DB; ++db) {
+        const u32x2 w = {pack_bf16x2(acc[k][db][0] * oscale, acc[k][db][1] * oscale),
+                         pack_bf16x2(acc[k][db][2] * oscale, acc[k][db][3] * oscale)};
+        *(u32x2*)(op + 32 * db) = w;
+      }
+    }
+  };
+
+  auto stage_math = [&](auto cst, auto act, const char* st) {
+    constexpr int C = decltype(cst)::value;
+    constexpr int ACT = decltype(act)::value;
+    bf16x8 qa[RPS][KS], oa[RPS][KS], tr[DB];
+    float lsq[RPS][4], dsq[RPS][4];
+#pragma unroll
+    for (int r = 0; r < RPS; ++r) {
+#pragma unroll
+      for (int ks = 0; ks < KS; ++ks) {
+        qa[r][ks] = *(const bf16x8*)(st + r * RB + aoff[ks]);
+        if (DKM) oa[r][ks] = *(const bf16x8*)(st + (RPS + r) * RB + aoff[ks]);
+      }
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        lsq[r][i] = *(const float*)(st + stoff + r * SB + 4 * i);
+        if (DKM) dsq[r][i] = *(const float*)(st + stoff + (RPS + r) * SB + 4 * i);
+      }
+    }
+    // dO^T (dV) or Q^T (dK) over the row pair
+    const int tbase = DKM ? 0 : RPS * RB;
+#pragma unroll
+    for (int db = 0; db < DB; ++db) {
+      const bf16x4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4bf16(LDS_PTR(bf16x4, st + tbase + toff[db]));
+      const bf16x4 hi = __builtin_amdgcn_ds_read_tr16_b64_v4bf16(LDS_PTR(bf16x4, st + tbase + RB + toff[db]));
+      tr[db] = __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7);
+    }
+    static_for<NS>([&](auto ttc) {
+      constexpr int tt = decltype(ttc)::value;  // 0: the tile's first group, 1: its last
+      constexpr int k = (C + tt) % NS;
+      if constexpr ((ACT >> k) & 1) {
+        float pv[RPS][4];
+#pragma unroll
+        for (int r = 0; r < RPS; ++r) {
+          f32x4 sc = xbias;
+#pragma unroll
+          for (int ks = 0; ks < KS; ++ks)
+            sc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(qa[r][ks], kreg[k][ks], sc, 0, 0, 0);
+          const bool masked = (tt == 0 && r == 0 && ylo) || (tt == 1 && r == 1 && yhi);
+          if constexpr (DKM) {
+            f32x4 dp = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+            for (int ks = 0; ks < KS; ++ks)
+              dp = __builtin_amdgcn_mfma_f32_16x16x32_bf16(oa[r][ks], vreg[k][ks], dp, 0, 0, 0);
+#pragma unroll
+            for (int e = 0; e < 4; ++e)
+              pv[r][e] = masked ? 0.f : __builtin_amdgcn_exp2f(sc[e] - lsq[r][e]) * (dp[e] - dsq[r][e]);
+          } else {
+#pragma unroll
+            for (int e = 0; e < 4; ++e) pv[r][e] = masked ? 0.f : __builtin_amdgcn_exp2f(sc[e] - lsq[r][e]);
+          }
+        }
+        const bf16x8 pb = __builtin_bit_cast(
+            bf16x8, ((u32x4){pack_bf16x2(pv[0][0], pv[0][1]), pack_bf16x2(pv[0][2], pv[0][3]),
+                             pack_bf16x2(pv[1][0], pv[1][1]), pack_bf16x2(pv[1][2], pv[1][3])}));
+#pragma unroll
+        for (int db = 0; db < DB; ++db)
+          acc[k][db] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(tr[db], pb, acc[k][db], 0, 0, 0);
+      }
+    });
+  };
+
+  // Tile 0's keys are staged through the ring before the ring starts.
+  dma_tile(0, 0);
+  wait_vmcnt(0);
+  start_tile(0, 0);
+  wait_lgkm0();
+  lds_barrier();
+#pragma unroll
+  for (int s = 0; s < NBUF - 1; ++s) issue();
+
+  uint32_t cur_off = 0;
+  auto group = [&](auto cst, auto act, int gr) {
+    constexpr int C = decltype(cst)::value;
+    for (int zc = 0; zc < nzq; ++zc) {
+      const bool starting = zc == 0 && gr > 0 && gr < NT;
+      if (starting)
+        wait_vmcnt(0);  // the tile's key copies as well
+      else
+        wait_vmcnt((NBUF - 2) * (LPT + 1));
+      lds_barrier();
+      issue();
+      if (starting) start_tile(C, (uint32_t)RING_B);
+      if (zc == 1 && gr + 1 < NT) dma_tile(gr + 1, (uint32_t)RING_B);
+      stage_math(cst, act, lds + cur_off);
+      cur_off = cur_off + STAGE_B == RING_B ? 0 : cur_off + STAGE_B;
+    }
+    const int jf = gr - (NS - 1);
+    if (jf >= 0 && jf < NT) finish_tile((C + 1) % NS, jf);
+  };
+  using ALL = std::integral_constant<int, (1 << NS) - 1>;
+  static_for<NS - 1>([&](auto ig) {
+    constexpr int G = decltype(ig)::value;
+    group(std::integral_constant<int, G>{}, std::integral_constant<int, (1 << (G + 1)) - 1>{}, G);
+  });
+  for (int gr = NS - 1;; gr += NS) {  // NG = NT + NS - 1 >= NS
+    bool done = false;
+    static_for<NS>([&](auto ii) {
+      constexpr int I = decltype(ii)::value;
+      if (!done) {
+        group(std::integral_constant<int, (NS - 1 + I) % NS>{}, ALL{}, gr + I);
+        done = gr + I + 1 >= NG;
+      }
+    });
+    if (done) break;
+  }
+  wait_vmcnt(0);
+#endif
+}
+
+
+template <int KY>
+__global__ __launch_bounds__(256, 2) void na3d_bwd_dq_strip_kernel(Na3dBwdParams p, BwdStrips sg) {
+  __shared__ __attribute__((aligned(1024))) char lds[dqs::LDS_B];
+  na3d_bwd_dq_strip_body<KY>(p, sg, lds, (int)__builtin_amdgcn_workgroup_id_x());
+}
+
+// The backward's small-window launch: dq, dV and dK on strips and the clamped
+// edge rows of each on the tile walks, as one grid (the parts are independent:
+// each writes its own rows of dq, dk or dv).  Part k takes workgroup ids
+// [base[k], base[k + 1]) (each part padded to a multiple of 8, so it keeps its
+// XCD-aware order); the long strip parts come first and the short edge
+// workgroups fill their tail.  Edge parts: dq top / bottom (rows [0, sq.y0) and
+// [sq.y1, Y)), dk/dv top / bottom (rows [0, skv.y0) and [skv.y1, Y)).
+struct BwdParts {
+  int base[8];   // dq strips, dV strips, dK strips, dq top, dq bottom, dkv top, dkv bottom, end
+  int nyt[4];    // 8-row tile rows of the four edge parts
+};
+
+template <int KY>
+__global__ __launch_bounds__(256, 2) void na3d_bwd_small_fused_kernel(Na3dBwdParams p, BwdStrips sq, BwdStrips skv,
+                                                                       BwdParts parts) {
+  constexpr int LB = dqs::LDS_B > dkvs::LDS_B ? dqs::LDS_B : dkvs::LDS_B;
+  static_assert(LB >= dql::NBUF * dql::STAGE && LB >= dkvl::NBUF * dkvl::STAGE, "one LDS buffer for every part");
+  __shared__ __attribute__((aligned(1024))) char lds[LB];
+  const int id = (int)__builtin_amdgcn_workgroup_id_x();
+  int k = 0;
+  while (k < 7 && id >= parts.base[k + 1]) ++k;  // uniform
+  const int w = id - parts.base[k];
+  switch (k) {
+    case 0:
+      if (w < sq.total) na3d_bwd_dq_strip_body<KY>(p, sq, lds, w);
+      break;
+    case 1:
+      if (w < skv.total) na3d_bwd_dkv_strip_body<KY, 0>(p, skv, lds, w);
+      break;
+    case 2:
+      if (w < skv.total) na3d_bwd_dkv_strip_body<KY, 1>(p, skv, lds, w);
+      break;
+    default: {
+      const int e = k - 3;  // 0, 1: dq top / bottom; 2, 3: dk/dv top / bottom
+      const BwdStrips& s = e < 2 ? sq : skv;
+      Na3dBwdParams pe = p;
+      pe.qy0 = (e & 1) ? s.y1 : 0;
+      pe.qny = (e & 1) ? p.Y - s.y1 : s.y0;
+      const int n = p.B * p.H * p.Z * parts.nyt[e] * p.nxt;
+      if (w < n) {
+        if (e < 2)
+          na3d_bwd_dq_lds_body<NA3D_BWD_NT>(pe, parts.nyt[e], lds, w);
+        else
+          na3d_bwd_dkv_lds_body<NA3D_BWD_NT>(pe, parts.nyt[e], lds, w);
+      }
+    }
+  }
+}
+
 // D_i = dO_i . O_i alone, for a backward given the forward's log-sum-exp:
 // LPR lanes per (token, head) row, 16 bytes of dO and of O each, closed by
 // xor shuffles.
@@ -1161,10 +1540,9 @@ static bool dq_strip_fits(const Na3dBwdParams& p) {
 
 // Strip work units: (b, h, z, 32-column box), the strip rows cut into chunks
 // only while that leaves fewer than one round of two workgroups per CU.
-static bool make_bwd_strips(const Na3dBwdParams& p, BwdStrips& sg) {
-  const int kr = p.ker[1] / 2;
-  sg.y0 = kr;
-  sg.y1 = p.Y - kr;
+static bool make_bwd_strips(const Na3dBwdParams& p, int y0, int y1, BwdStrips& sg) {
+  sg.y0 = y0;
+  sg.y1 = y1;
   sg.nxt = (p.X + 31) / 32;
   const int nty = (sg.y1 - sg.y0 + 1) / 2;
   const int64_t strips = (int64_t)p.B * p.H * p.Z * sg.nxt;
@@ -1175,6 +1553,34 @@ static bool make_bwd_strips(const Na3dBwdParams& p, BwdStrips& sg) {
   const int64_t total = strips * sg.nch;
   if (total <= 0 || total > 0x7fffffff) return false;
   sg.total = (int)total;
+  return true;
+}
+
+// dK / dV on strips (na3d_bwd_dkv_strip_kernel): the dq conditions, kz >= 3 (every
+// key slice then lies in at least two query slices' windows), at least two key rows
+// that no clamped query window reaches, and along x every wave's query block (16
+// columns from the first query holding its first key column) and every
+// workgroup's staged row (40 columns) covering their keys' inverse windows.
+static bool dkv_strip_fits(const Na3dBwdParams& p) {
+  if (!dq_strip_fits(p) || p.ker[0] < 3) return false;
+  const int kr = p.ker[1] / 2, kx = p.ker[2];
+  if (p.Y - 2 * (2 * kr + 1) < 2) return false;
+  int f0, n0, f1, n1;
+  for (int x0 = 0; x0 < p.X; x0 += 8) {
+    axis_inv(x0, p.X, kx, 1, f0, n0);
+    axis_inv(std::min(x0 + 7, p.X - 1), p.X, kx, 1, f1, n1);
+    if (f1 + n1 - f0 > 16) return false;
+  }
+  for (int x0 = 0; x0 < p.X; x0 += 32) {
+    axis_inv(x0, p.X, kx, 1, f0, n0);
+    axis_inv(std::min(x0 + 31, p.X - 1), p.X, kx, 1, f1, n1);
+    if (f1 + n1 - f0 > 40) return false;
+    for (int w = 1; w < 4 && x0 + 8 * w < p.X; ++w) {
+      int fw, nw;
+      axis_inv(x0 + 8 * w, p.X, kx, 1, fw, nw);
+      if (fw - f0 + 16 > 40) return false;
+    }
+  }
   return true;
 }
 
@@ -1207,8 +1613,37 @@ static int launch_bwd(const Na3dBwdParams& p, hipStream_t st) {
   const int nyt_lds = (p.Y + 4 * NT - 1) / (4 * NT);
   const dim3 grid_lds((unsigned)((int64_t)p.B * p.H * p.Z * nyt_lds * p.nxt));
   if (sizeof(T) == 2 && D == 64 && mfma_ok(p)) {
+    // dq, dV and dK on strips with every clamped edge in one launch
+    BwdStrips sq, skv;
+    const int kr = p.ker[1] / 2, ek = 2 * kr + 1;
+    if (dkv_strip_fits(p) && make_bwd_strips(p, kr, p.Y - kr, sq) && make_bwd_strips(p, ek, p.Y - ek, skv)) {
+      static_assert(NT == NA3D_BWD_NT, "edge parts: workgroups of 4 NT rows");
+      BwdParts parts;
+      const int rows[4] = {sq.y0, p.Y - sq.y1, skv.y0, p.Y - skv.y1};
+      int64_t count[7] = {sq.total, skv.total, skv.total, 0, 0, 0, 0};
+      for (int e = 0; e < 4; ++e) {
+        parts.nyt[e] = (rows[e] + 4 * NT - 1) / (4 * NT);
+        count[3 + e] = (int64_t)p.B * p.H * p.Z * parts.nyt[e] * p.nxt;
+      }
+      int64_t base = 0;
+      for (int k = 0; k < 7; ++k) {
+        if (base > 0x7fffffff) return fail(STRATA_HIP_EUNSUPPORTED, "na3d_bwd: problem too large for one launch");
+        parts.base[k] = (int)base;
+        base += (count[k] + 7) / 8 * 8;
+      }
+      if (base > 0x7fffffff) return fail(STRATA_HIP_EUNSUPPORTED, "na3d_bwd: problem too large for one launch");
+      parts.base[7] = (int)base;
+      if (p.ker[1] == 5)
+        hipLaunchKernelGGL(na3d_bwd_small_fused_kernel<5>, dim3((unsigned)base), block, 0, st, p, sq, skv, parts);
+      else
+        hipLaunchKernelGGL(na3d_bwd_small_fused_kernel<7>, dim3((unsigned)base), block, 0, st, p, sq, skv, parts);
+      return check_launch("na3d_bwd kernels");
+    }
+  }
+  if (sizeof(T) == 2 && D == 64 && mfma_ok(p)) {
     BwdStrips sg;
-    if (dq_strip_fits(p) && make_bwd_strips(p, sg)) {
+    const int kr = p.ker[1] / 2;
+    if (dq_strip_fits(p) && make_bwd_strips(p, kr, p.Y - kr, sg)) {
       // the unclamped rows on strips, the clamped ones at each y edge on the tile walk
       static_assert(NT == 2, "edge rows: workgroups of 8 rows");
       launch_dq_strips(p, sg, st);
