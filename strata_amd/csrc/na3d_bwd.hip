@@ -8,12 +8,14 @@
 //   dQ_i  = scale * sum_{j in W(i)} dS_ij k_j
 //   dK_j  = scale * sum_{i : j in W(i)} dS_ij q_i,   dV_j = sum_{i : j in W(i)} p_ij dO_i
 //
-// Three kernels, each a wave per 4 x 4 tile of tokens, four waves side by side
-// along x per workgroup.  bf16 with head_dim 64, dilation 1 and kx <= 13 (the
-// training shapes) runs MFMA versions (below: dq and dk/dv stage the
-// workgroup's shared K/V or Q/dO rows in LDS); the general VALU versions (4
-// lanes per token, D/4 head dims per lane, dot products closed by two xor
-// shuffles) take everything else:
+// Three steps, prep, dq and dk/dv.  bf16 with head_dim 64, dilation 1 and
+// kx <= 13 (the training shapes) runs MFMA versions that stage the
+// workgroup's shared K/V or Q/dO rows in LDS; for ky in {5, 7}, kx <= 9,
+// kz >= 3 (the block's windows) dq, dV and dK walk strips like the forward
+// (the rows whose windows are not clamped) and the clamped edge rows walk
+// tiles, all in one launch (na3d_bwd_small_fused_kernel).  The general VALU
+// versions (4 lanes per token, D/4 head dims per lane, dot products closed by
+// two xor shuffles) take everything else:
 //   prep: per query, log2-sum-exp of its scores (recomputed, unless the caller
 //         passes the forward's, strata_hip_na3d_fwd's lse output: then only
 //         D_i) and D_i, into a caller-provided fp32 workspace;
