@@ -13,7 +13,8 @@ from .conftest import rel_l2
 pytestmark = pytest.mark.gpu
 
 
-def _block_case(gpu, B, Z, Y, X, C, H, kernel, seed=0, gated=False, qk_norm=False, qk_norm_affine=False):
+def _block_case(gpu, B, Z, Y, X, C, H, kernel, seed=0, gated=False, qk_norm=False, qk_norm_affine=False,
+                base=10000.0, ls_patch=1):
     g = torch.Generator().manual_seed(1)
     blk = StrataBlock(C, H, kernel, gated=gated, qk_norm=qk_norm, qk_norm_affine=qk_norm_affine)
     init_xavier_(blk, g)
@@ -28,14 +29,14 @@ def _block_case(gpu, B, Z, Y, X, C, H, kernel, seed=0, gated=False, qk_norm=Fals
     blk = blk.to(gpu).bfloat16()
     gx = torch.Generator().manual_seed(seed)
     x = torch.randn(B, Z, Y, X, C, generator=gx).bfloat16()
-    lat, lon = P.synthetic_tile_latlon(B, Y, X, gx)
-    ls = P.default_rope_length_scale(1)
-    cos, sin = P.stereographic_rope_tables(lat, lon, C // H, 10000.0, ls)
+    ls = P.default_rope_length_scale(ls_patch)
+    lat, lon = P.synthetic_tile_latlon(B, Y, X, gx, spacing=ls)
+    cos, sin = P.stereographic_rope_tables(lat, lon, C // H, base, ls)
     with torch.no_grad():
         out = blk(x.to(gpu), (cos.to(gpu), sin.to(gpu)))
     # fp32 oracle on the same bf16 inputs and bf16-rounded weights
     params = {k: v.bfloat16().float() for k, v in params.items()}
-    c64, s64 = R.tables(lat, lon, C // H, 10000.0, ls)
+    c64, s64 = R.tables(lat, lon, C // H, base, ls)
     ref = OB.block_forward(x.float(), params, H, kernel, c64.float(), s64.float(), gated=gated, qk_norm=qk_norm)
     return out, ref
 
@@ -58,6 +59,13 @@ def test_block_qk_norm(gpu):
 def test_block_production_variant(gpu):
     """Gated attention + qk RMSNorm with elementwise weights, 1024 wide (16 x 64 heads)."""
     out, ref = _block_case(gpu, 1, 4, 12, 12, 1024, 16, (3, 7, 7), gated=True, qk_norm=True, qk_norm_affine=True)
+    assert rel_l2(out.float(), ref) <= 1e-2
+
+
+def test_block_production_window(gpu):
+    """The production attention on a reduced grid: window (3,3,3), gated, qk RMSNorm without
+    weights, RoPE base 100 at the patch-4 length scale, 1024 wide (16 x 64 heads)."""
+    out, ref = _block_case(gpu, 1, 6, 24, 24, 1024, 16, (3, 3, 3), gated=True, qk_norm=True, base=100.0, ls_patch=4)
     assert rel_l2(out.float(), ref) <= 1e-2
 
 

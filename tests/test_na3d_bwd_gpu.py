@@ -29,6 +29,8 @@ CASES = [  # shape [B, Z, Y, X, H, D], kernel, dilation
     # cut into one-tile chunks
     ((2, 4, 20, 40, 2, 64), (3, 7, 7), (1, 1, 1)),
     ((1, 3, 33, 16, 3, 64), (3, 5, 5), (1, 1, 1)),
+    # the production window (3,3,3) at head_dim 64 (the tile walks)
+    ((1, 5, 24, 20, 2, 64), (3, 3, 3), (1, 1, 1)),
 ]
 
 
@@ -165,6 +167,11 @@ def test_bwd_with_forward_lse_matches_recompute(gpu, case):
     given = torch.ops.strata_hip.na3d_bwd(qg, kg, vg, out, dg, list(kernel), list(dil), None, lse)
     recomputed = torch.ops.strata_hip.na3d_bwd(qg, kg, vg, out, dg, list(kernel), list(dil), None)
     ref = O.na3d_backward(q, k, v, dout, kernel, dil)
+    # The two lse values differ in the last bits (the forward sums bf16 probabilities), and
+    # every bf16 output rounds on its own: the paths agree to about the bf16 rounding noise
+    # (measured 1.6e-3 to 2.2e-3, lower for wider windows) and each matches the oracle
+    # (about 3e-3).
     for name, a, b, r in zip(("dq", "dk", "dv"), given, recomputed, ref):
-        assert rel_l2(a.float(), b.float()) <= 2e-3, name
         assert rel_l2(a.float().cpu(), r) <= 1e-2, name
+        assert rel_l2(b.float().cpu(), r) <= 1e-2, name
+        assert rel_l2(a.float(), b.float()) <= 4e-3, name
