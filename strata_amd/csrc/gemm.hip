@@ -295,9 +295,11 @@ __device__ __forceinline__ int gswz(int chunk, int row) {
 
 // Large-tile GEMM for K % BK == 0: a BM x BN output tile per workgroup of
 // WGM x WGN waves (128 x 64 each, v_mfma_f32_32x32x16_bf16).  A/B tiles of BK
-// columns stream from global memory straight into an LDS ring of NST stages
-// (buffer_load ... lds) that runs NST - 1 stages ahead of the MFMAs, one
-// barrier per stage.
+// columns stream from global memory straight into a double-buffered LDS ring
+// (buffer_load ... lds) one stage ahead of the MFMAs, one barrier per stage.
+// The ring runs on across the tiles of the persistent walk: the last K step
+// of a tile issues the next tile's first stage, whose copy then lands while
+// the epilogue runs in the other slot.
 template <int BM, int BN, int WGM, int WGN, int BK, int NST, int ACT, int RES>
 __device__ __forceinline__ void gemm_dma_body(const GemmParams& p) {
   constexpr int NW = WGM * WGN;
@@ -311,36 +313,13 @@ __device__ __forceinline__ void gemm_dma_body(const GemmParams& p) {
   constexpr int XCH = XB / 1024;          // 1-KiB DMAs of the x tile
   constexpr int STAGE = XB + BN * ROWB;
   constexpr int LPW = STAGE / 1024 / NW;  // 1-KiB DMAs per wave per stage
-  constexpr int PD = NST - 1;             // stages in flight ahead of the MFMAs
+  constexpr int HM = FM / 2;              // accumulator rows (of 32) per epilogue half
+  constexpr int SLAB = HM * 32 * WTN * 2;  // one wave's epilogue slab: half its tile
   static_assert(CH == 4 || CH == 8, "BK must be 32 or 64");
-  static_assert(WTM == 128 && (WTN == 64 || WTN == 128) && STAGE % (1024 * NW) == 0, "wave tile / stage layout");
-  constexpr int LDS_BYTES = NST * STAGE > NW * WTM * WTN * 2 ? NST * STAGE : NW * WTM * WTN * 2;
-  static_assert((PD - 1) * LPW <= 16, "wait_vmcnt range");
-  __shared__ __attribute__((aligned(1024))) char lds[LDS_BYTES];  // ring, then the epilogue slabs
-
-  // Persistent: a workgroup walks tiles id, id + grid, ...  With a grid that
-  // is a multiple of 8, tile index t stays on the XCD that runs workgroup id
-  // (the dispatcher deals workgroups round-robin over the 8 XCDs), and each
-  // XCD takes a contiguous block of tiles, 32 neighbours in flight at once.
-  const int ntiles = p.mt * p.nt;
-  const int wg_id = (int)__builtin_amdgcn_workgroup_id_x();
-  for (int t = wg_id; t < ntiles; t += (int)gridDim.x) {
-  if (t != wg_id) lds_barrier();  // the previous tile's epilogue has read its slabs
-  const int wg = [&] {
-    const int xcd = t & 7, local = t >> 3, q = ntiles >> 3, rem = ntiles & 7;
-    return xcd < rem ? xcd * (q + 1) + local : rem * (q + 1) + (xcd - rem) * q + local;
-  }();
-  // Tiles in groups of GRP row panels x every column panel, row panel fastest:
-  // an XCD's 32 concurrent tiles share 4 panels of x and 8 of w (measured at
-  // the block's shapes with the stores below: 1-2% faster than one row panel
-  // x all columns).
-  constexpr int GRP = 4;
-  const int gi = wg / (GRP * p.nt), li = wg % (GRP * p.nt);
-  const int gmn = min(GRP, p.mt - gi * GRP);  // row panels in this (possibly last) group
-  const int tm = gi * GRP + li % gmn;
-  const int tn = li / gmn;
-  const int64_t m0 = (int64_t)tm * BM;
-  const int64_t n0 = (int64_t)tn * BN;
+  static_assert(NST == 2, "double-buffered ring");
+  static_assert(WTM == 128 && WTN == 64 && STAGE % (1024 * NW) == 0, "wave tile / stage layout");
+  static_assert(NW * SLAB <= STAGE, "the epilogue slabs fit one ring slot");
+  __shared__ __attribute__((aligned(1024))) char lds[NST * STAGE];  // ring; slabs in the slot last read
 
   const int tid = (int)__builtin_amdgcn_workitem_id_x();
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -349,28 +328,50 @@ __device__ __forceinline__ void gemm_dma_body(const GemmParams& p) {
   const int l32 = lane & 31, hi = lane >> 5;
   const uint32_t lds_base = (uint32_t)(uintptr_t)(__attribute__((address_space(3))) char*)lds;
 
-  // DMA lane offsets: DMA c = j*NW + wave of a stage covers RPC rows of the x
-  // tile (c < XCH) or of the w tile; lane i fills row RPC*(c%XCH) + i/CH, slot i%CH.
-  uint32_t voff[LPW];
-#pragma unroll
-  for (int j = 0; j < LPW; ++j) {
+  // Persistent: a workgroup walks tiles id, id + grid, ...  With a grid that
+  // is a multiple of 8, tile index t stays on the XCD that runs workgroup id
+  // (the dispatcher deals workgroups round-robin over the 8 XCDs), and each
+  // XCD takes a contiguous block of tiles, 32 neighbours in flight at once.
+  // Tiles in groups of GRP row panels x every column panel, row panel fastest:
+  // an XCD's 32 concurrent tiles share 4 panels of x and 8 of w (measured at
+  // the block's shapes with the stores below: 1-2% faster than one row panel
+  // x all columns).
+  const int ntiles = p.mt * p.nt;
+  const int wg_id = (int)__builtin_amdgcn_workgroup_id_x();
+  auto tile_origin = [&](int t, int64_t& m0, int64_t& n0) {
+    const int xcd = t & 7, local = t >> 3, q = ntiles >> 3, rem = ntiles & 7;
+    const int wg = xcd < rem ? xcd * (q + 1) + local : rem * (q + 1) + (xcd - rem) * q + local;
+    constexpr int GRP = 4;
+    const int gi = wg / (GRP * p.nt), li = wg % (GRP * p.nt);
+    const int gmn = min(GRP, p.mt - gi * GRP);  // row panels in this (possibly last) group
+    m0 = (int64_t)(gi * GRP + li % gmn) * BM;
+    n0 = (int64_t)(li / gmn) * BN;
+  };
+
+  // DMA j = c / NW of a stage (c = j*NW + wave) covers RPC rows of the x tile
+  // (c < XCH) or of the w tile; lane i fills row RPC*(c%XCH) + i/CH, slot i%CH.
+  // Rows past M (or N) get the out-of-range offset and read as zero.
+  auto dma_off = [&](int j, int64_t m0, int64_t n0) -> uint32_t {
     const int c = j * NW + wave;
     const bool isw = c >= XCH;
     const int row = RPC * (isw ? c - XCH : c) + lane / CH;
     const int lc = gswz<CH>(lane % CH, row);
-    const int64_t grow = (isw ? n0 : m0) + row;
-    const int64_t ld = isw ? p.ldw : p.ldx;
-    const bool ok = grow < (isw ? p.N : p.M);
-    voff[j] = ok ? (uint32_t)(row * ld * 2 + lc * 16) : OOB;
-  }
-  const char* xrow0 = (const char*)(p.x + m0 * p.ldx);
-  const char* wrow0 = (const char*)(p.w + n0 * p.ldw);
-  auto issue = [&](int kt, int buf) {
-    const u32x4 rx = make_rsrc(xrow0 + (int64_t)kt * BK * 2, OOB);
-    const u32x4 rw = make_rsrc(wrow0 + (int64_t)kt * BK * 2, OOB);
+    const bool ok = (isw ? n0 : m0) + row < (isw ? p.N : p.M);
+    return ok ? (uint32_t)(row * (isw ? p.ldw : p.ldx) * 2 + lc * 16) : OOB;
+  };
+  auto issue_at = [&](int64_t m0, int64_t n0, const uint32_t* vo, int kt, int buf) {
+    const u32x4 rx = make_rsrc((const char*)(p.x + m0 * p.ldx) + (int64_t)kt * BK * 2, OOB);
+    const u32x4 rw = make_rsrc((const char*)(p.w + n0 * p.ldw) + (int64_t)kt * BK * 2, OOB);
     const uint32_t dst = lds_base + buf * STAGE + wave * 1024;
 #pragma unroll
-    for (int j = 0; j < LPW; ++j) dma_row16(j * NW + wave >= XCH ? rw : rx, dst + j * NW * 1024, voff[j]);
+    for (int j = 0; j < LPW; ++j) dma_row16(j * NW + wave >= XCH ? rw : rx, dst + j * NW * 1024, vo[j]);
+  };
+  // A tile's first stage, with offsets computed on the spot.
+  auto issue_first = [&](int64_t m0, int64_t n0, int buf) {
+    uint32_t vo[LPW];
+#pragma unroll
+    for (int j = 0; j < LPW; ++j) vo[j] = dma_off(j, m0, n0);
+    issue_at(m0, n0, vo, 0, buf);
   };
 
   // LDS read offsets of the MFMA operands for K sub-steps kk = 0, 1; kk = 2, 3
@@ -386,6 +387,24 @@ __device__ __forceinline__ void gemm_dma_body(const GemmParams& p) {
     const int row = wm * WTM + 32 * j + l32;
     for (int kk = 0; kk < 2; ++kk) boff[j][kk] = row * ROWB + gswz<CH>(2 * kk + hi, row) * 16;
   }
+
+  const int nk = (int)(p.K / BK);
+  // Ring slots: `rd` holds the next stage to read, `wr` takes the next issue
+  // (and, after a tile's last K step, that tile's epilogue slabs).
+  int rd = 0, wr = 1;
+  bool first_in_flight = false;  // the current tile's first stage was issued by the previous tile
+  for (int t = wg_id; t < ntiles; t += (int)gridDim.x) {
+  int64_t m0, n0;
+  tile_origin(t, m0, n0);
+  const int tn = t + (int)gridDim.x;  // the next tile of this workgroup
+  int64_t m0n = 0, n0n = 0;
+  if (tn < ntiles) tile_origin(tn, m0n, n0n);
+
+  uint32_t voff[LPW];
+#pragma unroll
+  for (int j = 0; j < LPW; ++j) voff[j] = dma_off(j, m0, n0);
+  // Slot rd was last read two K steps ago (or never): no barrier needed.
+  if (!first_in_flight) issue_at(m0, n0, voff, 0, rd);
 
   // The bias enters as the C operand of each accumulator's first MFMA (no
   // zero fill, no add in the epilogue): acc[i][j][4q + e] holds column
@@ -415,24 +434,30 @@ __device__ __forceinline__ void gemm_dma_body(const GemmParams& p) {
     }
 
   f32x16 acc[FN][FM];
-  const int nk = (int)(p.K / BK);
-#pragma unroll
-  for (int s = 0; s < PD; ++s)
-    if (s < nk) issue(s, s);
-  int rd = 0, wr = PD;  // ring slots read by this stage / filled by the next issue
+  first_in_flight = false;
   // One K step; FIRST: the step that starts every accumulator from the bias.
   auto kstep = [&](int kt, auto first) {
     constexpr bool FIRST = decltype(first)::value;
-    // stage kt has landed once at most (stages issued after it) x LPW DMAs are pending
-    const int later = min(PD - 1, nk - 1 - kt);
-    wait_vmcnt(later * LPW);
-    lds_barrier();
-    if (kt + PD < nk) {
-      issue(kt + PD, wr);
-      wr = wr + 1 == NST ? 0 : wr + 1;
+    // Loads and stores share vmcnt and may complete out of order with respect
+    // to each other, so the wait is for everything issued: the stage read now
+    // (issued one step ago) and, at a tile's first step, the previous tile's
+    // output stores.
+    wait_vmcnt(0);
+    lds_barrier();  // the stage has landed for every wave; slot wr is free
+    if (kt + 1 < nk) {
+      issue_at(m0, n0, voff, kt + 1, wr);
+    } else if (tn < ntiles) {
+      // The next tile's first stage.  Its origin passes through an empty asm
+      // so that its lane offsets are computed here, not hoisted out of the K
+      // loop into registers held across it.
+      int64_t mn = m0n, nn = n0n;
+      asm volatile("" : "+s"(mn), "+s"(nn));
+      issue_first(mn, nn, wr);
+      first_in_flight = true;
     }
     const char* st = lds + rd * STAGE;
-    rd = rd + 1 == NST ? 0 : rd + 1;
+    rd ^= 1;
+    wr ^= 1;
     // Operand fragments double-buffered in registers: the LDS reads of K
     // sub-step kk + 1 are issued before the MFMAs of kk, so their latency
     // hides behind those MFMAs.
@@ -464,67 +489,76 @@ __device__ __forceinline__ void gemm_dma_body(const GemmParams& p) {
   kstep(0, std::true_type{});
   for (int kt = 1; kt < nk; ++kt) kstep(kt, std::false_type{});
 
-  // ---- epilogue through LDS ----
+  // ---- epilogue through LDS, in two halves of the wave tile ----
   // Phase 1: activation on the accumulators (the bias is already in them), bf16 into this wave's
-  // WTM x WTN slab of LDS (rows of SRB bytes, 16-byte chunks swizzled by row).
+  // slab (64 rows of SRB bytes, 16-byte chunks swizzled by row) in ring slot wr, the slot the
+  // last K step read; slot rd meanwhile receives the next tile's first stage.
   // Phase 2: each lane reads 16 contiguous bytes of a row, combines the
   // residual read the same way, and writes 16 bytes: CPR lanes cover a row.
   // Loads and stores share vmcnt on gfx9 (a load issued after a store waits
   // for it), so every residual load is issued before the first store, into
-  // registers the accumulators have freed.  Tiles inside the matrix skip
-  // every bounds check.
+  // registers the first half's accumulators have freed.  Tiles inside the
+  // matrix skip every bounds check.  The slab is rewritten by the second half
+  // only after the first half's reads (one wave, in order).
   constexpr int SRB = WTN * 2, CPR = WTN / 8, RPI = 64 / CPR, NIT = WTM / RPI;
   lds_barrier();  // every wave is done reading the last stage
-  char* slab = lds + wave * (WTM * WTN * 2);
-#pragma unroll
-  for (int i = 0; i < FN; ++i)
-#pragma unroll
-    for (int q = 0; q < 4; ++q) {
-      const int nl = 32 * i + 8 * q + 4 * hi;  // local column of this lane's quad
-#pragma unroll
-      for (int j = 0; j < FM; ++j) {
-        float v[4];
-#pragma unroll
-        for (int e = 0; e < 4; ++e) v[e] = act_t<ACT>(acc[i][j][4 * q + e]);
-        const int ml = 32 * j + l32;
-        const u32x2 w2 = {pack_bf16x2(v[0], v[1]), pack_bf16x2(v[2], v[3])};
-        *(u32x2*)(slab + ml * SRB + (((nl >> 3) ^ (ml & 7)) << 4) + 8 * hi) = w2;
-      }
-    }
+  char* slab = lds + wr * STAGE + wave * SLAB;
   const int c = lane % CPR;  // logical 16-byte chunk = 8 output columns
   const int64_t gn = gn0 + 8 * c;
   u32x4 r4[NIT];
-  if constexpr (RES != RES_NONE_T) {
 #pragma unroll
-    for (int it = 0; it < NIT; ++it) {
-      const int64_t gm = gm0 + RPI * it + lane / CPR;
-      r4[it] = (u32x4){0u, 0u, 0u, 0u};
-      if (full || (gm < p.M && gn + 8 <= p.N)) r4[it] = *(const u32x4*)(p.res + gm * p.ldr + gn);
-    }
-  }
+  for (int half = 0; half < 2; ++half) {
 #pragma unroll
-  for (int it = 0; it < NIT; ++it) {
-    const int ml = RPI * it + lane / CPR;
-    const u32x4 w4 = *(const u32x4*)(slab + ml * SRB + ((c ^ (ml & 7)) << 4));
-    const int64_t gm = gm0 + ml;
-    u32x4 o = w4;
+    for (int i = 0; i < FN; ++i)
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        const int nl = 32 * i + 8 * q + 4 * hi;  // local column of this lane's quad
+#pragma unroll
+        for (int jj = 0; jj < HM; ++jj) {
+          const int j = half * HM + jj;
+          float v[4];
+#pragma unroll
+          for (int e = 0; e < 4; ++e) v[e] = act_t<ACT>(acc[i][j][4 * q + e]);
+          const int ml = 32 * jj + l32;
+          const u32x2 w2 = {pack_bf16x2(v[0], v[1]), pack_bf16x2(v[2], v[3])};
+          *(u32x2*)(slab + ml * SRB + (((nl >> 3) ^ (ml & 7)) << 4) + 8 * hi) = w2;
+        }
+      }
     if constexpr (RES != RES_NONE_T) {
+      if (half == 0) {  // all residual rows, into the registers the first half's accumulators freed
 #pragma unroll
-      for (int e = 0; e < 4; ++e)
-        o[e] = pack_bf16x2(combine_t<RES>(bf16_lo(w4[e]), bf16_lo(r4[it][e])),
-                           combine_t<RES>(bf16_hi(w4[e]), bf16_hi(r4[it][e])));
+        for (int it = 0; it < NIT; ++it) {
+          const int64_t gm = gm0 + RPI * it + lane / CPR;
+          r4[it] = (u32x4){0u, 0u, 0u, 0u};
+          if (full || (gm < p.M && gn + 8 <= p.N)) r4[it] = *(const u32x4*)(p.res + gm * p.ldr + gn);
+        }
+      }
     }
-    if (full || (gm < p.M && gn + 8 <= p.N)) {
-      // Streaming store: the output is not read again here, and a tile-round's
-      // outputs (32 MB over the grid) would otherwise push the x and w panels
-      // out of L2 (M = 131072, N = 4096, K = 1024 with GELU: 1.32 -> 1.27 ms).
-      __builtin_nontemporal_store(o, (u32x4*)(p.out + gm * p.ldo + gn));
-    } else if (gm < p.M && gn < p.N) {
-      for (int e = 0; e < 8 && gn + e < p.N; ++e) {  // ragged last columns
-        const uint32_t wd = w4[e >> 1];
-        float ov = (e & 1) ? bf16_hi(wd) : bf16_lo(wd);
-        if constexpr (RES != RES_NONE_T) ov = combine_t<RES>(ov, (float)p.res[gm * p.ldr + gn + e]);
-        p.out[gm * p.ldo + gn + e] = (bf16)ov;
+#pragma unroll
+    for (int it = half * (NIT / 2); it < (half + 1) * (NIT / 2); ++it) {
+      const int ml = RPI * it + lane / CPR;   // row of the wave tile
+      const int sl = ml - half * (WTM / 2);   // row of the slab
+      const u32x4 w4 = *(const u32x4*)(slab + sl * SRB + ((c ^ (sl & 7)) << 4));
+      const int64_t gm = gm0 + ml;
+      u32x4 o = w4;
+      if constexpr (RES != RES_NONE_T) {
+#pragma unroll
+        for (int e = 0; e < 4; ++e)
+          o[e] = pack_bf16x2(combine_t<RES>(bf16_lo(w4[e]), bf16_lo(r4[it][e])),
+                             combine_t<RES>(bf16_hi(w4[e]), bf16_hi(r4[it][e])));
+      }
+      if (full || (gm < p.M && gn + 8 <= p.N)) {
+        // Streaming store: the output is not read again here, and a tile-round's
+        // outputs (32 MB over the grid) would otherwise push the x and w panels
+        // out of L2 (M = 131072, N = 4096, K = 1024 with GELU: 1.32 -> 1.27 ms).
+        __builtin_nontemporal_store(o, (u32x4*)(p.out + gm * p.ldo + gn));
+      } else if (gm < p.M && gn < p.N) {
+        for (int e = 0; e < 8 && gn + e < p.N; ++e) {  // ragged last columns
+          const uint32_t wd = w4[e >> 1];
+          float ov = (e & 1) ? bf16_hi(wd) : bf16_lo(wd);
+          if constexpr (RES != RES_NONE_T) ov = combine_t<RES>(ov, (float)p.res[gm * p.ldr + gn + e]);
+          p.out[gm * p.ldo + gn + e] = (bf16)ov;
+        }
       }
     }
   }
