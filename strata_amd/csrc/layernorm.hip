@@ -1,6 +1,8 @@
 // Non-affine LayerNorm over the channel dimension, bf16 in/out, fp32 stats.
-// One wave per row; each lane keeps its 16-byte runs of the row in registers
-// (rows up to 4096 channels) so the row is read from HBM once.
+// One wave per row (or, when a row's 16-byte runs split evenly over 32 lanes
+// but not over 64, e.g. 768 channels, half a wave per row); each lane keeps
+// its 16-byte runs of the row in registers (rows up to 4096 channels) so the
+// row is read from HBM once.
 #include "common.h"
 
 namespace strata {
@@ -13,18 +15,30 @@ __device__ __forceinline__ float wave_sum(float v) {
   return v;
 }
 
+// Sum over the LPR lanes that share a row (aligned groups of LPR lanes).
+template <int LPR>
+__device__ __forceinline__ float row_sum(float v) {
+#pragma unroll
+  for (int o = LPR / 2; o > 0; o >>= 1) v += __shfl_xor(v, o);
+  return v;
+}
+
+// LPR lanes per row (64 or 32): 256 / LPR rows per 256-thread block; NR
+// register slots of 16 bytes per lane (at least C / 8 / LPR: the instance is
+// picked by the row length, so short rows keep few registers and many waves).
+template <int LPR, int NR>
 __global__ __launch_bounds__(256) void layer_norm_kernel(const bf16* __restrict__ x, bf16* __restrict__ out, int64_t M,
                                                          int C, int64_t ldx, int64_t ldo, float eps) {
-  const int64_t row = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
-  if (row >= M) return;
-  const int lane = threadIdx.x & 63;
+  const int64_t row = (int64_t)blockIdx.x * (256 / LPR) + (threadIdx.x / LPR);
+  if (row >= M) return;  // uniform over a row's lanes
+  const int lane = threadIdx.x % LPR;
   const int runs = C / 8;
   const bf16* xr = x + row * ldx;
-  u32x4 v[LN_MAX_RUNS];
+  u32x4 v[NR];
   float s = 0.f;
 #pragma unroll
-  for (int r = 0; r < LN_MAX_RUNS; ++r) {
-    const int run = lane + 64 * r;
+  for (int r = 0; r < NR; ++r) {
+    const int run = lane + LPR * r;
     v[r] = (u32x4){0u, 0u, 0u, 0u};
     if (run < runs) {
       v[r] = *(const u32x4*)(xr + 8 * run);
@@ -32,11 +46,11 @@ __global__ __launch_bounds__(256) void layer_norm_kernel(const bf16* __restrict_
       for (int w = 0; w < 4; ++w) s += bf16_lo(v[r][w]) + bf16_hi(v[r][w]);
     }
   }
-  const float mean = wave_sum(s) / C;
+  const float mean = row_sum<LPR>(s) / C;
   float q = 0.f;
 #pragma unroll
-  for (int r = 0; r < LN_MAX_RUNS; ++r) {
-    if (lane + 64 * r < runs) {
+  for (int r = 0; r < NR; ++r) {
+    if (lane + LPR * r < runs) {
 #pragma unroll
       for (int w = 0; w < 4; ++w) {
         const float a = bf16_lo(v[r][w]) - mean, b = bf16_hi(v[r][w]) - mean;
@@ -45,11 +59,11 @@ __global__ __launch_bounds__(256) void layer_norm_kernel(const bf16* __restrict_
       }
     }
   }
-  const float rstd = rsqrtf(wave_sum(q) / C + eps);
+  const float rstd = rsqrtf(row_sum<LPR>(q) / C + eps);
   bf16* orow = out + row * ldo;
 #pragma unroll
-  for (int r = 0; r < LN_MAX_RUNS; ++r) {
-    const int run = lane + 64 * r;
+  for (int r = 0; r < NR; ++r) {
+    const int run = lane + LPR * r;
     if (run < runs) {
       u32x4 o;
 #pragma unroll
@@ -156,9 +170,28 @@ extern "C" int strata_hip_layer_norm(const strata_hip_layer_norm_args* a, void* 
   if (a->ldx < a->c || a->ldo < a->c || a->ldx % 8 || a->ldo % 8 || ((uintptr_t)a->x & 15) || ((uintptr_t)a->out & 15))
     return fail(STRATA_HIP_EINVAL, "layer_norm: rows must be 16-byte aligned with strides >= c");
   if (!(a->eps >= 0.f)) return fail(STRATA_HIP_EINVAL, "layer_norm: eps must be non-negative");
-  const int64_t blocks = (a->m + 3) / 4;
+  // Half a wave per row when the runs fill 32 lanes evenly and 64 lanes would
+  // leave half of them idle on the last run (768 channels: 3 runs on 32 lanes
+  // instead of 2 on 64, the second half empty).
+  const int runs = (int)(a->c / 8);
+  const bool half = runs % 64 != 0 && runs % 32 == 0;
+  const int rows_per_block = half ? 8 : 4;
+  const int64_t blocks = (a->m + rows_per_block - 1) / rows_per_block;
   if (blocks > 0x7fffffff) return fail(STRATA_HIP_EUNSUPPORTED, "layer_norm: too many rows");
-  hipLaunchKernelGGL(layer_norm_kernel, dim3((unsigned)blocks), dim3(256), 0, (hipStream_t)stream, (const bf16*)a->x,
-                     (bf16*)a->out, a->m, (int)a->c, a->ldx, a->ldo, a->eps);
+  const int per_lane = (runs + (half ? 32 : 64) - 1) / (half ? 32 : 64);
+  auto launch = [&](auto kern) {
+    hipLaunchKernelGGL(kern, dim3((unsigned)blocks), dim3(256), 0, (hipStream_t)stream, (const bf16*)a->x,
+                       (bf16*)a->out, a->m, (int)a->c, a->ldx, a->ldo, a->eps);
+  };
+  if (half) {
+    if (per_lane <= 2) launch(layer_norm_kernel<32, 2>);
+    else if (per_lane <= 4) launch(layer_norm_kernel<32, 4>);
+    else if (per_lane <= 8) launch(layer_norm_kernel<32, 8>);
+    else launch(layer_norm_kernel<32, 16>);
+  } else {
+    if (per_lane <= 2) launch(layer_norm_kernel<64, 2>);
+    else if (per_lane <= 4) launch(layer_norm_kernel<64, 4>);
+    else launch(layer_norm_kernel<64, 8>);
+  }
   return check_launch("layer_norm_kernel");
 }

@@ -180,11 +180,14 @@ def _rows(M):
 
 GEMM_PROD = [
     # M, N, K, act, res_op, residual: fc1 + GELU at configs[3]; its backward epilogue (GELU' * dout);
-    # the gate (a * sigmoid); a ragged M with more tiles than CUs at K = 256
+    # the gate (a * sigmoid); a ragged M with more tiles than CUs at K = 256; ragged M and N with
+    # more tiles than CUs at one and two K steps per tile (the ring runs on from tile to tile)
     (131072, 4096, 1024, _lib.ACT_GELU_TANH, _lib.RES_ADD, False),
     (131072, 4096, 1024, _lib.ACT_GELU_TANH_GRAD, _lib.RES_MUL, True),
     (131072, 1024, 1024, _lib.ACT_SIGMOID, _lib.RES_MUL, True),
     (16421, 4096, 256, _lib.ACT_GELU_TANH, _lib.RES_ADD, True),
+    (8300, 2104, 64, _lib.ACT_GELU_TANH, _lib.RES_ADD, True),
+    (4100, 4200, 128, _lib.ACT_SIGMOID, _lib.RES_MUL, False),
 ]
 
 

@@ -244,7 +244,7 @@ def test_rope_pack_stereographic_tables(gpu):
     assert torch.equal(v.cpu(), qkv.view(B, Z, 64, 64, 3, H, D)[..., 2, :, :])
 
 
-@pytest.mark.parametrize("C", [64, 768, 1024, 4096])
+@pytest.mark.parametrize("C", [64, 256, 768, 1024, 3840, 4096])
 def test_layer_norm(gpu, C):
     g = torch.Generator().manual_seed(C)
     x = (_randn((257, C), g) * 3 + 1).bfloat16()
