@@ -76,6 +76,8 @@ __global__ __launch_bounds__(256) void layer_norm_kernel(const bf16* __restrict_
 
 // Backward of the non-affine LayerNorm, one wave per row as above:
 //   xh = (x - mean) * rstd,  dx = rstd * (dy - mean(dy) - xh * mean(dy * xh)).
+// NR register slots of 16 bytes per lane for each of x and dy, as above.
+template <int NR>
 __global__ __launch_bounds__(256) void layer_norm_bwd_kernel(const bf16* __restrict__ x, const bf16* __restrict__ dy,
                                                              bf16* __restrict__ dx, int64_t M, int C, int64_t ld,
                                                              float eps) {
@@ -83,10 +85,10 @@ __global__ __launch_bounds__(256) void layer_norm_bwd_kernel(const bf16* __restr
   if (row >= M) return;
   const int lane = threadIdx.x & 63;
   const int runs = C / 8;
-  u32x4 v[LN_MAX_RUNS], g[LN_MAX_RUNS];
+  u32x4 v[NR], g[NR];
   float s = 0.f;
 #pragma unroll
-  for (int r = 0; r < LN_MAX_RUNS; ++r) {
+  for (int r = 0; r < NR; ++r) {
     const int run = lane + 64 * r;
     v[r] = g[r] = (u32x4){0u, 0u, 0u, 0u};
     if (run < runs) {
@@ -99,7 +101,7 @@ __global__ __launch_bounds__(256) void layer_norm_bwd_kernel(const bf16* __restr
   const float mean = wave_sum(s) / C;
   float q = 0.f;
 #pragma unroll
-  for (int r = 0; r < LN_MAX_RUNS; ++r) {
+  for (int r = 0; r < NR; ++r) {
     if (lane + 64 * r < runs) {
 #pragma unroll
       for (int w = 0; w < 4; ++w) {
@@ -112,7 +114,7 @@ __global__ __launch_bounds__(256) void layer_norm_bwd_kernel(const bf16* __restr
   const float rstd = rsqrtf(wave_sum(q) / C + eps);
   float sg = 0.f, sgx = 0.f;
 #pragma unroll
-  for (int r = 0; r < LN_MAX_RUNS; ++r) {
+  for (int r = 0; r < NR; ++r) {
     if (lane + 64 * r < runs) {
 #pragma unroll
       for (int w = 0; w < 4; ++w) {
@@ -125,7 +127,7 @@ __global__ __launch_bounds__(256) void layer_norm_bwd_kernel(const bf16* __restr
   }
   const float mg = wave_sum(sg) / C, mgx = wave_sum(sgx) / C;
 #pragma unroll
-  for (int r = 0; r < LN_MAX_RUNS; ++r) {
+  for (int r = 0; r < NR; ++r) {
     const int run = lane + 64 * r;
     if (run < runs) {
       u32x4 o;
@@ -155,8 +157,14 @@ extern "C" int strata_hip_layer_norm_bwd(const strata_hip_layer_norm_bwd_args* a
   if (!(a->eps >= 0.f)) return fail(STRATA_HIP_EINVAL, "layer_norm_bwd: eps must be non-negative");
   const int64_t blocks = (a->m + 3) / 4;
   if (blocks > 0x7fffffff) return fail(STRATA_HIP_EUNSUPPORTED, "layer_norm_bwd: too many rows");
-  hipLaunchKernelGGL(layer_norm_bwd_kernel, dim3((unsigned)blocks), dim3(256), 0, (hipStream_t)stream,
-                     (const bf16*)a->x, (const bf16*)a->dy, (bf16*)a->dx, a->m, (int)a->c, a->ld, a->eps);
+  const int per_lane = (int)((a->c / 8 + 63) / 64);
+  auto launch = [&](auto kern) {
+    hipLaunchKernelGGL(kern, dim3((unsigned)blocks), dim3(256), 0, (hipStream_t)stream, (const bf16*)a->x,
+                       (const bf16*)a->dy, (bf16*)a->dx, a->m, (int)a->c, a->ld, a->eps);
+  };
+  if (per_lane <= 2) launch(layer_norm_bwd_kernel<2>);
+  else if (per_lane <= 4) launch(layer_norm_bwd_kernel<4>);
+  else launch(layer_norm_bwd_kernel<8>);
   return check_launch("layer_norm_bwd_kernel");
 }
 

@@ -18,7 +18,7 @@ from .conftest import rel_l2
 pytestmark = pytest.mark.gpu
 
 
-@pytest.mark.parametrize("C", [64, 768, 1024, 4096])
+@pytest.mark.parametrize("C", [64, 768, 1024, 2048, 3840, 4096])
 def test_layer_norm_backward(gpu, C):
     g = torch.Generator().manual_seed(0)
     x = (torch.randn(3, 37, C, generator=g) * 2 + 0.5).bfloat16()
