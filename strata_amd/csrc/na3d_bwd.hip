@@ -1454,12 +1454,18 @@ __global__ __launch_bounds__(256, 2) void na3d_bwd_dq_strip_kernel(Na3dBwdParams
 // edge rows of each on the tile walks, as one grid (the parts are independent:
 // each writes its own rows of dq, dk or dv).  Part k takes workgroup ids
 // [base[k], base[k + 1]) (each part padded to a multiple of 8, so it keeps its
-// XCD-aware order); the long strip parts come first and the short edge
-// workgroups fill their tail.  Edge parts: dq top / bottom (rows [0, sq.y0) and
-// [sq.y1, Y)), dk/dv top / bottom (rows [0, skv.y0) and [skv.y1, Y)).
+// XCD-aware order); the strip parts come first, the edge workgroups fill their
+// tail (measured: the edge parts first is 2.5% slower).  Edge parts: dq top /
+// bottom (rows [0, sq.y0) and [sq.y1, Y): ky/2 rows, on workgroups of one
+// 4-row tile, BWD_DQE_NT), dk/dv top / bottom (rows [0, skv.y0) and
+// [skv.y1, Y): 2 (ky/2) + 1 rows, on workgroups of two 4-row tiles,
+// BWD_DKVE_NT).  Measured against 8-row workgroups for both: configs[1]
+// 0.454 -> 0.428 ms (4-row dk/dv edges as well: 0.445 ms).
+constexpr int BWD_DQE_NT = 1;
+constexpr int BWD_DKVE_NT = 2;
 struct BwdParts {
   int base[8];   // dq strips, dV strips, dK strips, dq top, dq bottom, dkv top, dkv bottom, end
-  int nyt[4];    // 8-row tile rows of the four edge parts
+  int nyt[4];    // tile rows of the four edge parts
 };
 
 template <int KY>
@@ -1491,9 +1497,9 @@ __global__ __launch_bounds__(256, 2) void na3d_bwd_small_fused_kernel(Na3dBwdPar
       const int n = p.B * p.H * p.Z * parts.nyt[e] * p.nxt;
       if (w < n) {
         if (e < 2)
-          na3d_bwd_dq_lds_body<NA3D_BWD_NT>(pe, parts.nyt[e], lds, w);
+          na3d_bwd_dq_lds_body<BWD_DQE_NT>(pe, parts.nyt[e], lds, w);
         else
-          na3d_bwd_dkv_lds_body<NA3D_BWD_NT>(pe, parts.nyt[e], lds, w);
+          na3d_bwd_dkv_lds_body<BWD_DKVE_NT>(pe, parts.nyt[e], lds, w);
       }
     }
   }
@@ -1624,7 +1630,8 @@ static int launch_bwd(const Na3dBwdParams& p, hipStream_t st) {
       const int rows[4] = {sq.y0, p.Y - sq.y1, skv.y0, p.Y - skv.y1};
       int64_t count[7] = {sq.total, skv.total, skv.total, 0, 0, 0, 0};
       for (int e = 0; e < 4; ++e) {
-        parts.nyt[e] = (rows[e] + 4 * NT - 1) / (4 * NT);
+        const int ert = 4 * (e < 2 ? BWD_DQE_NT : BWD_DKVE_NT);  // rows per edge workgroup
+        parts.nyt[e] = (rows[e] + ert - 1) / ert;
         count[3 + e] = (int64_t)p.B * p.H * p.Z * parts.nyt[e] * p.nxt;
       }
       int64_t base = 0;
