@@ -392,7 +392,55 @@ def bench_backward(device, reps, warmup):
         ms = e0.elapsed_time(e1) / reps
         res[f"{name}_ms"] = round(ms, 4)
         res[f"{name}_tflops"] = round(flops / (ms * 1e-3) / 1e12, 1)
+    res.update(_block_train_step(device, reps, warmup))
     return res
+
+
+def _block_train_step(device, reps, warmup):
+    """One training step of the configs[3] block: forward with autograd, then backward of
+    a random output gradient into the input and every parameter (bf16 weights, as the
+    forward bench). FLOPs: 3x the block's GEMMs (forward, input and weight gradients) and
+    NA3D at 1 + 2.5 times its forward count."""
+    import torch
+
+    from strata_amd import rope as P
+    from strata_amd.modules import StrataBlock, init_xavier_
+
+    B, Z, Y, X, C, H = 4, 8, 64, 64, 1024, 16
+    blk = StrataBlock(C, H, (3, 7, 7))
+    init_xavier_(blk, torch.Generator().manual_seed(1))
+    blk = blk.to(device).bfloat16().train()
+    gx = torch.Generator(device=device).manual_seed(0)
+    x = torch.randn(B, Z, Y, X, C, generator=gx, device=device).bfloat16().requires_grad_(True)
+    dy = torch.randn(B, Z, Y, X, C, generator=gx, device=device).bfloat16()
+    lat, lon = P.synthetic_tile_latlon(B, Y, X, torch.Generator().manual_seed(0))
+    rope = P.stereographic_rope_tables(lat.to(device), lon.to(device), C // H, 10000.0, P.default_rope_length_scale(1))
+
+    def step():
+        blk.zero_grad(set_to_none=True)
+        x.grad = None
+        blk(x, rope).backward(dy)
+
+    for _ in range(max(warmup, 1)):
+        step()
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record()
+    for _ in range(reps):
+        step()
+    e1.record()
+    torch.cuda.synchronize()
+    ms = e0.elapsed_time(e1) / reps
+    assert torch.isfinite(x.grad.float()).all(), "block backward produced non-finite input gradients"
+    M = B * Z * Y * X
+    flops = 3 * 24.0 * M * C * C + 3.5 * 4.0 * M * 147 * C
+    return {
+        "block_train_workload": "configs[3] block [4,8,64,64,1024] forward + backward (input and parameter "
+                                "gradients), 16x64 heads, W=(3,7,7), Xavier seed 1",
+        "block_train_ms": round(ms, 3),
+        "block_train_tokens_per_s": M / (ms * 1e-3),
+        "block_train_tflops": round(flops / (ms * 1e-3) / 1e12, 1),
+    }
 
 
 def _cpu_affinity() -> int:

@@ -275,6 +275,26 @@ typedef struct strata_hip_gemm_args {
 
 int strata_hip_gemm_bias_act(const strata_hip_gemm_args* args, void* stream);
 
+/* Bias gradient of the GEMM backward (nn.Linear's d bias: the output gradient
+ * summed over rows, as torch autograd forms it when training reaches the
+ * block's Linears through train.py:1161):  out[n] = sum_m g[m, n].
+ * g: [M, N] bf16, row stride ldg (>= N; N and ldg multiples of 8 elements,
+ * g 16-byte aligned); out: [N] bf16; workspace: fp32, 16-byte aligned, at
+ * least strata_hip_bias_grad_workspace(M, N) elements (per-chunk partial
+ * sums).  fp32 accumulation in an order fixed by the shape: the result repeats
+ * bit for bit. */
+typedef struct strata_hip_bias_grad_args {
+  const void* g;
+  void* out;
+  float* workspace;
+  int64_t m;
+  int64_t n;
+  int64_t ldg;
+} strata_hip_bias_grad_args;
+
+int64_t strata_hip_bias_grad_workspace(int64_t m, int64_t n);
+int strata_hip_bias_grad(const strata_hip_bias_grad_args* args, void* stream);
+
 /* ---------------------------------------------------------------------------
  * Non-affine LayerNorm over the last dimension (the block's two pre-norms,
  * which carry no parameters in the state-dict manifests

@@ -182,6 +182,17 @@ class LayerNormBwdArgs(ctypes.Structure):
     ]
 
 
+class BiasGradArgs(ctypes.Structure):
+    _fields_ = [
+        ("g", ctypes.c_void_p),
+        ("out", ctypes.c_void_p),
+        ("workspace", ctypes.c_void_p),
+        ("m", ctypes.c_int64),
+        ("n", ctypes.c_int64),
+        ("ldg", ctypes.c_int64),
+    ]
+
+
 class RopePackBwdArgs(ctypes.Structure):
     _fields_ = [
         ("dq", ctypes.c_void_p),
@@ -261,6 +272,8 @@ EXPORTS = {
     "strata_hip_na3d_bwd_noalloc": ([ctypes.POINTER(Na3dBwdArgs), ctypes.c_void_p], ctypes.c_int),
     "strata_hip_rope_qkv_pack": ([ctypes.POINTER(RopePackArgs), ctypes.c_void_p], ctypes.c_int),
     "strata_hip_gemm_bias_act": ([ctypes.POINTER(GemmArgs), ctypes.c_void_p], ctypes.c_int),
+    "strata_hip_bias_grad": ([ctypes.POINTER(BiasGradArgs), ctypes.c_void_p], ctypes.c_int),
+    "strata_hip_bias_grad_workspace": ([ctypes.c_int64, ctypes.c_int64], ctypes.c_int64),
     "strata_hip_layer_norm": ([ctypes.POINTER(LayerNormArgs), ctypes.c_void_p], ctypes.c_int),
     "strata_hip_layer_norm_bwd": ([ctypes.POINTER(LayerNormBwdArgs), ctypes.c_void_p], ctypes.c_int),
     "strata_hip_rope_qkv_pack_bwd": ([ctypes.POINTER(RopePackBwdArgs), ctypes.c_void_p], ctypes.c_int),

@@ -675,3 +675,129 @@ extern "C" int strata_hip_gemm_bias_act(const strata_hip_gemm_args* a, void* str
   }
   return launch_gemm<128, 128, 2, 2>(p, st);
 }
+
+// ---------------------------------------------------------------------------
+// Bias gradient of the GEMM backward: out[n] = sum over m of g[m, n].
+// Pass 1: a workgroup takes BG_ROWS rows x 128 columns.  A lane holds 8
+// consecutive columns (16-byte loads); the 16 lanes of a quarter-wave cover
+// the 128 columns of one row, so one load instruction reads 4 rows (1 KiB) and
+// each wave walks every 16th row from its own start.  The lanes' fp32 sums are
+// combined across the wave's quarters with two xor shuffles and across the
+// four waves in LDS in wave order, and written as the chunk's partial row.
+// Pass 2: per column, the chunks' partial rows are added by four threads (each
+// a fixed quarter of the chunks, in order) and the four sums in order.  The
+// order of every addition is fixed by the shape, so the result is the same bit
+// for bit on every call.
+// ---------------------------------------------------------------------------
+namespace strata {
+
+constexpr int BG_ROWS = 1024;  // rows per chunk (one partial row of the workspace each)
+
+__global__ __launch_bounds__(256) void bias_grad_partial_kernel(const bf16* __restrict__ g, float* __restrict__ part,
+                                                                int64_t M, int64_t N, int64_t ldg) {
+  __shared__ float red[4][128];
+  const int wave = (int)(threadIdx.x >> 6), lane = (int)(threadIdx.x & 63);
+  const int q = lane >> 4;                        // quarter of the wave: its row offset
+  const int cl = 8 * (lane & 15);                 // first of the lane's 8 columns in the block
+  const int64_t col = (int64_t)blockIdx.x * 128 + cl;
+  const int64_t chunk = blockIdx.y;
+  const int64_t r1 = min((chunk + 1) * (int64_t)BG_ROWS, M);
+  float s[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+  if (col < N) {
+    int64_t r = chunk * BG_ROWS + 4 * wave + q;  // rows r, r + 16, ...
+    const bf16* p = g + r * ldg + col;
+    for (; r + 7 * 16 < r1; r += 8 * 16, p += 8 * 16 * ldg) {
+      u32x4 v[8];
+#pragma unroll
+      for (int i = 0; i < 8; ++i) v[i] = *(const u32x4*)(p + i * 16 * ldg);
+#pragma unroll
+      for (int i = 0; i < 8; ++i)
+#pragma unroll
+        for (int w = 0; w < 4; ++w) {
+          s[2 * w] += bf16_lo(v[i][w]);
+          s[2 * w + 1] += bf16_hi(v[i][w]);
+        }
+    }
+    for (; r < r1; r += 16, p += 16 * ldg) {
+      const u32x4 v = *(const u32x4*)p;
+#pragma unroll
+      for (int w = 0; w < 4; ++w) {
+        s[2 * w] += bf16_lo(v[w]);
+        s[2 * w + 1] += bf16_hi(v[w]);
+      }
+    }
+  }
+#pragma unroll
+  for (int e = 0; e < 8; ++e) {
+    s[e] += __shfl_xor(s[e], 16);
+    s[e] += __shfl_xor(s[e], 32);
+  }
+  if (q == 0) {
+#pragma unroll
+    for (int e = 0; e < 8; ++e) red[wave][cl + e] = s[e];
+  }
+  __syncthreads();
+  if (wave == 0 && q == 0 && col < N) {
+    float t[8];
+#pragma unroll
+    for (int e = 0; e < 8; ++e) t[e] = ((red[0][cl + e] + red[1][cl + e]) + red[2][cl + e]) + red[3][cl + e];
+    float* o = part + chunk * N + col;
+    *(f32x4*)o = (f32x4){t[0], t[1], t[2], t[3]};
+    *(f32x4*)(o + 4) = (f32x4){t[4], t[5], t[6], t[7]};
+  }
+}
+
+// 64 columns per workgroup; thread (w, c) adds chunks [w * per, (w + 1) * per)
+// of column c, eight loads in flight, in chunk order.
+__global__ __launch_bounds__(256) void bias_grad_finish_kernel(const float* __restrict__ part, bf16* __restrict__ out,
+                                                               int64_t N, int64_t chunks) {
+  __shared__ float red[4][64];
+  const int w = (int)(threadIdx.x >> 6), c = (int)(threadIdx.x & 63);
+  const int64_t col = (int64_t)blockIdx.x * 64 + c;
+  const int64_t per = (chunks + 3) / 4;
+  const int64_t c0 = min(w * per, chunks), c1 = min(c0 + per, chunks);
+  float s = 0.f;
+  if (col < N) {
+    int64_t k = c0;
+    for (; k + 8 <= c1; k += 8) {
+      float v[8];
+#pragma unroll
+      for (int i = 0; i < 8; ++i) v[i] = part[(k + i) * N + col];
+#pragma unroll
+      for (int i = 0; i < 8; ++i) s += v[i];
+    }
+    for (; k < c1; ++k) s += part[k * N + col];
+  }
+  red[w][c] = s;
+  __syncthreads();
+  if (w == 0 && col < N) out[col] = (bf16)(((red[0][c] + red[1][c]) + red[2][c]) + red[3][c]);
+}
+
+static int64_t bias_grad_chunks(int64_t m) { return (m + BG_ROWS - 1) / BG_ROWS; }
+
+}  // namespace strata
+
+extern "C" int64_t strata_hip_bias_grad_workspace(int64_t m, int64_t n) {
+  return m > 0 && n > 0 ? strata::bias_grad_chunks(m) * n : 0;
+}
+
+extern "C" int strata_hip_bias_grad(const strata_hip_bias_grad_args* a, void* stream) {
+  using namespace strata;
+  if (!a) return fail(STRATA_HIP_EINVAL, "bias_grad: null args");
+  if (a->m < 0 || a->n < 0) return fail(STRATA_HIP_EINVAL, "bias_grad: bad m/n");
+  if (a->n == 0) return STRATA_HIP_OK;
+  if (!a->out || (a->m > 0 && (!a->g || !a->workspace))) return fail(STRATA_HIP_EINVAL, "bias_grad: null pointer");
+  if (a->n % 8 || (a->m > 1 && (a->ldg < a->n || a->ldg % 8)) || ((uintptr_t)a->g & 15) || ((uintptr_t)a->workspace & 15))
+    return fail(STRATA_HIP_EINVAL,
+                "bias_grad: n and the row stride must be multiples of 8 (stride >= n), g and workspace 16-byte aligned");
+  const int64_t chunks = bias_grad_chunks(a->m);
+  const int64_t cblocks = (a->n + 127) / 128;
+  if (chunks > 65535 || cblocks > 0x7fffffff) return fail(STRATA_HIP_EUNSUPPORTED, "bias_grad: too many rows");
+  hipStream_t st = (hipStream_t)stream;
+  if (a->m > 0)
+    hipLaunchKernelGGL(bias_grad_partial_kernel, dim3((unsigned)cblocks, (unsigned)chunks), dim3(256), 0, st,
+                       (const bf16*)a->g, a->workspace, a->m, a->n, a->m > 1 ? a->ldg : a->n);
+  hipLaunchKernelGGL(bias_grad_finish_kernel, dim3((unsigned)((a->n + 63) / 64)), dim3(256), 0, st,
+                     (const float*)a->workspace, (bf16*)a->out, a->n, a->m > 0 ? chunks : 0);
+  return check_launch("bias_grad kernels");
+}

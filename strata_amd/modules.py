@@ -157,10 +157,15 @@ class FusedNA3DAttention(nn.Module):
         if rope is not None:
             qw = self.q_norm.weight if self.q_norm is not None else None
             kw = self.k_norm.weight if self.k_norm is not None else None
-            # v is read straight out of qkv (a strided view): the pack writes q and k only
-            q, k, _ = ops.rope_qkv_pack(qkv, rope[0], rope[1], H, self.rope_layout, self.qk_norm, self.qk_norm_eps,
-                                        qw, kw, pack_v=False)
-            v = qkv.view(B, Z, Y, X, 3, H, D)[..., 2, :, :]
+            # Inference: v is read straight out of qkv (a strided view), the pack writes q and
+            # k only.  Training: the pack copies v too, so the backward writes d(qkv) in one
+            # pass (its v columns from dv) instead of zero-filling it, scattering dv into the
+            # view and adding the two.
+            train = torch.is_grad_enabled() and qkv.requires_grad
+            q, k, v = ops.rope_qkv_pack(qkv, rope[0], rope[1], H, self.rope_layout, self.qk_norm, self.qk_norm_eps,
+                                        qw, kw, pack_v=train)
+            if not train:
+                v = qkv.view(B, Z, Y, X, 3, H, D)[..., 2, :, :]
         else:
             qkv6 = qkv.view(B, Z, Y, X, 3, H, D)
             q, k, v = qkv6[..., 0, :, :], qkv6[..., 1, :, :], qkv6[..., 2, :, :]

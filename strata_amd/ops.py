@@ -516,13 +516,47 @@ def _gemm_backward(ctx, dout):
     x2 = x.reshape(-1, x.shape[-1])
     dx = (g2 @ w).reshape(x.shape) if ctx.needs_input_grad[0] else None
     dw = (g2.t() @ x2) if ctx.needs_input_grad[1] else None
-    db = g2.float().sum(0).to(bias.dtype) if ctx.has_bias and ctx.needs_input_grad[2] else None
+    db = None
+    if ctx.has_bias and ctx.needs_input_grad[2]:
+        db = bias_grad(g2) if g2.shape[-1] % 8 == 0 else g2.float().sum(0).to(bias.dtype)
     if not gate:
         dres = dout if ctx.has_res and ctx.needs_input_grad[3] else None
     return dx, dw, db, dres, None, None
 
 
 gemm_bias_act.register_autograd(_gemm_backward, setup_context=_gemm_setup_context)
+
+
+@torch.library.custom_op("strata_hip::bias_grad", mutates_args=())
+def bias_grad(g: Tensor) -> Tensor:
+    """Column sums of ``g`` ``[..., N]`` bf16 (fp32 accumulation in an order fixed by
+    the shape, rounded once to bf16): the bias gradient of a Linear whose output
+    gradient is ``g``.  N must be a multiple of 8."""
+    name = "bias_grad"
+    _require_gpu(name, g)
+    if g.dtype != torch.bfloat16:
+        raise ValueError(f"{name}: g must be bfloat16")
+    g2 = _rows(name, g, "g")
+    M, N = g2.shape
+    out = torch.empty(N, dtype=torch.bfloat16, device=g.device)
+    if N == 0:
+        return out
+    lib = _lib.load()
+    ws = torch.empty(max(int(lib.strata_hip_bias_grad_workspace(M, N)), 4), dtype=torch.float32, device=g.device)
+    a = _lib.BiasGradArgs()
+    a.g, a.out, a.workspace = g2.data_ptr(), out.data_ptr(), ws.data_ptr()
+    a.m, a.n, a.ldg = M, N, (g2.stride(0) if M > 1 else N)
+    with torch.cuda.device(g.device):
+        _lib.call("strata_hip_bias_grad", a, _stream(g))
+    return out
+
+
+@bias_grad.register_fake
+def _(g):
+    return g.new_empty((g.shape[-1],))
+
+
+bias_grad.register_autograd(_no_backward("strata_hip::bias_grad"))
 
 
 # ---------------------------------------------------------------------------

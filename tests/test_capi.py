@@ -21,6 +21,7 @@ STRUCTS = {
     "strata_hip_rope_pack_bwd_args": _lib.RopePackBwdArgs,
     "strata_hip_rope_pack_args": _lib.RopePackArgs,
     "strata_hip_gemm_args": _lib.GemmArgs,
+    "strata_hip_bias_grad_args": _lib.BiasGradArgs,
     "strata_hip_layer_norm_args": _lib.LayerNormArgs,
     "strata_hip_cube_pad_args": _lib.CubePadArgs,
     "strata_hip_cube_crop_args": _lib.CubeCropArgs,
@@ -110,6 +111,19 @@ def test_na3d_validation_rejects_before_launch(lib, over, msg):
     rc = lib.strata_hip_na3d_fwd(ctypes.byref(a), None)
     assert rc == _lib.EINVAL
     assert msg in lib.strata_hip_last_error().decode()
+
+
+def test_bias_grad_validation_and_workspace(lib):
+    assert lib.strata_hip_bias_grad_workspace(1000, 3072) == 3072  # one 1024-row chunk
+    assert lib.strata_hip_bias_grad_workspace(131072, 1024) == 128 * 1024
+    assert lib.strata_hip_bias_grad_workspace(0, 16) == 0
+    b = _lib.BiasGradArgs()
+    b.g = b.out = b.workspace = 0x1000
+    b.m, b.n, b.ldg = 64, 12, 12  # n not a multiple of 8
+    assert lib.strata_hip_bias_grad(ctypes.byref(b), None) == _lib.EINVAL
+    assert "multiples of 8" in lib.strata_hip_last_error().decode()
+    b.n, b.ldg, b.workspace = 16, 16, None
+    assert lib.strata_hip_bias_grad(ctypes.byref(b), None) == _lib.EINVAL
 
 
 def test_gemm_and_layernorm_validation(lib):

@@ -244,6 +244,26 @@ def test_rope_pack_stereographic_tables(gpu):
     assert torch.equal(v.cpu(), qkv.view(B, Z, 64, 64, 3, H, D)[..., 2, :, :])
 
 
+@pytest.mark.parametrize("M, N, ld", [(131072, 1024, 1024), (1000, 3072, 3072), (5, 8, 8), (300, 512, 520),
+                                        (0, 16, 16)])
+def test_bias_grad_vs_fp64(gpu, M, N, ld):
+    """Column sums (the GEMM backward's bias gradient) against float64, rows strided
+    when ld > N, and bit for bit the same on a second call."""
+    g = torch.Generator().manual_seed(M + N)
+    full = (_randn((max(M, 1), ld), g) * 2 + 0.25).bfloat16()[:M]
+    x = full.to(gpu)[:, :N]
+    out = torch.ops.strata_hip.bias_grad(x)
+    again = torch.ops.strata_hip.bias_grad(x)
+    torch.cuda.synchronize()
+    ref = full[:, :N].double().sum(0)
+    assert out.shape == (N,) and out.dtype == torch.bfloat16
+    assert torch.equal(out, again)
+    if M == 0:
+        assert (out == 0).all()
+    else:
+        assert ((out.double().cpu() - ref).abs() <= ref.abs() * 2**-8 + 1e-3 * M**0.5).all()
+
+
 @pytest.mark.parametrize("C", [64, 256, 768, 1024, 3840, 4096])
 def test_layer_norm(gpu, C):
     g = torch.Generator().manual_seed(C)
