@@ -40,12 +40,13 @@ struct Na3dParams {
   int dil[3];
   float scale;
   int64_t qs[5], ks[5], vs[5], os[5];
-  float* lse;  // [B, ext0, ext1, ext2, H] log2-sum-exp of the log2-unit scores, or null
+  float* lse;  // [B, ext0, lse_ext1, ext2, H] log2-sum-exp of the log2-unit scores, or null
+  int lse_ext1;  // y extent of the lse array: the caller's box, also for a y sub-box (lse then shifted)
 };
 
 // Index of query (box coordinates ez, ey, ex) in the lse output.
 __device__ __forceinline__ int64_t lse_index(const Na3dParams& p, int b, int ez, int ey, int ex, int h) {
-  return ((((int64_t)b * p.ext[0] + ez) * p.ext[1] + ey) * p.ext[2] + ex) * p.H + h;
+  return ((((int64_t)b * p.ext[0] + ez) * p.lse_ext1 + ey) * p.ext[2] + ex) * p.H + h;
 }
 
 // ---------------------------------------------------------------------------
@@ -678,6 +679,7 @@ __device__ __forceinline__ void na3d_strip_tile_exact(const Na3dParams* pp, Stri
     }
   }
   if (!valid) return;
+  if (p.lse && dq == 0) p.lse[lse_index(p, t.b, rz - p.org[0], ry - p.org[1], rx - p.org[2], t.h)] = m + __log2f(l);
   const float inv = 1.f / l;
   char* op = (char*)p.o + 2 * ((int64_t)t.b * p.os[0] + (int64_t)(rz - p.org[0]) * p.os[1] +
                                (int64_t)(ry - p.org[1]) * p.os[2] + (int64_t)(rx - p.org[2]) * p.os[3] +
@@ -1148,8 +1150,9 @@ constexpr int strip_fast_lds_bytes() {
 }
 
 // `lds`: the workgroup's LDS (strip_fast_lds_bytes), 1 KiB aligned; `id`: its
-// work-unit index in [0, sg.total) (as na3d_mfma_body).
-template <int D, int TX, int RPS, int NBUF, int KY>
+// work-unit index in [0, sg.total) (as na3d_mfma_body).  LSE: write p.lse (a
+// separate instance, so the inference kernels carry none of it).
+template <int D, int TX, int RPS, int NBUF, int KY, bool LSE = false>
 __device__ __forceinline__ void na3d_strip_fast_body(const Na3dParams p, const Na3dStrips sg, char* lds, int id) {
 #if defined(__HIP_DEVICE_COMPILE__)
   constexpr int NWX = NA3D_NWX;
@@ -1345,6 +1348,9 @@ __device__ __forceinline__ void na3d_strip_fast_body(const Na3dParams p, const N
     const int qy = ys + TY * j + trow;
     const bool valid = qy < ye && qx < qx1;
     if (valid) {
+      // p = 2^s with no reference: the row sum's log2 is the log2-sum-exp itself
+      if (LSE && g == 0)
+        p.lse[lse_index(p, b, rz - p.org[0], gy + dy * qy - p.org[1], gx + dx * qx - p.org[2], h)] = __log2f(l);
       const float inv = 1.f / l;
       char* op = obase + ooff + (int64_t)qy * orow;
 #pragma unroll
@@ -1562,10 +1568,10 @@ __device__ __forceinline__ void na3d_strip_fast_body(const Na3dParams p, const N
 
 // Two workgroups per CU (the 13-row window: 64 KiB of LDS each, ~230 VGPRs);
 // three for 5-row windows (48 KiB of LDS, 163 VGPRs; wider windows would spill).
-template <int D, int TX, int RPS, int NBUF, int KY>
+template <int D, int TX, int RPS, int NBUF, int KY, bool LSE>
 __global__ __launch_bounds__(256, TX == 8 && KY <= 5 ? 3 : 2) void na3d_strip_fast_kernel(Na3dParams p, Na3dStrips sg) {
   __shared__ __attribute__((aligned(1024))) char lds[strip_fast_lds_bytes<D, TX, RPS, NBUF>()];
-  na3d_strip_fast_body<D, TX, RPS, NBUF, KY>(p, sg, lds, (int)__builtin_amdgcn_workgroup_id_x());
+  na3d_strip_fast_body<D, TX, RPS, NBUF, KY, LSE>(p, sg, lds, (int)__builtin_amdgcn_workgroup_id_x());
 }
 
 // Small windows in one launch: the regular strips of the rows whose y window is
@@ -1574,7 +1580,7 @@ __global__ __launch_bounds__(256, TX == 8 && KY <= 5 ? 3 : 2) void na3d_strip_fa
 // edge workgroups fill the strips' tail instead of running after them.  Workgroup
 // ids [0, n0) take the strips, [n0, n0 + n1) the top edge, the rest the bottom
 // edge; n0 and n1 are multiples of 8, so each part keeps its XCD-aware tile order.
-template <int KY>
+template <int KY, bool LSE>
 __global__ __launch_bounds__(256, KY <= 5 ? 3 : 2) void na3d_small_fused_kernel(Na3dParams mid, Na3dStrips sg,
                                                                                Na3dParams e0, Na3dTiles t0,
                                                                                Na3dParams e1, Na3dTiles t1, int n0,
@@ -1584,7 +1590,7 @@ __global__ __launch_bounds__(256, KY <= 5 ? 3 : 2) void na3d_small_fused_kernel(
   __shared__ __attribute__((aligned(1024))) char lds[LS > LE ? LS : LE];
   const int id = (int)__builtin_amdgcn_workgroup_id_x();
   if (id < n0) {
-    if (id < sg.total) na3d_strip_fast_body<64, 8, 2, 2, KY>(mid, sg, lds, id);
+    if (id < sg.total) na3d_strip_fast_body<64, 8, 2, 2, KY, LSE>(mid, sg, lds, id);
   } else if (id < n0 + n1) {
     if (id - n0 < t0.total) na3d_mfma_body<64, 8, NTYE, 2, 2>(e0, t0, lds, id - n0);
   } else if (id - n0 - n1 < t1.total) {
@@ -1724,8 +1730,12 @@ static int launch_strip(const Na3dParams& p, hipStream_t st) {
   const int total = sg.total;
   if (total == 0) return STRATA_HIP_OK;
   if constexpr (FAST) {
-    hipLaunchKernelGGL((na3d_strip_fast_kernel<D, TX, RPS, NBUF, KY>), dim3((unsigned)total), dim3(64 * NA3D_NWX), 0, st,
-                       p, sg);
+    if (p.lse)
+      hipLaunchKernelGGL((na3d_strip_fast_kernel<D, TX, RPS, NBUF, KY, true>), dim3((unsigned)total),
+                         dim3(64 * NA3D_NWX), 0, st, p, sg);
+    else
+      hipLaunchKernelGGL((na3d_strip_fast_kernel<D, TX, RPS, NBUF, KY, false>), dim3((unsigned)total),
+                         dim3(64 * NA3D_NWX), 0, st, p, sg);
     return check_launch("na3d_strip_fast_kernel");
   } else {
     hipLaunchKernelGGL((na3d_strip_kernel<D, TX, RPS, NBUF>), dim3((unsigned)total), dim3(64 * NA3D_NWX), 0, st, p, sg);
@@ -1765,11 +1775,11 @@ static bool strip_regular(const Na3dParams& p) {
 
 // Small windows on regular strips (na3d_strip_fast_kernel with 2 x 8 tiles and
 // two rows per stage): head_dim 64, kx <= 9 (an 8-column tile's x-union fits one
-// 16-key block), ky in {5, 7, 9}, kz >= 2, no y dilation, and no lse output.
+// 16-key block), ky in {5, 7, 9}, kz >= 2, no y dilation.
 // Only query rows whose y window is not clamped form regular strips; the host
 // splits the query box in y and gives the clamped edge rows to the general kernel.
 static bool small_strip_fits(const Na3dParams& p) {
-  if (p.D != 64 || p.lse || p.ker[0] < 2 || p.ker[2] > 9 || p.dil[1] != 1) return false;
+  if (p.D != 64 || p.ker[0] < 2 || p.ker[2] > 9 || p.dil[1] != 1) return false;
   if (p.ker[1] != 5 && p.ker[1] != 7 && p.ker[1] != 9) return false;
   if (p.L[1] >= 4096) return false;
   const int64_t* sd[3] = {p.qs, p.ks, p.vs};
@@ -1785,6 +1795,7 @@ static int launch_mfma_d(const Na3dParams& p, hipStream_t st);
 static Na3dParams y_sub_box(const Na3dParams& p, int y0, int y1) {
   Na3dParams s = p;
   s.o = (char*)p.o + 2 * (int64_t)(y0 - p.org[1]) * p.os[2];
+  if (p.lse) s.lse = p.lse + (int64_t)(y0 - p.org[1]) * p.ext[2] * p.H;
   s.org[1] = y0;
   s.ext[1] = y1 - y0;
   return s;
@@ -1807,13 +1818,28 @@ static int launch_small_strips(const Na3dParams& p, hipStream_t st) {
   const dim3 grid((unsigned)total), block(64 * NA3D_NWX);
   switch (p.ker[1]) {
     case 5:
-      hipLaunchKernelGGL(na3d_small_fused_kernel<5>, grid, block, 0, st, mid, sg, e0, t0, e1, t1, (int)n0, (int)n1);
+      if (p.lse)
+        hipLaunchKernelGGL((na3d_small_fused_kernel<5, true>), grid, block, 0, st, mid, sg, e0, t0, e1, t1, (int)n0,
+                           (int)n1);
+      else
+        hipLaunchKernelGGL((na3d_small_fused_kernel<5, false>), grid, block, 0, st, mid, sg, e0, t0, e1, t1, (int)n0,
+                           (int)n1);
       break;
     case 7:
-      hipLaunchKernelGGL(na3d_small_fused_kernel<7>, grid, block, 0, st, mid, sg, e0, t0, e1, t1, (int)n0, (int)n1);
+      if (p.lse)
+        hipLaunchKernelGGL((na3d_small_fused_kernel<7, true>), grid, block, 0, st, mid, sg, e0, t0, e1, t1, (int)n0,
+                           (int)n1);
+      else
+        hipLaunchKernelGGL((na3d_small_fused_kernel<7, false>), grid, block, 0, st, mid, sg, e0, t0, e1, t1, (int)n0,
+                           (int)n1);
       break;
     default:
-      hipLaunchKernelGGL(na3d_small_fused_kernel<9>, grid, block, 0, st, mid, sg, e0, t0, e1, t1, (int)n0, (int)n1);
+      if (p.lse)
+        hipLaunchKernelGGL((na3d_small_fused_kernel<9, true>), grid, block, 0, st, mid, sg, e0, t0, e1, t1, (int)n0,
+                           (int)n1);
+      else
+        hipLaunchKernelGGL((na3d_small_fused_kernel<9, false>), grid, block, 0, st, mid, sg, e0, t0, e1, t1, (int)n0,
+                           (int)n1);
       break;
   }
   return check_launch("na3d_small_fused_kernel");
@@ -1877,6 +1903,7 @@ extern "C" int strata_hip_na3d_fwd(const strata_hip_na3d_args* a, void* stream) 
   }
   p.scale = a->scale;
   p.lse = a->lse;
+  p.lse_ext1 = a->q_extent[1];
   if (p.lse && ((uintptr_t)p.lse & 3u)) return fail(STRATA_HIP_EINVAL, "na3d: lse must be 4-byte aligned");
   if ((int64_t)p.B * p.ext[0] * p.ext[1] * p.ext[2] == 0) return STRATA_HIP_OK;
   hipStream_t st = (hipStream_t)stream;
@@ -1915,9 +1942,7 @@ extern "C" int strata_hip_na3d_fwd(const strata_hip_na3d_args* a, void* stream) 
       return launch_mfma_d<32>(p, st);
     case 64:
       if (strip_fits(p))
-        // the regular-strip kernel keeps no softmax reference: no lse output
-        return strip_regular(p) && !p.lse ? launch_strip<64, 4, 4, 2, true>(p, st)
-                                          : launch_strip<64, 4, 4, 2, false>(p, st);
+        return strip_regular(p) ? launch_strip<64, 4, 4, 2, true>(p, st) : launch_strip<64, 4, 4, 2, false>(p, st);
       if (small_strip_fits(p) && !std::getenv("STRATA_HIP_NA3D_NO_SMALL_STRIPS")) return launch_small_strips(p, st);
       return launch_mfma_d<64>(p, st);
     default:

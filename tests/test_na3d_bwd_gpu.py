@@ -105,39 +105,69 @@ def test_bwd_mfma_matches_valu_path(gpu, case, monkeypatch):
         assert rel_l2(a.float(), b.float()) <= 1e-2
 
 
-def _plain_takes_small_strips(shape, kernel, dil, dtype):
-    """Whether a whole-grid forward without lse runs the reference-free small-window
-    strip kernel (bf16, head_dim 64, kz >= 2, kx <= 9, ky in {5, 7, 9}, no y dilation,
-    at least two query rows whose y window is not clamped); the lse request cannot."""
-    Y, D = shape[2], shape[5]
-    return (dtype == torch.bfloat16 and D == 64 and kernel[0] >= 2 and kernel[2] <= 9 and kernel[1] in (5, 7, 9)
-            and dil[1] == 1 and Y - 2 * (kernel[1] // 2) >= 2)
-
-
 @pytest.mark.parametrize("case", CASES, ids=str)
 @pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16], ids=["f32", "bf16"])
 def test_forward_lse_vs_oracle(gpu, case, dtype):
-    """The forward's log2-sum-exp (scalar, general MFMA and strip kernels) against
-    the oracle's, and the output unchanged by asking for it: bit for bit when one
-    kernel serves both requests, within bf16 rounding when the plain request runs
-    the reference-free small-window strips."""
+    """The forward's log2-sum-exp (scalar, general MFMA and strip kernels, the
+    reference-free strips included: their row sum is 2^lse itself) against the
+    oracle's, and the output unchanged by asking for it, bit for bit (the same
+    kernels serve both requests)."""
     shape, kernel, dil = case
     (q, k, v, _), (qg, kg, vg, _) = _inputs(shape, 5, dtype, gpu)
     out, lse = torch.ops.strata_hip.na3d_fwd_lse(qg, kg, vg, list(kernel), list(dil), None)
     plain = _fwd(qg, kg, vg, kernel, dil)
-    if _plain_takes_small_strips(shape, kernel, dil, dtype):
-        assert rel_l2(out.float(), plain.float()) <= 4e-3
-    else:
-        assert torch.equal(out, plain)
+    assert torch.equal(out, plain)
     _, ref = O.na3d(q, k, v, kernel, dil, compute_dtype=torch.float64, return_lse=True)
     # bf16: the kernels score bf16(scale*log2(e)*q) against k, a 2^-9 relative rounding of q
     tol = 1e-4 if dtype == torch.float32 else 3e-2
     assert (lse.double().cpu() - ref).abs().max().item() <= tol
 
 
+def _box_lse(qg, kg, vg, kernel, org, ext):
+    """The C ABI's forward over a query box with the lse output; (out, lse)."""
+    from strata_amd import _lib
+
+    H = qg.shape[4]
+    out = torch.empty((1, *ext, H, 64), dtype=torch.bfloat16, device=qg.device)
+    lse = torch.empty((1, *ext, H), dtype=torch.float32, device=qg.device)
+    a = _lib.Na3dArgs()
+    a.q, a.k, a.v, a.out, a.lse = qg.data_ptr(), kg.data_ptr(), vg.data_ptr(), out.data_ptr(), lse.data_ptr()
+    a.dtype, a.batch, a.heads, a.head_dim, a.scale = _lib.BF16, 1, H, 64, 64**-0.5
+    a.grid[:], a.q_origin[:], a.q_extent[:] = qg.shape[1:4], org, ext
+    a.kernel[:], a.dilation[:] = kernel, [1, 1, 1]
+    a.q_stride[:], a.k_stride[:], a.v_stride[:] = ([qg.stride(i) for i in range(5)],) * 3
+    a.o_stride[:] = [out.stride(i) for i in range(5)]
+    _lib.call("strata_hip_na3d_fwd", a, torch.cuda.current_stream().cuda_stream)
+    torch.cuda.synchronize()
+    return out, lse
+
+
+def test_forward_lse_exact_path_on_the_regular_strip(gpu):
+    """A query with a key scoring ~162 log2 units overflows the reference-free strip
+    softmax; the tile's exact recompute writes its lse (~162) as well as its output."""
+    shape = (1, 3, 20, 28, 1, 64)
+    g = torch.Generator().manual_seed(8)
+    q, k, v = (torch.randn(shape, generator=g) for _ in range(3))
+    u = torch.zeros(64)
+    u[:32] = 1.0 / 32**0.5
+    w = torch.zeros(64)
+    w[32:] = 1.0 / 32**0.5
+    q[0, 1, 9, 10, 0] = 30.0 * u
+    k[0, 1, 9, 10, 0] = 2.0 * w
+    k[0, 2, 12, 14, 0] = 30.0 * u
+    q, k, v = (t.bfloat16() for t in (q, k, v))
+    org, ext = (0, 6, 6), (3, 8, 16)
+    out, lse = _box_lse(q.to(gpu), k.to(gpu), v.to(gpu), (3, 13, 13), org, ext)
+    ref_o, ref_l = O.na3d(q, k, v, (3, 13, 13), q_origin=org, q_extent=ext, compute_dtype=torch.float64,
+                          return_lse=True)
+    assert torch.isfinite(lse).all()
+    assert rel_l2(out.float().cpu(), ref_o.float()) <= 1e-2
+    assert (lse.double().cpu() - ref_l).abs().max().item() <= 3e-2
+    assert lse[0, 1, 3, 4, 0].item() > 150
+
+
 def test_forward_lse_of_a_query_box_on_the_regular_strip_shape(gpu):
-    """A halo-interior box that would take the reference-free strip kernel takes
-    the strip kernel with a softmax reference when the lse is asked for."""
+    """A halo-interior box on the reference-free strip kernel, with the lse asked for."""
     from strata_amd import _lib
 
     shape, kernel, org, ext = (1, 3, 24, 30, 2, 64), (3, 13, 13), (0, 6, 7), (3, 10, 13)
