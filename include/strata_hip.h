@@ -275,6 +275,14 @@ typedef struct strata_hip_gemm_args {
 
 int strata_hip_gemm_bias_act(const strata_hip_gemm_args* args, void* stream);
 
+/* fc1 -> GELU(tanh) for training (the Mlp of screamcast/checkpoint_compat.py:243-249
+ * under loss.backward(), train.py:1161): strata_hip_gemm_bias_act with act =
+ * GELU_TANH and no residual, and in the same launch dact = gelu'(x @ w^T + bias),
+ * bf16 [M, N] with out's row stride ldo, the derivative the backward multiplies
+ * by the upstream gradient (instead of recomputing the GEMM).  K must be a
+ * multiple of 64 (STRATA_HIP_EUNSUPPORTED otherwise: the caller then recomputes). */
+int strata_hip_gemm_gelu_save(const strata_hip_gemm_args* args, void* dact, void* stream);
+
 /* Bias gradient of the GEMM backward (nn.Linear's d bias: the output gradient
  * summed over rows, as torch autograd forms it when training reaches the
  * block's Linears through train.py:1161):  out[n] = sum_m g[m, n].

@@ -272,6 +272,7 @@ EXPORTS = {
     "strata_hip_na3d_bwd_noalloc": ([ctypes.POINTER(Na3dBwdArgs), ctypes.c_void_p], ctypes.c_int),
     "strata_hip_rope_qkv_pack": ([ctypes.POINTER(RopePackArgs), ctypes.c_void_p], ctypes.c_int),
     "strata_hip_gemm_bias_act": ([ctypes.POINTER(GemmArgs), ctypes.c_void_p], ctypes.c_int),
+    "strata_hip_gemm_gelu_save": ([ctypes.POINTER(GemmArgs), ctypes.c_void_p, ctypes.c_void_p], ctypes.c_int),
     "strata_hip_bias_grad": ([ctypes.POINTER(BiasGradArgs), ctypes.c_void_p], ctypes.c_int),
     "strata_hip_bias_grad_workspace": ([ctypes.c_int64, ctypes.c_int64], ctypes.c_int64),
     "strata_hip_layer_norm": ([ctypes.POINTER(LayerNormArgs), ctypes.c_void_p], ctypes.c_int),

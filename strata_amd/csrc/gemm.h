@@ -12,6 +12,7 @@ struct GemmParams {
   const bf16* bias;
   const bf16* res;
   bf16* out;
+  bf16* out2;  // the SAVE instance of the DMA kernel: gelu'(pre-activation), row stride ldo
   int64_t M, N, K;
   int64_t ldx, ldw, ldr, ldo;
   int act;

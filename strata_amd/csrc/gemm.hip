@@ -300,7 +300,9 @@ __device__ __forceinline__ int gswz(int chunk, int row) {
 // The ring runs on across the tiles of the persistent walk: the last K step
 // of a tile issues the next tile's first stage, whose copy then lands while
 // the epilogue runs in the other slot.
-template <int BM, int BN, int WGM, int WGN, int BK, int NST, int ACT, int RES>
+// SAVE: also write act'(pre-activation) (GELU(tanh) only) to p.out2, for a
+// backward that then needs no recomputed GEMM.
+template <int BM, int BN, int WGM, int WGN, int BK, int NST, int ACT, int RES, bool SAVE = false>
 __device__ __forceinline__ void gemm_dma_body(const GemmParams& p) {
   constexpr int NW = WGM * WGN;
   constexpr int WTM = BM / WGM;  // 128
@@ -561,6 +563,46 @@ __device__ __forceinline__ void gemm_dma_body(const GemmParams& p) {
         }
       }
     }
+    if constexpr (SAVE) {  // the derivative of the same half through the same slab, to out2
+      static_assert(ACT == STRATA_HIP_ACT_GELU_TANH, "SAVE: GELU(tanh) only");
+#pragma unroll
+      for (int i = 0; i < FN; ++i)
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+          const int nl = 32 * i + 8 * q + 4 * hi;
+#pragma unroll
+          for (int jj = 0; jj < HM; ++jj) {
+            const int j = half * HM + jj;
+            float v[4];
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+              // recomputed, not shared with the first pass: sharing would hold the whole
+              // half's sigmoids in registers between the two passes
+              float xv = acc[i][j][4 * q + e];
+              asm volatile("" : "+v"(xv));
+              v[e] = gelu_tanh_grad(xv);
+            }
+            const int ml = 32 * jj + l32;
+            const u32x2 w2 = {pack_bf16x2(v[0], v[1]), pack_bf16x2(v[2], v[3])};
+            *(u32x2*)(slab + ml * SRB + (((nl >> 3) ^ (ml & 7)) << 4) + 8 * hi) = w2;
+          }
+        }
+#pragma unroll
+      for (int it = half * (NIT / 2); it < (half + 1) * (NIT / 2); ++it) {
+        const int ml = RPI * it + lane / CPR;
+        const int sl = ml - half * (WTM / 2);
+        const u32x4 w4 = *(const u32x4*)(slab + sl * SRB + ((c ^ (sl & 7)) << 4));
+        const int64_t gm = gm0 + ml;
+        if (full || (gm < p.M && gn + 8 <= p.N)) {
+          __builtin_nontemporal_store(w4, (u32x4*)(p.out2 + gm * p.ldo + gn));
+        } else if (gm < p.M && gn < p.N) {
+          for (int e = 0; e < 8 && gn + e < p.N; ++e) {
+            const uint32_t wd = w4[e >> 1];
+            p.out2[gm * p.ldo + gn + e] = (bf16)((e & 1) ? bf16_hi(wd) : bf16_lo(wd));
+          }
+        }
+      }
+    }
   }
   }  // tiles
 }
@@ -569,9 +611,9 @@ __device__ __forceinline__ void gemm_dma_body(const GemmParams& p) {
 // 128 KiB ring.  (Measured alternatives at the block's shapes, all slower:
 // 256 x 128 tiles at two workgroups per CU; K step 32 with 3-5 stages; four
 // waves of 128 x 128 with the accumulators in AGPRs.)
-template <int ACT, int RES>
+template <int ACT, int RES, bool SAVE = false>
 __global__ __launch_bounds__(512, 1) void gemm_dma_kernel(GemmParams p) {
-  gemm_dma_body<256, 256, 2, 4, 64, 2, ACT, RES>(p);
+  gemm_dma_body<256, 256, 2, 4, 64, 2, ACT, RES, SAVE>(p);
 }
 
 template <int ACT>
@@ -611,27 +653,31 @@ static int launch_gemm(GemmParams p, hipStream_t st) {
 
 using namespace strata;
 
-extern "C" int strata_hip_gemm_bias_act(const strata_hip_gemm_args* a, void* stream) {
+namespace strata {
+
+// Argument checks shared by the GEMM entry points; fills p (tile counts aside).
+static int gemm_params(const strata_hip_gemm_args* a, GemmParams& p) {
   if (!a) return fail(STRATA_HIP_EINVAL, "gemm: null args");
   if (a->m < 0 || a->n < 0 || a->k <= 0) return fail(STRATA_HIP_EINVAL, "gemm: bad m/n/k");
-  if (a->m == 0 || a->n == 0) return STRATA_HIP_OK;
-  if (!a->x || !a->w || !a->out) return fail(STRATA_HIP_EINVAL, "gemm: null x, w or out");
-  if (a->k % 8 != 0) return fail(STRATA_HIP_EINVAL, "gemm: k must be a multiple of 8");
-  if (a->ldx < a->k || a->ldw < a->k || a->ldo < a->n || (a->residual && a->ldr < a->n))
-    return fail(STRATA_HIP_EINVAL, "gemm: row stride smaller than the row length");
-  if (a->ldx % 8 || a->ldw % 8 || a->ldo % 4 || (a->residual && a->ldr % 4))
-    return fail(STRATA_HIP_EINVAL, "gemm: x/w row strides must be multiples of 8, out/residual of 4");
-  if (((uintptr_t)a->x & 15) || ((uintptr_t)a->w & 15) || ((uintptr_t)a->out & 7) ||
-      (a->residual && ((uintptr_t)a->residual & 7)) || (a->bias && ((uintptr_t)a->bias & 7)))
-    return fail(STRATA_HIP_EINVAL, "gemm: x/w must be 16-byte aligned, out/residual/bias 8-byte aligned");
+  if (a->m > 0 && a->n > 0) {
+    if (!a->x || !a->w || !a->out) return fail(STRATA_HIP_EINVAL, "gemm: null x, w or out");
+    if (a->k % 8 != 0) return fail(STRATA_HIP_EINVAL, "gemm: k must be a multiple of 8");
+    if (a->ldx < a->k || a->ldw < a->k || a->ldo < a->n || (a->residual && a->ldr < a->n))
+      return fail(STRATA_HIP_EINVAL, "gemm: row stride smaller than the row length");
+    if (a->ldx % 8 || a->ldw % 8 || a->ldo % 4 || (a->residual && a->ldr % 4))
+      return fail(STRATA_HIP_EINVAL, "gemm: x/w row strides must be multiples of 8, out/residual of 4");
+    if (((uintptr_t)a->x & 15) || ((uintptr_t)a->w & 15) || ((uintptr_t)a->out & 7) ||
+        (a->residual && ((uintptr_t)a->residual & 7)) || (a->bias && ((uintptr_t)a->bias & 7)))
+      return fail(STRATA_HIP_EINVAL, "gemm: x/w must be 16-byte aligned, out/residual/bias 8-byte aligned");
+  }
   if (a->act < STRATA_HIP_ACT_NONE || a->act > STRATA_HIP_ACT_SIGMOID_GRAD) return fail(STRATA_HIP_EINVAL, "gemm: bad act");
   if (a->res_op != STRATA_HIP_RES_ADD && a->res_op != STRATA_HIP_RES_MUL) return fail(STRATA_HIP_EINVAL, "gemm: bad res_op");
-  GemmParams p;
   p.x = (const bf16*)a->x;
   p.w = (const bf16*)a->w;
   p.bias = (const bf16*)a->bias;
   p.res = (const bf16*)a->residual;
   p.out = (bf16*)a->out;
+  p.out2 = nullptr;
   p.M = a->m;
   p.N = a->n;
   p.K = a->k;
@@ -641,6 +687,29 @@ extern "C" int strata_hip_gemm_bias_act(const strata_hip_gemm_args* a, void* str
   p.ldo = a->ldo;
   p.act = a->act;
   p.res_op = a->res_op;
+  return STRATA_HIP_OK;
+}
+
+// The large-tile kernels stream 64-wide K steps with 32-bit lane offsets
+// inside a 256-row block: K a multiple of 64, row strides small enough.
+// Sets the tile counts; the persistent grid is one workgroup per CU (the
+// 128 KiB ring admits one).
+static bool gemm_big(GemmParams& p, dim3& grid) {
+  if (!(p.K % 64 == 0 && 256 * p.ldx * 2 + 4096 < (int64_t)OOB && 256 * p.ldw * 2 + 4096 < (int64_t)OOB)) return false;
+  p.mt = (int)((p.M + 255) / 256);
+  p.nt = (int)((p.N + 255) / 256);
+  const int64_t total = (int64_t)p.mt * p.nt;
+  const int cus = device_cus();
+  grid = dim3((unsigned)(total < cus ? total : cus));
+  return total <= 0x7fffffff;
+}
+
+}  // namespace strata
+
+extern "C" int strata_hip_gemm_bias_act(const strata_hip_gemm_args* a, void* stream) {
+  GemmParams p;
+  if (const int rc = gemm_params(a, p)) return rc;
+  if (a->m == 0 || a->n == 0) return STRATA_HIP_OK;
   hipStream_t st = (hipStream_t)stream;
   // Plain GEMMs (no activation; bias and an added residual at most) go to
   // hipBLASLt; the fused epilogues, and anything it declines, run here.
@@ -652,17 +721,8 @@ extern "C" int strata_hip_gemm_bias_act(const strata_hip_gemm_args* a, void* str
                   "gemm: hipblasLtCreate failed on this device (plain GEMMs run on hipBLASLt; "
                   "STRATA_HIP_GEMM=native selects the hand-written kernels)");
   }
-  // The large-tile kernels stream 64-wide K steps with 32-bit lane offsets
-  // inside a 256-row block: K a multiple of 64, row strides small enough.
-  const bool big = p.K % 64 == 0 && 256 * p.ldx * 2 + 4096 < (int64_t)OOB && 256 * p.ldw * 2 + 4096 < (int64_t)OOB;
-  if (big) {
-    p.mt = (int)((p.M + 255) / 256);
-    p.nt = (int)((p.N + 255) / 256);
-    const int64_t total = (int64_t)p.mt * p.nt;
-    if (total > 0x7fffffff) return fail(STRATA_HIP_EUNSUPPORTED, "gemm: problem too large for one launch");
-    // one persistent workgroup per CU (the 128 KiB ring admits one)
-    const int cus = device_cus();
-    const dim3 grid((unsigned)(total < cus ? total : cus));
+  dim3 grid;
+  if (gemm_big(p, grid)) {
     switch (p.act) {
       case STRATA_HIP_ACT_GELU_TANH: launch_dma_act<STRATA_HIP_ACT_GELU_TANH>(p, grid, st); break;
       case STRATA_HIP_ACT_GELU_ERF: launch_dma_act<STRATA_HIP_ACT_GELU_ERF>(p, grid, st); break;
@@ -674,6 +734,22 @@ extern "C" int strata_hip_gemm_bias_act(const strata_hip_gemm_args* a, void* str
     return check_launch("gemm_dma_kernel");
   }
   return launch_gemm<128, 128, 2, 2>(p, st);
+}
+
+extern "C" int strata_hip_gemm_gelu_save(const strata_hip_gemm_args* a, void* dact, void* stream) {
+  GemmParams p;
+  if (const int rc = gemm_params(a, p)) return rc;
+  if (a->act != STRATA_HIP_ACT_GELU_TANH || a->residual)
+    return fail(STRATA_HIP_EINVAL, "gemm_gelu_save: act must be GELU_TANH, with no residual");
+  if (a->m == 0 || a->n == 0) return STRATA_HIP_OK;
+  if (!dact || ((uintptr_t)dact & 7)) return fail(STRATA_HIP_EINVAL, "gemm_gelu_save: dact must be 8-byte aligned");
+  p.out2 = (bf16*)dact;
+  dim3 grid;
+  if (!gemm_big(p, grid))
+    return fail(STRATA_HIP_EUNSUPPORTED, "gemm_gelu_save: needs K a multiple of 64 (the large-tile kernel)");
+  hipLaunchKernelGGL((gemm_dma_kernel<STRATA_HIP_ACT_GELU_TANH, RES_NONE_T, true>), grid, dim3(512), 0,
+                     (hipStream_t)stream, p);
+  return check_launch("gemm_dma_kernel (gelu save)");
 }
 
 // ---------------------------------------------------------------------------

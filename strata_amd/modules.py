@@ -35,7 +35,9 @@ class GemmGeluMlp(nn.Module):
     Drop-in for physicsnemo's ``Mlp`` (layer indices 0/2 per
     screamcast/checkpoint_compat.py:243-249; GELU(tanh) per
     screamcast/strata_wrappers.py:76-100): fc1 + bias + GELU is one launch,
-    fc2 + bias (+ the block's residual) another.
+    fc2 + bias (+ the block's residual) another.  Under autograd (tanh GELU,
+    in_features a multiple of 64) fc1's launch also writes gelu'(pre-activation),
+    which the backward multiplies by the upstream gradient.
     """
 
     def __init__(self, in_features: int, hidden_features: int, out_features: Optional[int] = None,
@@ -61,7 +63,12 @@ class GemmGeluMlp(nn.Module):
 
     def forward(self, x: Tensor, residual: Optional[Tensor] = None) -> Tensor:
         fc1, act, fc2 = self.layers
-        h = ops.gemm_bias_act(x, fc1.weight, fc1.bias, None, _ACT[act.approximate])
+        train = torch.is_grad_enabled() and (x.requires_grad or fc1.weight.requires_grad)
+        if train and act.approximate == "tanh" and x.shape[-1] % 64 == 0:
+            # fc1's launch also writes gelu'(pre-activation) for the backward (no recomputed GEMM)
+            h, _ = ops.gemm_gelu_train(x, fc1.weight, fc1.bias)
+        else:
+            h = ops.gemm_bias_act(x, fc1.weight, fc1.bias, None, _ACT[act.approximate])
         return ops.gemm_bias_act(h, fc2.weight, fc2.bias, residual, _lib.ACT_NONE)
 
 

@@ -12,6 +12,7 @@ have backwards on HIP kernels; the other ops' autograd formulas raise.
 
 from __future__ import annotations
 
+import ctypes
 import math
 from typing import Optional, Sequence
 
@@ -27,6 +28,8 @@ __all__ = [
     "na3d",
     "rope_qkv_pack",
     "gemm_bias_act",
+    "gemm_gelu_train",
+    "bias_grad",
     "layer_norm",
     "cube_pad_faces",
     "cube_crop",
@@ -525,6 +528,77 @@ def _gemm_backward(ctx, dout):
 
 
 gemm_bias_act.register_autograd(_gemm_backward, setup_context=_gemm_setup_context)
+
+
+@torch.library.custom_op("strata_hip::gemm_gelu_train", mutates_args=())
+def gemm_gelu_train(x: Tensor, w: Tensor, bias: Optional[Tensor]) -> tuple[Tensor, Tensor]:
+    """``gelu_tanh(x @ w.T + bias)`` and, from the same launch, its derivative at the
+    pre-activation ``gelu_tanh'(x @ w.T + bias)`` (bf16): the MLP's fc1 under autograd,
+    whose backward then multiplies the upstream gradient by the saved derivative
+    instead of recomputing the GEMM.  K must be a multiple of 64."""
+    name = "gemm_gelu_train"
+    _require_gpu(name, x, w, bias)
+    for t, nm in ((x, "x"), (w, "w"), (bias, "bias")):
+        if t is not None and t.dtype != torch.bfloat16:
+            raise ValueError(f"{name}: {nm} must be bfloat16, got {t.dtype}")
+    K = x.shape[-1]
+    if w.dim() != 2 or w.shape[1] != K:
+        raise ValueError(f"{name}: w must be [N, {K}], got {tuple(w.shape)}")
+    N = w.shape[0]
+    if bias is not None and tuple(bias.shape) != (N,):
+        raise ValueError(f"{name}: bias must be [{N}]")
+    x2, w2 = _rows(name, x, "x"), _rows(name, w, "w")
+    b2 = bias.contiguous() if bias is not None else None
+    out = torch.empty((*x.shape[:-1], N), dtype=torch.bfloat16, device=x.device)
+    dact = torch.empty_like(out)
+    M = x2.shape[0]
+    if M == 0 or N == 0:
+        return out, dact
+    a = _lib.GemmArgs()
+    a.x, a.w = x2.data_ptr(), w2.data_ptr()
+    a.bias = b2.data_ptr() if b2 is not None else None
+    a.residual = None
+    a.out = out.data_ptr()
+    a.m, a.n, a.k = M, N, K
+    a.ldx, a.ldw = x2.stride(0) if M > 1 else K, w2.stride(0) if N > 1 else K
+    a.ldr, a.ldo = 0, N
+    a.act, a.res_op = _lib.ACT_GELU_TANH, _lib.RES_ADD
+    lib = _lib.load()
+    with torch.cuda.device(x.device):
+        rc = lib.strata_hip_gemm_gelu_save(ctypes.byref(a), ctypes.c_void_p(dact.data_ptr()),
+                                           ctypes.c_void_p(_stream(x)))
+    if rc != _lib.OK:
+        raise _lib.StrataHipError("strata_hip_gemm_gelu_save", rc, lib.strata_hip_last_error().decode())
+    return out, dact
+
+
+@gemm_gelu_train.register_fake
+def _(x, w, bias):
+    shape = (*x.shape[:-1], w.shape[0])
+    return x.new_empty(shape), x.new_empty(shape)
+
+
+def _gelu_train_setup_context(ctx, inputs, output):
+    x, w, bias = inputs
+    _, dact = output
+    ctx.has_bias = bias is not None
+    ctx.mark_non_differentiable(dact)
+    ctx.save_for_backward(x, w, dact)
+
+
+def _gelu_train_backward(ctx, dout, _ddact):
+    x, w, dact = ctx.saved_tensors
+    g2 = (dact * dout).reshape(-1, dact.shape[-1])  # the gradient at the pre-activation
+    x2 = x.reshape(-1, x.shape[-1])
+    dx = (g2 @ w).reshape(x.shape) if ctx.needs_input_grad[0] else None
+    dw = (g2.t() @ x2) if ctx.needs_input_grad[1] else None
+    db = None
+    if ctx.has_bias and ctx.needs_input_grad[2]:
+        db = bias_grad(g2) if g2.shape[-1] % 8 == 0 else g2.float().sum(0).to(torch.bfloat16)
+    return dx, dw, db
+
+
+gemm_gelu_train.register_autograd(_gelu_train_backward, setup_context=_gelu_train_setup_context)
 
 
 @torch.library.custom_op("strata_hip::bias_grad", mutates_args=())

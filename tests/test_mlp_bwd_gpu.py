@@ -50,6 +50,29 @@ def test_gemm_autograd_vs_torch(gpu, shape, act):
         assert rel_l2(a.grad.float().cpu(), bref.grad) <= 1e-2, name
 
 
+@pytest.mark.parametrize("shape", [(300, 512, 256), (4096, 1024, 1024), (1000, 4104, 128)], ids=str)
+def test_gemm_gelu_train(gpu, shape):
+    """fc1 for training: its GELU output equals the inference launch's bit for bit, the
+    saved derivative is gelu'(x @ w.T + b) within bf16 rounding, and its autograd (the
+    derivative times the upstream gradient, then plain GEMMs and the bias gradient)
+    matches torch's Linear + GELU(tanh) backward."""
+    M, N, K = shape
+    g = torch.Generator().manual_seed(3)
+    x, w, b, dout = _bf((M, K), g), _bf((N, K), g, K**-0.5), _bf((N,), g), _bf((M, N), g)
+    xg, wg, bg = (t.to(gpu).requires_grad_(True) for t in (x, w, b))
+    out, dact = ops.gemm_gelu_train(xg, wg, bg)
+    plain = ops.gemm_bias_act(x.to(gpu), w.to(gpu), b.to(gpu), None, _lib.ACT_GELU_TANH)
+    assert torch.equal(out.detach(), plain)
+    a = (x.double() @ w.double().T + b.double()).requires_grad_(True)
+    (ga,) = torch.autograd.grad(F.gelu(a, approximate="tanh"), a, torch.ones_like(a))
+    assert rel_l2(dact.float().cpu(), ga.float()) <= 1e-2
+    out.backward(dout.to(gpu))
+    ref = [t.float().requires_grad_(True) for t in (x, w, b)]
+    F.gelu(F.linear(*ref), approximate="tanh").backward(dout.float())
+    for name, got, r in zip("xwb", (xg, wg, bg), ref):
+        assert rel_l2(got.grad.float().cpu(), r.grad) <= 1e-2, name
+
+
 def test_mlp_module_backward(gpu):
     torch.manual_seed(0)
     mlp = GemmGeluMlp(256, 1024)
