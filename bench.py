@@ -118,16 +118,18 @@ def bench_block(device, steps, warmup):
         t_ln, h = timed(lambda: ops.layer_norm(x, 1e-6))
         t_qkv, qkv = timed(lambda: ops.gemm_bias_act(h, attn.qkv.weight, attn.qkv.bias, None, 0))
         # as the block: the pack writes q and k, v is read out of qkv as a strided view
-        t_rope, (q, k, _) = timed(lambda: ops.rope_qkv_pack(qkv, cos, sin, H, 0, pack_v=False))
-        v = qkv.view(B, Z, Y, X, 3, H, C // H)[..., 2, :, :]
-        t_na, a = timed(lambda: ops.na3d_fwd(q, k, v, [3, 7, 7], [1, 1, 1], None, [0, 0, 0], [Z, Y, X]))
+        # as the block at inference: the pack writes k only, NA3D rotates the queries itself
+        t_rope, (_, k, _) = timed(lambda: ops.rope_qkv_pack(qkv, cos, sin, H, 0, pack_v=False, pack_q=False))
+        q6 = qkv.view(B, Z, Y, X, 3, H, C // H)
+        q, v = q6[..., 0, :, :], q6[..., 2, :, :]
+        t_na, a = timed(lambda: ops.na3d_fwd_rope_q(q, k, v, cos, sin, [3, 7, 7], [1, 1, 1], None))
         a = a.view(B, Z, Y, X, C)
         t_proj, x1 = timed(lambda: ops.gemm_bias_act(a, attn.proj.weight, attn.proj.bias, x, 0))
         t_fc1, f = timed(lambda: ops.gemm_bias_act(h, mlp.layers[0].weight, mlp.layers[0].bias, None, 1))
         t_fc2, _ = timed(lambda: ops.gemm_bias_act(f, mlp.layers[2].weight, mlp.layers[2].bias, x1, 0))
     gemm_flops = {"qkv": 2 * M * C * 3 * C, "proj": 2 * M * C * C, "fc1": 2 * M * C * 4 * C, "fc2": 2 * M * 4 * C * C}
     na_flops = 4.0 * M * H * 147 * (C // H)
-    rope_bytes = M * 2 * C * 2 * 2 + B * Y * X * (C // H // 2) * 4 * 2  # q/k columns read + q/k write + tables
+    rope_bytes = M * C * 2 * 2 + B * Y * X * (C // H // 2) * 4 * 2  # k columns read + k written + tables
     kernels = {
         "layer_norm_ms": t_ln,
         "qkv_gemm_ms": t_qkv,
@@ -185,16 +187,19 @@ def bench_cfg1(device, steps, warmup):
     _, _, _, qkv, cos, sin, _, _ = cfg1_inputs(torch.device("cpu"))
     qkv, cos, sin = qkv.to(device), cos.to(device), sin.to(device)
     pack = torch.ops.strata_hip.rope_qkv_pack
-    na = torch.ops.strata_hip.na3d_fwd
+    na = torch.ops.strata_hip.na3d_fwd_rope_q
 
-    def run_pack():  # q and k; v is read out of qkv as a strided view (as the block does)
-        return pack(qkv, cos, sin, H, 0, False, 1e-6, None, None, False)
+    # As the block runs it at inference: the pack rotates and writes k only; NA3D reads
+    # q (unrotated, rotated inside the kernel) and v straight out of qkv as strided views.
+    def run_pack():
+        return pack(qkv, cos, sin, H, 0, False, 1e-6, None, None, False, False)
 
-    q, k, _ = run_pack()
+    _, k, _ = run_pack()
+    q = qkv.view(B, Z, Y, X, 3, H, D)[..., 0, :, :]
     v = qkv.view(B, Z, Y, X, 3, H, D)[..., 2, :, :]
 
     def run_na():
-        return na(q, k, v, [3, 7, 7], [1, 1, 1], None, [0, 0, 0], [Z, Y, X])
+        return na(q, k, v, cos, sin, [3, 7, 7], [1, 1, 1], None)
 
     def timed(fn):
         for _ in range(warmup):
@@ -211,11 +216,11 @@ def bench_cfg1(device, steps, warmup):
     t_pack, t_na = timed(run_pack), timed(run_na)
     M = B * Z * Y * X
     flops = 4.0 * M * H * 147 * D
-    na_bytes = 4 * M * H * D * 2  # q, k, v read once, o written once
-    pack_bytes = M * 2 * H * D * 2 * 2 + cos.numel() * 4 * 2  # q/k columns read, q/k written, tables read
+    na_bytes = 4 * M * H * D * 2  # q, k, v read once, o written once (the RoPE tables: L2-resident)
+    pack_bytes = M * H * D * 2 * 2 + cos.numel() * 4 * 2  # k columns read, k written, tables read
     return {
         "workload": "configs[1] stereographic RoPE (level index in z: pairs x|y|level = 12|12|8, base 1e4) + "
-        "QKV pack (q, k; v read from qkv as a strided view), then NA3D W=(3,7,7) on [2,8,64,64,8,64] bf16, "
+        "QKV pack (k only; q rotated inside the NA3D kernel, q and v read from qkv as strided views), NA3D W=(3,7,7) on [2,8,64,64,8,64] bf16, "
         "q/k/v ~ N(0,1) seed 0",
         "na3d_ms": round(t_na, 4),
         "na3d_tflops": round(flops / (t_na * 1e-3) / 1e12, 1),

@@ -105,6 +105,27 @@ typedef struct strata_hip_na3d_args {
 int strata_hip_na3d_fwd(const strata_hip_na3d_args* args, void* stream);
 
 /* ---------------------------------------------------------------------------
+ * NA3D forward with the queries' rotary embedding applied inside the kernel.
+ * Replaces the query half of the attention forward's RoPE followed by
+ * natten.na3d (screamcast/strata_wrappers.py:331-338, the stereographic RoPE
+ * helpers imported at :52): q is the UNROTATED query (e.g. a strided view of
+ * the qkv projection's output), k already rotated (strata_hip_rope_qkv_pack
+ * with q = NULL), and the result equals strata_hip_na3d_fwd on
+ * q' = rope(q), q' rounded to bf16 as the pack rounds it.  Half layout only
+ * (pair j = (j, j + 32)); cos, sin: fp32 [B, table_z, Y, X, 32] contiguous,
+ * 16-byte aligned, indexed by each query's full-grid position; table_z = 1
+ * (broadcast over z) or Z.  bf16, head_dim 64, args->lse must be NULL (the
+ * backward needs the rotated q: training keeps the pack).  Windows and
+ * layouts that run the wide-window strip kernels (kx 10-13, ky 13) return
+ * STRATA_HIP_EUNSUPPORTED; strata_hip_na3d_fwd_rope_q_supported() answers the
+ * same question without launching (1 = supported, 0 = not).
+ * ------------------------------------------------------------------------- */
+int strata_hip_na3d_fwd_rope_q(const strata_hip_na3d_args* args, const float* cos, const float* sin, int32_t table_z,
+                               void* stream);
+int strata_hip_na3d_fwd_rope_q_supported(const strata_hip_na3d_args* args, const float* cos, const float* sin,
+                                         int32_t table_z);
+
+/* ---------------------------------------------------------------------------
  * NA3D backward: dq, dk, dv of natten.na3d for out = na3d(q, k, v) over the
  * whole grid (the autograd function of NATTEN 0.21.5 that training reaches
  * through train.py:1161), same windows, kernel, dilation and scale as the
@@ -168,6 +189,8 @@ int strata_hip_na3d_bwd_noalloc(const strata_hip_na3d_bwd_args* args, void* stre
  * the pairs of q and k; v is copied.  Any of q/k/v may alias nothing else.
  * v may be NULL: then only q and k are written (a caller that reads v straight
  * out of qkv, as a view with token stride qkv_row_stride, saves the copy).
+ * q may be NULL too: then only k (and v) are written, for a caller that
+ * rotates the queries inside NA3D (strata_hip_na3d_fwd_rope_q).
  *
  * qk_norm = 1 applies RMSNorm over D to every (token, head) of q and k before
  * the rotation, x * rsqrt(mean(x^2) + qk_norm_eps) * weight (fp32 math;

@@ -268,6 +268,10 @@ class StateUpdateArgs(ctypes.Structure):
 
 EXPORTS = {
     "strata_hip_na3d_fwd": ([ctypes.POINTER(Na3dArgs), ctypes.c_void_p], ctypes.c_int),
+    "strata_hip_na3d_fwd_rope_q": (
+        [ctypes.POINTER(Na3dArgs), ctypes.c_void_p, ctypes.c_void_p, ctypes.c_int32, ctypes.c_void_p], ctypes.c_int),
+    "strata_hip_na3d_fwd_rope_q_supported": (
+        [ctypes.POINTER(Na3dArgs), ctypes.c_void_p, ctypes.c_void_p, ctypes.c_int32], ctypes.c_int),
     "strata_hip_na3d_bwd": ([ctypes.POINTER(Na3dBwdArgs), ctypes.c_void_p], ctypes.c_int),
     "strata_hip_na3d_bwd_noalloc": ([ctypes.POINTER(Na3dBwdArgs), ctypes.c_void_p], ctypes.c_int),
     "strata_hip_rope_qkv_pack": ([ctypes.POINTER(RopePackArgs), ctypes.c_void_p], ctypes.c_int),

@@ -42,7 +42,30 @@ struct Na3dParams {
   int64_t qs[5], ks[5], vs[5], os[5];
   float* lse;  // [B, ext0, lse_ext1, ext2, H] log2-sum-exp of the log2-unit scores, or null
   int lse_ext1;  // y extent of the lse array: the caller's box, also for a y sub-box (lse then shifted)
+  // Rotary embedding of the queries inside the kernel (head_dim 64, half layout:
+  // pair j = (j, j + 32)), or rc == null: fp32 cos / sin tables [B, rzt, L1, L2, 32]
+  // indexed by each query's full-grid position, rzt = 1 or L0.
+  const float* rc;
+  const float* rs;
+  int rzt;
 };
+
+// Row of the query-RoPE tables for the full-grid position (b, z, y, x).
+__device__ __forceinline__ int64_t rope_row(const Na3dParams& p, int b, int z, int y, int x) {
+  return (((int64_t)b * p.rzt + (p.rzt == 1 ? 0 : z)) * p.L[1] + y) * p.L[2] + x;
+}
+
+// Rotate one lane's query pairs: lo holds dims j0 .. j0 + 7, hi dims j0 + 32 .. j0 + 39
+// (pairs j0 .. j0 + 7 of the half layout), c / s their cos / sin; each rotated value
+// is rounded to bf16 as the RoPE pack rounds q (rope_pack.hip, rot8).
+__device__ __forceinline__ void rope_q_pairs(bf16x8& lo, bf16x8& hi, const float* c, const float* s) {
+#pragma unroll
+  for (int e = 0; e < 8; ++e) {
+    const float a = (float)lo[e], b = (float)hi[e];
+    lo[e] = (bf16)(a * c[e] - b * s[e]);
+    hi[e] = (bf16)(a * s[e] + b * c[e]);
+  }
+}
 
 // Index of query (box coordinates ez, ey, ex) in the lse output.
 __device__ __forceinline__ int64_t lse_index(const Na3dParams& p, int b, int ez, int ey, int ex, int h) {
@@ -223,7 +246,8 @@ constexpr int mfma_lds_bytes() {
 // `lds`: the workgroup's LDS (mfma_lds_bytes), 1 KiB aligned; `id`: its tile
 // index in [0, tg.total) (the kernels pass their workgroup id; the fused
 // small-window kernel an offset one, in a block of ids starting at a multiple of 8).
-template <int D, int TX, int NTY, int RPS, int NBUF>
+// ROPE: rotate the queries (p.rc / p.rs tables; head_dim 64, half layout).
+template <int D, int TX, int NTY, int RPS, int NBUF, bool ROPE = false>
 __device__ __forceinline__ void na3d_mfma_body(const Na3dParams p, const Na3dTiles tg, char* lds, int id) {
 #if defined(__HIP_DEVICE_COMPILE__)  // the body is device code only; the host pass needs just the signature
   constexpr int NWX = NA3D_NWX;
@@ -340,6 +364,17 @@ __device__ __forceinline__ void na3d_mfma_body(const Na3dParams p, const Na3dTil
       for (int ks = 0; ks < KS; ++ks) {
         qreg[tt][ks] = *(const bf16x8*)(qp + 32 * ks + 8 * g);
         kself[tt][ks] = *(const bf16x8*)(kp + 32 * ks + 8 * g);
+      }
+      if constexpr (ROPE && D == 64) {
+        {  // the queries' rotation, pairs 8g .. 8g + 7 of this lane
+          const int64_t ro = rope_row(p, b, rz, rqy, rqx) * 32 + 8 * g;
+          float c[8], sn[8];
+          *(f32x4*)&c[0] = *(const f32x4*)(p.rc + ro);
+          *(f32x4*)&c[4] = *(const f32x4*)(p.rc + ro + 4);
+          *(f32x4*)&sn[0] = *(const f32x4*)(p.rs + ro);
+          *(f32x4*)&sn[4] = *(const f32x4*)(p.rs + ro + 4);
+          rope_q_pairs(qreg[tt][0], qreg[tt][1], c, sn);
+        }
       }
     }
     // Q must land before the DMA ring starts: the compiler does not see the
@@ -630,7 +665,7 @@ struct StripTile {
 // non-finite inputs).  Lane l handles query l >> 2 (row-major in the tile)
 // and the head-dim quarter l & 3 (16 values); invalid queries (past the
 // chunk's last row or column) compute a clamped copy and store nothing.
-template <int TX = 4>
+template <int TX = 4, bool ROPE = false>
 __device__ __forceinline__ void na3d_strip_tile_exact(const Na3dParams* pp, StripTile t) {
 #if defined(__HIP_DEVICE_COMPILE__)
   constexpr int TY = 16 / TX;
@@ -650,9 +685,21 @@ __device__ __forceinline__ void na3d_strip_tile_exact(const Na3dParams* pp, Stri
   float qf[16], acc[16];
 #pragma unroll
   for (int i = 0; i < 16; ++i) {
-    qf[i] = (float)qp[i] * c2;
+    qf[i] = (float)qp[i];
     acc[i] = 0.f;
   }
+  if constexpr (ROPE) {  // the queries' rotation (head_dim 64): this lane's dims 16dq .. 16dq + 15, partners 32 apart
+    const bf16* pp2 = dq < 2 ? qp + 32 : qp - 32;
+    const int64_t ro = rope_row(p, t.b, rz, ry, rx) * 32 + 16 * (dq & 1);
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+      const float o = qf[i], q2 = (float)pp2[i], c = p.rc[ro + i], sn = p.rs[ro + i];
+      // dims d < 32: a = own, b = partner (a c - b s); d >= 32: a = partner, b = own (a s + b c)
+      qf[i] = (float)(bf16)(dq < 2 ? o * c - q2 * sn : q2 * sn + o * c);
+    }
+  }
+#pragma unroll
+  for (int i = 0; i < 16; ++i) qf[i] *= c2;
   float m = -INFINITY, l = 0.f;
   const bf16* kb = (const bf16*)p.k + (int64_t)t.b * p.ks[0] + (int64_t)t.h * p.ks[4] + 16 * dq;
   const bf16* vb = (const bf16*)p.v + (int64_t)t.b * p.vs[0] + (int64_t)t.h * p.vs[4] + 16 * dq;
@@ -1144,15 +1191,18 @@ __global__ __launch_bounds__(256, 2) void na3d_strip_kernel(Na3dParams p, Na3dSt
 // the ones-operand MFMA.)
 // LDS bytes of one workgroup of the regular-strip kernel: the K/V ring and the
 // staged Q of the next tile.
-template <int D, int TX, int RPS, int NBUF>
+template <int D, int TX, int RPS, int NBUF, bool ROPE = false>
 constexpr int strip_fast_lds_bytes() {
-  return NBUF * 2 * RPS * ((NA3D_NWX - 1) * TX + 16) * D * 2 + NA3D_NWX * 16 * D * 2;
+  // ring + staged Q (+ ROPE: each wave's 16 queries' cos and sin rows, 32 pairs of fp32)
+  return NBUF * 2 * RPS * ((NA3D_NWX - 1) * TX + 16) * D * 2 + NA3D_NWX * 16 * D * 2 + (ROPE ? NA3D_NWX * 4096 : 0);
 }
 
 // `lds`: the workgroup's LDS (strip_fast_lds_bytes), 1 KiB aligned; `id`: its
 // work-unit index in [0, sg.total) (as na3d_mfma_body).  LSE: write p.lse (a
 // separate instance, so the inference kernels carry none of it).
-template <int D, int TX, int RPS, int NBUF, int KY, bool LSE = false>
+// ROPE: rotate the queries (p.rc / p.rs tables, head_dim 64, half layout); each tile's
+// cos / sin rows are copied into LDS beside its Q.
+template <int D, int TX, int RPS, int NBUF, int KY, bool LSE = false, bool ROPE = false>
 __device__ __forceinline__ void na3d_strip_fast_body(const Na3dParams p, const Na3dStrips sg, char* lds, int id) {
 #if defined(__HIP_DEVICE_COMPILE__)
   constexpr int NWX = NA3D_NWX;
@@ -1183,7 +1233,9 @@ __device__ __forceinline__ void na3d_strip_fast_body(const Na3dParams p, const N
   static_assert(QWB == KS * 1024, "16 query rows are KS 1-KiB loads");
   static_assert(QTB <= RING_B, "tile 0's Q is staged through the ring");
 
-  static_assert(RING_B + QTB == strip_fast_lds_bytes<D, TX, RPS, NBUF>(), "LDS size");
+  constexpr int TQB = ROPE ? NWX * 4096 : 0;  // per wave: cos rows of its 16 queries (2 KiB), then sin rows
+  static_assert(RING_B + QTB + TQB == strip_fast_lds_bytes<D, TX, RPS, NBUF, ROPE>(), "LDS size");
+  static_assert(!ROPE || (D == 64 && NBUF == 2 && TX * TY == 16), "query RoPE: head_dim 64, every wait drains the copies");
 
   // ---- work unit (as na3d_strip_body) ----
   int t = xcd_tile_order(sg.total, id);
@@ -1274,7 +1326,10 @@ __device__ __forceinline__ void na3d_strip_fast_body(const Na3dParams p, const N
     const int rx = gx + dx * min(xw0 + n % TX, qx1 - 1);
     qxo[i] = (uint32_t)((int64_t)rx * p.qs[3] * 2 + (int64_t)gy * p.qs[2] * 2) + 16 * (lane % CPK);
   }
-  // Copy Q of tile j (this wave's 16 queries) to LDS at `off`.
+  // Copy Q of tile j (this wave's 16 queries) to LDS at `off`; ROPE: also the
+  // queries' cos and sin rows (128 bytes each; lane l of copy i takes 16 bytes
+  // of query 8i + l/8) to this wave's part of the table area.
+  const uint32_t tq_lds = lds_base + (uint32_t)(RING_B + QTB) + (uint32_t)wave * 4096;
   auto dma_q = [&](int j, uint32_t off) {
     const int yt0 = ys + TY * j;
     const uint32_t m0 = lds_base + off + (uint32_t)wave * QWB;
@@ -1283,6 +1338,17 @@ __device__ __forceinline__ void na3d_strip_fast_body(const Na3dParams p, const N
       const int n = lane / CPK + i * (64 / CPK);
       const uint32_t qy = (uint32_t)min(yt0 + n / TX, ye - 1);
       dma_row16(rq, m0 + i * 1024, qxo[i] + qy * qs2);
+    }
+    if constexpr (ROPE) {
+      const u32x4 rc4 = make_rsrc(p.rc, OOB), rs4 = make_rsrc(p.rs, OOB);
+#pragma unroll
+      for (int i = 0; i < 2; ++i) {
+        const int n = lane / 8 + 8 * i;
+        const int ry = gy + dy * min(yt0 + n / TX, ye - 1), rx = gx + dx * min(xw0 + n % TX, qx1 - 1);
+        const uint32_t o = (uint32_t)(rope_row(p, b, rz, ry, rx) * 128) + 16 * (lane % 8);
+        dma_row16(rc4, tq_lds + i * 1024, o);
+        dma_row16(rs4, tq_lds + 2048 + i * 1024, o);
+      }
     }
   };
   // ---- output: one (batch, z, head) slice ----
@@ -1329,11 +1395,20 @@ __device__ __forceinline__ void na3d_strip_fast_body(const Na3dParams p, const N
   auto start_tile = [&](int k, uint32_t off) {
     const char* qb = lds + off + wave * QWB;
 #pragma unroll
-    for (int ks = 0; ks < KS; ++ks) {
-      qreg[k][ks] = *(const bf16x8*)(qb + n16 * D * 2 + (4 * ks + g) * 16);
+    for (int ks = 0; ks < KS; ++ks) qreg[k][ks] = *(const bf16x8*)(qb + n16 * D * 2 + (4 * ks + g) * 16);
+    if constexpr (ROPE) {  // pairs 8g .. 8g + 7 of query n16: dims in qreg[k][0], partners in qreg[k][1]
+      const char* tb = lds + RING_B + QTB + wave * 4096 + n16 * 128 + g * 32;
+      float c[8], sn[8];
+      *(f32x4*)&c[0] = *(const f32x4*)(tb);
+      *(f32x4*)&c[4] = *(const f32x4*)(tb + 16);
+      *(f32x4*)&sn[0] = *(const f32x4*)(tb + 2048);
+      *(f32x4*)&sn[4] = *(const f32x4*)(tb + 2048 + 16);
+      rope_q_pairs(qreg[k][0], qreg[k][1], c, sn);
+    }
+#pragma unroll
+    for (int ks = 0; ks < KS; ++ks)
 #pragma unroll
       for (int e = 0; e < 8; ++e) qreg[k][ks][e] = (bf16)((float)qreg[k][ks][e] * c2);
-    }
 #pragma unroll
     for (int db = 0; db < DB; ++db) oacc[k][db] = (f32x4){0.f, 0.f, 0.f, 0.f};
     lacc[k] = (f32x4){0.f, 0.f, 0.f, 0.f};
@@ -1561,7 +1636,7 @@ __device__ __forceinline__ void na3d_strip_fast_body(const Na3dParams p, const N
     __builtin_amdgcn_s_waitcnt(0);
     for (int j = 0; j < NT; ++j)
       if (j < 64 ? ((bad_tiles >> j) & 1) : bad_high)
-        na3d_strip_tile_exact<TX>(&p, StripTile{b, h, gz, gy, gx, iz, ys + TY * j, ye, xw0, qx1});
+        na3d_strip_tile_exact<TX, ROPE>(&p, StripTile{b, h, gz, gy, gx, iz, ys + TY * j, ye, xw0, qx1});
   }
 #endif
 }
@@ -1580,21 +1655,21 @@ __global__ __launch_bounds__(256, TX == 8 && KY <= 5 ? 3 : 2) void na3d_strip_fa
 // edge workgroups fill the strips' tail instead of running after them.  Workgroup
 // ids [0, n0) take the strips, [n0, n0 + n1) the top edge, the rest the bottom
 // edge; n0 and n1 are multiples of 8, so each part keeps its XCD-aware tile order.
-template <int KY, bool LSE>
+template <int KY, bool LSE, bool ROPE = false>
 __global__ __launch_bounds__(256, KY <= 5 ? 3 : 2) void na3d_small_fused_kernel(Na3dParams mid, Na3dStrips sg,
                                                                                Na3dParams e0, Na3dTiles t0,
                                                                                Na3dParams e1, Na3dTiles t1, int n0,
                                                                                int n1) {
   constexpr int NTYE = KY <= 5 ? 1 : 2;
-  constexpr int LS = strip_fast_lds_bytes<64, 8, 2, 2>(), LE = mfma_lds_bytes<64, 8, 2, 2>();
+  constexpr int LS = strip_fast_lds_bytes<64, 8, 2, 2, ROPE>(), LE = mfma_lds_bytes<64, 8, 2, 2>();
   __shared__ __attribute__((aligned(1024))) char lds[LS > LE ? LS : LE];
   const int id = (int)__builtin_amdgcn_workgroup_id_x();
   if (id < n0) {
-    if (id < sg.total) na3d_strip_fast_body<64, 8, 2, 2, KY, LSE>(mid, sg, lds, id);
+    if (id < sg.total) na3d_strip_fast_body<64, 8, 2, 2, KY, LSE, ROPE>(mid, sg, lds, id);
   } else if (id < n0 + n1) {
-    if (id - n0 < t0.total) na3d_mfma_body<64, 8, NTYE, 2, 2>(e0, t0, lds, id - n0);
+    if (id - n0 < t0.total) na3d_mfma_body<64, 8, NTYE, 2, 2, ROPE>(e0, t0, lds, id - n0);
   } else if (id - n0 - n1 < t1.total) {
-    na3d_mfma_body<64, 8, NTYE, 2, 2>(e1, t1, lds, id - n0 - n1);
+    na3d_mfma_body<64, 8, NTYE, 2, 2, ROPE>(e1, t1, lds, id - n0 - n1);
   }
 }
 
@@ -1816,6 +1891,23 @@ static int launch_small_strips(const Na3dParams& p, hipStream_t st) {
   if (!ok || total > 0x7fffffff) return fail(STRATA_HIP_EUNSUPPORTED, "na3d: problem too large for one launch");
   if (total == 0) return STRATA_HIP_OK;
   const dim3 grid((unsigned)total), block(64 * NA3D_NWX);
+  if (p.rc) {  // the queries' rotation in the kernel (inference: no lse)
+    switch (p.ker[1]) {
+      case 5:
+        hipLaunchKernelGGL((na3d_small_fused_kernel<5, false, true>), grid, block, 0, st, mid, sg, e0, t0, e1, t1,
+                           (int)n0, (int)n1);
+        break;
+      case 7:
+        hipLaunchKernelGGL((na3d_small_fused_kernel<7, false, true>), grid, block, 0, st, mid, sg, e0, t0, e1, t1,
+                           (int)n0, (int)n1);
+        break;
+      default:
+        hipLaunchKernelGGL((na3d_small_fused_kernel<9, false, true>), grid, block, 0, st, mid, sg, e0, t0, e1, t1,
+                           (int)n0, (int)n1);
+        break;
+    }
+    return check_launch("na3d_small_fused_kernel (query RoPE)");
+  }
   switch (p.ker[1]) {
     case 5:
       if (p.lse)
@@ -1861,7 +1953,8 @@ static bool aligned16(const void* ptr) { return ((uintptr_t)ptr & 15u) == 0; }
 
 using namespace strata;
 
-extern "C" int strata_hip_na3d_fwd(const strata_hip_na3d_args* a, void* stream) {
+// Argument checks and kernel parameters shared by the forward entry points.
+static int na3d_prepare(const strata_hip_na3d_args* a, Na3dParams& p) {
   if (!a) return fail(STRATA_HIP_EINVAL, "na3d: null args");
   if (!a->q || !a->k || !a->v || !a->out) return fail(STRATA_HIP_EINVAL, "na3d: null tensor pointer");
   if (a->dtype != STRATA_HIP_F32 && a->dtype != STRATA_HIP_BF16)
@@ -1880,7 +1973,6 @@ extern "C" int strata_hip_na3d_fwd(const strata_hip_na3d_args* a, void* stream) 
     if (a->q_origin[i] < 0 || a->q_extent[i] < 0 || a->q_origin[i] + a->q_extent[i] > L)
       return fail(STRATA_HIP_EINVAL, std::string("na3d: query box outside the grid on axis ") + axis[i]);
   }
-  Na3dParams p;
   p.q = a->q;
   p.k = a->k;
   p.v = a->v;
@@ -1904,12 +1996,15 @@ extern "C" int strata_hip_na3d_fwd(const strata_hip_na3d_args* a, void* stream) 
   p.scale = a->scale;
   p.lse = a->lse;
   p.lse_ext1 = a->q_extent[1];
+  p.rc = p.rs = nullptr;
+  p.rzt = 1;
   if (p.lse && ((uintptr_t)p.lse & 3u)) return fail(STRATA_HIP_EINVAL, "na3d: lse must be 4-byte aligned");
-  if ((int64_t)p.B * p.ext[0] * p.ext[1] * p.ext[2] == 0) return STRATA_HIP_OK;
-  hipStream_t st = (hipStream_t)stream;
+  return STRATA_HIP_OK;
+}
 
-  if (a->dtype == STRATA_HIP_F32) return launch_scalar<float>(p, st);
-
+// The bf16 MFMA kernels' layout conditions: 16-byte aligned tensors, strides in
+// whole 16-byte chunks, and key/value rows that one buffer descriptor covers.
+static bool na3d_mfma_ok(const Na3dParams& p) {
   bool mfma_ok = (p.D == 32 || p.D == 64 || p.D == 128) && p.ker[2] <= 15;
   if (mfma_ok) {
     const void* ptrs[4] = {p.q, p.k, p.v, p.o};
@@ -1936,6 +2031,16 @@ extern "C" int strata_hip_na3d_fwd(const strata_hip_na3d_args* a, void* stream) 
     }
     if (16 + p.ker[1] - 1 > 64) mfma_ok = false;
   }
+  return mfma_ok;
+}
+
+extern "C" int strata_hip_na3d_fwd(const strata_hip_na3d_args* a, void* stream) {
+  Na3dParams p;
+  if (const int rc = na3d_prepare(a, p)) return rc;
+  if ((int64_t)p.B * p.ext[0] * p.ext[1] * p.ext[2] == 0) return STRATA_HIP_OK;
+  hipStream_t st = (hipStream_t)stream;
+  if (a->dtype == STRATA_HIP_F32) return launch_scalar<float>(p, st);
+  const bool mfma_ok = na3d_mfma_ok(p);
   if (!mfma_ok) return launch_scalar<bf16>(p, st);
   switch (p.D) {
     case 32:
@@ -1948,4 +2053,43 @@ extern "C" int strata_hip_na3d_fwd(const strata_hip_na3d_args* a, void* stream) 
     default:
       return launch_mfma_d<128>(p, st);
   }
+}
+
+// The query-RoPE forward's checks; fills p with the tables set.
+static int rope_q_setup(const strata_hip_na3d_args* a, const float* cos, const float* sin, int32_t table_z,
+                        Na3dParams& p) {
+  if (const int rc = na3d_prepare(a, p)) return rc;
+  if (!cos || !sin) return fail(STRATA_HIP_EINVAL, "na3d_fwd_rope_q: null cos or sin table");
+  if (((uintptr_t)cos & 15u) || ((uintptr_t)sin & 15u))
+    return fail(STRATA_HIP_EINVAL, "na3d_fwd_rope_q: cos and sin must be 16-byte aligned");
+  if (table_z != 1 && table_z != p.L[0]) return fail(STRATA_HIP_EINVAL, "na3d_fwd_rope_q: table_z must be 1 or the grid's z");
+  if (a->dtype != STRATA_HIP_BF16 || p.D != 64 || p.lse)
+    return fail(STRATA_HIP_EUNSUPPORTED, "na3d_fwd_rope_q: bf16, head_dim 64 and no lse output only");
+  if ((int64_t)p.B * table_z * p.L[1] * p.L[2] * 128 >= (int64_t)OOB)
+    return fail(STRATA_HIP_EUNSUPPORTED, "na3d_fwd_rope_q: tables too large for 31-bit offsets");
+  const int kr = p.ker[1] / 2;
+  const int r0 = p.org[1] > kr ? p.org[1] : kr, r1 = p.org[1] + p.ext[1] < p.L[1] - kr ? p.org[1] + p.ext[1] : p.L[1] - kr;
+  if (!na3d_mfma_ok(p) || strip_fits(p) || !small_strip_fits(p) || r1 - r0 < 2 ||
+      std::getenv("STRATA_HIP_NA3D_NO_SMALL_STRIPS"))
+    return fail(STRATA_HIP_EUNSUPPORTED,
+                "na3d_fwd_rope_q: this window or layout runs a kernel without the query rotation "
+                "(rotate q in strata_hip_rope_qkv_pack and call strata_hip_na3d_fwd)");
+  p.rc = cos;
+  p.rs = sin;
+  p.rzt = table_z;
+  return STRATA_HIP_OK;
+}
+
+extern "C" int strata_hip_na3d_fwd_rope_q_supported(const strata_hip_na3d_args* a, const float* cos, const float* sin,
+                                                    int32_t table_z) {
+  Na3dParams p;
+  return rope_q_setup(a, cos, sin, table_z, p) == STRATA_HIP_OK ? 1 : 0;
+}
+
+extern "C" int strata_hip_na3d_fwd_rope_q(const strata_hip_na3d_args* a, const float* cos, const float* sin,
+                                          int32_t table_z, void* stream) {
+  Na3dParams p;
+  if (const int rc = rope_q_setup(a, cos, sin, table_z, p)) return rc;
+  if ((int64_t)p.B * p.ext[0] * p.ext[1] * p.ext[2] == 0) return STRATA_HIP_OK;
+  return launch_small_strips(p, (hipStream_t)stream);  // the small-window launch (rope_q_setup checked it applies)
 }

@@ -132,6 +132,7 @@ __global__ __launch_bounds__(256) void rope_pack_half_kernel(RopeParams p, int64
     const bf16* src = p.qkv + tok * p.ld + (int64_t)h * p.D + 8 * c;
 #pragma unroll
     for (int t = 0; t < 2; ++t) {
+      if (t == 0 && !p.q) continue;  // uniform: k only (the queries are rotated inside NA3D)
       raw[r][2 * t] = *(const u32x4*)(src + t * C);
       raw[r][2 * t + 1] = *(const u32x4*)(src + t * C + half);
     }
@@ -150,7 +151,7 @@ __global__ __launch_bounds__(256) void rope_pack_half_kernel(RopeParams p, int64
 #pragma unroll
   for (int r = 0; r < ROPE_R; ++r) {
     if (!ok[r]) continue;  // uniform over the lanes of a head
-    half_run(p, raw[r][0], raw[r][1], p.q + dst[r], cs[r], sn[r], cc[r], cph, p.qw);
+    if (p.q) half_run(p, raw[r][0], raw[r][1], p.q + dst[r], cs[r], sn[r], cc[r], cph, p.qw);
     half_run(p, raw[r][2], raw[r][3], p.k + dst[r], cs[r], sn[r], cc[r], cph, p.kw);
     if (p.v) {
       *(u32x4*)(p.v + dst[r]) = raw[r][4];
@@ -197,7 +198,7 @@ __global__ __launch_bounds__(256) void rope_pack_inter_kernel(RopeParams p, int6
   *(f32x4*)&cs[0] = *(const f32x4*)(p.cos + trow);
   *(f32x4*)&sn[0] = *(const f32x4*)(p.sin + trow);
   const int64_t dst = tok * C + (int64_t)h * p.D + 8 * c;
-  *(u32x4*)(p.q + dst) = rot_inter(p, *(const u32x4*)(src), cs, sn, c, cph, p.qw);
+  if (p.q) *(u32x4*)(p.q + dst) = rot_inter(p, *(const u32x4*)(src), cs, sn, c, cph, p.qw);  // uniform
   *(u32x4*)(p.k + dst) = rot_inter(p, *(const u32x4*)(src + C), cs, sn, c, cph, p.kw);
   if (p.v) *(u32x4*)(p.v + dst) = *(const u32x4*)(src + 2 * C);
 }
@@ -478,8 +479,8 @@ extern "C" int strata_hip_rope_qkv_pack_bwd(const strata_hip_rope_pack_bwd_args*
 
 extern "C" int strata_hip_rope_qkv_pack(const strata_hip_rope_pack_args* a, void* stream) {
   if (!a) return fail(STRATA_HIP_EINVAL, "rope_qkv_pack: null args");
-  if (!a->qkv || !a->cos || !a->sin || !a->q || !a->k)
-    return fail(STRATA_HIP_EINVAL, "rope_qkv_pack: null pointer");
+  if (!a->qkv || !a->cos || !a->sin || !a->k)
+    return fail(STRATA_HIP_EINVAL, "rope_qkv_pack: null pointer");  // q may be NULL: k (and v) only
   if (a->batch < 0 || a->grid[0] <= 0 || a->grid[1] <= 0 || a->grid[2] <= 0 || a->heads <= 0)
     return fail(STRATA_HIP_EINVAL, "rope_qkv_pack: bad batch/grid/heads");
   if (a->table_z != 1 && a->table_z != a->grid[0])

@@ -169,6 +169,18 @@ class FusedNA3DAttention(nn.Module):
             # pass (its v columns from dv) instead of zero-filling it, scattering dv into the
             # view and adding the two.
             train = torch.is_grad_enabled() and qkv.requires_grad
+            if not train and not self.qk_norm and self.rope_layout == _lib.ROPE_HALF:
+                # Inference: the queries can be rotated inside the small-window NA3D kernel,
+                # q read unrotated straight out of qkv, so the pack writes k only.
+                qkv6 = qkv.view(B, Z, Y, X, 3, H, D)
+                q, v = qkv6[..., 0, :, :], qkv6[..., 2, :, :]
+                kst = [Z * Y * X * H * D, Y * X * H * D, X * H * D, H * D, D]
+                if ops.na3d_rope_q_supported(q, kst, v, rope[0], rope[1], self.kernel_size, self.dilation,
+                                             self.scale):
+                    _, k, _ = ops.rope_qkv_pack(qkv, rope[0], rope[1], H, self.rope_layout, pack_v=False,
+                                                pack_q=False)
+                    a = ops.na3d_fwd_rope_q(q, k, v, rope[0], rope[1], self.kernel_size, self.dilation, self.scale)
+                    return self._gate(x, a.view(B, Z, Y, X, C))
             q, k, v = ops.rope_qkv_pack(qkv, rope[0], rope[1], H, self.rope_layout, self.qk_norm, self.qk_norm_eps,
                                         qw, kw, pack_v=train)
             if not train:
@@ -177,7 +189,9 @@ class FusedNA3DAttention(nn.Module):
             qkv6 = qkv.view(B, Z, Y, X, 3, H, D)
             q, k, v = qkv6[..., 0, :, :], qkv6[..., 1, :, :], qkv6[..., 2, :, :]
         a = ops.na3d(q, k, v, self.kernel_size, self.dilation, self.scale)
-        a = a.view(B, Z, Y, X, C)
+        return self._gate(x, a.view(B, Z, Y, X, C))
+
+    def _gate(self, x: Tensor, a: Tensor) -> Tensor:
         if self.gate_proj is not None:  # a * sigmoid(x @ Wg^T + bg) in one GEMM
             a = ops.gemm_bias_act(x, self.gate_proj.weight, self.gate_proj.bias, a, _lib.ACT_SIGMOID, _lib.RES_MUL)
         return a

@@ -130,6 +130,15 @@ def _na3d_launch(name, q, k, v, kernel, dilation, scale, q_origin, q_extent, lse
     out = torch.empty((B, *q_extent, H, D), dtype=q.dtype, device=q.device)
     if out.numel() == 0:
         return out
+    a = _na3d_args(q, k, v, out, dt, qs, ks, vs, kernel, dilation, scale, q_origin, q_extent)
+    a.lse = lse.data_ptr() if lse is not None else None
+    with torch.cuda.device(q.device):
+        _lib.call("strata_hip_na3d_fwd", a, _stream(q))
+    return out
+
+
+def _na3d_args(q, k, v, out, dt, qs, ks, vs, kernel, dilation, scale, q_origin, q_extent) -> "_lib.Na3dArgs":
+    B, Z, Y, X, H, D = q.shape
     a = _lib.Na3dArgs()
     a.q, a.k, a.v, a.out = q.data_ptr(), k.data_ptr(), v.data_ptr(), out.data_ptr()
     a.dtype = dt
@@ -144,10 +153,83 @@ def _na3d_launch(name, q, k, v, kernel, dilation, scale, q_origin, q_extent, lse
     a.k_stride[:] = ks
     a.v_stride[:] = vs
     a.o_stride[:] = [out.stride(i) for i in range(5)]
-    a.lse = lse.data_ptr() if lse is not None else None
+    a.lse = None
+    return a
+
+
+def _rope_q_tables(name, q, cos, sin):
+    B, Z, Y, X, H, D = q.shape
+    if cos.dtype != torch.float32 or sin.dtype != torch.float32:
+        raise ValueError(f"{name}: cos/sin tables must be float32")
+    if cos.shape != sin.shape or cos.dim() != 5 or tuple(cos.shape[2:]) != (Y, X, D // 2) or cos.shape[0] != B \
+            or cos.shape[1] not in (1, Z):
+        raise ValueError(f"{name}: cos/sin must be [B, 1|Z, Y, X, D/2] = [{B}, 1|{Z}, {Y}, {X}, {D // 2}], "
+                         f"got {tuple(cos.shape)}")
+    return cos.contiguous(), sin.contiguous(), int(cos.shape[1])
+
+
+def na3d_rope_q_supported(q: Tensor, k_strides: Sequence[int], v: Tensor, cos: Tensor, sin: Tensor,
+                          kernel: Sequence[int], dilation: Sequence[int], scale: Optional[float] = None) -> bool:
+    """Whether ``na3d_fwd_rope_q`` takes these shapes, strides and window (the
+    small-window kernels: bf16, head_dim 64, half-layout tables); k is described by
+    its strides only (the k-only pack writes it contiguous)."""
+    name = "na3d_rope_q_supported"
+    if not (q.is_cuda and v.is_cuda and cos.is_cuda and sin.is_cuda) or q.dtype != torch.bfloat16 \
+            or v.dtype != torch.bfloat16 or q.dim() != 6 or q.shape != v.shape:
+        return False
+    try:
+        cos_c, sin_c, zt = _rope_q_tables(name, q, cos, sin)
+        qs, vs = _token_strides(name, q), _token_strides(name, v)
+    except ValueError:
+        return False
+    Z, Y, X = q.shape[1:4]
+    kernel, dilation = _triple("kernel", kernel), _triple("dilation", dilation)
+    # k's pointer is not dereferenced by the query; q's stands in for it (aligned alike)
+    a = _na3d_args(q, q, v, q, _dtype_code(name, q), qs, list(k_strides), vs, kernel, dilation, scale, [0, 0, 0],
+                   [Z, Y, X])
+    a.o_stride[:] = list(k_strides)
+    lib = _lib.load()
+    return bool(lib.strata_hip_na3d_fwd_rope_q_supported(ctypes.byref(a), cos_c.data_ptr(), sin_c.data_ptr(), zt))
+
+
+@torch.library.custom_op("strata_hip::na3d_fwd_rope_q", mutates_args=())
+def na3d_fwd_rope_q(q: Tensor, k: Tensor, v: Tensor, cos: Tensor, sin: Tensor, kernel: Sequence[int],
+                    dilation: Sequence[int], scale: Optional[float]) -> Tensor:
+    """``na3d_fwd`` over the full grid with the queries' rotary embedding applied
+    inside the kernel: q is unrotated (e.g. a strided view of the qkv output), k
+    already rotated (``rope_qkv_pack(..., pack_q=False)``), cos/sin the half-layout
+    tables ``[B, 1|Z, Y, X, D/2]`` fp32.  Equals ``na3d_fwd(rope(q), k, v)`` with
+    rope(q) rounded to bf16 as the pack rounds it.  Inference only (no lse); raises
+    for shapes ``na3d_rope_q_supported`` rejects.  Fuses the query half of the
+    attention's RoPE (screamcast/strata_wrappers.py:331-338) into the NATTEN call."""
+    name = "na3d_fwd_rope_q"
+    _require_gpu(name, q, k, v, cos, sin)
+    if not (q.shape == k.shape == v.shape):
+        raise ValueError(f"{name}: q, k, v must share one shape")
+    if not (q.dtype == k.dtype == v.dtype == torch.bfloat16):
+        raise ValueError(f"{name}: q, k, v must be bfloat16")
+    cos_c, sin_c, zt = _rope_q_tables(name, q, cos, sin)
+    qs, ks, vs = _token_strides(name, q), _token_strides(name, k), _token_strides(name, v)
+    B, Z, Y, X, H, D = q.shape
+    kernel, dilation = _triple("kernel", kernel), _triple("dilation", dilation)
+    out = torch.empty((B, Z, Y, X, H, D), dtype=q.dtype, device=q.device)
+    if out.numel() == 0:
+        return out
+    a = _na3d_args(q, k, v, out, _dtype_code(name, q), qs, ks, vs, kernel, dilation, scale, [0, 0, 0], [Z, Y, X])
+    lib = _lib.load()
     with torch.cuda.device(q.device):
-        _lib.call("strata_hip_na3d_fwd", a, _stream(q))
+        rc = lib.strata_hip_na3d_fwd_rope_q(ctypes.byref(a), cos_c.data_ptr(), sin_c.data_ptr(), zt,
+                                            ctypes.c_void_p(_stream(q)))
+    if rc != _lib.OK:
+        msg = lib.strata_hip_last_error().decode(errors="replace")
+        raise (ValueError if rc == _lib.EINVAL else _lib.StrataHipError)(
+            *((f"{name}: {msg}",) if rc == _lib.EINVAL else ("strata_hip_na3d_fwd_rope_q", rc, msg)))
     return out
+
+
+@na3d_fwd_rope_q.register_fake
+def _(q, k, v, cos, sin, kernel, dilation, scale):
+    return q.new_empty(q.shape)
 
 
 @na3d_fwd.register_fake
@@ -285,7 +367,8 @@ def na3d(q: Tensor, k: Tensor, v: Tensor, kernel: Sequence[int], dilation: Seque
 @torch.library.custom_op("strata_hip::rope_qkv_pack", mutates_args=())
 def rope_qkv_pack(qkv: Tensor, cos: Tensor, sin: Tensor, heads: int, rope_layout: int, qk_norm: bool = False,
                   qk_norm_eps: float = 1e-6, q_norm_weight: Optional[Tensor] = None,
-                  k_norm_weight: Optional[Tensor] = None, pack_v: bool = True) -> tuple[Tensor, Tensor, Tensor]:
+                  k_norm_weight: Optional[Tensor] = None, pack_v: bool = True,
+                  pack_q: bool = True) -> tuple[Tensor, Tensor, Tensor]:
     """Split ``attn.qkv``'s output into heads-last q, k, v and rotate q, k.
 
     qkv: ``[B, Z, Y, X, 3*H*D]`` bf16 (column order (3, H, D), last dim
@@ -298,6 +381,8 @@ def rope_qkv_pack(qkv: Tensor, cos: Tensor, sin: Tensor, heads: int, rope_layout
     tensor is returned in its place): the caller reads v straight out of qkv as
     the strided view ``qkv.view(B, Z, Y, X, 3, H, D)[..., 2, :, :]``, which the
     NA3D op takes as it is, and the pack moves a third fewer bytes.
+    pack_q=False leaves q out likewise, for ``na3d_fwd_rope_q``, which rotates the
+    queries inside the attention kernel.
     """
     name = "rope_qkv_pack"
     _require_gpu(name, qkv, cos, sin)
@@ -329,14 +414,14 @@ def rope_qkv_pack(qkv: Tensor, cos: Tensor, sin: Tensor, heads: int, rope_layout
             t = t.contiguous()
         wts.append(t)
     shape = (B, Z, Y, X, heads, D)
-    q = torch.empty(shape, dtype=qkv.dtype, device=qkv.device)
-    k = torch.empty_like(q)
-    v = torch.empty_like(q) if pack_v else q.new_empty(0)
-    if q.numel() == 0:
+    k = torch.empty(shape, dtype=qkv.dtype, device=qkv.device)
+    q = torch.empty_like(k) if pack_q else k.new_empty(0)
+    v = torch.empty_like(k) if pack_v else k.new_empty(0)
+    if k.numel() == 0:
         return q, k, v
     a = _lib.RopePackArgs()
     a.qkv, a.cos, a.sin = flat.data_ptr(), cos_c.data_ptr(), sin_c.data_ptr()
-    a.q, a.k, a.v = q.data_ptr(), k.data_ptr(), (v.data_ptr() if pack_v else None)
+    a.q, a.k, a.v = (q.data_ptr() if pack_q else None), k.data_ptr(), (v.data_ptr() if pack_v else None)
     a.batch = B
     a.grid[:] = [Z, Y, X]
     a.table_z = cos.shape[1]
@@ -353,15 +438,16 @@ def rope_qkv_pack(qkv: Tensor, cos: Tensor, sin: Tensor, heads: int, rope_layout
 
 @rope_qkv_pack.register_fake
 def _(qkv, cos, sin, heads, rope_layout, qk_norm=False, qk_norm_eps=1e-6, q_norm_weight=None, k_norm_weight=None,
-      pack_v=True):
+      pack_v=True, pack_q=True):
     B, Z, Y, X, C3 = qkv.shape
     D = C3 // (3 * heads)
     shape = (B, Z, Y, X, heads, D)
-    return qkv.new_empty(shape), qkv.new_empty(shape), qkv.new_empty(shape if pack_v else (0,))
+    return (qkv.new_empty(shape if pack_q else (0,)), qkv.new_empty(shape),
+            qkv.new_empty(shape if pack_v else (0,)))
 
 
 def _rope_setup_context(ctx, inputs, output):
-    qkv, cos, sin, heads, rope_layout, qk_norm, qk_norm_eps, q_norm_weight, k_norm_weight, pack_v = inputs
+    qkv, cos, sin, heads, rope_layout, qk_norm, qk_norm_eps, q_norm_weight, k_norm_weight, pack_v, _pack_q = inputs
     ctx.qk_norm, ctx.heads, ctx.layout, ctx.pack_v = bool(qk_norm), int(heads), int(rope_layout), bool(pack_v)
     ctx.qk_norm_eps = float(qk_norm_eps)
     ctx.qkv_shape = tuple(qkv.shape)
@@ -380,8 +466,8 @@ def _rope_backward(ctx, dq, dk, dv):
     cos, sin = ctx.saved_tensors[:2]
     B, Z, Y, X, C3 = ctx.qkv_shape
     D = C3 // (3 * ctx.heads)
-    grads = [g.contiguous() if g is not None else torch.zeros((B, Z, Y, X, ctx.heads, D), dtype=torch.bfloat16,
-                                                                 device=cos.device) for g in (dq, dk)]
+    grads = [g.contiguous() if (g is not None and g.numel()) else
+             torch.zeros((B, Z, Y, X, ctx.heads, D), dtype=torch.bfloat16, device=cos.device) for g in (dq, dk)]
     dv = dv.contiguous() if (ctx.pack_v and dv is not None) else None
     dqkv = torch.empty(ctx.qkv_shape, dtype=torch.bfloat16, device=cos.device)
     a = _lib.RopePackBwdArgs()
@@ -412,7 +498,7 @@ def _rope_backward(ctx, dq, dk, dv):
             _lib.call("strata_hip_rope_qkv_pack_bwd", a, _stream(dqkv))
     if ctx.qk_norm:
         dws = [d.to(w.dtype) if d is not None else None for d, w in zip(dws, ctx.saved_tensors[3:])]
-    return dqkv, None, None, None, None, None, None, dws[0], dws[1], None
+    return dqkv, None, None, None, None, None, None, dws[0], dws[1], None, None
 
 
 rope_qkv_pack.register_autograd(_rope_backward, setup_context=_rope_setup_context)

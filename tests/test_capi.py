@@ -154,9 +154,13 @@ def test_gemm_and_layernorm_validation(lib):
     r.v = None  # v may be NULL (only q and k written): validation goes on to the next check
     assert lib.strata_hip_rope_qkv_pack(ctypes.byref(r), None) == _lib.EINVAL
     assert "power of two" in lib.strata_hip_last_error().decode()
-    r.q = None
+    r.q = None  # q may be NULL as well (k only, the queries rotated inside NA3D): on to the next check
+    assert lib.strata_hip_rope_qkv_pack(ctypes.byref(r), None) == _lib.EINVAL
+    assert "power of two" in lib.strata_hip_last_error().decode()
+    saved_k, r.k = r.k, None  # k is always written
     assert lib.strata_hip_rope_qkv_pack(ctypes.byref(r), None) == _lib.EINVAL
     assert "null pointer" in lib.strata_hip_last_error().decode()
+    r.k = saved_k
     g.k = g.ldx = g.ldw = 16
     g.res_op = 5
     assert lib.strata_hip_gemm_bias_act(ctypes.byref(g), None) == _lib.EINVAL
@@ -287,3 +291,30 @@ def test_dealias_axis_validation(lib):
     assert "both" in lib.strata_hip_last_error().decode()
     a.mean, a.batch = None, 0
     assert lib.strata_hip_dealias_axis(ctypes.byref(a), None) == _lib.OK
+
+
+def test_na3d_rope_q_validation(lib):
+    """The fused query-RoPE entry point checks its tables before launching (no GPU needed)."""
+    a = _lib.Na3dArgs()
+    a.q = a.k = a.v = a.out = 4096
+    a.dtype, a.batch, a.heads, a.head_dim = _lib.BF16, 1, 2, 64
+    a.grid[:] = [4, 16, 16]
+    a.q_extent[:] = [4, 16, 16]
+    a.kernel[:] = [3, 7, 7]
+    a.dilation[:] = [1, 1, 1]
+    a.scale = 0.125
+    for st in (a.q_stride, a.k_stride, a.v_stride, a.o_stride):
+        st[:] = [4 * 16 * 16 * 128, 16 * 16 * 128, 16 * 128, 128, 64]
+    assert lib.strata_hip_na3d_fwd_rope_q(ctypes.byref(a), None, None, 1, None) == _lib.EINVAL
+    assert "null cos" in lib.strata_hip_last_error().decode()
+    assert lib.strata_hip_na3d_fwd_rope_q(ctypes.byref(a), 4096, 4104, 1, None) == _lib.EINVAL
+    assert "16-byte aligned" in lib.strata_hip_last_error().decode()
+    assert lib.strata_hip_na3d_fwd_rope_q(ctypes.byref(a), 4096, 8192, 3, None) == _lib.EINVAL
+    assert "table_z" in lib.strata_hip_last_error().decode()
+    assert lib.strata_hip_na3d_fwd_rope_q_supported(ctypes.byref(a), 4096, 8192, 1) == 1
+    a.kernel[:] = [3, 13, 13]  # the wide-window strip kernels carry no query rotation
+    assert lib.strata_hip_na3d_fwd_rope_q_supported(ctypes.byref(a), 4096, 8192, 1) == 0
+    assert lib.strata_hip_na3d_fwd_rope_q(ctypes.byref(a), 4096, 8192, 1, None) == _lib.EUNSUPPORTED
+    a.kernel[:] = [3, 7, 7]
+    a.dtype = _lib.F32
+    assert lib.strata_hip_na3d_fwd_rope_q_supported(ctypes.byref(a), 4096, 8192, 1) == 0
