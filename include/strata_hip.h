@@ -6,13 +6,9 @@
  * step's state normalisation / patchify and state update, and the NA3D backward.
  *
  * Conventions shared by every entry point
- *   - All pointers are device pointers owned by the caller.  The hand-written
- *     kernels allocate and free no device memory and keep no state between
- *     calls.  The one exception is strata_hip_gemm_bias_act without an
- *     activation (a plain GEMM), which runs hipBLASLt: on first use per device
- *     it creates a hipBLASLt handle (which allocates) and it keeps a host-side
- *     plan cache per shape; it uses no workspace.  The environment variable
- *     STRATA_HIP_GEMM=native keeps every GEMM on the hand-written kernels.
+ *   - All pointers are device pointers owned by the caller.  Every kernel is
+ *     hand-written; the library allocates and frees no device memory, keeps no
+ *     state between calls and links no library beyond the HIP runtime.
  *   - `stream` is a hipStream_t (passed as void* so that the header needs no
  *     HIP include).  Work is enqueued asynchronously on that stream; there is
  *     no device synchronisation inside the library.

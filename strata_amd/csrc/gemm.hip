@@ -9,10 +9,9 @@
 // as one 8-byte write after bias, GELU and residual.
 //
 // Two kernels: gemm_dma_kernel (K % 64 == 0; 256 x 256 tiles, 8 waves,
-// global->LDS streaming) for the block's fused-epilogue GEMMs, and
-// gemm_bias_act_kernel (128 x 128 tiles, register-staged loads) for any other
-// K.  Plain GEMMs (no activation, bias and an added residual at most) are
-// handed to hipBLASLt first (gemm_lt.cpp).
+// global->LDS streaming) for every GEMM of the block and the rollout, plain or
+// with a fused epilogue, and gemm_bias_act_kernel (128 x 128 tiles,
+// register-staged loads) for any other K.
 #include "gemm.h"
 
 namespace strata {
@@ -711,16 +710,6 @@ extern "C" int strata_hip_gemm_bias_act(const strata_hip_gemm_args* a, void* str
   if (const int rc = gemm_params(a, p)) return rc;
   if (a->m == 0 || a->n == 0) return STRATA_HIP_OK;
   hipStream_t st = (hipStream_t)stream;
-  // Plain GEMMs (no activation; bias and an added residual at most) go to
-  // hipBLASLt; the fused epilogues, and anything it declines, run here.
-  if (gemm_lt_enabled()) {
-    const int lt = gemm_lt(p, st);
-    if (lt == STRATA_HIP_OK) return STRATA_HIP_OK;
-    if (lt == GEMM_LT_FAILED)
-      return fail(STRATA_HIP_ELAUNCH,
-                  "gemm: hipblasLtCreate failed on this device (plain GEMMs run on hipBLASLt; "
-                  "STRATA_HIP_GEMM=native selects the hand-written kernels)");
-  }
   dim3 grid;
   if (gemm_big(p, grid)) {
     switch (p.act) {

@@ -2065,6 +2065,9 @@ static int rope_q_setup(const strata_hip_na3d_args* a, const float* cos, const f
   if (table_z != 1 && table_z != p.L[0]) return fail(STRATA_HIP_EINVAL, "na3d_fwd_rope_q: table_z must be 1 or the grid's z");
   if (a->dtype != STRATA_HIP_BF16 || p.D != 64 || p.lse)
     return fail(STRATA_HIP_EUNSUPPORTED, "na3d_fwd_rope_q: bf16, head_dim 64 and no lse output only");
+  for (int i = 0; i < 3; ++i)
+    if (p.org[i] != 0 || p.ext[i] != p.L[i])
+      return fail(STRATA_HIP_EUNSUPPORTED, "na3d_fwd_rope_q: the query box must be the full grid");
   if ((int64_t)p.B * table_z * p.L[1] * p.L[2] * 128 >= (int64_t)OOB)
     return fail(STRATA_HIP_EUNSUPPORTED, "na3d_fwd_rope_q: tables too large for 31-bit offsets");
   const int kr = p.ker[1] / 2;

@@ -19,27 +19,29 @@ def _qkv(B, Z, Y, X, H, g, dev, scale=1.0):
     return (torch.randn(B, Z, Y, X, 3 * H * 64, generator=g) * scale).bfloat16().to(dev)
 
 
-@pytest.mark.parametrize("shape, kernel, zt", [
-    ((2, 8, 64, 64, 8), (3, 7, 7), 1),
-    ((2, 8, 64, 64, 8), (3, 7, 7), 8),     # configs[1]: tables with the level index in z
-    ((1, 8, 32, 32, 4), (3, 9, 9), 1),
-    ((1, 6, 24, 40, 2), (3, 5, 5), 6),
-    ((1, 4, 20, 24, 2), (3, 7, 7), 1),     # short strips, ragged columns
+@pytest.mark.parametrize("shape, kernel, zt, dil", [
+    ((2, 8, 64, 64, 8), (3, 7, 7), 1, (1, 1, 1)),
+    ((2, 8, 64, 64, 8), (3, 7, 7), 8, (1, 1, 1)),     # configs[1]: tables with the level index in z
+    ((1, 8, 32, 32, 4), (3, 9, 9), 1, (1, 1, 1)),
+    ((1, 6, 24, 40, 2), (3, 5, 5), 6, (1, 1, 1)),
+    ((1, 4, 20, 24, 2), (3, 7, 7), 1, (1, 1, 1)),     # short strips, ragged columns
+    ((1, 8, 32, 40, 2), (3, 7, 7), 8, (2, 1, 2)),     # z and x dilation: residue classes, level tables
+    ((1, 6, 24, 30, 2), (3, 5, 5), 1, (2, 1, 3)),
 ])
-def test_rope_q_fused_matches_pack_then_na3d(gpu, shape, kernel, zt):
+def test_rope_q_fused_matches_pack_then_na3d(gpu, shape, kernel, zt, dil):
     B, Z, Y, X, H = shape
-    g = torch.Generator().manual_seed(sum(shape) + zt)
+    g = torch.Generator().manual_seed(sum(shape) + zt + sum(dil))
     qkv = _qkv(B, Z, Y, X, H, g, gpu)
     cos, sin = _tables(B, zt, Y, X, g, gpu)
     q6 = qkv.view(B, Z, Y, X, 3, H, 64)
     v = q6[..., 2, :, :]
     q_ref, k_ref, _ = ops.rope_qkv_pack(qkv, cos, sin, H, _lib.ROPE_HALF, pack_v=False)
-    ref = ops.na3d_fwd(q_ref, k_ref, v, list(kernel), [1, 1, 1], None, [0, 0, 0], [Z, Y, X])
+    ref = ops.na3d_fwd(q_ref, k_ref, v, list(kernel), list(dil), None, [0, 0, 0], [Z, Y, X])
     _, k, _ = ops.rope_qkv_pack(qkv, cos, sin, H, _lib.ROPE_HALF, pack_v=False, pack_q=False)
     assert torch.equal(k, k_ref)
     kst = [Z * Y * X * H * 64, Y * X * H * 64, X * H * 64, H * 64, 64]
-    assert ops.na3d_rope_q_supported(q6[..., 0, :, :], kst, v, cos, sin, kernel, [1, 1, 1])
-    out = ops.na3d_fwd_rope_q(q6[..., 0, :, :], k, v, cos, sin, list(kernel), [1, 1, 1], None)
+    assert ops.na3d_rope_q_supported(q6[..., 0, :, :], kst, v, cos, sin, kernel, list(dil))
+    out = ops.na3d_fwd_rope_q(q6[..., 0, :, :], k, v, cos, sin, list(kernel), list(dil), None)
     torch.cuda.synchronize()
     # q' is rounded to bf16 the way the pack rounds it: equal up to the order of the
     # rotation's two products (fused multiply-add contraction)

@@ -76,8 +76,12 @@ def test_noalloc_at_the_scratch_maximum_and_beyond(gpu):
     _both(gpu, (4, 8, 64, 64, 16, 64), (3, 7, 7), 4, True)
     lib = _lib.load()
     shape = (5, 8, 64, 64, 16, 64)
-    t = torch.empty(64, dtype=torch.bfloat16, device=gpu)  # never touched: the call is refused first
-    a = _args(*(t.view(1, 1, 1, 1, 1, 64).expand(shape) for _ in range(8)), None, (3, 7, 7))
+    # real tensors of the refused shape (8 x 335 MB): should the host check ever let the
+    # call through, every access still lands inside its own allocation
+    ts = [torch.zeros(shape, dtype=torch.bfloat16, device=gpu) for _ in range(8)]
+    a = _args(*ts, None, (3, 7, 7))
     rc = lib.strata_hip_na3d_bwd_noalloc(ctypes.byref(a), ctypes.c_void_p(torch.cuda.current_stream().cuda_stream))
+    torch.cuda.synchronize()
     assert rc == _lib.EUNSUPPORTED
     assert "scratch maximum" in lib.strata_hip_last_error().decode()
+    del ts
