@@ -1,0 +1,476 @@
+"""Host-side replay of the address arithmetic of the hand-written kernels (test
+infrastructure, CPU only).
+
+For a given launch, each function below recomputes, with the kernel's own index
+formulas (the source lines are named in each docstring), every global byte range
+the launch reads or writes, as [lo, hi) intervals relative to the base pointer
+of the tensor's allocation, and the 32-bit quantities the kernel forms (buffer
+lane offsets, record counts, grid sizes).  ``Access`` keeps, per tensor, the
+smallest lo and the largest hi and flags any 32-bit value out of range, so a
+test can assert that a launch at a given shape stays inside its allocations
+without running it.
+
+Where an address is a sum of a part that depends only on the workgroup (tile
+origin, batch, head, K step) and a part that depends only on the lane, and no
+bounds mask couples them, the extremes over their Cartesian product are the
+sums of the parts' extremes: that is how full GEMM tiles, LayerNorm rows and
+the batch / head axes of NA3D are covered, exactly.  Everything under a mask
+(ragged GEMM tiles, clamped NA3D windows, partial stages) is replayed lane by
+lane (numpy, int64).  Offsets are affine in the K step and in the stage index,
+so those loops are evaluated at their first and last iteration.
+"""
+
+from __future__ import annotations
+
+import math
+from dataclasses import dataclass, field
+
+import numpy as np
+
+OOB = 0x7FFFFFF0  # common.h: out-of-range lane offset / record count
+
+
+@dataclass
+class Access:
+    """Per-tensor extremes of the byte ranges a launch touches."""
+
+    lo: dict = field(default_factory=dict)
+    hi: dict = field(default_factory=dict)
+    bad32: list = field(default_factory=list)
+
+    def add(self, name: str, start: np.ndarray, nbytes: int | np.ndarray, mask: np.ndarray | None = None):
+        start = np.asarray(start, dtype=np.int64)
+        end = start + np.asarray(nbytes, dtype=np.int64)
+        if mask is not None:
+            shape = np.broadcast_shapes(start.shape, end.shape, np.shape(mask))
+            m = np.broadcast_to(np.asarray(mask, dtype=bool), shape)
+            if not m.any():
+                return
+            start, end = np.broadcast_to(start, shape)[m], np.broadcast_to(end, shape)[m]
+        if start.size == 0:
+            return
+        lo, hi = int(start.min()), int(end.max())
+        self.lo[name] = min(self.lo.get(name, lo), lo)
+        self.hi[name] = max(self.hi.get(name, hi), hi)
+
+    def add_sum(self, name: str, outer: np.ndarray, inner: np.ndarray, nbytes: int):
+        """Accesses at outer[i] + inner[j] for every pair (i, j), nbytes each."""
+        outer, inner = np.asarray(outer, dtype=np.int64), np.asarray(inner, dtype=np.int64)
+        if outer.size == 0 or inner.size == 0:
+            return
+        self.add(name, np.array([outer.min() + inner.min()]), np.array([outer.max() + inner.max() + nbytes]) -
+                 np.array([outer.min() + inner.min()]))
+
+    def u32(self, what: str, values, limit: int = 1 << 32):
+        v = np.asarray(values, dtype=np.int64)
+        if v.size and (v.min() < 0 or v.max() >= limit):
+            self.bad32.append(f"{what}: {int(v.min())}..{int(v.max())} outside [0, {limit})")
+
+    def lane_offsets(self, what: str, voff, nbytes: int = 16):
+        """Buffer lane offsets: every offset but the out-of-range sentinel must keep
+        its nbytes below the descriptor's record count OOB (else the load reads zeros)."""
+        v = np.asarray(voff, dtype=np.int64)
+        v = v[v != OOB]
+        if v.size and (v.min() < 0 or v.max() + nbytes > OOB):
+            self.bad32.append(f"{what}: lane offsets {int(v.min())}..{int(v.max())} reach past {OOB:#x}")
+
+    def check(self, sizes: dict) -> list:
+        """Problems: ranges outside [0, sizes[name]) and 32-bit overflows."""
+        out = list(self.bad32)
+        for name in self.lo:
+            if self.lo[name] < 0 or self.hi[name] > sizes[name]:
+                out.append(f"{name}: touches [{self.lo[name]}, {self.hi[name]}) of a {sizes[name]}-byte allocation")
+        return out
+
+
+def span(rows: int, cols: int, ld: int, esize: int = 2) -> int:
+    """Bytes of a [rows, cols] view with row stride ld (elements)."""
+    return 0 if rows == 0 else esize * ((rows - 1) * ld + cols)
+
+
+# ---------------------------------------------------------------------------
+# GEMM: gemm_dma_body<256, 256, 2, 4, 64, 2, ...> (strata_amd/csrc/gemm.hip)
+# ---------------------------------------------------------------------------
+def _xcd_order(n: int, ids: np.ndarray) -> np.ndarray:
+    """common.h xcd_tile_order / gemm.hip tile_origin's first step."""
+    xcd, local = ids & 7, ids >> 3
+    q, rem = n >> 3, n & 7
+    return np.where(xcd < rem, xcd * (q + 1) + local, rem * (q + 1) + (xcd - rem) * q + local)
+
+
+def gemm_tile_origins(M: int, N: int) -> tuple[np.ndarray, np.ndarray]:
+    """(m0, n0) of every persistent-walk tile index t (gemm.hip tile_origin)."""
+    mt, nt = -(-M // 256), -(-N // 256)
+    ntiles = mt * nt
+    wg = _xcd_order(ntiles, np.arange(ntiles, dtype=np.int64))
+    GRP = 4
+    gi, li = wg // (GRP * nt), wg % (GRP * nt)
+    gmn = np.minimum(GRP, mt - gi * GRP)
+    return (gi * GRP + li % gmn) * 256, (li // gmn) * 256
+
+
+def _gswz8(chunk, row):
+    return chunk ^ ((row & 7) ^ ((row >> 3) & 1))
+
+
+def _gemm_dma_offsets(m0, n0, M, N, ldx, ldw):
+    """Lane offsets voff[j] of a stage's x / w copies (gemm.hip dma_off), broadcast
+    over [tile, wave, lane]; and whether each copy reads w."""
+    wave = np.arange(8)[None, :, None]
+    lane = np.arange(64)[None, None, :]
+    out = []
+    for j in range(8):  # LPW = 8 copies of 1 KiB per wave, c = j * NW + wave
+        c = j * 8 + wave
+        isw = c >= 32
+        row = 8 * np.where(isw, c - 32, c) + lane // 8
+        lc = _gswz8(lane % 8, row)
+        ok = np.where(isw, n0 + row < N, m0 + row < M)
+        ld = np.where(isw, ldw, ldx)
+        out.append((np.where(ok, row * ld * 2 + lc * 16, OOB), np.broadcast_to(isw, ok.shape)))
+    return out
+
+
+def _gemm_epilogue_lanes():
+    """(row, column) offsets inside the tile of every 16-byte epilogue store
+    (gemm.hip: wave (wm, wn) = (w / 4, w % 4), lane chunk c = lane % 8, rows
+    RPI * it + lane / 8 of its 128-row half-tile pair), shape [wave, it, lane]."""
+    wave = np.arange(8)[:, None, None]
+    it = np.arange(16)[None, :, None]
+    lane = np.arange(64)[None, None, :]
+    rows = (wave // 4) * 128 + 8 * it + lane // 8
+    cols = (wave % 4) * 64 + 8 * (lane % 8)
+    return np.broadcast_to(rows, (8, 16, 64)), np.broadcast_to(cols, (8, 16, 64))
+
+
+def gemm_dma_launch(M: int, N: int, K: int, ldx: int, ldw: int, ldo: int, ldr: int | None = None,
+                    bias: bool = False, save: bool = False, cus: int = 256) -> Access:
+    """Every global access of one gemm_dma_kernel launch (gemm.hip gemm_dma_body:
+    dma_off / issue_at for the x and w stages, the bias loads into binit, the
+    residual loads r4 and the output (and SAVE) stores of the epilogue).
+    Full tiles (every row < M, every column < N: no mask anywhere) by the
+    separable sum tile base + lane offset; the ragged tiles of the last row and
+    column panels lane by lane."""
+    acc = Access()
+    assert K % 64 == 0 and 256 * ldx * 2 + 4096 < OOB and 256 * ldw * 2 + 4096 < OOB  # gemm_big
+    mt, nt = -(-M // 256), -(-N // 256)
+    acc.u32("tiles", [mt * nt], 1 << 31)
+    m0, n0 = gemm_tile_origins(M, N)
+    nk = K // 64
+    full = (m0 + 256 <= M) & (n0 + 256 <= N)
+    outs = [("out", ldo)] + ([("res", ldr)] if ldr is not None else []) + ([("out2", ldo)] if save else [])
+    # ---- full tiles: offsets inside a full tile do not depend on which tile it is
+    if full.any():
+        fm, fn = m0[full], n0[full]
+        for voff, isw in _gemm_dma_offsets(np.int64(0), np.int64(0), 1 << 62, 1 << 62, ldx, ldw):
+            acc.lane_offsets("gemm dma", voff)
+            for kt in (0, nk - 1):
+                acc.add_sum("x", 2 * (fm * ldx + kt * 64), voff[~isw], 16)
+                acc.add_sum("w", 2 * (fn * ldw + kt * 64), voff[isw], 16)
+        rows, cols = _gemm_epilogue_lanes()
+        for name, ld in outs:
+            acc.add_sum(name, 2 * (fm * ld + fn), 2 * (rows * ld + cols), 16)
+        if bias:
+            acc.add_sum("bias", 2 * fn, 2 * np.arange(0, 256, 4), 8)
+    # ---- ragged tiles, lane by lane
+    rg = ~full
+    if rg.any():
+        m0r, n0r = m0[rg][:, None, None], n0[rg][:, None, None]
+        for voff, isw in _gemm_dma_offsets(m0r, n0r, M, N, ldx, ldw):
+            acc.lane_offsets("gemm dma", voff)
+            live = voff + 16 <= OOB
+            for kt in (0, nk - 1):
+                base = np.where(isw, 2 * (n0r * ldw + kt * 64), 2 * (m0r * ldx + kt * 64))
+                acc.add("x", base + voff, 16, live & ~isw)
+                acc.add("w", base + voff, 16, live & isw)
+        wave = np.arange(8)[None, :, None]
+        lane = np.arange(64)[None, None, :]
+        gm0, gn0 = m0r + (wave // 4) * 128, n0r + (wave % 4) * 64
+        gn = gn0 + 8 * (lane % 8)
+        for it in range(16):
+            gm = gm0 + 8 * it + lane // 8
+            whole = (gm < M) & (gn + 8 <= N)
+            ragged = ~whole & (gm < M) & (gn < N)
+            for name, ld in outs:
+                acc.add(name, 2 * (gm * ld + gn), 16, whole)
+                for e in range(8):
+                    acc.add(name, 2 * (gm * ld + gn + e), 2, ragged & (gn + e < N))
+        if bias:
+            hi = lane // 32
+            for i in range(2):
+                for q in range(4):
+                    g = gn0 + 32 * i + 8 * q + 4 * hi
+                    acc.add("bias", 2 * g, 8, g + 4 <= N)
+                    for e in range(4):
+                        acc.add("bias", 2 * (g + e), 2, (g + 4 > N) & (g + e < N))
+    return acc
+
+
+def gemm_sizes(M, N, K, ldx, ldw, ldo, ldr=None, bias=False, save=False) -> dict:
+    s = {"x": span(M, K, ldx), "w": span(N, K, ldw), "out": span(M, N, ldo)}
+    if ldr is not None:
+        s["res"] = span(M, N, ldr)
+    if bias:
+        s["bias"] = 2 * N
+    if save:
+        s["out2"] = span(M, N, ldo)
+    return s
+
+
+# ---------------------------------------------------------------------------
+# LayerNorm (strata_amd/csrc/layernorm.hip layer_norm_kernel<LPR, NR>)
+# ---------------------------------------------------------------------------
+def layer_norm_launch(M: int, C: int, ldx: int, ldo: int) -> Access:
+    acc = Access()
+    LPR = 64 if (C // 8) % 64 == 0 or (C // 8) % 32 != 0 else 32
+    rows_per_block = 256 // LPR
+    blocks = -(-M // rows_per_block)
+    acc.u32("layer_norm grid", [blocks], 1 << 31)
+    row = np.arange(M, dtype=np.int64)  # rows >= M return before any access
+    run = np.arange(C // 8, dtype=np.int64)  # every run some lane holds (lane + LPR * r < runs)
+    acc.add_sum("x", 2 * row * ldx, 16 * run, 16)
+    acc.add_sum("out", 2 * row * ldo, 16 * run, 16)
+    return acc
+
+
+# ---------------------------------------------------------------------------
+# RoPE + QKV pack, half layout (strata_amd/csrc/rope_pack.hip rope_pack_half_kernel)
+# ---------------------------------------------------------------------------
+def rope_pack_half_launch(B, Z, Y, X, H, D, ld, Zt, pack_q=True, pack_v=False, chunk=1 << 22) -> Access:
+    acc = Access()
+    cph = D // 16
+    C = H * D
+    total = B * Z * Y * X * H * cph
+    slice_ = -(-total // 2)
+    slice_ = -(-slice_ // 64) * 64
+    acc.u32("rope_pack grid", [-(-slice_ // 256)], 1 << 31)
+    # Every address grows with the thread index except the table row, which repeats
+    # per z-slice (Zt = 1) and is largest in the last batch entry: the first and the
+    # last chunk of threads (each longer than a z-slice of tokens) hold the extremes.
+    assert chunk >= Y * X * H * cph or total <= 2 * chunk
+    starts = sorted({0, max(0, total - chunk)})
+    for s0 in starts:
+        idx = np.arange(s0, min(total, s0 + chunk), dtype=np.int64)
+        c = idx % cph
+        th = idx // cph
+        h = th % H
+        tok = th // H
+        src = tok * ld + h * D + 8 * c
+        x, r = tok % X, tok // X
+        y, r = r % Y, r // Y
+        z, b = r % Z, r // Z
+        trow = ((b * Zt + (0 if Zt == 1 else z)) * Y + y) * X + x
+        for t in (0, 1):
+            if t == 0 and not pack_q:
+                continue
+            acc.add("qkv", 2 * (src + t * C), 16)
+            acc.add("qkv", 2 * (src + t * C + D // 2), 16)
+        if pack_v:
+            acc.add("qkv", 2 * (src + 2 * C), 16)
+            acc.add("qkv", 2 * (src + 2 * C + D // 2), 16)
+        acc.add("tables", 4 * (trow * (D // 2) + 8 * c), 32)
+        dst = tok * C + h * D + 8 * c
+        for name in (["q"] if pack_q else []) + ["k"] + (["v"] if pack_v else []):
+            acc.add(name, 2 * dst, 16)
+            acc.add(name, 2 * (dst + D // 2), 16)
+    return acc
+
+
+# ---------------------------------------------------------------------------
+# NA3D, general MFMA kernel (strata_amd/csrc/na3d.hip na3d_mfma_body, D = 64)
+# ---------------------------------------------------------------------------
+def _sub_len(L, g, d):
+    return (L - g + d - 1) // d
+
+
+def _win_start(i, L, k):
+    return np.minimum(np.maximum(i - k // 2, 0), L - k)
+
+
+def _sub_first(o, g, d):
+    return 0 if o <= g else (o - g + d - 1) // d
+
+
+def _sub_end(o, e, g, d):
+    hi = o + e
+    return 0 if hi <= g else (hi - g + d - 1) // d
+
+
+def _blocked_tile(w, nz, ny, nx):
+    BZ = BY = BX = 4
+    zb = w // (BZ * ny * nx)
+    r = w - zb * BZ * ny * nx
+    bz = np.minimum(BZ, nz - zb * BZ)
+    yb = r // (bz * BY * nx)
+    r = r - yb * bz * BY * nx
+    by = np.minimum(BY, ny - yb * BY)
+    xb = r // (bz * by * BX)
+    r = r - xb * bz * by * BX
+    bx = np.minimum(BX, nx - xb * BX)
+    x = xb * BX + r % bx
+    r = r // bx
+    return zb * BZ + r // by, yb * BY + r % by, x
+
+
+def na3d_general_launch(B, L, H, ker, dil, qs, ks, vs, os_, org=(0, 0, 0), ext=None, D=64) -> Access:
+    """Every global access of one na3d_mfma_kernel launch (na3d.hip: make_tiles,
+    the tile decode, the Q and own-key loads, the K/V stage descriptors (issue)
+    and lane offsets (voff), the output stores)."""
+    assert D == 64
+    ext = tuple(L) if ext is None else tuple(ext)
+    kx = ker[2]
+    TX = 16 if kx == 1 else 8 if kx <= 9 else 4 if kx <= 13 else 2
+    NTY, NWX = 4, 4
+    TY = 16 // TX
+    WY, WQX = NTY * TY, NWX * TX
+    LW = (NWX - 1) * TX + 16
+    KPK = 512 // D
+    LWP = -(-LW // KPK) * KPK
+    RB = LWP * D * 2
+    RKB = RB // 1024
+
+    def stage_b(rps):
+        return 2 * rps * RB
+
+    RPS = 4 if TX <= 4 and 2 * stage_b(4) <= 81920 else 2
+    LPT = 2 * RPS * RKB // NWX
+    CPK = D // 8
+    acc = Access()
+    nq = [max(_sub_end(org[a], ext[a], g, dil[a]) - _sub_first(org[a], g, dil[a]) for g in range(dil[a]))
+          for a in range(3)]
+    nzt, nyt, nxt = nq[0], -(-nq[1] // WY), -(-nq[2] // WQX)
+    nres = dil[0] * dil[1] * dil[2]
+    total = nxt * nyt * nzt * nres * H * B
+    acc.u32("na3d workgroups", [total], 1 << 31)
+    wg = _xcd_order(total, np.arange(total, dtype=np.int64))
+    per = nxt * nyt * nzt
+    t = wg // per
+    zt, yt, xt = _blocked_tile(wg - t * per, nzt, nyt, nxt)
+    res = t % nres
+    t = t // nres
+    h, b = t % H, t // H
+    dz, dy, dx = dil
+    gx, gy, gz = res % dx, (res // dx) % dy, res // (dx * dy)
+    Lz = np.array([_sub_len(L[0], g, dz) for g in range(dz)])[gz]
+    Ly = np.array([_sub_len(L[1], g, dy) for g in range(dy)])[gy]
+    Lx = np.array([_sub_len(L[2], g, dx) for g in range(dx)])[gx]
+    f = lambda a, g, d: np.array([_sub_first(org[a], i, d) for i in range(d)])[g]  # noqa: E731
+    e = lambda a, g, d: np.array([_sub_end(org[a], ext[a], i, d) for i in range(d)])[g]  # noqa: E731
+    qz0, qz1 = f(0, gz, dz), e(0, gz, dz)
+    qy0, qy1 = f(1, gy, dy), e(1, gy, dy)
+    qx0, qx1 = f(2, gx, dx), e(2, gx, dx)
+    iz, y0, x0 = qz0 + zt, qy0 + yt * WY, qx0 + xt * WQX
+    live = (iz < qz1) & (y0 < qy1) & (x0 < qx1)  # the rest return before any access
+    # Batch and head enter every address as b * stride[0] + h * stride[4] and no mask
+    # depends on them: the first and last of each bound the rest exactly.
+    live &= ((h == 0) | (h == H - 1)) & ((b == 0) | (b == B - 1))
+    sel = lambda a: a[live]  # noqa: E731
+    iz, y0, x0, h, b, gx, gy, gz, Lz, Ly, Lx, qy1, qx1 = map(sel, (iz, y0, x0, h, b, gx, gy, gz, Lz, Ly, Lx, qy1, qx1))
+    kz, ky = ker[0], ker[1]
+    sz = _win_start(iz, Lz, kz)
+    Y0 = _win_start(y0, Ly, ky)
+    NR = _win_start(np.minimum(y0 + WY - 1, qy1 - 1), Ly, ky) + ky - Y0
+    NQ = -(-NR // RPS)
+    X0 = _win_start(x0, Lx, kx)
+    acc.u32("y-union rows (<= 64: 32-bit stage masks)", NR, 65)
+    col = lambda a: a[:, None]  # noqa: E731  (workgroup axis, then lanes of the whole workgroup)
+    wave = np.arange(256)[None, :] // 64
+    lane = np.arange(256)[None, :] % 64
+    n16, g = lane & 15, lane >> 4
+    # ---- Q and own-key loads (per tile tt of the wave)
+    xw0 = col(x0) + wave * TX
+    qx = xw0 + n16 % TX
+    qxc = np.minimum(qx, col(qx1) - 1)
+    rqx = col(gx) + dx * qxc
+    rz = gz + dz * iz
+    for tt in range(NTY):
+        qyl = col(y0) + tt * TY + n16 // TX
+        rqy = col(gy) + dy * np.minimum(qyl, col(qy1) - 1)
+        for name, st in (("q", qs), ("k", ks)):
+            p = col(b) * st[0] + col(rz) * st[1] + rqy * st[2] + rqx * st[3] + col(h) * st[4]
+            for kk in range(D // 32):
+                acc.add(name, 2 * (p + 32 * kk + 8 * g), 16)
+        # ---- output of tile tt: queries inside the box only
+        ok = (qyl < col(qy1)) & (qx < col(qx1))
+        oz, oy, ox = col(rz) - org[0], col(gy) + dy * qyl - org[1], col(gx) + dx * qx - org[2]
+        op = col(b) * os_[0] + oz * os_[1] + oy * os_[2] + ox * os_[3] + col(h) * os_[4]
+        for db in range(D // 16):
+            acc.add("out", 2 * (op + 16 * db + 4 * g), 8, ok)
+    # ---- K/V stages: descriptor at (z slice, row group cp), lane offsets voff[j]
+    for tensor, name, st in ((0, "k", ks), (1, "v", vs)):
+        rowb = 2 * dy * st[2]
+        for j in range(LPT):
+            gc = j * NWX + wave
+            reg = gc // RKB
+            ten, row = reg // RPS, reg % RPS
+            key = (gc % RKB) * KPK + lane // CPK
+            c = (lane % CPK) ^ (key & 7)  # swz<64>
+            keyok = (key < LW) & (col(X0) + key < col(Lx))
+            voff = np.where(keyok, row * rowb + (col(gx) + dx * (col(X0) + key)) * st[3] * 2 + 16 * c, OOB)
+            acc.lane_offsets("na3d dma", np.where(ten == tensor, voff, OOB))
+            for cp_sel in ("first", "last"):
+                cp = np.zeros_like(NQ) if cp_sel == "first" else NQ - 1
+                nrow = np.minimum(np.maximum(NR - RPS * cp, 0), RPS)
+                nrec = nrow * rowb
+                acc.u32("na3d record count", nrec)
+                for cz in (0, kz - 1):
+                    base = 2 * (b * st[0] + h * st[4] + (gz + dz * (sz + cz)) * st[1] + (gy + dy * (Y0 + RPS * cp)) * st[2])
+                    inrec = (ten == tensor) & (voff + 16 <= col(nrec))
+                    acc.add(name, col(base) + voff, 16, inrec)
+    return acc
+
+
+def tensor_bytes(shape, strides, esize=2) -> int:
+    """Bytes from a view's first element to one past its last (non-negative strides)."""
+    if any(s == 0 for s in shape):
+        return 0
+    return esize * (sum((n - 1) * s for n, s in zip(shape, strides)) + 1)
+
+
+def contiguous_strides(shape):
+    st, acc = [], 1
+    for n in reversed(shape):
+        st.append(acc)
+        acc *= n
+    return list(reversed(st))
+
+
+def production_block_launches(B, Z, Y, X, C, H, kernel, mlp_ratio=4, gated=True, cus=256):
+    """(name, Access, sizes) of every hand-written launch of one StrataBlock forward
+    at inference with qk-norm (strata_amd/modules.py StrataBlock.forward,
+    FusedNA3DAttention.attention): LN, qkv GEMM, pack (q and k, v read from qkv),
+    general NA3D, the gate GEMM, proj + residual, LN, fc1 + GELU, fc2 + residual."""
+    D = C // H
+    M = B * Z * Y * X
+    F = int(C * mlp_ratio)
+    out = []
+    out.append(("layer_norm 1", layer_norm_launch(M, C, C, C), {"x": span(M, C, C), "out": span(M, C, C)}))
+    out.append(("qkv gemm", gemm_dma_launch(M, 3 * C, C, C, C, 3 * C, bias=True, cus=cus),
+                gemm_sizes(M, 3 * C, C, C, C, 3 * C, bias=True)))
+    out.append(("rope pack (q, k; qk-norm)", rope_pack_half_launch(B, Z, Y, X, H, D, 3 * C, 1),
+                {"qkv": span(M, 3 * C, 3 * C), "q": 2 * M * C, "k": 2 * M * C, "tables": 4 * B * Y * X * D // 2}))
+    tok = [Z * Y * X * H * D, Y * X * H * D, X * H * D, H * D, D]
+    vst = [Z * Y * X * 3 * C, Y * X * 3 * C, X * 3 * C, 3 * C, D]
+    acc = na3d_general_launch(B, (Z, Y, X), H, kernel, (1, 1, 1), tok, tok, vst, tok)
+    # v is the view qkv[..., 2, :, :]: its base is 2C elements into the qkv allocation
+    vsz = span(M, 3 * C, 3 * C) - 2 * 2 * C
+    out.append(("na3d (general kernel)", acc, {"q": 2 * M * C, "k": 2 * M * C, "v": vsz, "out": 2 * M * C}))
+    if gated:
+        out.append(("gate gemm (sigmoid, x residual)", gemm_dma_launch(M, C, C, C, C, C, C, bias=True, cus=cus),
+                    gemm_sizes(M, C, C, C, C, C, C, bias=True)))
+    out.append(("proj gemm + residual", gemm_dma_launch(M, C, C, C, C, C, C, bias=True, cus=cus),
+                gemm_sizes(M, C, C, C, C, C, C, bias=True)))
+    out.append(("layer_norm 2", layer_norm_launch(M, C, C, C), {"x": span(M, C, C), "out": span(M, C, C)}))
+    out.append(("fc1 gemm + gelu", gemm_dma_launch(M, F, C, C, C, F, bias=True, cus=cus),
+                gemm_sizes(M, F, C, C, C, F, bias=True)))
+    out.append(("fc2 gemm + residual", gemm_dma_launch(M, C, F, F, F, C, C, bias=True, cus=cus),
+                gemm_sizes(M, C, F, F, F, C, C, bias=True)))
+    return out
+
+
+def cdiv(a, b):
+    return -(-a // b)
+
+
+__all__ = ["Access", "OOB", "gemm_dma_launch", "gemm_sizes", "gemm_tile_origins", "layer_norm_launch",
+           "rope_pack_half_launch", "na3d_general_launch", "production_block_launches", "span", "tensor_bytes",
+           "contiguous_strides", "cdiv", "math"]
