@@ -598,7 +598,7 @@ def cpu_baselines(full: bool):
     def run1():
         return O.na3d(R.apply_rope(q1, c1, s1), R.apply_rope(k1, c1, s1), v1, (3, 7, 7))
 
-    t1, _ = _median_time(run1, 5 if full else 3, 1 if full else 0)
+    t1, _ = _median_time(run1, 5, 1)  # one warm-up, then the median of 5
     out["configs[1]"] = {"seconds": round(t1, 3), "gflops": round(4.0 * 2 * 8 * 64 * 64 * 8 * 147 * 64 / t1 / 1e9, 2)}
     # the block
     B3 = 4 if full else 1

@@ -38,6 +38,13 @@ __device__ __forceinline__ uint32_t pack_bf16x2(float a, float b) {
 __device__ __forceinline__ float bf16_lo(uint32_t w) { return __uint_as_float(w << 16); }
 __device__ __forceinline__ float bf16_hi(uint32_t w) { return __uint_as_float(w & 0xffff0000u); }
 
+// ---- rotary embedding of one channel pair (a, b) by angle (cos c, sin s) ----
+// a' = a c - b s and b' = a s + b c with the fused multiply-adds written out, so
+// every kernel that rotates (the RoPE pack, the query rotation inside NA3D, the
+// qkv GEMM's RoPE epilogue) rounds alike and their outputs agree bit for bit.
+__device__ __forceinline__ float rope_rot_a(float a, float b, float c, float s) { return fmaf(a, c, -(b * s)); }
+__device__ __forceinline__ float rope_rot_b(float a, float b, float c, float s) { return fmaf(a, s, b * c); }
+
 // ---- global -> LDS streaming (buffer_load ... lds) ------------------------
 constexpr uint32_t OOB = 0x7ffffff0u;  // lane offset / record count that reads as zero
 
@@ -51,6 +58,7 @@ __device__ __forceinline__ void wait_vmcnt(int n) {
     STRATA_VMCNT(0) STRATA_VMCNT(1) STRATA_VMCNT(2) STRATA_VMCNT(3) STRATA_VMCNT(4) STRATA_VMCNT(5)
     STRATA_VMCNT(6) STRATA_VMCNT(7) STRATA_VMCNT(8) STRATA_VMCNT(9) STRATA_VMCNT(10) STRATA_VMCNT(11)
     STRATA_VMCNT(12) STRATA_VMCNT(13) STRATA_VMCNT(14) STRATA_VMCNT(15) STRATA_VMCNT(16)
+    STRATA_VMCNT(24) STRATA_VMCNT(32)
 #undef STRATA_VMCNT
     default:
       __builtin_amdgcn_s_waitcnt((7 << 4) | (15 << 8));  // vmcnt(0)

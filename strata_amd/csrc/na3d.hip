@@ -62,8 +62,8 @@ __device__ __forceinline__ void rope_q_pairs(bf16x8& lo, bf16x8& hi, const float
 #pragma unroll
   for (int e = 0; e < 8; ++e) {
     const float a = (float)lo[e], b = (float)hi[e];
-    lo[e] = (bf16)(a * c[e] - b * s[e]);
-    hi[e] = (bf16)(a * s[e] + b * c[e]);
+    lo[e] = (bf16)rope_rot_a(a, b, c[e], s[e]);
+    hi[e] = (bf16)rope_rot_b(a, b, c[e], s[e]);
   }
 }
 
@@ -695,7 +695,7 @@ __device__ __forceinline__ void na3d_strip_tile_exact(const Na3dParams* pp, Stri
     for (int i = 0; i < 16; ++i) {
       const float o = qf[i], q2 = (float)pp2[i], c = p.rc[ro + i], sn = p.rs[ro + i];
       // dims d < 32: a = own, b = partner (a c - b s); d >= 32: a = partner, b = own (a s + b c)
-      qf[i] = (float)(bf16)(dq < 2 ? o * c - q2 * sn : q2 * sn + o * c);
+      qf[i] = (float)(bf16)(dq < 2 ? rope_rot_a(o, q2, c, sn) : rope_rot_b(q2, o, c, sn));
     }
   }
 #pragma unroll

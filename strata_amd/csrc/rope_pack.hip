@@ -74,8 +74,8 @@ __device__ __forceinline__ void rot8(const float* a, const float* b, const float
   for (int w = 0; w < 4; ++w) {
     const float a0 = a[2 * w], a1 = a[2 * w + 1], b0 = b[2 * w], b1 = b[2 * w + 1];
     const float c0 = c[2 * w], c1 = c[2 * w + 1], s0 = s[2 * w], s1 = s[2 * w + 1];
-    oa[w] = pack_bf16x2(a0 * c0 - b0 * s0, a1 * c1 - b1 * s1);
-    ob[w] = pack_bf16x2(a0 * s0 + b0 * c0, a1 * s1 + b1 * c1);
+    oa[w] = pack_bf16x2(rope_rot_a(a0, b0, c0, s0), rope_rot_a(a1, b1, c1, s1));
+    ob[w] = pack_bf16x2(rope_rot_b(a0, b0, c0, s0), rope_rot_b(a1, b1, c1, s1));
   }
 }
 
@@ -176,7 +176,7 @@ __device__ __forceinline__ u32x4 rot_inter(const RopeParams& p, const u32x4& a, 
 #pragma unroll
   for (int k = 0; k < 4; ++k) {
     const float x0 = f[2 * k], x1 = f[2 * k + 1];
-    o[k] = pack_bf16x2(x0 * c[k] - x1 * s[k], x0 * s[k] + x1 * c[k]);
+    o[k] = pack_bf16x2(rope_rot_a(x0, x1, c[k], s[k]), rope_rot_b(x0, x1, c[k], s[k]));
   }
   return o;
 }

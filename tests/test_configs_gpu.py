@@ -61,6 +61,7 @@ def test_cfg1_rope_level_pack_na3d_full(gpu):
     assert torch.equal(kf, kr)
     print(f"  fused vs pack-then-NA3D: identical {torch.equal(out_f, out)}, rel-L2 {rel_l2(out_f, out):.2e}",
           flush=True)
+    assert torch.equal(out_f, out)  # the same rotation arithmetic and tile math
     assert torch.equal(vr.cpu(), v)
     co, so = R.tables(lat, lon, D, 10000.0, ls, levels=Z, level_pairs=8)
     for b, h in ((0, 0), (1, 7), (0, 5)):
