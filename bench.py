@@ -625,14 +625,16 @@ def cpu_baselines(full: bool):
 
 
 def load_traffic():
-    """HBM bytes per NA3D launch from the committed rocprofv3 --pmc summary, if any."""
+    """HBM bytes per NA3D launch from the committed rocprofv3 --pmc summary, if any, and
+    the kernel (with its source commit) that summary was measured on."""
     p = ROOT / "profiles" / "na3d_cfg2_traffic.json"
     if p.exists():
         try:
-            return json.loads(p.read_text()).get("traffic_bytes")
+            d = json.loads(p.read_text())
+            return d.get("traffic_bytes"), f"{d.get('kernel')} (na3d.hip at {d.get('kernel_source_commit')})"
         except (ValueError, OSError):
-            return None
-    return None
+            return None, None
+    return None, None
 
 
 def main():
@@ -721,7 +723,8 @@ def main():
             "peak": PEAK_HBM_GBPS,
             "unit": "GB/s",
             "frac": round(alg_bytes / (ms * 1e-3) / 1e9 / PEAK_HBM_GBPS, 4),
-            "traffic": load_traffic(),
+            "traffic": load_traffic()[0],
+            "traffic_kernel": load_traffic()[1],
             "algorithmic_bytes": alg_bytes,
             "mfma": {"achieved": round(tflops, 2), "peak": PEAK_BF16_TFLOPS, "unit": "TFLOP/s",
                      "frac": round(tflops / PEAK_BF16_TFLOPS, 4)},
