@@ -7,7 +7,9 @@ is not in the reference tree.  Semantics restated from NATTEN's published
 definition (Hassani et al., "Neighborhood Attention Transformer", CVPR 2023,
 and the NATTEN docs): on each axis of length L with odd kernel k and dilation
 d, query i attends the k keys of its residue class g = i mod d nearest to it,
-i.e. the window is shifted (never truncated) at the edges.  3D windows are the
+i.e. the window is shifted (never truncated) at the edges.  A kernel equal to
+the whole undilated axis (even or odd) is every key of the axis: the depth-wise
+attention of alternate blocks uses (Z, 1, 1), full attention over each column.  3D windows are the
 Cartesian product of the per-axis windows; layout is heads-last
 [B, Z, Y, X, H, D].
 
@@ -38,8 +40,8 @@ def window_start(i: int, length: int, kernel: int, dilation: int = 1) -> int:
 
 def axis_keys(length: int, kernel: int, dilation: int = 1) -> Tensor:
     """LongTensor ``[length, kernel]``: key coordinates of every query on one axis."""
-    if kernel % 2 == 0 or kernel < 1:
-        raise ValueError(f"kernel size must be odd and positive, got {kernel}")
+    if kernel < 1 or (kernel % 2 == 0 and not (kernel == length and dilation == 1)):
+        raise ValueError(f"kernel size must be odd and positive (or the whole undilated axis), got {kernel}")
     if kernel * dilation > length:
         raise ValueError(f"kernel*dilation ({kernel}*{dilation}) exceeds axis length {length}")
     starts = torch.tensor([window_start(i, length, kernel, dilation) for i in range(length)], dtype=torch.long)

@@ -1235,7 +1235,7 @@ __device__ __forceinline__ void na3d_strip_fast_body(const Na3dParams p, const N
 
   constexpr int TQB = ROPE ? NWX * 4096 : 0;  // per wave: cos rows of its 16 queries (2 KiB), then sin rows
   static_assert(RING_B + QTB + TQB == strip_fast_lds_bytes<D, TX, RPS, NBUF, ROPE>(), "LDS size");
-  static_assert(!ROPE || (D == 64 && NBUF == 2 && TX * TY == 16), "query RoPE: head_dim 64, every wait drains the copies");
+  static_assert(!ROPE || (D == 64 && TX * TY == 16), "query RoPE: head_dim 64");
 
   // ---- work unit (as na3d_strip_body) ----
   int t = xcd_tile_order(sg.total, id);
@@ -1570,8 +1570,11 @@ __device__ __forceinline__ void na3d_strip_fast_body(const Na3dParams p, const N
     constexpr int C = decltype(cst)::value;
     for (int zc = 0; zc < kz; ++zc) {
       const bool starting = zc == 0 && gr > 0 && gr < NT;
+      // The stage read now was issued NBUF - 1 issues ago.  At a tile's start its Q
+      // copy (issued after the issue of the group's second slice) must have landed
+      // too: only the kz - 2 later issues may still be in flight.
       if (starting)
-        wait_vmcnt(0);  // the tile's Q copy as well
+        wait_vmcnt((NBUF - 2 < kz - 2 ? NBUF - 2 : kz - 2) * LPT);
       else
         wait_vmcnt((NBUF - 2) * LPT);
       lds_barrier();
@@ -1655,17 +1658,21 @@ __global__ __launch_bounds__(256, TX == 8 && KY <= 5 ? 3 : 2) void na3d_strip_fa
 // edge workgroups fill the strips' tail instead of running after them.  Workgroup
 // ids [0, n0) take the strips, [n0, n0 + n1) the top edge, the rest the bottom
 // edge; n0 and n1 are multiples of 8, so each part keeps its XCD-aware tile order.
-template <int KY, bool LSE, bool ROPE = false>
+// Ring depth of the strips: three stages for ky 7 and 9 without the query rotation
+// (68 KiB of LDS, still two workgroups per CU; configs[3] plain 0.343 -> 0.328 ms,
+// configs[1] 0.088 -> 0.086 ms); two where a third stage would cost occupancy (ky 5
+// runs three workgroups per CU at 48 KiB; the rotation's tables take another 16 KiB).
+template <int KY, bool LSE, bool ROPE = false, int NBUF = (ROPE || KY <= 5) ? 2 : 3>
 __global__ __launch_bounds__(256, KY <= 5 ? 3 : 2) void na3d_small_fused_kernel(Na3dParams mid, Na3dStrips sg,
                                                                                Na3dParams e0, Na3dTiles t0,
                                                                                Na3dParams e1, Na3dTiles t1, int n0,
                                                                                int n1) {
   constexpr int NTYE = KY <= 5 ? 1 : 2;
-  constexpr int LS = strip_fast_lds_bytes<64, 8, 2, 2, ROPE>(), LE = mfma_lds_bytes<64, 8, 2, 2>();
+  constexpr int LS = strip_fast_lds_bytes<64, 8, 2, NBUF, ROPE>(), LE = mfma_lds_bytes<64, 8, 2, 2>();
   __shared__ __attribute__((aligned(1024))) char lds[LS > LE ? LS : LE];
   const int id = (int)__builtin_amdgcn_workgroup_id_x();
   if (id < n0) {
-    if (id < sg.total) na3d_strip_fast_body<64, 8, 2, 2, KY, LSE, ROPE>(mid, sg, lds, id);
+    if (id < sg.total) na3d_strip_fast_body<64, 8, 2, NBUF, KY, LSE, ROPE>(mid, sg, lds, id);
   } else if (id < n0 + n1) {
     if (id - n0 < t0.total) na3d_mfma_body<64, 8, NTYE, 2, 2, ROPE>(e0, t0, lds, id - n0);
   } else if (id - n0 - n1 < t1.total) {
@@ -1964,8 +1971,11 @@ static int na3d_prepare(const strata_hip_na3d_args* a, Na3dParams& p) {
   for (int i = 0; i < 3; ++i) {
     const int L = a->grid[i], k = a->kernel[i], d = a->dilation[i];
     if (L <= 0) return fail(STRATA_HIP_EINVAL, std::string("na3d: grid size must be positive on axis ") + axis[i]);
-    if (k <= 0 || (k % 2) == 0)
-      return fail(STRATA_HIP_EINVAL, std::string("na3d: kernel size must be odd and positive on axis ") + axis[i]);
+    // Odd, or the whole undilated axis (every query then attends the full axis,
+    // the window depth-wise attention uses along z).
+    if (k <= 0 || ((k % 2) == 0 && !(k == L && d == 1)))
+      return fail(STRATA_HIP_EINVAL,
+                  std::string("na3d: kernel size must be odd and positive (or the whole axis) on axis ") + axis[i]);
     if (d <= 0) return fail(STRATA_HIP_EINVAL, std::string("na3d: dilation must be positive on axis ") + axis[i]);
     if ((int64_t)k * d > L)
       return fail(STRATA_HIP_EINVAL,

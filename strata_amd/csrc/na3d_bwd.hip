@@ -1763,8 +1763,10 @@ static int na3d_bwd_run(const strata_hip_na3d_bwd_args* a, float* workspace, voi
   for (int i = 0; i < 3; ++i) {
     const int L = a->grid[i], k = a->kernel[i], d = a->dilation[i];
     if (L <= 0) return fail(STRATA_HIP_EINVAL, std::string("na3d_bwd: grid size must be positive on axis ") + axis[i]);
-    if (k <= 0 || (k % 2) == 0)
-      return fail(STRATA_HIP_EINVAL, std::string("na3d_bwd: kernel size must be odd and positive on axis ") + axis[i]);
+    // Odd, or the whole undilated axis (as the forward; axis_inv then spans the axis).
+    if (k <= 0 || ((k % 2) == 0 && !(k == L && d == 1)))
+      return fail(STRATA_HIP_EINVAL,
+                  std::string("na3d_bwd: kernel size must be odd and positive (or the whole axis) on axis ") + axis[i]);
     if (d <= 0) return fail(STRATA_HIP_EINVAL, std::string("na3d_bwd: dilation must be positive on axis ") + axis[i]);
     if ((int64_t)d * k > L)
       return fail(STRATA_HIP_EINVAL, std::string("na3d_bwd: dilation * kernel exceeds the grid on axis ") + axis[i]);

@@ -82,14 +82,25 @@ class FusedNA3DAttention(nn.Module):
     normalises q and k per head inside the RoPE pack kernel; with
     ``qk_norm_affine`` the weights live in ``attn.q_norm`` / ``attn.k_norm``
     (nn.RMSNorm, registered after the manifest keys).
+
+    ``depthwise``: the block attends along the depth (z) axis only, every token
+    to the whole column of tokens at its (y, x): NA3D with the window (Z, 1, 1)
+    of the input's Z, the same qkv / proj / gate parameters (the production
+    manifest's blocks all carry the same keys).  This is this build's reading of
+    ``do_alt_depthwise_attn`` (screamcast/config.py:101-103, passed at
+    screamcast/strata_wrappers.py:329; "depth" is the vertical axis of
+    ``input_shape=(depth, height, width)``, :317); the arithmetic lives in
+    physicsnemo, absent here, so parity of the convention is unpinned.
     """
 
     def __init__(self, dim: int, num_heads: int, kernel_size, dilation=1, qkv_bias: bool = True,
                  gated: bool = False, rope_layout: int = _lib.ROPE_HALF, scale: Optional[float] = None,
-                 qk_norm: bool = False, qk_norm_affine: bool = False, qk_norm_eps: float = 1e-6):
+                 qk_norm: bool = False, qk_norm_affine: bool = False, qk_norm_eps: float = 1e-6,
+                 depthwise: bool = False):
         super().__init__()
         if dim % num_heads:
             raise ValueError("dim must be divisible by num_heads")
+        self.depthwise = depthwise
         self.dim, self.num_heads = dim, num_heads
         self.head_dim = dim // num_heads
         self.kernel_size = _triple(kernel_size)
@@ -115,7 +126,7 @@ class FusedNA3DAttention(nn.Module):
     @classmethod
     def from_attention(cls, attn: nn.Module, num_heads: int, kernel_size, dilation=1, qk_norm: bool = False,
                        qk_norm_eps: float = 1e-6, rope_layout: int = _lib.ROPE_HALF,
-                       scale: Optional[float] = None) -> "FusedNA3DAttention":
+                       scale: Optional[float] = None, depthwise: bool = False) -> "FusedNA3DAttention":
         """Wrap an existing attention module, sharing its Linear (and RMSNorm) children.
 
         The children are re-registered in the module's own order, so the state-dict
@@ -151,12 +162,20 @@ class FusedNA3DAttention(nn.Module):
         new.rope_layout = rope_layout
         new.scale = scale
         new.qk_norm, new.qk_norm_eps = qk_norm, qk_norm_eps
+        new.depthwise = depthwise
         return new
+
+    def window(self, z: int) -> tuple[list[int], list[int]]:
+        """NA3D kernel and dilation for an input of depth ``z``."""
+        if self.depthwise:
+            return [z, 1, 1], [1, 1, 1]
+        return self.kernel_size, self.dilation
 
     def attention(self, x: Tensor, rope: Optional[tuple[Tensor, Tensor]] = None) -> Tensor:
         """Attention output before the projection, ``[B, Z, Y, X, C]``."""
         B, Z, Y, X, C = x.shape
         H, D = self.num_heads, self.head_dim
+        kernel, dilation = self.window(Z)
         qkv = ops.gemm_bias_act(x, self.qkv.weight, self.qkv.bias, None, _lib.ACT_NONE)
         if rope is None and self.qk_norm:  # normalise in the pack kernel with identity rotations
             ident = torch.ones(B, 1, Y, X, D // 2, device=x.device)
@@ -175,11 +194,10 @@ class FusedNA3DAttention(nn.Module):
                 qkv6 = qkv.view(B, Z, Y, X, 3, H, D)
                 q, v = qkv6[..., 0, :, :], qkv6[..., 2, :, :]
                 kst = [Z * Y * X * H * D, Y * X * H * D, X * H * D, H * D, D]
-                if ops.na3d_rope_q_supported(q, kst, v, rope[0], rope[1], self.kernel_size, self.dilation,
-                                             self.scale):
+                if ops.na3d_rope_q_supported(q, kst, v, rope[0], rope[1], kernel, dilation, self.scale):
                     _, k, _ = ops.rope_qkv_pack(qkv, rope[0], rope[1], H, self.rope_layout, pack_v=False,
                                                 pack_q=False)
-                    a = ops.na3d_fwd_rope_q(q, k, v, rope[0], rope[1], self.kernel_size, self.dilation, self.scale)
+                    a = ops.na3d_fwd_rope_q(q, k, v, rope[0], rope[1], kernel, dilation, self.scale)
                     return self._gate(x, a.view(B, Z, Y, X, C))
             q, k, v = ops.rope_qkv_pack(qkv, rope[0], rope[1], H, self.rope_layout, self.qk_norm, self.qk_norm_eps,
                                         qw, kw, pack_v=train)
@@ -188,7 +206,7 @@ class FusedNA3DAttention(nn.Module):
         else:
             qkv6 = qkv.view(B, Z, Y, X, 3, H, D)
             q, k, v = qkv6[..., 0, :, :], qkv6[..., 1, :, :], qkv6[..., 2, :, :]
-        a = ops.na3d(q, k, v, self.kernel_size, self.dilation, self.scale)
+        a = ops.na3d(q, k, v, kernel, dilation, self.scale)
         return self._gate(x, a.view(B, Z, Y, X, C))
 
     def _gate(self, x: Tensor, a: Tensor) -> Tensor:
@@ -213,11 +231,12 @@ class StrataBlock(nn.Module):
 
     def __init__(self, dim: int, num_heads: int, kernel_size, mlp_ratio: float = 4.0, dilation=1,
                  qkv_bias: bool = True, gated: bool = False, eps: float = 1e-6, qk_norm: bool = False,
-                 qk_norm_affine: bool = False, qk_norm_eps: float = 1e-6):
+                 qk_norm_affine: bool = False, qk_norm_eps: float = 1e-6, depthwise: bool = False):
         super().__init__()
         self.eps = eps
         self.attn = FusedNA3DAttention(dim, num_heads, kernel_size, dilation, qkv_bias, gated,
-                                       qk_norm=qk_norm, qk_norm_affine=qk_norm_affine, qk_norm_eps=qk_norm_eps)
+                                       qk_norm=qk_norm, qk_norm_affine=qk_norm_affine, qk_norm_eps=qk_norm_eps,
+                                       depthwise=depthwise)
         self.mlp = GemmGeluMlp(dim, int(dim * mlp_ratio))
 
     def forward(self, x: Tensor, rope: Optional[tuple[Tensor, Tensor]] = None) -> Tensor:
@@ -257,7 +276,7 @@ def _is_attention(m: nn.Module) -> bool:
 
 
 def swap_attention(model: nn.Module, num_heads, kernel_size, dilation=1, qk_norm=False, qk_norm_eps: float = 1e-6,
-                   rope_layout: int = _lib.ROPE_HALF, scale: Optional[float] = None) -> int:
+                   rope_layout: int = _lib.ROPE_HALF, scale: Optional[float] = None, depthwise=False) -> int:
     """Replace every attention-shaped child (``nn.Linear`` children ``qkv`` [3C, C] and
     ``proj`` [C, C], optionally ``gate_proj`` and RMSNorms ``q_norm`` / ``k_norm``) by a
     :class:`FusedNA3DAttention` sharing those modules: the qkv GEMM, the (qk-norm +)
@@ -267,9 +286,10 @@ def swap_attention(model: nn.Module, num_heads, kernel_size, dilation=1, qk_norm
     (screamcast/strata_wrappers.py:76-100, applied at :342 and :509): modules are
     found by structure, parameters are shared, and state-dict keys and
     ``named_parameters()`` order stay as they were (tests/test_param_order.py:87-119).
-    ``num_heads``, ``kernel_size``, ``dilation`` and ``qk_norm`` are either one value
-    for every swapped module or a sequence with one entry per module, in
-    ``model.modules()`` order (a per-block dilation schedule, for instance).
+    ``num_heads``, ``kernel_size``, ``dilation``, ``qk_norm`` and ``depthwise`` are either
+    one value for every swapped module or a sequence with one entry per module, in
+    ``model.modules()`` order (a per-block dilation schedule, or
+    :func:`alternating_depthwise`, for instance).
     Returns the number of modules swapped; raises ``RuntimeError`` if there were
     none (as ``_use_tanh_gelu`` does)."""
     targets = [(parent, name, child) for parent in list(model.modules())
@@ -293,7 +313,8 @@ def swap_attention(model: nn.Module, num_heads, kernel_size, dilation=1, qk_norm
             pick(kernel_size, i, lambda v: isinstance(v, int) or (len(v) == 3 and all(isinstance(t, int) for t in v))),
             pick(dilation, i, lambda v: isinstance(v, int) or (len(v) == 3 and all(isinstance(t, int) for t in v))),
             pick(qk_norm, i, lambda v: isinstance(v, bool)),
-            qk_norm_eps, rope_layout, scale)
+            qk_norm_eps, rope_layout, scale,
+            pick(depthwise, i, lambda v: isinstance(v, bool)))
         setattr(parent, name, new)
     return len(targets)
 
@@ -313,6 +334,15 @@ def interleaved_dilations(n_layers: int, na_dilation: int, kernel_size, grid, in
         return [[1, 1, 1] for _ in range(n_layers)]
     odd = [na_dilation if kk * na_dilation <= L else 1 for kk, L in zip(k, grid)]
     return [[1, 1, 1] if i % 2 == 0 else list(odd) for i in range(n_layers)]
+
+
+def alternating_depthwise(n_layers: int, alternate: bool = True) -> list[bool]:
+    """Per-block depth-wise flags for ``do_alt_depthwise_attn`` ("depthwise attention every
+    other DiTBlock", screamcast/config.py:101-103).  Which blocks alternate is defined in
+    physicsnemo (absent here); this build's convention, parity unpinned: odd-indexed blocks
+    are depth-wise, even ones keep the neighbourhood window.  Feed the result to
+    ``swap_attention(..., depthwise=...)`` or to ``StrataBlock(depthwise=...)``."""
+    return [alternate and i % 2 == 1 for i in range(n_layers)]
 
 
 def init_xavier_(module: nn.Module, generator: torch.Generator) -> None:

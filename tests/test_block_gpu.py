@@ -14,9 +14,9 @@ pytestmark = pytest.mark.gpu
 
 
 def _block_case(gpu, B, Z, Y, X, C, H, kernel, seed=0, gated=False, qk_norm=False, qk_norm_affine=False,
-                base=10000.0, ls_patch=1):
+                base=10000.0, ls_patch=1, depthwise=False):
     g = torch.Generator().manual_seed(1)
-    blk = StrataBlock(C, H, kernel, gated=gated, qk_norm=qk_norm, qk_norm_affine=qk_norm_affine)
+    blk = StrataBlock(C, H, kernel, gated=gated, qk_norm=qk_norm, qk_norm_affine=qk_norm_affine, depthwise=depthwise)
     init_xavier_(blk, g)
     if gated:
         with torch.no_grad():
@@ -37,7 +37,8 @@ def _block_case(gpu, B, Z, Y, X, C, H, kernel, seed=0, gated=False, qk_norm=Fals
     # fp32 oracle on the same bf16 inputs and bf16-rounded weights
     params = {k: v.bfloat16().float() for k, v in params.items()}
     c64, s64 = R.tables(lat, lon, C // H, base, ls)
-    ref = OB.block_forward(x.float(), params, H, kernel, c64.float(), s64.float(), gated=gated, qk_norm=qk_norm)
+    ref_kernel = (Z, 1, 1) if depthwise else kernel
+    ref = OB.block_forward(x.float(), params, H, ref_kernel, c64.float(), s64.float(), gated=gated, qk_norm=qk_norm)
     return out, ref
 
 
@@ -66,6 +67,15 @@ def test_block_production_window(gpu):
     """The production attention on a reduced grid: window (3,3,3), gated, qk RMSNorm without
     weights, RoPE base 100 at the patch-4 length scale, 1024 wide (16 x 64 heads)."""
     out, ref = _block_case(gpu, 1, 6, 24, 24, 1024, 16, (3, 3, 3), gated=True, qk_norm=True, base=100.0, ls_patch=4)
+    assert rel_l2(out.float(), ref) <= 1e-2
+
+
+@pytest.mark.parametrize("Z", [6, 7])
+def test_block_depthwise(gpu, Z):
+    """Depth-wise block (every token attends its whole z column: window (Z, 1, 1), even and
+    odd Z) with the production flags: gated, qk RMSNorm, RoPE base 100, 1024 wide."""
+    out, ref = _block_case(gpu, 1, Z, 12, 12, 1024, 16, (3, 3, 3), gated=True, qk_norm=True, base=100.0, ls_patch=4,
+                           depthwise=True)
     assert rel_l2(out.float(), ref) <= 1e-2
 
 

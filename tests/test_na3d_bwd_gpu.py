@@ -31,6 +31,10 @@ CASES = [  # shape [B, Z, Y, X, H, D], kernel, dilation
     ((1, 3, 33, 16, 3, 64), (3, 5, 5), (1, 1, 1)),
     # the production window (3,3,3) at head_dim 64 (the tile walks)
     ((1, 5, 24, 20, 2, 64), (3, 3, 3), (1, 1, 1)),
+    # depth-wise attention: the whole z column, even (a kernel equal to the axis) and odd
+    ((1, 8, 6, 7, 2, 64), (8, 1, 1), (1, 1, 1)),
+    ((1, 24, 4, 5, 2, 64), (24, 1, 1), (1, 1, 1)),
+    ((1, 7, 5, 6, 1, 32), (7, 1, 1), (1, 1, 1)),
 ]
 
 

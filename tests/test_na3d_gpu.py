@@ -336,3 +336,36 @@ def test_small_window_strips_match_general_kernel(gpu, monkeypatch):
     monkeypatch.setenv("STRATA_HIP_NA3D_NO_SMALL_STRIPS", "1")
     b = _run(q, k, v, (3, 7, 7))
     assert rel_l2(a.float(), b.float()) <= 5e-3
+
+
+def _column_attention(q, k, v, scale=None):
+    """Softmax attention of every token over its whole z column (float64): the textbook
+    dense attention, independent of the NA3D oracle's window tables."""
+    B, Z, Y, X, H, D = q.shape
+    scale = D**-0.5 if scale is None else scale
+    qc, kc, vc = (t.double().permute(0, 2, 3, 4, 1, 5) for t in (q, k, v))  # [B, Y, X, H, Z, D]
+    p = torch.softmax(scale * qc @ kc.transpose(-1, -2), dim=-1)
+    return (p @ vc).permute(0, 4, 1, 2, 3, 5)
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+@pytest.mark.parametrize("Z", [8, 24, 5])
+def test_depthwise_window_is_column_attention(gpu, dtype, Z):
+    """Window (Z, 1, 1): every query attends its whole z column, for even Z (a kernel equal
+    to the whole axis) and odd Z; the production depth of 24 among them."""
+    q, k, v = _rand((1, Z, 6, 10, 4, 64), 3, dtype, gpu)
+    print(f"depthwise {dtype} Z={Z}", flush=True)
+    out = _run(q, k, v, (Z, 1, 1))
+    ref = _column_attention(q.cpu(), k.cpu(), v.cpu())
+    if dtype == torch.float32:
+        assert (out.cpu().double() - ref).abs().max().item() <= F32_TOL
+    else:
+        assert rel_l2(out.float(), ref) <= BF16_TOL
+
+
+def test_even_kernel_short_of_the_axis_is_refused(gpu):
+    q, k, v = _rand((1, 8, 6, 6, 2, 64), 4, torch.bfloat16, gpu)
+    with pytest.raises(ValueError, match="odd"):
+        _run(q, k, v, (6, 1, 1))
+    with pytest.raises(ValueError, match="odd"):
+        _run(q, k, v, (8, 1, 1), dilation=(2, 1, 1))

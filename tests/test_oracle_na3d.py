@@ -121,6 +121,38 @@ def test_rejects_even_or_oversized_kernel():
         O.na3d(q, q, q, (2, 3, 3))
     with pytest.raises(ValueError):
         O.na3d(q, q, q, (5, 3, 3))
+    with pytest.raises(ValueError):  # even and the whole axis, but dilated
+        O.axis_keys(4, 4, 2)
+
+
+def _column_softmax(q, k, v):
+    """Dense softmax attention over the z axis only, written directly (float64)."""
+    B, Z, Y, X, H, D = q.shape
+    out = torch.empty_like(q)
+    for b in range(B):
+        for y in range(Y):
+            for x in range(X):
+                for h in range(H):
+                    s = (q[b, :, y, x, h] @ k[b, :, y, x, h].T) * D**-0.5
+                    out[b, :, y, x, h] = torch.softmax(s, dim=-1) @ v[b, :, y, x, h]
+    return out
+
+
+@pytest.mark.parametrize("Z", [4, 5, 6])
+def test_depthwise_window_is_column_softmax(Z):
+    """Window (Z, 1, 1), even Z included (a kernel equal to the whole axis): every query
+    attends its whole z column and nothing else."""
+    assert O.axis_keys(Z, Z).tolist() == [list(range(Z))] * Z
+    g = torch.Generator().manual_seed(11)
+    shape = (1, Z, 3, 4, 2, 8)
+    q, k, v = (torch.randn(shape, generator=g, dtype=torch.float64) for _ in range(3))
+    ref = _column_softmax(q, k, v)
+    assert (O.na3d(q, k, v, (Z, 1, 1), compute_dtype=torch.float64) - ref).abs().max().item() < 1e-12
+    assert (O.na3d_bruteforce(q, k, v, (Z, 1, 1)) - ref).abs().max().item() < 1e-12
+    # a planted mistake: a window one key short of the column (odd kernel Z - 1 when Z is
+    # even, the nearest NATTEN window) does not reproduce it
+    if Z % 2 == 0:
+        assert (O.na3d(q, k, v, (Z - 1, 1, 1), compute_dtype=torch.float64) - ref).abs().max().item() > 1e-3
 
 
 def test_flop_count_cfg2():

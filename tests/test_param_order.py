@@ -182,3 +182,23 @@ def test_interleaved_dilation_schedule():
     s = interleaved_dilations(4, 3, (3, 5, 5), (8, 16, 16))
     assert s[0] == s[2] == [1, 1, 1] and s[1] == s[3] == [1, 3, 3]  # 3*3 > 8 keeps z undilated
     assert interleaved_dilations(3, 3, 3, (24, 144, 144))[1] == [3, 3, 3]
+
+
+def test_alternating_depthwise_schedule_keeps_keys_and_order():
+    """The production flags (gated, qk-norm, do_alt_depthwise_attn): odd blocks attend their
+    z column (window (Z, 1, 1) of the input's Z), even blocks keep (3, 3, 3); the manifest's
+    keys, order and parameter objects are unchanged."""
+    from strata_amd.modules import alternating_depthwise
+
+    assert alternating_depthwise(4) == [False, True, False, True]
+    assert alternating_depthwise(3, alternate=False) == [False] * 3
+    names = _names(SWEEP1)
+    model = _tree_from_manifest(names)
+    before = dict(model.named_parameters())
+    swap_attention(model.strata, 4, 3, qk_norm=True, depthwise=alternating_depthwise(32))
+    after = list(model.named_parameters())
+    assert [n for n, _ in after] == names and all(p is before[n] for n, p in after)
+    blocks = list(model.strata.blocks.children())
+    assert [b.attn.depthwise for b in blocks[:4]] == [False, True, False, True]
+    assert blocks[0].attn.window(24) == ([3, 3, 3], [1, 1, 1])
+    assert blocks[1].attn.window(24) == ([24, 1, 1], [1, 1, 1])
