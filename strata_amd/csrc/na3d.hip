@@ -1682,6 +1682,135 @@ __global__ __launch_bounds__(256, KY <= 5 ? 3 : 2) void na3d_small_fused_kernel(
 
 
 // ---------------------------------------------------------------------------
+// Depth-wise (column) attention: window (Z, 1, 1) over the whole z axis, Z <= 32,
+// head_dim 64, bf16, the whole grid as the query box.  Every token attends the Z
+// tokens of its own (y, x) column; the tile kernels above would compute a 16 x 16
+// score block per 16 useful pairs here.
+//
+// One wave per (batch, y, x, head) column, four per workgroup (consecutive heads
+// of one column: their rows are 128 bytes apart).  The column's Q, K and V rows
+// are loaded with whole-line loads (lane l: row l / 8 + 8 c, 16-byte chunk l % 8;
+// rows past Z zero) and pass in turn through the wave's 4 KiB of LDS (chunk slot
+// (l % 8) ^ (row % 8)) into the MFMA layouts.  S^T = K Q^T on v_mfma_f32_32x32x16_bf16 (keys on M, queries
+// on N, Z padded to 32); the softmax runs over a lane's 16 keys and its partner
+// lane's (l ^ 32) other 16.  O^T = V^T P^T: P^T comes from the score lanes as they
+// are (k-index 8 hi + m of k-step t is key 16 t + 4 hi + m for m < 4 and
+// 16 t + 8 + 4 hi + m - 4 otherwise, the keys the score layout gives lane half hi),
+// and V^T gathers the same keys' values of one dimension from LDS.  Lane
+// (query n, hi) ends holding O^T rows 32 db + 8 i + 4 hi + e, four consecutive dims
+// that it writes to the buffer's row n, read back and stored as whole rows.
+// ---------------------------------------------------------------------------
+__global__ __launch_bounds__(256) void na3d_column_kernel(Na3dParams p, int64_t items) {
+#if defined(__HIP_DEVICE_COMPILE__)
+  __shared__ __attribute__((aligned(16))) bf16 sh[4][32 * 64];  // per wave: Q, then K, then V rows
+  const int tid = (int)__builtin_amdgcn_workitem_id_x();
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int lane = tid & 63;
+  const int64_t item = (int64_t)__builtin_amdgcn_workgroup_id_x() * 4 + wave;
+  if (item >= items) return;  // uniform over the wave; no barrier below
+  int64_t t = item;
+  const int h = (int)(t % p.H);
+  t /= p.H;
+  const int x = (int)(t % p.L[2]);
+  t /= p.L[2];
+  const int y = (int)(t % p.L[1]);
+  const int b = (int)(t / p.L[1]);
+  const int Z = p.L[0];
+  const int n = lane & 31, hi = lane >> 5;
+  const bf16* src[3] = {
+      (const bf16*)p.q + (int64_t)b * p.qs[0] + (int64_t)y * p.qs[2] + (int64_t)x * p.qs[3] + (int64_t)h * p.qs[4],
+      (const bf16*)p.k + (int64_t)b * p.ks[0] + (int64_t)y * p.ks[2] + (int64_t)x * p.ks[3] + (int64_t)h * p.ks[4],
+      (const bf16*)p.v + (int64_t)b * p.vs[0] + (int64_t)y * p.vs[2] + (int64_t)x * p.vs[3] + (int64_t)h * p.vs[4]};
+  const int64_t zs[3] = {p.qs[1], p.ks[1], p.vs[1]};
+  bf16* const sw = sh[wave];
+  // element (row r, dim d) of the staged tensor
+  auto at = [](int r, int d) { return r * 64 + 8 * ((d >> 3) ^ (r & 7)) + (d & 7); };
+
+  u32x4 w[3][4];  // all three tensors' loads in flight at once
+#pragma unroll
+  for (int tt = 0; tt < 3; ++tt)
+#pragma unroll
+    for (int c = 0; c < 4; ++c) {
+      const int r = lane / 8 + 8 * c;
+      w[tt][c] = (u32x4){0u, 0u, 0u, 0u};
+      if (r < Z) w[tt][c] = *(const u32x4*)(src[tt] + (int64_t)r * zs[tt] + 8 * (lane % 8));
+    }
+  // Through the wave's one LDS buffer in turn (its own rows only: no barrier); the
+  // waits order each tensor's fragment reads before the next tensor's writes.
+  auto stage = [&](int tt) {
+    wait_lgkm0();
+#pragma unroll
+    for (int c = 0; c < 4; ++c) *(u32x4*)&sw[at(lane / 8 + 8 * c, 8 * (lane % 8))] = w[tt][c];
+    wait_lgkm0();
+  };
+  bf16x8 qf[4], kf[4];
+  stage(0);
+#pragma unroll
+  for (int st = 0; st < 4; ++st) qf[st] = *(const bf16x8*)&sw[at(n, 16 * st + 8 * hi)];
+  stage(1);
+#pragma unroll
+  for (int st = 0; st < 4; ++st) kf[st] = *(const bf16x8*)&sw[at(n, 16 * st + 8 * hi)];
+  stage(2);
+  // Scores S^T[key][query], log2 units.
+  f32x16 sacc = {};
+#pragma unroll
+  for (int st = 0; st < 4; ++st) sacc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kf[st], qf[st], sacc, 0, 0, 0);
+  const float c2 = p.scale * 1.4426950408889634f;
+  float m = -INFINITY;
+#pragma unroll
+  for (int j = 0; j < 16; ++j) {
+    const int key = 8 * (j >> 2) + 4 * hi + (j & 3);
+    sacc[j] = key < Z ? sacc[j] * c2 : -INFINITY;
+    m = fmaxf(m, sacc[j]);
+  }
+  m = fmaxf(m, __shfl_xor(m, 32));
+  float l = 0.f;
+#pragma unroll
+  for (int j = 0; j < 16; ++j) {
+    sacc[j] = __builtin_amdgcn_exp2f(sacc[j] - m);  // masked keys: 2^-inf = 0
+    l += sacc[j];
+  }
+  l += __shfl_xor(l, 32);
+
+  // O^T = V^T P^T over two k-steps of 16 keys, two blocks of 32 dims.
+  f32x16 oacc[2] = {};
+#pragma unroll
+  for (int kt = 0; kt < 2; ++kt) {
+    bf16x8 pb;
+#pragma unroll
+    for (int mm = 0; mm < 8; ++mm) pb[mm] = (bf16)sacc[4 * (2 * kt + (mm >> 2)) + (mm & 3)];
+#pragma unroll
+    for (int db = 0; db < 2; ++db) {
+      bf16x8 va;
+#pragma unroll
+      for (int mm = 0; mm < 8; ++mm) va[mm] = sw[at(16 * kt + 8 * (mm >> 2) + 4 * hi + (mm & 3), 32 * db + n)];
+      oacc[db] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(va, pb, oacc[db], 0, 0, 0);
+    }
+  }
+  // The output goes back through the LDS buffer (row = query) so that each store
+  // instruction writes whole 128-byte rows.
+  const float inv = 1.f / l;
+  wait_lgkm0();  // the V gathers are done
+#pragma unroll
+  for (int db = 0; db < 2; ++db)
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const u32x2 ow = {pack_bf16x2(oacc[db][4 * i] * inv, oacc[db][4 * i + 1] * inv),
+                        pack_bf16x2(oacc[db][4 * i + 2] * inv, oacc[db][4 * i + 3] * inv)};
+      *(u32x2*)&sw[at(n, 32 * db + 8 * i + 4 * hi)] = ow;
+    }
+  wait_lgkm0();
+  bf16* o = (bf16*)p.o + (int64_t)b * p.os[0] + (int64_t)y * p.os[2] + (int64_t)x * p.os[3] + (int64_t)h * p.os[4];
+#pragma unroll
+  for (int c = 0; c < 4; ++c) {
+    const int r = lane / 8 + 8 * c;
+    if (r < Z) *(u32x4*)(o + (int64_t)r * p.os[1] + 8 * (lane % 8)) = *(const u32x4*)&sw[at(r, 8 * (lane % 8))];
+  }
+  if (p.lse && hi == 0 && n < Z) p.lse[lse_index(p, b, n, y, x, h)] = m + __log2f(l);
+#endif
+}
+
+// ---------------------------------------------------------------------------
 // Host side
 // ---------------------------------------------------------------------------
 template <typename T>
@@ -1956,6 +2085,22 @@ static int launch_mfma_d(const Na3dParams& p, hipStream_t st) {
 
 static bool aligned16(const void* ptr) { return ((uintptr_t)ptr & 15u) == 0; }
 
+// Depth-wise windows for na3d_column_kernel: (Z, 1, 1) with Z <= 32, undilated, head_dim
+// 64, the whole grid as the query box (the MFMA layout conditions hold: na3d_mfma_ok).
+static bool column_fits(const Na3dParams& p) {
+  return p.D == 64 && p.ker[0] == p.L[0] && p.L[0] <= 32 && p.ker[1] == 1 && p.ker[2] == 1 && p.dil[0] == 1 &&
+         p.dil[1] == 1 && p.dil[2] == 1 && p.org[0] == 0 && p.org[1] == 0 && p.org[2] == 0 && p.ext[0] == p.L[0] &&
+         p.ext[1] == p.L[1] && p.ext[2] == p.L[2] && p.lse_ext1 == p.ext[1];
+}
+
+static int launch_column(const Na3dParams& p, hipStream_t st) {
+  const int64_t items = (int64_t)p.B * p.L[1] * p.L[2] * p.H;
+  const int64_t wgs = (items + 3) / 4;
+  if (wgs > 0x7fffffff) return fail(STRATA_HIP_EUNSUPPORTED, "na3d: problem too large for one launch");
+  hipLaunchKernelGGL(na3d_column_kernel, dim3((unsigned)wgs), dim3(256), 0, st, p, items);
+  return check_launch("na3d_column_kernel");
+}
+
 }  // namespace strata
 
 using namespace strata;
@@ -2052,6 +2197,7 @@ extern "C" int strata_hip_na3d_fwd(const strata_hip_na3d_args* a, void* stream) 
   if (a->dtype == STRATA_HIP_F32) return launch_scalar<float>(p, st);
   const bool mfma_ok = na3d_mfma_ok(p);
   if (!mfma_ok) return launch_scalar<bf16>(p, st);
+  if (column_fits(p)) return launch_column(p, st);
   switch (p.D) {
     case 32:
       return launch_mfma_d<32>(p, st);

@@ -349,10 +349,11 @@ def _column_attention(q, k, v, scale=None):
 
 
 @pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
-@pytest.mark.parametrize("Z", [8, 24, 5])
+@pytest.mark.parametrize("Z", [8, 24, 5, 32, 1, 40])
 def test_depthwise_window_is_column_attention(gpu, dtype, Z):
     """Window (Z, 1, 1): every query attends its whole z column, for even Z (a kernel equal
-    to the whole axis) and odd Z; the production depth of 24 among them."""
+    to the whole axis) and odd Z; the production depth of 24 among them.  bf16 Z <= 32 runs
+    the column kernel (Z = 1 and 32 at its ends), Z = 40 the tile kernels."""
     q, k, v = _rand((1, Z, 6, 10, 4, 64), 3, dtype, gpu)
     print(f"depthwise {dtype} Z={Z}", flush=True)
     out = _run(q, k, v, (Z, 1, 1))
@@ -369,3 +370,18 @@ def test_even_kernel_short_of_the_axis_is_refused(gpu):
         _run(q, k, v, (6, 1, 1))
     with pytest.raises(ValueError, match="odd"):
         _run(q, k, v, (8, 1, 1), dilation=(2, 1, 1))
+
+
+def test_depthwise_lse_and_strided_views(gpu):
+    """The column kernel with lse (the training forward) and q / v as strided views of a
+    packed qkv buffer, against the oracle's log2-sum-exp and outputs."""
+    B, Z, Y, X, H = 2, 24, 5, 6, 3
+    g = torch.Generator().manual_seed(8)
+    qkv = torch.randn(B, Z, Y, X, 3, H, 64, generator=g).bfloat16()
+    q, k, v = qkv[..., 0, :, :], qkv[..., 1, :, :].contiguous(), qkv[..., 2, :, :]
+    qg = qkv.to(gpu)
+    out, lse = torch.ops.strata_hip.na3d_fwd_lse(qg[..., 0, :, :], k.to(gpu), qg[..., 2, :, :], [Z, 1, 1],
+                                                 [1, 1, 1], None)
+    ref, ref_lse = O.na3d(q, k, v, (Z, 1, 1), compute_dtype=torch.float64, return_lse=True)
+    assert rel_l2(out.float(), ref) <= BF16_TOL
+    assert (lse.double().cpu() - ref_lse).abs().max().item() <= 2e-2
