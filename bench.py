@@ -165,41 +165,54 @@ def bench_production(device, steps, warmup):
     """The production block on one rollout tile: (24, 144, 144) tokens x 1024, 16 x 64
     heads, window (3, 3, 3), gated, non-affine qk RMSNorm, RoPE base 100 at the patch-4
     length scale (scripts/ace/run_screamcast_nudged.py:156-165 tile 512 + halo 32 at
-    patch 4; train_configs.py:303-317 block flags)."""
+    patch 4; train_configs.py:303-317 block flags).  The production config also sets
+    do_alt_depthwise_attn (train_configs.py:316): every other block attends its whole
+    z column instead (window (24, 1, 1)); that block is timed as well."""
     import torch
 
     from strata_amd import rope as P
     from strata_amd.modules import StrataBlock, init_xavier_
 
     B, Z, Y, X, C, H, kernel = 1, 24, 144, 144, 1024, 16, (3, 3, 3)
-    blk = StrataBlock(C, H, kernel, gated=True, qk_norm=True)
-    init_xavier_(blk, torch.Generator().manual_seed(1))
-    blk = blk.to(device).bfloat16().eval()
     x = torch.randn(B, Z, Y, X, C, generator=torch.Generator(device=device).manual_seed(0), device=device).bfloat16()
     ls = P.default_rope_length_scale(4)
     lat, lon = P.synthetic_tile_latlon(B, Y, X, torch.Generator().manual_seed(0), spacing=ls)
     rope = P.stereographic_rope_tables(lat.to(device), lon.to(device), C // H, 100.0, ls)
-    with torch.no_grad():
-        for _ in range(warmup):
-            y = blk(x, rope)
-        torch.cuda.synchronize()
-        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-        e0.record()
-        for _ in range(steps):
-            y = blk(x, rope)
-        e1.record()
-        torch.cuda.synchronize()
-    assert torch.isfinite(y.float()).all(), "production block produced non-finite values"
-    ms = e0.elapsed_time(e1) / steps
+
+    def timed_block(depthwise):
+        blk = StrataBlock(C, H, kernel, gated=True, qk_norm=True, depthwise=depthwise)
+        init_xavier_(blk, torch.Generator().manual_seed(1))
+        blk = blk.to(device).bfloat16().eval()
+        with torch.no_grad():
+            for _ in range(warmup):
+                y = blk(x, rope)
+            torch.cuda.synchronize()
+            e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            e0.record()
+            for _ in range(steps):
+                y = blk(x, rope)
+            e1.record()
+            torch.cuda.synchronize()
+        assert torch.isfinite(y.float()).all(), "production block produced non-finite values"
+        return e0.elapsed_time(e1) / steps
+
+    ms = timed_block(False)
+    ms_dw = timed_block(True)
     M = B * Z * Y * X
-    flops = 2.0 * M * C * C * (3 + 1 + 1 + 8) + 4.0 * M * H * 27 * (C // H)  # qkv, gate, proj, fc1+fc2; NA3D
+    gemm = 2.0 * M * C * C * (3 + 1 + 1 + 8)  # qkv, gate, proj, fc1+fc2
+    flops = gemm + 4.0 * M * H * 27 * (C // H)
+    flops_dw = gemm + 4.0 * M * H * Z * (C // H)
     return {
         "workload": "production block: (24,144,144) tokens x 1024, 16x64 heads, W=(3,3,3), gated, qk RMSNorm, "
-        "RoPE base 100 (patch-4 length scale), MLP 4096 GELU(tanh), Xavier seed 1",
+        "RoPE base 100 (patch-4 length scale), MLP 4096 GELU(tanh), Xavier seed 1; the alternate "
+        "depth-wise block: window (24,1,1)",
         "ms_per_step": round(ms, 3),
         "tokens_per_s": M / (ms * 1e-3),
         "block_tflops": round(flops / (ms * 1e-3) / 1e12, 1),
         "pct_bf16_peak": round(100.0 * flops / (ms * 1e-3) / 1e12 / PEAK_BF16_TFLOPS, 2),
+        "depthwise_ms_per_step": round(ms_dw, 3),
+        "depthwise_block_tflops": round(flops_dw / (ms_dw * 1e-3) / 1e12, 1),
+        "pair_tokens_per_s": M / ((ms + ms_dw) * 1e-3),  # M tokens through one block of each kind
     }
 
 
