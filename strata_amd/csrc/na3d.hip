@@ -1986,12 +1986,12 @@ static bool strip_regular(const Na3dParams& p) {
 
 // Small windows on regular strips (na3d_strip_fast_kernel with 2 x 8 tiles and
 // two rows per stage): head_dim 64, kx <= 9 (an 8-column tile's x-union fits one
-// 16-key block), ky in {5, 7, 9}, kz >= 2, no y dilation.
+// 16-key block), ky in {3, 5, 7, 9}, kz >= 2, no y dilation.
 // Only query rows whose y window is not clamped form regular strips; the host
 // splits the query box in y and gives the clamped edge rows to the general kernel.
 static bool small_strip_fits(const Na3dParams& p) {
   if (p.D != 64 || p.ker[0] < 2 || p.ker[2] > 9 || p.dil[1] != 1) return false;
-  if (p.ker[1] != 5 && p.ker[1] != 7 && p.ker[1] != 9) return false;
+  if (p.ker[1] != 3 && p.ker[1] != 5 && p.ker[1] != 7 && p.ker[1] != 9) return false;
   if (p.L[1] >= 4096) return false;
   const int64_t* sd[3] = {p.qs, p.ks, p.vs};
   for (int t = 0; t < 3; ++t)
@@ -2029,6 +2029,10 @@ static int launch_small_strips(const Na3dParams& p, hipStream_t st) {
   const dim3 grid((unsigned)total), block(64 * NA3D_NWX);
   if (p.rc) {  // the queries' rotation in the kernel (inference: no lse)
     switch (p.ker[1]) {
+      case 3:
+        hipLaunchKernelGGL((na3d_small_fused_kernel<3, false, true>), grid, block, 0, st, mid, sg, e0, t0, e1, t1,
+                           (int)n0, (int)n1);
+        break;
       case 5:
         hipLaunchKernelGGL((na3d_small_fused_kernel<5, false, true>), grid, block, 0, st, mid, sg, e0, t0, e1, t1,
                            (int)n0, (int)n1);
@@ -2045,6 +2049,14 @@ static int launch_small_strips(const Na3dParams& p, hipStream_t st) {
     return check_launch("na3d_small_fused_kernel (query RoPE)");
   }
   switch (p.ker[1]) {
+    case 3:
+      if (p.lse)
+        hipLaunchKernelGGL((na3d_small_fused_kernel<3, true>), grid, block, 0, st, mid, sg, e0, t0, e1, t1, (int)n0,
+                           (int)n1);
+      else
+        hipLaunchKernelGGL((na3d_small_fused_kernel<3, false>), grid, block, 0, st, mid, sg, e0, t0, e1, t1, (int)n0,
+                           (int)n1);
+      break;
     case 5:
       if (p.lse)
         hipLaunchKernelGGL((na3d_small_fused_kernel<5, true>), grid, block, 0, st, mid, sg, e0, t0, e1, t1, (int)n0,

@@ -292,6 +292,11 @@ SMALL_CASES = [
     ((1, 4, 30, 20, 2, 64), (3, 5, 5), (1, 1, 1), (0, 10, 0), (4, 20, 20)),
     # a single unclamped row: no regular strip, the general kernel alone
     ((1, 3, 7, 16, 1, 64), (3, 7, 7), (1, 1, 1), (0, 0, 0), None),
+    # the production window (3,3,3): two tile slots, one clamped row at each y edge
+    ((1, 5, 24, 20, 2, 64), (3, 3, 3), (1, 1, 1), (0, 0, 0), None),
+    ((2, 4, 19, 37, 2, 64), (3, 3, 3), (1, 1, 1), (1, 2, 3), (3, 15, 30)),
+    ((1, 6, 12, 16, 2, 64), (3, 3, 3), (2, 1, 2), (0, 0, 0), None),
+    ((1, 3, 3, 16, 1, 64), (3, 3, 3), (1, 1, 1), (0, 0, 0), None),
 ]
 
 
@@ -327,14 +332,15 @@ def test_small_window_strip_score_out_of_range(gpu):
         assert rel_l2(out[idx].float().cpu(), ref[idx]) <= BF16_TOL, idx
 
 
-def test_small_window_strips_match_general_kernel(gpu, monkeypatch):
+@pytest.mark.parametrize("kernel", [(3, 7, 7), (3, 3, 3)])
+def test_small_window_strips_match_general_kernel(gpu, monkeypatch, kernel):
     """The same configs[3]-like launch through the strip path and, with it
     switched off, through the general kernel: both within bf16 rounding."""
     g = torch.Generator(device=gpu).manual_seed(5)
     q, k, v = (torch.randn((1, 8, 64, 64, 4, 64), generator=g, device=gpu).bfloat16() for _ in range(3))
-    a = _run(q, k, v, (3, 7, 7))
+    a = _run(q, k, v, kernel)
     monkeypatch.setenv("STRATA_HIP_NA3D_NO_SMALL_STRIPS", "1")
-    b = _run(q, k, v, (3, 7, 7))
+    b = _run(q, k, v, kernel)
     assert rel_l2(a.float(), b.float()) <= 5e-3
 
 

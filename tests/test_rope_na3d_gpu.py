@@ -27,6 +27,8 @@ def _qkv(B, Z, Y, X, H, g, dev, scale=1.0):
     ((1, 4, 20, 24, 2), (3, 7, 7), 1, (1, 1, 1)),     # short strips, ragged columns
     ((1, 8, 32, 40, 2), (3, 7, 7), 8, (2, 1, 2)),     # z and x dilation: residue classes, level tables
     ((1, 6, 24, 30, 2), (3, 5, 5), 1, (2, 1, 3)),
+    ((1, 6, 24, 40, 2), (3, 3, 3), 1, (1, 1, 1)),     # the production window
+    ((1, 4, 16, 24, 2), (3, 3, 3), 4, (1, 1, 1)),
 ])
 def test_rope_q_fused_matches_pack_then_na3d(gpu, shape, kernel, zt, dil):
     B, Z, Y, X, H = shape
