@@ -1535,12 +1535,12 @@ static bool mfma_ok(const Na3dBwdParams& p) {
          ((int64_t)p.Y + 1) * row * 4 < (int64_t)OOB && !std::getenv("STRATA_HIP_NA3D_BWD_VALU");
 }
 
-// dq on strips (na3d_bwd_dq_strip_kernel): kx <= 9, ky in {5, 7}, kz >= 2, at
+// dq on strips (na3d_bwd_dq_strip_kernel): kx <= 9, ky in {3, 5, 7}, kz >= 2, at
 // least two unclamped rows, and one (b, z) slice of Q / dO / statistics within
 // 31-bit offsets.  STRATA_HIP_NA3D_BWD_NO_STRIPS=1 switches the path off.
 static bool dq_strip_fits(const Na3dBwdParams& p) {
   const int ky = p.ker[1];
-  if (p.ker[0] < 2 || p.ker[2] > 9 || (ky != 5 && ky != 7)) return false;  // ky = 9 would spill
+  if (p.ker[0] < 2 || p.ker[2] > 9 || (ky != 3 && ky != 5 && ky != 7)) return false;  // ky = 9 would spill
   if (p.Y - 2 * (ky / 2) < 2) return false;
   if ((int64_t)p.Y * p.X * p.H * 64 * 2 >= 0x7fffffffLL) return false;
   return !std::getenv("STRATA_HIP_NA3D_BWD_NO_STRIPS");
@@ -1595,6 +1595,7 @@ static bool dkv_strip_fits(const Na3dBwdParams& p) {
 static void launch_dq_strips(const Na3dBwdParams& p, const BwdStrips& sg, hipStream_t st) {
   const dim3 grid((unsigned)sg.total), block(256);
   switch (p.ker[1]) {
+    case 3: hipLaunchKernelGGL(na3d_bwd_dq_strip_kernel<3>, grid, block, 0, st, p, sg); break;
     case 5: hipLaunchKernelGGL(na3d_bwd_dq_strip_kernel<5>, grid, block, 0, st, p, sg); break;
     default: hipLaunchKernelGGL(na3d_bwd_dq_strip_kernel<7>, grid, block, 0, st, p, sg); break;
   }
@@ -1642,7 +1643,9 @@ static int launch_bwd(const Na3dBwdParams& p, hipStream_t st) {
       }
       if (base > 0x7fffffff) return fail(STRATA_HIP_EUNSUPPORTED, "na3d_bwd: problem too large for one launch");
       parts.base[7] = (int)base;
-      if (p.ker[1] == 5)
+      if (p.ker[1] == 3)
+        hipLaunchKernelGGL(na3d_bwd_small_fused_kernel<3>, dim3((unsigned)base), block, 0, st, p, sq, skv, parts);
+      else if (p.ker[1] == 5)
         hipLaunchKernelGGL(na3d_bwd_small_fused_kernel<5>, dim3((unsigned)base), block, 0, st, p, sq, skv, parts);
       else
         hipLaunchKernelGGL(na3d_bwd_small_fused_kernel<7>, dim3((unsigned)base), block, 0, st, p, sq, skv, parts);

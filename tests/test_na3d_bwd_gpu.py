@@ -29,8 +29,10 @@ CASES = [  # shape [B, Z, Y, X, H, D], kernel, dilation
     # cut into one-tile chunks
     ((2, 4, 20, 40, 2, 64), (3, 7, 7), (1, 1, 1)),
     ((1, 3, 33, 16, 3, 64), (3, 5, 5), (1, 1, 1)),
-    # the production window (3,3,3) at head_dim 64 (the tile walks)
+    # the production window (3,3,3) at head_dim 64 (dq, dV and dK strips with their clamped
+    # edges; a ragged 32-column box and two batches)
     ((1, 5, 24, 20, 2, 64), (3, 3, 3), (1, 1, 1)),
+    ((2, 4, 21, 40, 2, 64), (3, 3, 3), (1, 1, 1)),
     # depth-wise attention: the whole z column, even (a kernel equal to the axis) and odd
     ((1, 8, 6, 7, 2, 64), (8, 1, 1), (1, 1, 1)),
     ((1, 24, 4, 5, 2, 64), (24, 1, 1), (1, 1, 1)),
