@@ -1682,6 +1682,470 @@ __global__ __launch_bounds__(256, KY <= 5 ? 3 : 2) void na3d_small_fused_kernel(
 
 
 // ---------------------------------------------------------------------------
+// Small windows on query regions (na3d_region_kernel): kz = 3, ky = KY, kx <= KY (odd),
+// head_dim 64, bf16; any dilation and query box.  The template covers KY in {3, 5, 7};
+// the host takes it for ky = 3 (region_fits), where it beats the strips.
+//
+// A workgroup of 8 waves owns a region of 8 query rows x 16 query columns of one
+// (batch, head, dilation residue) at every query z of the box, and walks the key
+// z-slices those queries' windows reach once, in order.  Stage s copies the
+// (7 + KY) x (15 + KY) keys of slice s that any window of the region can touch
+// (K, then V; keys past the grid read as zero) into an LDS ring (three stages where
+// they fit, else two), so a K/V slice crosses L2 -> LDS once per region instead of
+// once per query z.  The copies of a stage are issued a share per row pair during
+// the stage before it, beside the MFMAs, not in one burst after the barrier (one
+// workgroup per CU: every wave reaches the barrier together).  Wave w owns the
+// 2 x 8 tile at rows 2 (w >> 1), columns 8 (w & 1) of the region at every z: the
+// tile of query z zq lives in register slot (zq - zbase) & 3 during the three stages
+// whose slice its z window holds (at most four tiles overlap, at the clamped z ends;
+// three in the interior, where the stage loop, unrolled four times, knows the live
+// slots at compile time).  Per stage a wave reads each of its tile's KY + 1 key rows
+// (one 16-key block: the tile's 8 + kx - 1 columns) once and feeds every live slot.
+// Rows 1 .. KY - 1 of a tile's union lie in both query rows' windows; rows 0 and KY
+// are complementary (query row 0 always takes row 0; query row 1 takes exactly one
+// of them), so they form one PV step and share one exponential.  Every clamped edge
+// (z, y and x) is a mask: there is no separate edge kernel.  Softmax as the strip
+// kernels: p = 2^s of the log2-unit scores, the x window as the QK MFMA's C operand,
+// row sums by a ones-operand MFMA, a range check per tile and an exact recompute of
+// the rare tiles that leave the range.
+// ---------------------------------------------------------------------------
+struct Na3dRegions {
+  int nrx, nry;  // regions per (batch, head, residue) along x and along y
+  int nres;      // dil_z * dil_y * dil_x
+  int total;     // workgroups
+};
+
+template <int KY>
+struct RegionGeom {
+  static constexpr int NRY = 7 + KY;                 // key rows a region's windows reach
+  static constexpr int LW = 15 + KY;                 // keys per row (kx <= KY)
+  static constexpr int NK = (NRY * LW + 7) / 8 * 8;  // keys per tensor, whole 1-KiB copies
+  static constexpr int REG_B = NK * 128;             // bytes of one tensor's keys (head_dim 64)
+  static constexpr int STAGE_B = 2 * REG_B;          // K, then V
+  static constexpr int NDMA = 2 * NK / 8;            // 1-KiB copies per stage
+  static constexpr int DPW = (NDMA + 7) / 8;         // per wave (copy 8 j + wave)
+  static constexpr int IDLE_B = (8 * DPW - NDMA) * 1024;   // where the waves' idle copies land
+  static constexpr int NBUF = 3 * STAGE_B + IDLE_B <= 160 * 1024 ? 3 : 2;  // ring stages: three where they fit
+  static constexpr int LDS_B = NBUF * STAGE_B + IDLE_B;
+  static_assert(LDS_B <= 160 * 1024, "the ring fits the CU's LDS");
+};
+
+template <int KY, bool LSE, bool ROPE>
+__global__ __launch_bounds__(512, 1) void na3d_region_kernel(Na3dParams p, Na3dRegions rg) {
+#if defined(__HIP_DEVICE_COMPILE__)
+  using G = RegionGeom<KY>;
+  constexpr int LW = G::LW, NRY = G::NRY, REG_B = G::REG_B, STAGE_B = G::STAGE_B, NDMA = G::NDMA, DPW = G::DPW;
+  constexpr int NP = (KY + 1) / 2;  // PV steps of a tile: row pairs (0, KY), (1, 2), (3, 4), ...
+  constexpr int RB = LW * 128;      // bytes of one region row (a multiple of 256: rows keep the bank pattern)
+  constexpr uint32_t LMIN_BITS = (127u - 100u) << 23;  // 2^-100
+  constexpr uint32_t INF_BITS = 0x7f800000u;
+  static_assert(RB % 256 == 0, "row starts keep the chunk swizzle conflict-free");
+  __shared__ __attribute__((aligned(1024))) char lds[G::LDS_B];
+
+  // ---- work unit: (batch, head, residue, region y, region x), x fastest ----
+  int t = xcd_tile_order(rg.total, (int)__builtin_amdgcn_workgroup_id_x());
+  const int rx = t % rg.nrx;
+  t /= rg.nrx;
+  const int ry = t % rg.nry;
+  t /= rg.nry;
+  const int res = t % rg.nres;
+  t /= rg.nres;
+  const int h = t % p.H;
+  const int b = t / p.H;
+  const int dz = p.dil[0], dy = p.dil[1], dx = p.dil[2];
+  const int gx = res % dx, gy = (res / dx) % dy, gz = res / (dx * dy);
+  const int Lz = sub_len(p.L[0], gz, dz), Ly = sub_len(p.L[1], gy, dy), Lx = sub_len(p.L[2], gx, dx);
+  const int qz0 = sub_first(p.org[0], gz, dz), qz1 = sub_end(p.org[0], p.ext[0], gz, dz);
+  const int qy0 = sub_first(p.org[1], gy, dy), qy1 = sub_end(p.org[1], p.ext[1], gy, dy);
+  const int qx0 = sub_first(p.org[2], gx, dx), qx1 = sub_end(p.org[2], p.ext[2], gx, dx);
+  const int y0 = qy0 + 8 * ry, x0 = qx0 + 16 * rx;
+  if (qz0 >= qz1 || y0 >= qy1 || x0 >= qx1) return;  // uniform over the workgroup
+  const int kz = p.ker[0], kx = p.ker[2];
+  const int RY0 = win_start(y0, Ly, KY), RX0 = win_start(x0, Lx, kx);  // the region's first key row / column
+
+  const int tid = (int)__builtin_amdgcn_workitem_id_x();
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int lane = tid & 63, n16 = lane & 15, g = lane >> 4;
+  const uint32_t lds_base = (uint32_t)(uintptr_t)(__attribute__((address_space(3))) char*)lds;
+
+  // ---- this wave's tile: query rows yt, yt + 1, columns xt .. xt + 7 ----
+  const int yt = y0 + 2 * (wave >> 1), xt = x0 + 8 * (wave & 1);
+  const int by = win_start(min(yt, qy1 - 1), Ly, KY) - RY0;  // the tile's first union row in the region (<= 6)
+  // first region column of the tile's 16-key block: its 8 + kx - 1 columns start at
+  // or after it and end inside the region's LW
+  const int bx = (wave & 1) ? min(win_start(min(xt, qx1 - 1), Lx, kx) - RX0, LW - 16) : 0;
+  const int tq = n16 >> 3;  // this lane's query: row tq, column n16 & 7 of the tile
+  const int qyc = min(yt + tq, qy1 - 1), qxc = min(xt + (n16 & 7), qx1 - 1);
+  const bool qvalid = yt + tq < qy1 && xt + (n16 & 7) < qx1;
+  // the lane's y window covers union rows [d, d + KY), d in {0, 1}: d = 1 means row KY, not row 0
+  const bool rowky = win_start(qyc, Ly, KY) - RY0 - by == 1;
+  f32x4 xbias;  // 0 or -inf for keys bx + 4g + i of the block (x window): the QK MFMA's C operand
+  {
+    const int sx = win_start(qxc, Lx, kx);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int kc = RX0 + bx + 4 * g + i;
+      xbias[i] = (kc >= sx && kc < sx + kx) ? 0.f : -INFINITY;
+    }
+  }
+
+  // ---- LDS read offsets within a stage (row r of the tile's union adds r * RB);
+  // chunk c of the key in region column col sits at slot c ^ (col & 7) ----
+  uint32_t koff[2], voff[4];
+#pragma unroll
+  for (int ks = 0; ks < 2; ++ks) {
+    const int col = bx + n16;
+    koff[ks] = (uint32_t)(by * RB + col * 128 + 16 * ((4 * ks + g) ^ (col & 7)));
+  }
+  {
+    const int col = bx + 4 * g + (n16 >> 2), dq = n16 & 3;
+#pragma unroll
+    for (int db = 0; db < 4; ++db)
+      voff[db] = (uint32_t)(REG_B + by * RB + col * 128 + 16 * ((2 * db + (dq >> 1)) ^ (col & 7)) + 8 * (dq & 1));
+  }
+
+  // ---- copies: stage copy J = 8 j + wave (J < NDMA / 2: K keys 8J .. 8J + 7 of the
+  // region, row-major; else the same keys of V); lane l fills slot l & 7 of key l / 8 ----
+  const int64_t rowk = 2 * (int64_t)dy * p.ks[2], rowv = 2 * (int64_t)dy * p.vs[2];
+  uint32_t doff[DPW];
+#pragma unroll
+  for (int j = 0; j < DPW; ++j) {
+    const int J = 8 * j + wave;
+    const bool isv = J >= NDMA / 2;
+    const int f = 8 * (isv ? J - NDMA / 2 : J) + lane / 8;
+    const int row = f / LW, col = f % LW;
+    const bool ok = J < NDMA && f < NRY * LW && RY0 + row < Ly && RX0 + col < Lx;
+    const int64_t o = row * (isv ? rowv : rowk) + (int64_t)(gx + dx * (RX0 + col)) * 2 * (isv ? p.vs[3] : p.ks[3]) +
+                      16 * ((lane & 7) ^ (col & 7));
+    doff[j] = ok ? (uint32_t)o : OOB;
+  }
+  const char* kbase = (const char*)p.k + 2 * ((int64_t)b * p.ks[0] + (int64_t)h * p.ks[4] + (int64_t)gz * p.ks[1] +
+                                              (int64_t)(gy + dy * RY0) * p.ks[2]);
+  const char* vbase = (const char*)p.v + 2 * ((int64_t)b * p.vs[0] + (int64_t)h * p.vs[4] + (int64_t)gz * p.vs[1] +
+                                              (int64_t)(gy + dy * RY0) * p.vs[2]);
+  const int64_t zk = 2 * (int64_t)dz * p.ks[1], zv = 2 * (int64_t)dz * p.vs[1];
+  // Copies j in [J0, J1) of the wave into the ring slot at byte `slot`, from the K and V
+  // descriptors of one slice.  Copy J >= NDMA (the last of some waves) reads zeros into
+  // the idle area past the ring, so no copy sits under a branch.
+  uint32_t ddst[DPW];  // destination of copy j within a slot (or the idle area, minus the slot)
+#pragma unroll
+  for (int j = 0; j < DPW; ++j) {
+    const int J = 8 * j + wave;
+    ddst[j] = J >= NDMA ? 0u : (uint32_t)(J >= NDMA / 2 ? REG_B + 1024 * (J - NDMA / 2) : 1024 * J);
+    if (J >= NDMA) doff[j] = OOB;
+  }
+  const uint32_t idle_dst = lds_base + (uint32_t)(G::NBUF * STAGE_B) + 1024u * (uint32_t)max(0, 8 * (DPW - 1) + wave - NDMA);
+  auto issue_part = [&](const u32x4& rk, const u32x4& rv, uint32_t slot, auto j0c, auto j1c) {
+    constexpr int J0 = decltype(j0c)::value, J1 = decltype(j1c)::value;
+    static_for<DPW>([&](auto jc) {
+      constexpr int j = decltype(jc)::value;
+      if constexpr (j >= J0 && j < J1) {
+        const int J = 8 * j + wave;  // uniform
+        const bool isv = J >= NDMA / 2;
+        dma_row16(isv ? rv : rk, J >= NDMA ? idle_dst : lds_base + slot + ddst[j], doff[j]);
+      }
+    });
+  };
+  auto issue = [&](int s, uint32_t slot) {
+    const u32x4 rk = make_rsrc(kbase + s * zk, OOB), rv = make_rsrc(vbase + s * zv, OOB);
+    issue_part(rk, rv, slot, std::integral_constant<int, 0>{}, std::integral_constant<int, DPW>{});
+  };
+
+  // ---- queries: lane (row tq, column n16 & 7) loads dims 8g .. 8g + 7 and 32 + 8g .. 32 + 8g + 7 ----
+  const char* qlane = (const char*)p.q + 2 * ((int64_t)b * p.qs[0] + (int64_t)h * p.qs[4] + (int64_t)gz * p.qs[1] +
+                                              (int64_t)(gy + dy * qyc) * p.qs[2] + (int64_t)(gx + dx * qxc) * p.qs[3]);
+  const int64_t qzs = 2 * (int64_t)dz * p.qs[1];
+  auto load_q = [&](int zq, bf16x8 (&qv)[2]) {
+    const char* a = qlane + zq * qzs;
+    qv[0] = *(const bf16x8*)(a + 16 * g);
+    qv[1] = *(const bf16x8*)(a + 64 + 16 * g);
+  };
+  // ROPE: cos / sin of pairs 8g .. 8g + 7 (half layout: dims j and j + 32) of the lane's query
+  auto load_rope = [&](int zq, f32x4 (&c)[2], f32x4 (&sn)[2]) {
+    if constexpr (ROPE) {
+      const int64_t r = rope_row(p, b, gz + dz * zq, gy + dy * qyc, gx + dx * qxc) * 32 + 8 * g;
+      c[0] = *(const f32x4*)(p.rc + r);
+      c[1] = *(const f32x4*)(p.rc + r + 4);
+      sn[0] = *(const f32x4*)(p.rs + r);
+      sn[1] = *(const f32x4*)(p.rs + r + 4);
+    }
+  };
+  char* olane = (char*)p.o + 2 * ((int64_t)b * p.os[0] + (int64_t)h * p.os[4] + (int64_t)(gz - p.org[0]) * p.os[1] +
+                                  (int64_t)(gy + dy * qyc - p.org[1]) * p.os[2] +
+                                  (int64_t)(gx + dx * qxc - p.org[2]) * p.os[3]) +
+                8 * g;
+  const int64_t ozs = 2 * (int64_t)dz * p.os[1];
+  const float c2 = p.scale * 1.4426950408889634f;  // scores in log2 units
+
+  // ---- tile slots ----
+  bf16x8 qreg[4][2];
+  f32x4 oacc[4][4];
+  f32x4 lacc[4];
+  typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
+  bf16x8_t ones = {(bf16)1.f, (bf16)1.f, (bf16)1.f, (bf16)1.f, (bf16)1.f, (bf16)1.f, (bf16)1.f, (bf16)1.f};
+  // A tile enters slot k: its queries (rotated with ROPE) pre-scaled to log2 units.
+  auto start = [&](auto kc, const bf16x8 (&qv)[2], const f32x4 (&c)[2], const f32x4 (&sn)[2]) {
+    constexpr int k = decltype(kc)::value;
+    bf16x8 lo = qv[0], hi = qv[1];
+    if constexpr (ROPE) {
+      float cc[8], ss[8];
+      *(f32x4*)&cc[0] = c[0];
+      *(f32x4*)&cc[4] = c[1];
+      *(f32x4*)&ss[0] = sn[0];
+      *(f32x4*)&ss[4] = sn[1];
+      rope_q_pairs(lo, hi, cc, ss);
+    }
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      qreg[k][0][e] = (bf16)((float)lo[e] * c2);
+      qreg[k][1][e] = (bf16)((float)hi[e] * c2);
+    }
+#pragma unroll
+    for (int db = 0; db < 4; ++db) oacc[k][db] = (f32x4){0.f, 0.f, 0.f, 0.f};
+    lacc[k] = (f32x4){0.f, 0.f, 0.f, 0.f};
+  };
+
+  // Deferred output of one finished tile: stored at the next stage's start, after
+  // that stage's copies are issued, so the stage-start wait does not cover a
+  // store issued just before it.
+  u32x2 pend[4];
+  char* pend_ptr = nullptr;
+  float pend_lse = 0.f;
+  float* pend_lse_ptr = nullptr;
+  bool pend_on = false;  // uniform
+  auto flush = [&]() {
+    if (pend_on) {
+      if (qvalid) {
+#pragma unroll
+        for (int db = 0; db < 4; ++db) *(u32x2*)(pend_ptr + 32 * db) = pend[db];
+        if (LSE && g == 0) *pend_lse_ptr = pend_lse;
+      }
+      pend_on = false;
+    }
+  };
+  // Normalise slot k's tile (query z zq); true if it needs the exact path.
+  auto finish = [&](auto kc, int zq) {
+    constexpr int k = decltype(kc)::value;
+    const float l = lacc[k][0];
+    float osum = 0.f;
+#pragma unroll
+    for (int db = 0; db < 4; ++db)
+      osum += fabsf(oacc[k][db][0]) + fabsf(oacc[k][db][1]) + fabsf(oacc[k][db][2]) + fabsf(oacc[k][db][3]);
+    const float inv = 1.f / l;
+    u32x2 w[4];
+#pragma unroll
+    for (int db = 0; db < 4; ++db)
+      w[db] = (u32x2){pack_bf16x2(oacc[k][db][0] * inv, oacc[k][db][1] * inv),
+                      pack_bf16x2(oacc[k][db][2] * inv, oacc[k][db][3] * inv)};
+    char* op = olane + zq * ozs;
+    float* lp = nullptr;
+    if (LSE) lp = p.lse + lse_index(p, b, gz + dz * zq - p.org[0], gy + dy * qyc - p.org[1], gx + dx * qxc - p.org[2], h);
+    if (!pend_on) {
+#pragma unroll
+      for (int db = 0; db < 4; ++db) pend[db] = w[db];
+      pend_ptr = op;
+      pend_lse = __log2f(l);
+      pend_lse_ptr = lp;
+      pend_on = true;
+    } else if (qvalid) {  // a second tile in one stage (the clamped z ends): store now
+#pragma unroll
+      for (int db = 0; db < 4; ++db) *(u32x2*)(op + 32 * db) = w[db];
+      if (LSE && g == 0) *lp = __log2f(l);
+    }
+    const bool ok = __float_as_uint(l) - LMIN_BITS < INF_BITS - LMIN_BITS && __float_as_uint(osum) < INF_BITS;
+    return __builtin_amdgcn_ballot_w64(qvalid && !ok) != 0;
+  };
+
+  auto exp_pack = [&](const f32x4& sv) {
+    return (u32x2){pack_bf16x2(__builtin_amdgcn_exp2f(sv[0]), __builtin_amdgcn_exp2f(sv[1])),
+                   pack_bf16x2(__builtin_amdgcn_exp2f(sv[2]), __builtin_amdgcn_exp2f(sv[3]))};
+  };
+  // One stage's math on the slots in ACT (a compile-time mask; 0xF at the z ends,
+  // where inactive slots compute into accumulators their next tile resets).
+  // hook(pc) runs after pair pc's operand reads (the stage's copies go out there, a
+  // share per pair, so the CU's address path streams them beside the MFMAs rather
+  // than in one burst after the barrier).
+  auto stage_math = [&](auto actc, uint32_t cur, auto&& hook) {
+    constexpr int ACT = decltype(actc)::value;
+    const char* st = lds + cur;
+    asm volatile("" : "+v"(ones));  // keep the ones operand resident
+    static_for<NP>([&](auto pc) {
+      constexpr int PI = decltype(pc)::value;
+      constexpr int RA = PI == 0 ? 0 : 2 * PI - 1, RBW = PI == 0 ? KY : 2 * PI;
+      bf16x8 ak[2][2];
+#pragma unroll
+      for (int ks = 0; ks < 2; ++ks) {
+        ak[0][ks] = *(const bf16x8*)(st + RA * RB + koff[ks]);
+        ak[1][ks] = *(const bf16x8*)(st + RBW * RB + koff[ks]);
+      }
+      bf16x8 av[4];
+#pragma unroll
+      for (int db = 0; db < 4; ++db) {
+        const bf16x4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4bf16(LDS_PTR(bf16x4, st + voff[db] + RA * RB));
+        const bf16x4 hi = __builtin_amdgcn_ds_read_tr16_b64_v4bf16(LDS_PTR(bf16x4, st + voff[db] + RBW * RB));
+        av[db] = __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7);
+      }
+      hook(pc);
+      f32x4 sc[4][2];  // every live slot's scores first, so the exponentials wait on none of them
+      static_for<4>([&](auto kc) {
+        constexpr int k = decltype(kc)::value;
+        if constexpr ((ACT >> k) & 1) {
+          sc[k][0] = xbias;
+          sc[k][1] = xbias;
+#pragma unroll
+          for (int ks = 0; ks < 2; ++ks) {
+            sc[k][0] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ak[0][ks], qreg[k][ks], sc[k][0], 0, 0, 0);
+            sc[k][1] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ak[1][ks], qreg[k][ks], sc[k][1], 0, 0, 0);
+          }
+        }
+      });
+      static_for<4>([&](auto kc) {
+        constexpr int k = decltype(kc)::value;
+        if constexpr ((ACT >> k) & 1) {
+          const f32x4 sa = sc[k][0], sb = sc[k][1];
+          u32x2 pa, pb;
+          if constexpr (PI == 0) {  // rows 0 and KY: one exponential, split by the lane's y window
+            f32x4 m;
+#pragma unroll
+            for (int i = 0; i < 4; ++i) m[i] = rowky ? sb[i] : sa[i];
+            const u32x2 pm = exp_pack(m), zero = {0u, 0u};
+            pa = rowky ? zero : pm;
+            pb = rowky ? pm : zero;
+          } else {
+            pa = exp_pack(sa);
+            pb = exp_pack(sb);
+          }
+          const bf16x8 pp = __builtin_bit_cast(bf16x8, (u32x4){pa[0], pa[1], pb[0], pb[1]});
+          lacc[k] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ones, pp, lacc[k], 0, 0, 0);
+#pragma unroll
+          for (int db = 0; db < 4; ++db)
+            oacc[k][db] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(av[db], pp, oacc[k][db], 0, 0, 0);
+        }
+      });
+    });
+  };
+
+  // ---- the z walk: slices [S0, S1); the tiles live at stage s are zq in [zlo(s), zhi(s)]:
+  // zq = s - 1, s, s + 1 in the interior, plus s - 2 or s + 2 at the clamped z ends (at
+  // most four: the host checks).  The tile of query z zq holds slot (zq - zbase) & 3, so
+  // in the stage loop unrolled four times the interior slots are compile-time. ----
+  constexpr int H2 = 1;  // kz / 2 (kz = 3)
+  const int S0 = win_start(qz0, Lz, kz), S1 = win_start(qz1 - 1, Lz, kz) + kz;
+  const int zbase = S0 - 1;
+  auto zhi_of = [&](int s) { return s >= Lz - kz ? qz1 - 1 : min(qz1 - 1, s + H2); };
+  auto zlo_of = [&](int s) { return s - kz + 1 <= 0 ? qz0 : max(qz0, s - kz + 1 + H2); };
+  auto zstart = [&](int zq) { return win_start(zq, Lz, kz); };
+  auto slot_z = [&](int k, int zl) { return zl + ((k + zbase - zl) & 3); };  // the zq >= zl slot k holds
+
+  // Ring: stage s in slot (s - S0) % NBUF; stage s issues stage s + NBUF - 1 into the slot
+  // that stage s - 1 read (free once every wave has passed stage s's barrier).
+  constexpr int NBUF = G::NBUF;
+  issue(S0, 0);
+  if (NBUF == 3 && S0 + 1 < S1) issue(S0 + 1, STAGE_B);
+  {  // the tiles of the first slice: loaded here
+    const int zl = zlo_of(S0), zh = zhi_of(S0);
+    static_for<4>([&](auto kc) {
+      constexpr int k = decltype(kc)::value;
+      const int zq = slot_z(k, zl);
+      if (zq <= zh) {
+        bf16x8 qv[2];
+        f32x4 c[2], sn[2];
+        load_q(zq, qv);
+        load_rope(zq, c, sn);
+        start(kc, qv, c, sn);
+      }
+    });
+  }
+  // Prefetch of the next stage's first tile (with ROPE: its tables too); a second
+  // tile that starts in the same stage (the clamped z ends) loads at its start.
+  bf16x8 qpre[2];
+  f32x4 cpre[2], spre[2];
+  int pf_z = 1 << 30;  // query z of the prefetched tile (uniform)
+  auto prefetch = [&](int s) {  // the first tile starting at stage s, if any
+    const int zq = zhi_of(s - 1) + 1;
+    pf_z = 1 << 30;
+    if (s < S1 && zq <= zhi_of(s)) {
+      load_q(zq, qpre);
+      load_rope(zq, cpre, spre);
+      pf_z = zq;
+    }
+  };
+
+  uint64_t bad_lo = 0;  // tiles (zq < 64) for the exact path
+  bool bad_hi = false;
+  uint32_t cur = 0, wr = (NBUF - 1) * STAGE_B;
+  auto next_slot = [](uint32_t o) { return o + STAGE_B == NBUF * STAGE_B ? 0u : o + STAGE_B; };
+  for (int s4 = S0; s4 < S1; s4 += 4) {
+    static_for<4>([&](auto ic) {
+      constexpr int I = decltype(ic)::value;
+      constexpr int IDLE = (I + 3) & 3;  // the slot of zq = s +- 2 (stage s = s4 + I)
+      const int s = s4 + I;
+      if (s < S1) {
+        // Stage s's copies and the prefetched queries have landed once at most the copies
+        // of stage s + 1 (issued after them; loads complete in order) are outstanding.
+        if (NBUF == 3 && s > S0)
+          wait_vmcnt(DPW);
+        else
+          wait_vmcnt(0);
+        lds_barrier();  // every wave's copies of stage s have landed; slot wr is free
+        // the stage this one issues: past the walk's end the last slice again, into a slot
+        // nobody reads (the walk's last wait drains those copies)
+        const int sn = min(s + NBUF - 1, S1 - 1);
+        const u32x4 rk = make_rsrc(kbase + sn * zk, OOB), rv = make_rsrc(vbase + sn * zv, OOB);
+        flush();
+        const int zl = zlo_of(s), zh = zhi_of(s);
+        if (s > S0) {  // tiles starting at s: zq in (zhi(s - 1), zh]
+          static_for<4>([&](auto kc) {
+            constexpr int k = decltype(kc)::value;
+            const int zq = slot_z(k, zl);
+            if (zq <= zh && zstart(zq) == s) {
+              if (zq == pf_z) {
+                start(kc, qpre, cpre, spre);
+              } else {
+                bf16x8 qv[2];
+                f32x4 c[2], sn[2];
+                load_q(zq, qv);
+                load_rope(zq, c, sn);
+                start(kc, qv, c, sn);
+              }
+            }
+          });
+        }
+        prefetch(s + 1);
+        // slots of zq = s - 1, s, s + 1 (an idle one computes into accumulators its next tile resets)
+        stage_math(std::integral_constant<int, 0xF & ~(1 << IDLE)>{}, cur, [&](auto pc) {
+          constexpr int PI = decltype(pc)::value;
+          issue_part(rk, rv, wr, std::integral_constant<int, PI * DPW / NP>{},
+                     std::integral_constant<int, (PI + 1) * DPW / NP>{});
+        });
+        if (zl <= s - 2 || zh >= s + 2) stage_math(std::integral_constant<int, 1 << IDLE>{}, cur, [](auto) {});
+        static_for<4>([&](auto kc) {
+          constexpr int k = decltype(kc)::value;
+          const int zq = slot_z(k, zl);
+          if (zq <= zh && zstart(zq) + kz - 1 == s && finish(kc, zq)) {
+            if (zq < 64)
+              bad_lo |= 1ull << zq;
+            else
+              bad_hi = true;
+          }
+        });
+        cur = next_slot(cur);
+        wr = next_slot(wr);
+      }
+    });
+  }
+  wait_vmcnt(0);  // the copies issued past the walk's end land before the workgroup's LDS is released
+  flush();
+  if (bad_lo != 0 || bad_hi) {
+    __builtin_amdgcn_s_waitcnt(0);
+    for (int zq = qz0; zq < qz1; ++zq)
+      if (zq < 64 ? ((bad_lo >> zq) & 1) : bad_hi)
+        na3d_strip_tile_exact<8, ROPE>(&p, StripTile{b, h, gz, gy, gx, zq, yt, qy1, xt, qx1});
+  }
+#endif
+}
+
+// ---------------------------------------------------------------------------
 // Depth-wise (column) attention: window (Z, 1, 1) over the whole z axis, Z <= 32,
 // head_dim 64, bf16, the whole grid as the query box.  Every token attends the Z
 // tokens of its own (y, x) column; the tile kernels above would compute a 16 x 16
@@ -2113,6 +2577,69 @@ static int launch_column(const Na3dParams& p, hipStream_t st) {
   return check_launch("na3d_column_kernel");
 }
 
+// Query regions (na3d_region_kernel): kz = 3, ky in {3, 5, 7}, kx <= ky, head_dim 64;
+// one slice of K and V rows must fit 31-bit byte offsets (as the strips).
+// STRATA_HIP_NA3D_NO_REGIONS=1 switches the path off (the strips and the general
+// kernel then take these windows; the tests compare the two).
+static bool region_fits(const Na3dParams& p) {
+  // Taken for ky = 3 only: at (3,3,3) it beats the small-window strips by ~18% (one
+  // rollout tile: 1.21 -> 1.00 ms, with the query rotation 1.38 -> 1.14 ms); at (3,7,7)
+  // over 8 query z's the strips stay ahead (the z ends' extra slot passes and each
+  // workgroup's exposed first copies weigh more on an 8-slice walk than the saved
+  // copies: configs[3] 0.363 against 0.333 ms).
+  if (p.D != 64 || p.ker[0] != 3 || p.ker[1] != 3 || p.ker[2] > 3) return false;
+  const int64_t* sd[2] = {p.ks, p.vs};
+  for (int t = 0; t < 2; ++t)
+    if (((int64_t)(p.L[1] - 1) * sd[t][2] + (int64_t)(p.L[2] - 1) * sd[t][3] + p.D) * 2 >= (int64_t)OOB) return false;
+  // The z walk keeps at most four query z's live per stage s, the fourth being s - 2
+  // or s + 2 (its slot is the one the interior leaves idle): every z sub-grid length
+  // but 5 (where five overlap at s = 2).  Checked by brute force per residue class.
+  for (int gz = 0; gz < p.dil[0]; ++gz) {
+    const int Lz = sub_len(p.L[0], gz, p.dil[0]);
+    const int z0 = sub_first(p.org[0], gz, p.dil[0]), z1 = sub_end(p.org[0], p.ext[0], gz, p.dil[0]);
+    if (z1 <= z0) continue;
+    for (int s = win_start(z0, Lz, 3); s < win_start(z1 - 1, Lz, 3) + 3; ++s) {
+      int lo = 1 << 30, hi = -1, n = 0;
+      for (int zq = z0; zq < z1; ++zq) {
+        const int w = win_start(zq, Lz, 3);
+        if (w <= s && s < w + 3) {
+          lo = zq < lo ? zq : lo;
+          hi = zq > hi ? zq : hi;
+          ++n;
+        }
+      }
+      if (n > 4 || hi - lo + 1 != n || lo < s - 2 || hi > s + 2 || (lo == s - 2 && hi == s + 2)) return false;
+    }
+  }
+  return !std::getenv("STRATA_HIP_NA3D_NO_REGIONS");
+}
+
+template <int KY>
+static int launch_region_ky(const Na3dParams& p, const Na3dRegions& rg, hipStream_t st) {
+  const dim3 grid((unsigned)rg.total), block(512);
+  if (p.rc)
+    hipLaunchKernelGGL((na3d_region_kernel<KY, false, true>), grid, block, 0, st, p, rg);
+  else if (p.lse)
+    hipLaunchKernelGGL((na3d_region_kernel<KY, true, false>), grid, block, 0, st, p, rg);
+  else
+    hipLaunchKernelGGL((na3d_region_kernel<KY, false, false>), grid, block, 0, st, p, rg);
+  return check_launch("na3d_region_kernel");
+}
+
+static int launch_region(const Na3dParams& p, hipStream_t st) {
+  int nq[3];
+  box_queries(p, nq);
+  Na3dRegions rg;
+  rg.nrx = (nq[2] + 15) / 16;
+  rg.nry = (nq[1] + 7) / 8;
+  rg.nres = p.dil[0] * p.dil[1] * p.dil[2];
+  const int64_t total = (int64_t)rg.nrx * rg.nry * rg.nres * p.H * p.B;
+  if (total > 0x7fffffff) return fail(STRATA_HIP_EUNSUPPORTED, "na3d: problem too large for one launch");
+  rg.total = (int)total;
+  if (total == 0 || nq[0] == 0) return STRATA_HIP_OK;
+  return launch_region_ky<3>(p, rg, st);
+}
+
 }  // namespace strata
 
 using namespace strata;
@@ -2214,6 +2741,7 @@ extern "C" int strata_hip_na3d_fwd(const strata_hip_na3d_args* a, void* stream) 
     case 32:
       return launch_mfma_d<32>(p, st);
     case 64:
+      if (region_fits(p)) return launch_region(p, st);
       if (strip_fits(p))
         return strip_regular(p) ? launch_strip<64, 4, 4, 2, true>(p, st) : launch_strip<64, 4, 4, 2, false>(p, st);
       if (small_strip_fits(p) && !std::getenv("STRATA_HIP_NA3D_NO_SMALL_STRIPS")) return launch_small_strips(p, st);
@@ -2240,8 +2768,9 @@ static int rope_q_setup(const strata_hip_na3d_args* a, const float* cos, const f
     return fail(STRATA_HIP_EUNSUPPORTED, "na3d_fwd_rope_q: tables too large for 31-bit offsets");
   const int kr = p.ker[1] / 2;
   const int r0 = p.org[1] > kr ? p.org[1] : kr, r1 = p.org[1] + p.ext[1] < p.L[1] - kr ? p.org[1] + p.ext[1] : p.L[1] - kr;
-  if (!na3d_mfma_ok(p) || strip_fits(p) || !small_strip_fits(p) || r1 - r0 < 2 ||
-      std::getenv("STRATA_HIP_NA3D_NO_SMALL_STRIPS"))
+  const bool mfma_ok = na3d_mfma_ok(p);
+  if (!(mfma_ok && region_fits(p)) && (!mfma_ok || strip_fits(p) || !small_strip_fits(p) || r1 - r0 < 2 ||
+                                       std::getenv("STRATA_HIP_NA3D_NO_SMALL_STRIPS")))
     return fail(STRATA_HIP_EUNSUPPORTED,
                 "na3d_fwd_rope_q: this window or layout runs a kernel without the query rotation "
                 "(rotate q in strata_hip_rope_qkv_pack and call strata_hip_na3d_fwd)");
@@ -2262,5 +2791,6 @@ extern "C" int strata_hip_na3d_fwd_rope_q(const strata_hip_na3d_args* a, const f
   Na3dParams p;
   if (const int rc = rope_q_setup(a, cos, sin, table_z, p)) return rc;
   if ((int64_t)p.B * p.ext[0] * p.ext[1] * p.ext[2] == 0) return STRATA_HIP_OK;
-  return launch_small_strips(p, (hipStream_t)stream);  // the small-window launch (rope_q_setup checked it applies)
+  // the region or the small-window launch (rope_q_setup checked that one applies)
+  return region_fits(p) ? launch_region(p, (hipStream_t)stream) : launch_small_strips(p, (hipStream_t)stream);
 }

@@ -419,6 +419,178 @@ def na3d_general_launch(B, L, H, ker, dil, qs, ks, vs, os_, org=(0, 0, 0), ext=N
     return acc
 
 
+def region_geom(KY: int) -> dict:
+    """na3d.hip RegionGeom<KY>: the region kernel's LDS layout (head_dim 64)."""
+    NRY, LW = 7 + KY, 15 + KY
+    NK = -(-(NRY * LW) // 8) * 8
+    REG_B = NK * 128
+    NBUF = 3 if 3 * 2 * REG_B <= 160 * 1024 else 2
+    return dict(NRY=NRY, LW=LW, NK=NK, REG_B=REG_B, STAGE_B=2 * REG_B, NDMA=2 * NK // 8,
+                DPW=-(-(2 * NK // 8) // 8), NBUF=NBUF, LDS_B=NBUF * 2 * REG_B)
+
+
+def region_z_walk(Lz: int, qz0: int, qz1: int, kz: int = 3) -> list:
+    """The z walk of na3d_region_kernel for one residue class (the kernel's own
+    closed forms: zhi_of, zlo_of, slot_z, the interior mask 0xF & ~(1 << IDLE) and
+    the extra pass on slot IDLE), replayed stage by stage.  Returns a list of
+    problems: a live tile in no computed slot or sharing a slot, a tile that does
+    not start exactly at its first slice or finish at its last, more than four live."""
+    assert kz == 3
+    ws = lambda z: int(_win_start(z, Lz, kz))  # noqa: E731
+    S0, S1 = ws(qz0), ws(qz1 - 1) + kz
+    zbase = S0 - 1
+    zhi = lambda s: qz1 - 1 if s >= Lz - kz else min(qz1 - 1, s + 1)  # noqa: E731
+    zlo = lambda s: qz0 if s - kz + 1 <= 0 else max(qz0, s - kz + 1 + 1)  # noqa: E731
+    slot_z = lambda k, zl: zl + ((k + zbase - zl) & 3)  # noqa: E731
+    probs, started, finished, seen = [], {}, {}, {}
+    for s in range(S0, S1):
+        truth = [z for z in range(qz0, qz1) if ws(z) <= s < ws(z) + kz]
+        zl, zh = zlo(s), zhi(s)
+        if truth != list(range(zl, zh + 1)):
+            probs.append(f"s={s}: live {truth} != [{zl}, {zh}]")
+        idle = ((s - S0) + 3) & 3
+        comp = {k for k in range(4) if k != idle}
+        if zl <= s - 2 or zh >= s + 2:
+            comp.add(idle)
+        held = {}
+        for k in range(4):
+            z = slot_z(k, zl)
+            if z <= zh:
+                held[z] = k
+                if (z - zbase) & 3 != k:
+                    probs.append(f"s={s}: zq {z} in slot {k}")
+                if k not in comp:
+                    probs.append(f"s={s}: zq {z} (slot {k}) not computed")
+                if ws(z) == s:
+                    started[z] = started.get(z, 0) + 1
+                if ws(z) + kz - 1 == s:
+                    finished[z] = finished.get(z, 0) + 1
+                seen[z] = seen.get(z, 0) + 1
+        if sorted(held) != truth:
+            probs.append(f"s={s}: slots hold {sorted(held)}, live {truth}")
+        if len(truth) > 4:
+            probs.append(f"s={s}: {len(truth)} live")
+    for z in range(qz0, qz1):
+        if started.get(z) != 1 or finished.get(z) != 1 or seen.get(z) != kz:
+            probs.append(f"zq {z}: started {started.get(z)} finished {finished.get(z)} stages {seen.get(z)}")
+    return probs
+
+
+def region_fits_z(L0: int, dz: int, org0: int, ext0: int) -> bool:
+    """The host's z condition of region_fits (na3d.hip), restated."""
+    for g in range(dz):
+        Lz = _sub_len(L0, g, dz)
+        z0, z1 = _sub_first(org0, g, dz), _sub_end(org0, ext0, g, dz)
+        if z1 <= z0:
+            continue
+        for s in range(int(_win_start(z0, Lz, 3)), int(_win_start(z1 - 1, Lz, 3)) + 3):
+            live = [z for z in range(z0, z1) if _win_start(z, Lz, 3) <= s < _win_start(z, Lz, 3) + 3]
+            lo, hi = min(live, default=1 << 30), max(live, default=-1)
+            if len(live) > 4 or hi - lo + 1 != len(live) or lo < s - 2 or hi > s + 2 or (lo == s - 2 and hi == s + 2):
+                return False
+    return True
+
+
+def na3d_region_launch(B, L, H, ker, dil, qs, ks, vs, os_, org=(0, 0, 0), ext=None, rope_zt=None,
+                       lse=False) -> Access:
+    """Every global access of one na3d_region_kernel launch (na3d.hip: launch_region,
+    the work decode, the tile geometry (by, bx, the lane's query), the stage copies
+    (doff, issue), the query and RoPE-table loads (load_q, load_rope), the output
+    and lse stores (finish / flush)), plus the LDS extent of every read and copy."""
+    D = 64
+    ext = tuple(L) if ext is None else tuple(ext)
+    kz, KY, kx = ker
+    assert kz == 3 and KY in (3, 5, 7) and kx <= KY
+    G = region_geom(KY)
+    NRY, LW, REG_B, STAGE_B, NDMA, DPW = G["NRY"], G["LW"], G["REG_B"], G["STAGE_B"], G["NDMA"], G["DPW"]
+    RB = LW * 128
+    acc = Access()
+    nq = [max(_sub_end(org[a], ext[a], g, dil[a]) - _sub_first(org[a], g, dil[a]) for g in range(dil[a]))
+          for a in range(3)]
+    nrx, nry = -(-nq[2] // 16), -(-nq[1] // 8)
+    nres = dil[0] * dil[1] * dil[2]
+    total = nrx * nry * nres * H * B
+    acc.u32("na3d region workgroups", [total], 1 << 31)
+    t = _xcd_order(total, np.arange(total, dtype=np.int64))
+    rx = t % nrx
+    t = t // nrx
+    ry = t % nry
+    t = t // nry
+    res = t % nres
+    t = t // nres
+    h, b = t % H, t // H
+    dz, dy, dx = dil
+    gx, gy, gz = res % dx, (res // dx) % dy, res // (dx * dy)
+    Lz = np.array([_sub_len(L[0], g, dz) for g in range(dz)])[gz]
+    Ly = np.array([_sub_len(L[1], g, dy) for g in range(dy)])[gy]
+    Lx = np.array([_sub_len(L[2], g, dx) for g in range(dx)])[gx]
+    f = lambda a, g, d: np.array([_sub_first(org[a], i, d) for i in range(d)])[g]  # noqa: E731
+    e = lambda a, g, d: np.array([_sub_end(org[a], ext[a], i, d) for i in range(d)])[g]  # noqa: E731
+    qz0, qz1 = f(0, gz, dz), e(0, gz, dz)
+    qy0, qy1 = f(1, gy, dy), e(1, gy, dy)
+    qx0, qx1 = f(2, gx, dx), e(2, gx, dx)
+    y0, x0 = qy0 + 8 * ry, qx0 + 16 * rx
+    live = (qz0 < qz1) & (y0 < qy1) & (x0 < qx1)
+    live &= ((h == 0) | (h == H - 1)) & ((b == 0) | (b == B - 1))
+    sel = lambda a: a[live]  # noqa: E731
+    (y0, x0, h, b, gx, gy, gz, Lz, Ly, Lx, qz0, qz1, qy1, qx1) = map(
+        sel, (y0, x0, h, b, gx, gy, gz, Lz, Ly, Lx, qz0, qz1, qy1, qx1))
+    RY0, RX0 = _win_start(y0, Ly, KY), _win_start(x0, Lx, kx)
+    S0, S1 = _win_start(qz0, Lz, kz), _win_start(qz1 - 1, Lz, kz) + kz
+    col = lambda a: a[:, None]  # noqa: E731
+    wave = np.arange(512)[None, :] // 64
+    lane = np.arange(512)[None, :] % 64
+    n16, g = lane & 15, lane >> 4
+    # ---- tile geometry
+    yt, xt = col(y0) + 2 * (wave >> 1), col(x0) + 8 * (wave & 1)
+    by = _win_start(np.minimum(yt, col(qy1) - 1), col(Ly), KY) - col(RY0)
+    bx = np.where(wave & 1, np.minimum(_win_start(np.minimum(xt, col(qx1) - 1), col(Lx), kx) - col(RX0), LW - 16), 0)
+    acc.u32("region: tile union row", by, NRY - KY)  # by + KY <= NRY - 1
+    acc.u32("region: tile key column", bx, LW - 15)  # bx + 15 <= LW - 1
+    # LDS: the largest K and V read offsets (row KY of the union, chunk slot 7) and the copies
+    kmax = (by + KY) * RB + (bx + 15) * 128 + 16 * 7 + 16
+    vmax = REG_B + (by + KY) * RB + (bx + 15) * 128 + 16 * 7 + 8 + 8
+    acc.u32("region: LDS read past the stage", np.maximum(kmax, vmax), STAGE_B + 1)
+    tq = n16 >> 3
+    qyc, qxc = np.minimum(yt + tq, col(qy1) - 1), np.minimum(xt + (n16 & 7), col(qx1) - 1)
+    qvalid = (yt + tq < col(qy1)) & (xt + (n16 & 7) < col(qx1))
+    # ---- stage copies: doff (lane offsets) on the slice base of stages S0 and S1 - 1
+    for j in range(DPW):
+        J = 8 * j + wave
+        isv = J >= NDMA // 2
+        fk = 8 * np.where(isv, J - NDMA // 2, J) + lane // 8
+        row, kc = fk // LW, fk % LW
+        ok = (J < NDMA) & (fk < NRY * LW) & (col(RY0) + row < col(Ly)) & (col(RX0) + kc < col(Lx))
+        acc.u32("region: LDS copy destination", np.where(J < NDMA, np.where(isv, REG_B + 1024 * (J - NDMA // 2),
+                                                                             1024 * J) + 1024, 0), STAGE_B + 1)
+        for name, st in (("k", ks), ("v", vs)):
+            is_v = name == "v"
+            doff = row * 2 * dy * st[2] + (col(gx) + dx * (col(RX0) + kc)) * 2 * st[3] + 16 * ((lane & 7) ^ (kc & 7))
+            doff = np.where(ok & (isv == is_v), doff, OOB)
+            acc.lane_offsets("region dma", doff)
+            for s in (S0, S1 - 1):
+                base = 2 * (b * st[0] + h * st[4] + (gz + dz * s) * st[1] + (gy + dy * RY0) * st[2])
+                acc.add(name, col(base) + doff, 16, doff != OOB)
+    # ---- queries (and RoPE tables), outputs and lse at the first and last query z
+    for zq in (qz0, qz1 - 1):
+        rz, ry_, rx_ = col(gz + dz * zq), col(gy) + dy * qyc, col(gx) + dx * qxc
+        qp = 2 * (col(b) * qs[0] + col(h) * qs[4] + rz * qs[1] + ry_ * qs[2] + rx_ * qs[3])
+        acc.add("q", qp + 16 * g, 16)
+        acc.add("q", qp + 64 + 16 * g, 16)
+        if rope_zt is not None:
+            r = ((col(b) * rope_zt + (0 if rope_zt == 1 else rz)) * L[1] + ry_) * L[2] + rx_
+            for tname in ("cos", "sin"):
+                acc.add(tname, 4 * (r * 32 + 8 * g), 32)
+        op = 2 * (col(b) * os_[0] + col(h) * os_[4] + (rz - org[0]) * os_[1] + (ry_ - org[1]) * os_[2] +
+                  (rx_ - org[2]) * os_[3]) + 8 * g
+        for db in range(4):
+            acc.add("out", op + 32 * db, 8, qvalid)
+        if lse:
+            li = ((((col(b) * ext[0] + rz - org[0]) * ext[1] + ry_ - org[1]) * ext[2] + rx_ - org[2]) * H + col(h))
+            acc.add("lse", 4 * li, 4, qvalid & (g == 0))
+    return acc
+
+
 def tensor_bytes(shape, strides, esize=2) -> int:
     """Bytes from a view's first element to one past its last (non-negative strides)."""
     if any(s == 0 for s in shape):
@@ -450,10 +622,13 @@ def production_block_launches(B, Z, Y, X, C, H, kernel, mlp_ratio=4, gated=True,
                 {"qkv": span(M, 3 * C, 3 * C), "q": 2 * M * C, "k": 2 * M * C, "tables": 4 * B * Y * X * D // 2}))
     tok = [Z * Y * X * H * D, Y * X * H * D, X * H * D, H * D, D]
     vst = [Z * Y * X * 3 * C, Y * X * 3 * C, X * 3 * C, 3 * C, D]
-    acc = na3d_general_launch(B, (Z, Y, X), H, kernel, (1, 1, 1), tok, tok, vst, tok)
+    if kernel[0] == 3 and kernel[1] == 3 and kernel[2] <= 3 and region_fits_z(Z, 1, 0, Z):
+        acc, kname = na3d_region_launch(B, (Z, Y, X), H, kernel, (1, 1, 1), tok, tok, vst, tok), "na3d (region kernel)"
+    else:
+        acc, kname = na3d_general_launch(B, (Z, Y, X), H, kernel, (1, 1, 1), tok, tok, vst, tok), "na3d (general kernel)"
     # v is the view qkv[..., 2, :, :]: its base is 2C elements into the qkv allocation
     vsz = span(M, 3 * C, 3 * C) - 2 * 2 * C
-    out.append(("na3d (general kernel)", acc, {"q": 2 * M * C, "k": 2 * M * C, "v": vsz, "out": 2 * M * C}))
+    out.append((kname, acc, {"q": 2 * M * C, "k": 2 * M * C, "v": vsz, "out": 2 * M * C}))
     if gated:
         out.append(("gate gemm (sigmoid, x residual)", gemm_dma_launch(M, C, C, C, C, C, C, bias=True, cus=cus),
                     gemm_sizes(M, C, C, C, C, C, C, bias=True)))

@@ -49,7 +49,7 @@ def test_production_tile_reaches_past_2gib():
     assert acc.hi["out"] == sizes["out"] > 2**31
     acc, sizes = launches["fc1 gemm + gelu"]
     assert acc.hi["out"] == sizes["out"] > 4 * 10**9
-    acc, sizes = launches["na3d (general kernel)"]
+    acc, sizes = launches["na3d (region kernel)"]
     assert acc.hi["v"] == sizes["v"] and acc.hi["out"] == sizes["out"]
 
 
@@ -98,3 +98,52 @@ def test_na3d_general_kernel_small_shapes_cover_their_outputs():
     assert acc.check({"q": n, "k": n, "v": n, "out": n}) == []
     assert acc.lo["out"] == 0 and acc.hi["out"] == n
     assert acc.hi["k"] == n and acc.hi["v"] == n
+
+
+@pytest.mark.parametrize("Lz", list(range(1, 13)) + [16, 24, 25])
+def test_region_z_walk_schedules_every_tile_once(Lz):
+    """The region kernel's z walk (zlo / zhi closed forms, slot assignment, the interior
+    mask and the extra pass) holds every live query z in a computed slot of its own, and
+    each tile starts at its first slice and finishes at its last, for every query
+    z-range the host admits; the host refuses exactly the sub-grids where five overlap."""
+    if Lz < 3:
+        return
+    for z0 in range(Lz):
+        for z1 in range(z0 + 1, Lz + 1):
+            admitted = LM.region_fits_z(Lz, 1, z0, z1 - z0)
+            probs = LM.region_z_walk(Lz, z0, z1)
+            if admitted:
+                assert probs == [], (Lz, z0, z1, probs)
+    assert LM.region_fits_z(Lz, 1, 0, Lz) == (Lz != 5)
+
+
+@pytest.mark.parametrize("case", [
+    # B, L, H, ker, dil, org, ext, rope_zt, lse, v_in_qkv  (the host launches ky = 3; the
+    # template's other windows are replayed too)
+    (2, (8, 64, 64), 8, (3, 7, 7), (1, 1, 1), (0, 0, 0), None, 8, False, True),     # configs[1] (query RoPE)
+    (4, (8, 64, 64), 16, (3, 7, 7), (1, 1, 1), (0, 0, 0), None, 1, False, True),    # configs[3] block
+    (6, (16, 64, 64), 12, (3, 7, 7), (1, 1, 1), (0, 0, 0), None, None, True, True),  # configs[4] stage 1, lse
+    (1, (24, 144, 144), 16, (3, 3, 3), (1, 1, 1), (0, 0, 0), None, 1, False, True),  # production tile
+    (1, (7, 21, 27), 2, (3, 5, 5), (1, 1, 1), (0, 0, 0), None, None, True, False),   # ragged regions
+    (2, (9, 30, 37), 3, (3, 7, 5), (2, 1, 2), (0, 0, 0), None, None, False, False),  # dilation
+    (1, (8, 40, 48), 2, (3, 7, 7), (1, 1, 1), (2, 6, 5), (4, 21, 30), None, True, False),  # query box
+    (1, (6, 17, 19), 1, (3, 3, 1), (1, 3, 1), (0, 0, 0), None, None, False, False),
+])
+def test_region_kernel_launches_stay_inside_their_tensors(case):
+    B, L, H, ker, dil, org, ext, zt, lse, v_in_qkv = case
+    D = 64
+    C = H * D
+    tok = LM.contiguous_strides([B, *L, H, D])[:5]
+    vst = [L[0] * L[1] * L[2] * 3 * C, L[1] * L[2] * 3 * C, L[2] * 3 * C, 3 * C, D] if v_in_qkv else tok
+    ext_ = tuple(L) if ext is None else ext
+    ost = LM.contiguous_strides([B, *ext_, H, D])[:5]
+    acc = LM.na3d_region_launch(B, L, H, ker, dil, tok, tok, vst, ost, org=org, ext=ext, rope_zt=zt, lse=lse)
+    n = 2 * B * L[0] * L[1] * L[2] * C
+    no = 2 * B * ext_[0] * ext_[1] * ext_[2] * C
+    sizes = {"q": n, "k": n, "v": LM.span(n // (2 * C), 3 * C, 3 * C) - 4 * C if v_in_qkv else n, "out": no,
+             "lse": 4 * B * ext_[0] * ext_[1] * ext_[2] * H}
+    if zt is not None:
+        sizes["cos"] = sizes["sin"] = 4 * B * zt * L[1] * L[2] * 32
+    assert acc.check(sizes) == []
+    assert acc.lo["out"] == 0 and acc.hi["out"] == no  # every output reached, nothing past it
+
