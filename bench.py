@@ -216,6 +216,59 @@ def bench_production(device, steps, warmup):
     }
 
 
+def bench_pixel(device, steps, warmup):
+    """One pixel-stage block of the production two-stage model (train_configs.py:459-485:
+    pixel width 128, 2 heads x 64, attn_kernel 9 read as (9, 9, 9), qk RMSNorm; semantic
+    width 1024 at horizontal patch 4) on six 64 x 64 tiles of 24 levels, conditioned on
+    the semantic tokens [6, 24, 16, 16, 1024] by the bilinear / depth-wise / GELU /
+    projection adaLN (this build's convention).  Timed whole, and its modulation path
+    (upsample_dw_gelu + the 1024 -> 768 projection) alone."""
+    import torch
+
+    from strata_amd.modules import StrataPixelBlock, init_xavier_
+
+    B, Z, Y, X, C, H, Cs, f, kernel = 6, 24, 64, 64, 128, 2, 1024, 4, (9, 9, 9)
+    g = torch.Generator(device=device).manual_seed(0)
+    x = torch.randn(B, Z, Y, X, C, generator=g, device=device).bfloat16()
+    cond = torch.randn(B, Z, Y // f, X // f, Cs, generator=g, device=device).bfloat16()
+    blk = StrataPixelBlock(C, H, kernel, cond_dim=Cs, factor=f, qk_norm=True)
+    init_xavier_(blk, torch.Generator().manual_seed(1))
+    with torch.no_grad():
+        blk.adaln_bilinear_dw_proj.bias.normal_(0.0, 0.5, generator=torch.Generator().manual_seed(2))
+    blk = blk.to(device).bfloat16().eval()
+
+    def timed(fn):
+        with torch.no_grad():
+            for _ in range(warmup):
+                y = fn()
+            torch.cuda.synchronize()
+            e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            e0.record()
+            for _ in range(steps):
+                y = fn()
+            e1.record()
+            torch.cuda.synchronize()
+        assert torch.isfinite(y.float()).all(), "pixel block produced non-finite values"
+        return e0.elapsed_time(e1) / steps
+
+    ms = timed(lambda: blk(x, cond))
+    ms_mod = timed(lambda: blk.modulation(cond))
+    M = B * Z * Y * X
+    flops = 2.0 * M * C * C * (3 + 1 + 8) + 2.0 * M * Cs * 6 * C + 4.0 * M * H * 9 * 9 * 9 * (C // H)
+    up_bytes = 2.0 * (B * Z * (Y // f) * (X // f) * Cs + M * Cs)  # the upsampling kernel: cond read, c written
+    return {
+        "workload": "pixel-stage block (this build's adaLN convention): [6,24,64,64,128] bf16, 2x64 heads, "
+        "W=(9,9,9), qk RMSNorm, MLP 512 GELU(tanh); cond [6,24,16,16,1024] upsampled x4 (bilinear, "
+        "depth-wise 3x3, GELU) and projected 1024 -> 6x128; Xavier seed 1",
+        "ms_per_step": round(ms, 3),
+        "tokens_per_s": M / (ms * 1e-3),
+        "block_tflops": round(flops / (ms * 1e-3) / 1e12, 1),
+        "pct_bf16_peak": round(100.0 * flops / (ms * 1e-3) / 1e12 / PEAK_BF16_TFLOPS, 2),
+        "modulation_ms": round(ms_mod, 3),
+        "upsample_min_bytes_GB": round(up_bytes / 1e9, 3),
+    }
+
+
 def cfg1_inputs(device):
     """configs[1] inputs: q, k, v ~ N(0,1) [2,8,64,64,8,64] (seed 0, in that order), the
     stereographic tables of 64x64 tiles with the level index in z (pairs x | y | level =
@@ -752,6 +805,8 @@ def main():
     if not args.no_block:
         log("bench: timing the production block (one (24,144,144) x 1024 rollout tile)")
         result["production"] = bench_production(dev, 3, 1)
+        log("bench: timing the pixel-stage block")
+        result["pixel"] = bench_pixel(dev, 5, 2)
     if not args.no_rollout:
         log("bench: timing the configs[4] rollout")
         result["rollout"] = bench_rollout(dev, 2, 1)

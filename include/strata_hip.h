@@ -493,6 +493,57 @@ int strata_hip_state_update(const strata_hip_state_update_args* args, void* stre
 
 /* Library bookkeeping (no counterpart in the reference). */
 const char* strata_hip_last_error(void);
+/* ---------------------------------------------------------------------------
+ * Pixel-stage block (no counterpart in this library's reference interface: the
+ * block lives in physicsnemo, absent here; parameters adaln_bilinear_dw_{conv,proj}
+ * per tests/regression_data/pixeldit_...param_order.txt:245-256, enabled by
+ * use_bilinear_dw_gelu_project_adaln_pixel, screamcast/strata_wrappers.py:443,471-477).
+ * This build's convention: the semantic tokens cond [B, Z, Yc, Xc, Cs] are upsampled
+ * bilinearly by `factor` in y and x (align_corners = false), convolved depth-wise
+ * with 3x3 taps (zero padding), biased and passed through GELU(tanh); a GEMM then
+ * projects them to the six adaLN modulations of the pixel block, which uses
+ * strata_hip_layer_norm_modulate and strata_hip_gated_add around its attention and MLP.
+ * ------------------------------------------------------------------------- */
+typedef struct strata_hip_upsample_dw_gelu_args {
+  const void* cond;         /* [B, Z, Yc, Xc, Cs] bf16; strides (elements) over b, z, y, x; channels contiguous */
+  void* out;                /* [B, Z, Yc*factor, Xc*factor, Cs] bf16; strides over b, z, y, x */
+  const void* weight;       /* [9, Cs] bf16 taps, tap-major (tap 3 dy + dx of a Conv3d weight [Cs, 1, 1, 3, 3]) */
+  const void* bias;         /* [Cs] bf16 or null */
+  int32_t batch, depth, height, width, channels, factor;  /* height / width: the coarse grid */
+  int64_t cond_stride[4];
+  int64_t out_stride[4];
+} strata_hip_upsample_dw_gelu_args;
+
+int strata_hip_upsample_dw_gelu(const strata_hip_upsample_dw_gelu_args* args, void* stream);
+
+/* out = LN(x) * (1 + scale) + shift per row (non-affine LayerNorm, fp32 statistics);
+ * x, out, shift, scale: [M, C] bf16 with their own row strides (shift and scale may be
+ * column slices of one modulation tensor). */
+typedef struct strata_hip_layer_norm_modulate_args {
+  const void* x;
+  void* out;
+  const void* shift;
+  const void* scale;
+  int64_t m, c;
+  int64_t ldx, ldo, ld_shift, ld_scale;
+  float eps;
+  int32_t reserved;
+} strata_hip_layer_norm_modulate_args;
+
+int strata_hip_layer_norm_modulate(const strata_hip_layer_norm_modulate_args* args, void* stream);
+
+/* out = res + gate * y elementwise ([M, C] bf16, each with its own row stride). */
+typedef struct strata_hip_gated_add_args {
+  const void* res;
+  const void* gate;
+  const void* y;
+  void* out;
+  int64_t m, c;
+  int64_t ld_res, ld_gate, ld_y, ld_out;
+} strata_hip_gated_add_args;
+
+int strata_hip_gated_add(const strata_hip_gated_add_args* args, void* stream);
+
 int strata_hip_abi_version(void);
 
 #ifdef __cplusplus

@@ -121,6 +121,55 @@ class LayerNormArgs(ctypes.Structure):
     ]
 
 
+class UpsampleDwGeluArgs(ctypes.Structure):
+    _fields_ = [
+        ("cond", ctypes.c_void_p),
+        ("out", ctypes.c_void_p),
+        ("weight", ctypes.c_void_p),
+        ("bias", ctypes.c_void_p),
+        ("batch", ctypes.c_int32),
+        ("depth", ctypes.c_int32),
+        ("height", ctypes.c_int32),
+        ("width", ctypes.c_int32),
+        ("channels", ctypes.c_int32),
+        ("factor", ctypes.c_int32),
+        ("cond_stride", ctypes.c_int64 * 4),
+        ("out_stride", ctypes.c_int64 * 4),
+    ]
+
+
+class LayerNormModulateArgs(ctypes.Structure):
+    _fields_ = [
+        ("x", ctypes.c_void_p),
+        ("out", ctypes.c_void_p),
+        ("shift", ctypes.c_void_p),
+        ("scale", ctypes.c_void_p),
+        ("m", ctypes.c_int64),
+        ("c", ctypes.c_int64),
+        ("ldx", ctypes.c_int64),
+        ("ldo", ctypes.c_int64),
+        ("ld_shift", ctypes.c_int64),
+        ("ld_scale", ctypes.c_int64),
+        ("eps", ctypes.c_float),
+        ("reserved", ctypes.c_int32),
+    ]
+
+
+class GatedAddArgs(ctypes.Structure):
+    _fields_ = [
+        ("res", ctypes.c_void_p),
+        ("gate", ctypes.c_void_p),
+        ("y", ctypes.c_void_p),
+        ("out", ctypes.c_void_p),
+        ("m", ctypes.c_int64),
+        ("c", ctypes.c_int64),
+        ("ld_res", ctypes.c_int64),
+        ("ld_gate", ctypes.c_int64),
+        ("ld_y", ctypes.c_int64),
+        ("ld_out", ctypes.c_int64),
+    ]
+
+
 # Every function the header declares, with its ctypes signature.
 class CubePadArgs(ctypes.Structure):
     _fields_ = [
@@ -287,6 +336,9 @@ EXPORTS = {
     "strata_hip_state_patchify": ([ctypes.POINTER(StatePatchifyArgs), ctypes.c_void_p], ctypes.c_int),
     "strata_hip_dealias_axis": ([ctypes.POINTER(DealiasAxisArgs), ctypes.c_void_p], ctypes.c_int),
     "strata_hip_state_update": ([ctypes.POINTER(StateUpdateArgs), ctypes.c_void_p], ctypes.c_int),
+    "strata_hip_upsample_dw_gelu": ([ctypes.POINTER(UpsampleDwGeluArgs), ctypes.c_void_p], ctypes.c_int),
+    "strata_hip_layer_norm_modulate": ([ctypes.POINTER(LayerNormModulateArgs), ctypes.c_void_p], ctypes.c_int),
+    "strata_hip_gated_add": ([ctypes.POINTER(GatedAddArgs), ctypes.c_void_p], ctypes.c_int),
     "strata_hip_last_error": ([], ctypes.c_char_p),
     "strata_hip_abi_version": ([], ctypes.c_int),
 }

@@ -246,6 +246,56 @@ class StrataBlock(nn.Module):
         return self.mlp(h, residual=x)
 
 
+class StrataPixelBlock(nn.Module):
+    """Pixel-stage block conditioned on the semantic stage's tokens by a spatially
+    varying adaLN (``use_bilinear_dw_gelu_project_adaln_pixel``,
+    screamcast/strata_wrappers.py:443,471-477,490-495; parameters
+    tests/regression_data/pixeldit_...param_order.txt:245-256, in that order:
+    ``attn.qkv``, ``attn.proj``, ``mlp.layers.0``, ``mlp.layers.2``,
+    ``adaln_bilinear_dw_conv``, ``adaln_bilinear_dw_proj``).  The block itself
+    (physicsnemo's ``StrataPixel3DBlock``) is absent here; this build's convention,
+    parity unpinned beyond its parts, is DiT's adaLN-Zero with per-token modulations:
+
+        mod = adaln_bilinear_dw_proj(GELU_tanh(dwconv3x3(bilinear_up(cond))))
+            -> shift1, scale1, gate1, shift2, scale2, gate2      (each ``dim`` wide)
+        x = x + gate1 * proj(attn(LN(x) * (1 + scale1) + shift1))
+        x = x + gate2 * mlp(LN(x) * (1 + scale2) + shift2)
+
+    ``cond``: the semantic tokens ``[B, Z, Y / factor, X / factor, cond_dim]``
+    (``factor`` = the semantic stage's horizontal patch; its vertical patch is 1, as the
+    reference requires for this mode, screamcast/strata_wrappers.py:471-477).  The
+    upsampling, depth-wise convolution and GELU run in one HIP kernel, the projection
+    on the library's GEMM, the modulated LayerNorms and gated residuals in two more.
+    Inference only."""
+
+    def __init__(self, dim: int, num_heads: int, kernel_size, cond_dim: int, factor: int, mlp_ratio: float = 4.0,
+                 dilation=1, qkv_bias: bool = True, eps: float = 1e-6, qk_norm: bool = False,
+                 qk_norm_affine: bool = False, qk_norm_eps: float = 1e-6):
+        super().__init__()
+        self.eps, self.factor, self.dim = eps, int(factor), dim
+        self.attn = FusedNA3DAttention(dim, num_heads, kernel_size, dilation, qkv_bias, False, qk_norm=qk_norm,
+                                       qk_norm_affine=qk_norm_affine, qk_norm_eps=qk_norm_eps)
+        self.mlp = GemmGeluMlp(dim, int(dim * mlp_ratio))
+        self.adaln_bilinear_dw_conv = nn.Conv3d(cond_dim, cond_dim, (1, 3, 3), padding=(0, 1, 1), groups=cond_dim)
+        self.adaln_bilinear_dw_proj = nn.Linear(cond_dim, 6 * dim)
+
+    def modulation(self, cond: Tensor) -> Tensor:
+        """The six modulations ``[B, Z, Y, X, 6 * dim]`` from the semantic tokens."""
+        conv, proj = self.adaln_bilinear_dw_conv, self.adaln_bilinear_dw_proj
+        c = ops.upsample_dw_gelu(cond, conv.weight, conv.bias, self.factor)
+        return ops.gemm_bias_act(c, proj.weight, proj.bias, None, _lib.ACT_NONE)
+
+    def forward(self, x: Tensor, cond: Tensor, rope: Optional[tuple[Tensor, Tensor]] = None) -> Tensor:
+        if cond.shape[0] != x.shape[0] or cond.shape[1] != x.shape[1] or \
+                cond.shape[2] * self.factor != x.shape[2] or cond.shape[3] * self.factor != x.shape[3]:
+            raise ValueError(f"cond {tuple(cond.shape)} does not match x {tuple(x.shape)} at factor {self.factor}")
+        sh1, sc1, g1, sh2, sc2, g2 = self.modulation(cond).split(self.dim, dim=-1)
+        h = ops.layer_norm_modulate(x, sh1, sc1, self.eps)
+        x = ops.gated_add(x, g1, self.attn(h, rope))
+        h = ops.layer_norm_modulate(x, sh2, sc2, self.eps)
+        return ops.gated_add(x, g2, self.mlp(h))
+
+
 def swap_mlps(model: nn.Module) -> int:
     """Replace every ``Mlp``-shaped child (``layers = Sequential(Linear, GELU, Linear)``)
     by a :class:`GemmGeluMlp` sharing its parameters, in the pattern of the

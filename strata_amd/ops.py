@@ -36,6 +36,9 @@ __all__ = [
     "state_patchify",
     "dealias_axis",
     "state_update",
+    "upsample_dw_gelu",
+    "layer_norm_modulate",
+    "gated_add",
 ]
 
 
@@ -1042,3 +1045,115 @@ def _(pred, state, mean, std, src_channel, clamp_min, grid, patch, order):
 
 
 state_update.register_autograd(_no_backward("strata_hip::state_update"))
+
+
+# ---------------------------------------------------------------------------
+# Pixel-stage block pieces (adaLN conditioning from the semantic tokens)
+# ---------------------------------------------------------------------------
+def _cols_view(name: str, t: Tensor, what: str) -> Tensor:
+    """A [rows, C] view of t with unit column stride, 16-byte aligned rows (no copy when
+    t already is one, e.g. a column slice of the modulation tensor)."""
+    t2 = t.reshape(-1, t.shape[-1]) if t.dim() != 2 else t
+    if t2.stride(-1) != 1 or (t2.shape[0] > 1 and t2.stride(0) % 8) or t2.data_ptr() % 16:
+        t2 = t2.contiguous()
+    return t2
+
+
+@torch.library.custom_op("strata_hip::upsample_dw_gelu", mutates_args=())
+def upsample_dw_gelu(cond: Tensor, weight: Tensor, bias: Optional[Tensor], factor: int) -> Tensor:
+    """``GELU_tanh(dwconv3x3(bilinear_up(cond)) + bias)``: cond ``[B, Z, Yc, Xc, C]`` bf16
+    tokens upsampled by ``factor`` in y and x (align_corners = false), the depth-wise 3x3
+    taps ``weight`` (a Conv3d weight ``[C, 1, 1, 3, 3]``, or ``[C, 3, 3]``) with zero
+    padding; returns ``[B, Z, Yc * factor, Xc * factor, C]`` bf16."""
+    name = "upsample_dw_gelu"
+    _require_gpu(name, cond, weight, bias)
+    if cond.dtype != torch.bfloat16 or cond.dim() != 5:
+        raise ValueError(f"{name}: cond must be a bfloat16 [B, Z, Y, X, C] tensor")
+    B, Z, Yc, Xc, C = cond.shape
+    w = weight.reshape(C, 9).t().to(torch.bfloat16).contiguous()  # tap-major [9, C]
+    b = bias.to(torch.bfloat16).contiguous() if bias is not None else None
+    c = cond if cond.stride(-1) == 1 and cond.data_ptr() % 16 == 0 else cond.contiguous()
+    f = int(factor)
+    out = torch.empty((B, Z, Yc * f, Xc * f, C), dtype=torch.bfloat16, device=cond.device)
+    if out.numel() == 0:
+        return out
+    a = _lib.UpsampleDwGeluArgs()
+    a.cond, a.out, a.weight = c.data_ptr(), out.data_ptr(), w.data_ptr()
+    a.bias = b.data_ptr() if b is not None else None
+    a.batch, a.depth, a.height, a.width, a.channels, a.factor = B, Z, Yc, Xc, C, f
+    a.cond_stride[:] = [c.stride(i) for i in range(4)]
+    a.out_stride[:] = [out.stride(i) for i in range(4)]
+    with torch.cuda.device(cond.device):
+        _lib.call("strata_hip_upsample_dw_gelu", a, _stream(cond))
+    return out
+
+
+@upsample_dw_gelu.register_fake
+def _(cond, weight, bias, factor):
+    B, Z, Yc, Xc, C = cond.shape
+    return cond.new_empty((B, Z, Yc * factor, Xc * factor, C))
+
+
+upsample_dw_gelu.register_autograd(_no_backward("strata_hip::upsample_dw_gelu"))
+
+
+@torch.library.custom_op("strata_hip::layer_norm_modulate", mutates_args=())
+def layer_norm_modulate(x: Tensor, shift: Tensor, scale: Tensor, eps: float) -> Tensor:
+    """``LN(x) * (1 + scale) + shift`` over the last dim (non-affine LayerNorm, fp32
+    statistics); shift and scale have x's shape and may be column slices of one tensor."""
+    name = "layer_norm_modulate"
+    _require_gpu(name, x, shift, scale)
+    for t, w in ((x, "x"), (shift, "shift"), (scale, "scale")):
+        if t.dtype != torch.bfloat16 or t.shape != x.shape:
+            raise ValueError(f"{name}: {w} must be bfloat16 of x's shape")
+    x2, sh, sc = (_cols_view(name, t, w) for t, w in ((x, "x"), (shift, "shift"), (scale, "scale")))
+    out = torch.empty(x.shape, dtype=x.dtype, device=x.device)
+    if x2.shape[0] == 0:
+        return out
+    a = _lib.LayerNormModulateArgs()
+    a.x, a.out, a.shift, a.scale = x2.data_ptr(), out.data_ptr(), sh.data_ptr(), sc.data_ptr()
+    a.m, a.c = x2.shape
+    ld = lambda t: t.stride(0) if t.shape[0] > 1 else t.shape[1]  # noqa: E731
+    a.ldx, a.ldo, a.ld_shift, a.ld_scale = ld(x2), x2.shape[1], ld(sh), ld(sc)
+    a.eps = float(eps)
+    with torch.cuda.device(x.device):
+        _lib.call("strata_hip_layer_norm_modulate", a, _stream(x))
+    return out
+
+
+@layer_norm_modulate.register_fake
+def _(x, shift, scale, eps):
+    return torch.empty_like(x)
+
+
+layer_norm_modulate.register_autograd(_no_backward("strata_hip::layer_norm_modulate"))
+
+
+@torch.library.custom_op("strata_hip::gated_add", mutates_args=())
+def gated_add(res: Tensor, gate: Tensor, y: Tensor) -> Tensor:
+    """``res + gate * y`` (bf16, one shape; gate may be a column slice of a wider tensor)."""
+    name = "gated_add"
+    _require_gpu(name, res, gate, y)
+    for t, w in ((res, "res"), (gate, "gate"), (y, "y")):
+        if t.dtype != torch.bfloat16 or t.shape != res.shape:
+            raise ValueError(f"{name}: {w} must be bfloat16 of res's shape")
+    r2, g2, y2 = (_cols_view(name, t, w) for t, w in ((res, "res"), (gate, "gate"), (y, "y")))
+    out = torch.empty(res.shape, dtype=res.dtype, device=res.device)
+    if r2.shape[0] == 0:
+        return out
+    a = _lib.GatedAddArgs()
+    a.res, a.gate, a.y, a.out = r2.data_ptr(), g2.data_ptr(), y2.data_ptr(), out.data_ptr()
+    a.m, a.c = r2.shape
+    ld = lambda t: t.stride(0) if t.shape[0] > 1 else t.shape[1]  # noqa: E731
+    a.ld_res, a.ld_gate, a.ld_y, a.ld_out = ld(r2), ld(g2), ld(y2), r2.shape[1]
+    with torch.cuda.device(res.device):
+        _lib.call("strata_hip_gated_add", a, _stream(res))
+    return out
+
+
+@gated_add.register_fake
+def _(res, gate, y):
+    return torch.empty_like(res)
+
+
+gated_add.register_autograd(_no_backward("strata_hip::gated_add"))

@@ -1,5 +1,6 @@
 """Pins for the block oracle's qk RMSNorm (CPU, float64)."""
 
+import pytest
 import torch
 import torch.nn.functional as F
 
@@ -273,3 +274,86 @@ def test_planted_composition_mistakes_fail_the_pins():
             assert caught > 0, f"planted mistake not caught: {name}"
     finally:
         OB = real
+
+
+# ---------------------------------------------------------------------------
+# Pixel-stage block (this build's convention): its parts are pinned against torch's
+# own interpolate / conv3d / layer_norm, its composition against the plain block.
+# ---------------------------------------------------------------------------
+@pytest.mark.parametrize("shape, factor", [((1, 2, 3, 5, 4), 4), ((2, 1, 4, 4, 8), 2), ((1, 3, 1, 2, 3), 3),
+                                           ((1, 1, 5, 3, 2), 1)])
+def test_upsample_dw_gelu_is_interpolate_then_depthwise_conv(shape, factor):
+    g = torch.Generator().manual_seed(sum(shape) + factor)
+    C = shape[-1]
+    cond, w, b = torch.randn(shape, generator=g), torch.randn(C, 1, 1, 3, 3, generator=g), torch.randn(C, generator=g)
+    out = OB.upsample_dw_gelu(cond, w, b, factor)
+    c5 = cond.double().permute(0, 4, 1, 2, 3)
+    up = F.interpolate(c5, scale_factor=(1, factor, factor), mode="trilinear", align_corners=False)
+    ref = F.gelu(F.conv3d(up, w.double(), b.double(), padding=(0, 1, 1), groups=C), approximate="tanh")
+    assert torch.allclose(out, ref.permute(0, 2, 3, 4, 1), atol=1e-12)
+
+
+def test_bilinear_index_closed_forms():
+    """Factor 2 over 3 inputs: outputs 0, 1 sit on input 0 (clamped) and at 0.25; the last
+    output sits at 2.25 -> index pair (2, 2) (the edge repeats)."""
+    i0, i1, w = OB.bilinear_index(6, 3, 2)
+    assert i0.tolist() == [0, 0, 0, 1, 1, 2] and i1.tolist() == [1, 1, 1, 2, 2, 2]
+    assert torch.allclose(w, torch.tensor([0.0, 0.25, 0.75, 0.25, 0.75, 0.25], dtype=torch.float64))
+
+
+def _pixel_params(C, Cs, heads, g, zero_proj=False, gate_one=False):
+    p = {
+        "attn.qkv.weight": torch.randn(3 * C, C, generator=g) / C**0.5, "attn.qkv.bias": torch.randn(3 * C, generator=g),
+        "attn.proj.weight": torch.randn(C, C, generator=g) / C**0.5, "attn.proj.bias": torch.randn(C, generator=g),
+        "mlp.layers.0.weight": torch.randn(4 * C, C, generator=g) / C**0.5,
+        "mlp.layers.0.bias": torch.randn(4 * C, generator=g),
+        "mlp.layers.2.weight": torch.randn(C, 4 * C, generator=g) / (4 * C)**0.5,
+        "mlp.layers.2.bias": torch.randn(C, generator=g),
+        "adaln_bilinear_dw_conv.weight": torch.randn(Cs, 1, 1, 3, 3, generator=g),
+        "adaln_bilinear_dw_conv.bias": torch.randn(Cs, generator=g),
+        "adaln_bilinear_dw_proj.weight": torch.randn(6 * C, Cs, generator=g) / Cs**0.5,
+        "adaln_bilinear_dw_proj.bias": torch.randn(6 * C, generator=g),
+    }
+    if zero_proj or gate_one:
+        p["adaln_bilinear_dw_proj.weight"] = torch.zeros(6 * C, Cs)
+        p["adaln_bilinear_dw_proj.bias"] = torch.zeros(6 * C)
+    if gate_one:  # shift = scale = 0, gate = 1: the plain pre-norm block
+        p["adaln_bilinear_dw_proj.bias"][2 * C:3 * C] = 1.0
+        p["adaln_bilinear_dw_proj.bias"][5 * C:6 * C] = 1.0
+    return p
+
+
+def test_pixel_block_zero_modulation_is_identity():
+    """adaLN-Zero: a zero projection gives zero gates, so the block returns x."""
+    g = torch.Generator().manual_seed(1)
+    C, Cs, heads = 16, 8, 2
+    x, cond = torch.randn(1, 3, 8, 8, C, generator=g), torch.randn(1, 3, 2, 2, Cs, generator=g)
+    out = OB.pixel_block_forward(x, cond, _pixel_params(C, Cs, heads, g, zero_proj=True), heads, (3, 3, 3), 4)
+    assert torch.equal(out, x.double())
+
+
+def test_pixel_block_unit_gates_are_the_plain_block():
+    """shift = scale = 0 and gate = 1 everywhere: the pixel block is block_forward."""
+    g = torch.Generator().manual_seed(2)
+    C, Cs, heads = 16, 8, 2
+    x, cond = torch.randn(1, 3, 8, 8, C, generator=g), torch.randn(1, 3, 2, 2, Cs, generator=g)
+    p = _pixel_params(C, Cs, heads, g, gate_one=True)
+    out = OB.pixel_block_forward(x, cond, p, heads, (3, 3, 3), 4)
+    ref = OB.block_forward(x, p, heads, (3, 3, 3), None, None, dtype=torch.float64)
+    assert torch.allclose(out, ref, atol=1e-10)
+
+
+def test_pixel_block_planted_chunk_order_fails_the_unit_gate_pin():
+    """A restatement that takes the gates from the shift chunks (a plausible misreading of
+    the six-way split) leaves x unchanged under unit gates, failing the plain-block pin."""
+    g = torch.Generator().manual_seed(3)
+    C, Cs, heads = 16, 8, 2
+    x, cond = torch.randn(1, 3, 8, 8, C, generator=g), torch.randn(1, 3, 2, 2, Cs, generator=g)
+    p = _pixel_params(C, Cs, heads, g, gate_one=True)
+    # planted: modulation order (gate1, scale1, shift1, ...) -> the bias puts 1 in the shifts
+    q = dict(p)
+    bias = p["adaln_bilinear_dw_proj.bias"].view(6, C)
+    q["adaln_bilinear_dw_proj.bias"] = bias[[2, 1, 0, 5, 4, 3]].reshape(-1)
+    out = OB.pixel_block_forward(x, cond, q, heads, (3, 3, 3), 4)
+    ref = OB.block_forward(x, p, heads, (3, 3, 3), None, None, dtype=torch.float64)
+    assert not torch.allclose(out, ref, atol=1e-3)

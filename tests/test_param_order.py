@@ -25,7 +25,8 @@ import pytest
 import torch
 import torch.nn as nn
 
-from strata_amd.modules import FusedNA3DAttention, GemmGeluMlp, StrataBlock, swap_attention, swap_mlps
+from strata_amd.modules import (FusedNA3DAttention, GemmGeluMlp, StrataBlock, StrataPixelBlock, swap_attention,
+                                swap_mlps)
 
 from .conftest import GOLDEN
 
@@ -62,6 +63,19 @@ def test_strata_block_matches_every_production_block():
     for i in range(24):
         want = _block_names(p, "strata.backbone.blocks", i)
         assert want in (got, ungated), (i, want)
+
+
+def test_pixel_block_matches_every_production_pixel_block():
+    """The pixel-stage block registers the manifest's per-block names in order (its
+    two adaLN modules after the attention and the MLP) for the four production blocks."""
+    blk = StrataPixelBlock(128, 2, (3, 9, 9), cond_dim=64, factor=4)
+    got = [n for n, _ in blk.named_parameters()]
+    p = _names(PIXELDIT)
+    for i in range(4):
+        assert got == _block_names(p, "strata.pixel_blocks", i), i
+    shapes = dict((n, tuple(t.shape)) for n, t in blk.named_parameters())
+    assert shapes["adaln_bilinear_dw_conv.weight"] == (64, 1, 1, 3, 3)
+    assert shapes["adaln_bilinear_dw_proj.weight"] == (6 * 128, 64)
 
 
 class _RefAttention(nn.Module):
