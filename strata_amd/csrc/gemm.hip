@@ -496,19 +496,22 @@ __device__ __forceinline__ void gemm_dma_body(const GemmParams& p) {
   // last K step read; slot rd meanwhile receives the next tile's first stage.
   // Phase 2: each lane reads 16 contiguous bytes of a row, combines the
   // residual read the same way, and writes 16 bytes: CPR lanes cover a row.
+  // A half's slab rows are read back together (its LDS reads in flight at
+  // once, one wait) and a tile inside the matrix takes one branch for the
+  // whole half (a bounds branch per row made every row wait for its own LDS
+  // read before its store).
   // Loads and stores share vmcnt on gfx9 (a load issued after a store waits
-  // for it), so every residual load is issued before the first store, into
-  // registers the first half's accumulators have freed.  Tiles inside the
-  // matrix skip every bounds check.  The slab is rewritten by the second half
-  // only after the first half's reads (one wave, in order).
-  constexpr int SRB = WTN * 2, CPR = WTN / 8, RPI = 64 / CPR, NIT = WTM / RPI;
+  // for it), so every residual load is issued before the first store.  The
+  // slab is rewritten by the second half only after the first half's reads
+  // (one wave, in order).
+  constexpr int SRB = WTN * 2, CPR = WTN / 8, RPI = 64 / CPR, NIT = WTM / RPI, NH = NIT / 2;
   lds_barrier();  // every wave is done reading the last stage
   char* slab = lds + wr * STAGE + wave * SLAB;
   const int c = lane % CPR;  // logical 16-byte chunk = 8 output columns
   const int64_t gn = gn0 + 8 * c;
   u32x4 r4[NIT];
-#pragma unroll
-  for (int half = 0; half < 2; ++half) {
+  // Phase 1 for one half: f(accumulator) -> bf16 into the slab.
+  auto to_slab = [&](int half, auto f) {
 #pragma unroll
     for (int i = 0; i < FN; ++i)
 #pragma unroll
@@ -519,14 +522,73 @@ __device__ __forceinline__ void gemm_dma_body(const GemmParams& p) {
           const int j = half * HM + jj;
           float v[4];
 #pragma unroll
-          for (int e = 0; e < 4; ++e) v[e] = act_t<ACT>(acc[i][j][4 * q + e]);
+          for (int e = 0; e < 4; ++e) v[e] = f(acc[i][j][4 * q + e]);
           const int ml = 32 * jj + l32;
           const u32x2 w2 = {pack_bf16x2(v[0], v[1]), pack_bf16x2(v[2], v[3])};
           *(u32x2*)(slab + ml * SRB + (((nl >> 3) ^ (ml & 7)) << 4) + 8 * hi) = w2;
         }
       }
+  };
+  // Phase 2 for one half, to dst; WITH_RES: combine the residual (the output
+  // pass; the saved derivative takes none).
+  // GR rows are read back per group: all of a half, or half of one in the SAVE
+  // instance, whose accumulators all stay live through the first half.
+  constexpr int GR = SAVE ? NH / 2 : NH;
+  auto from_slab = [&](int half, bf16* dst, auto with_res) {
+    constexpr bool WR = decltype(with_res)::value && RES != RES_NONE_T;
+    const int64_t gmh = gm0 + half * (WTM / 2) + lane / CPR;  // this lane's row for slab row group 0
+#pragma unroll
+    for (int k0 = 0; k0 < NH; k0 += GR) {
+      u32x4 w4[GR];
+#pragma unroll
+      for (int k = 0; k < GR; ++k) {
+        const int sl = RPI * (k0 + k) + lane / CPR;  // row of the slab
+        w4[k] = *(const u32x4*)(slab + sl * SRB + ((c ^ (sl & 7)) << 4));
+      }
+      auto combined = [&](int k) {
+        u32x4 o = w4[k];
+        if constexpr (WR) {
+          const u32x4& r = r4[half * NH + k0 + k];
+#pragma unroll
+          for (int e = 0; e < 4; ++e)
+            o[e] = pack_bf16x2(combine_t<RES>(bf16_lo(w4[k][e]), bf16_lo(r[e])),
+                               combine_t<RES>(bf16_hi(w4[k][e]), bf16_hi(r[e])));
+        }
+        return o;
+      };
+      // Streaming stores: the output is not read again here, and a tile-round's
+      // outputs (32 MB over the grid) would otherwise push the x and w panels
+      // out of L2 (M = 131072, N = 4096, K = 1024 with GELU: 1.32 -> 1.27 ms).
+      if (full) {
+#pragma unroll
+        for (int k = 0; k < GR; ++k)
+          __builtin_nontemporal_store(combined(k), (u32x4*)(dst + (gmh + RPI * (k0 + k)) * p.ldo + gn));
+      } else {
+#pragma unroll
+        for (int k = 0; k < GR; ++k) {
+          const int64_t gm = gmh + RPI * (k0 + k);
+          if (gm < p.M && gn + 8 <= p.N) {
+            __builtin_nontemporal_store(combined(k), (u32x4*)(dst + gm * p.ldo + gn));
+          } else if (gm < p.M && gn < p.N) {
+            for (int e = 0; e < 8 && gn + e < p.N; ++e) {  // ragged last columns
+              const uint32_t wd = w4[k][e >> 1];
+              float ov = (e & 1) ? bf16_hi(wd) : bf16_lo(wd);
+              if constexpr (WR) ov = combine_t<RES>(ov, (float)p.res[gm * p.ldr + gn + e]);
+              dst[gm * p.ldo + gn + e] = (bf16)ov;
+            }
+          }
+        }
+      }
+    }
+  };
+#pragma unroll
+  for (int half = 0; half < 2; ++half) {
+    to_slab(half, [](float x) { return act_t<ACT>(x); });
     if constexpr (RES != RES_NONE_T) {
-      if (half == 0) {  // all residual rows, into the registers the first half's accumulators freed
+      // All residual rows, into the registers the first half's accumulators
+      // freed (loaded before that conversion, even the first half's rows
+      // alone spill 4-14 VGPRs).
+      if (half == 0) {
 #pragma unroll
         for (int it = 0; it < NIT; ++it) {
           const int64_t gm = gm0 + RPI * it + lane / CPR;
@@ -535,72 +597,16 @@ __device__ __forceinline__ void gemm_dma_body(const GemmParams& p) {
         }
       }
     }
-#pragma unroll
-    for (int it = half * (NIT / 2); it < (half + 1) * (NIT / 2); ++it) {
-      const int ml = RPI * it + lane / CPR;   // row of the wave tile
-      const int sl = ml - half * (WTM / 2);   // row of the slab
-      const u32x4 w4 = *(const u32x4*)(slab + sl * SRB + ((c ^ (sl & 7)) << 4));
-      const int64_t gm = gm0 + ml;
-      u32x4 o = w4;
-      if constexpr (RES != RES_NONE_T) {
-#pragma unroll
-        for (int e = 0; e < 4; ++e)
-          o[e] = pack_bf16x2(combine_t<RES>(bf16_lo(w4[e]), bf16_lo(r4[it][e])),
-                             combine_t<RES>(bf16_hi(w4[e]), bf16_hi(r4[it][e])));
-      }
-      if (full || (gm < p.M && gn + 8 <= p.N)) {
-        // Streaming store: the output is not read again here, and a tile-round's
-        // outputs (32 MB over the grid) would otherwise push the x and w panels
-        // out of L2 (M = 131072, N = 4096, K = 1024 with GELU: 1.32 -> 1.27 ms).
-        __builtin_nontemporal_store(o, (u32x4*)(p.out + gm * p.ldo + gn));
-      } else if (gm < p.M && gn < p.N) {
-        for (int e = 0; e < 8 && gn + e < p.N; ++e) {  // ragged last columns
-          const uint32_t wd = w4[e >> 1];
-          float ov = (e & 1) ? bf16_hi(wd) : bf16_lo(wd);
-          if constexpr (RES != RES_NONE_T) ov = combine_t<RES>(ov, (float)p.res[gm * p.ldr + gn + e]);
-          p.out[gm * p.ldo + gn + e] = (bf16)ov;
-        }
-      }
-    }
+    from_slab(half, p.out, std::true_type{});
     if constexpr (SAVE) {  // the derivative of the same half through the same slab, to out2
       static_assert(ACT == STRATA_HIP_ACT_GELU_TANH, "SAVE: GELU(tanh) only");
-#pragma unroll
-      for (int i = 0; i < FN; ++i)
-#pragma unroll
-        for (int q = 0; q < 4; ++q) {
-          const int nl = 32 * i + 8 * q + 4 * hi;
-#pragma unroll
-          for (int jj = 0; jj < HM; ++jj) {
-            const int j = half * HM + jj;
-            float v[4];
-#pragma unroll
-            for (int e = 0; e < 4; ++e) {
-              // recomputed, not shared with the first pass: sharing would hold the whole
-              // half's sigmoids in registers between the two passes
-              float xv = acc[i][j][4 * q + e];
-              asm volatile("" : "+v"(xv));
-              v[e] = gelu_tanh_grad(xv);
-            }
-            const int ml = 32 * jj + l32;
-            const u32x2 w2 = {pack_bf16x2(v[0], v[1]), pack_bf16x2(v[2], v[3])};
-            *(u32x2*)(slab + ml * SRB + (((nl >> 3) ^ (ml & 7)) << 4) + 8 * hi) = w2;
-          }
-        }
-#pragma unroll
-      for (int it = half * (NIT / 2); it < (half + 1) * (NIT / 2); ++it) {
-        const int ml = RPI * it + lane / CPR;
-        const int sl = ml - half * (WTM / 2);
-        const u32x4 w4 = *(const u32x4*)(slab + sl * SRB + ((c ^ (sl & 7)) << 4));
-        const int64_t gm = gm0 + ml;
-        if (full || (gm < p.M && gn + 8 <= p.N)) {
-          __builtin_nontemporal_store(w4, (u32x4*)(p.out2 + gm * p.ldo + gn));
-        } else if (gm < p.M && gn < p.N) {
-          for (int e = 0; e < 8 && gn + e < p.N; ++e) {
-            const uint32_t wd = w4[e >> 1];
-            p.out2[gm * p.ldo + gn + e] = (bf16)((e & 1) ? bf16_hi(wd) : bf16_lo(wd));
-          }
-        }
-      }
+      // recomputed, not shared with the first pass: sharing would hold the whole
+      // half's sigmoids in registers between the two passes
+      to_slab(half, [](float xv) {
+        asm volatile("" : "+v"(xv));
+        return gelu_tanh_grad(xv);
+      });
+      from_slab(half, p.out2, std::false_type{});
     }
   }
   }  // tiles
