@@ -298,8 +298,10 @@ int strata_hip_gemm_bias_act(const strata_hip_gemm_args* args, void* stream);
  * under loss.backward(), train.py:1161): strata_hip_gemm_bias_act with act =
  * GELU_TANH and no residual, and in the same launch dact = gelu'(x @ w^T + bias),
  * bf16 [M, N] with out's row stride ldo, the derivative the backward multiplies
- * by the upstream gradient (instead of recomputing the GEMM).  K must be a
- * multiple of 64 (STRATA_HIP_EUNSUPPORTED otherwise: the caller then recomputes). */
+ * by the upstream gradient (instead of recomputing the GEMM).  The argument
+ * rules of strata_hip_gemm_bias_act apply (K a multiple of 8); row strides too
+ * long for the large-tile kernel's 32-bit lane offsets (256 * ld * 2 bytes past
+ * 2^31) return STRATA_HIP_EUNSUPPORTED (the caller then recomputes). */
 int strata_hip_gemm_gelu_save(const strata_hip_gemm_args* args, void* dact, void* stream);
 
 /* Bias gradient of the GEMM backward (nn.Linear's d bias: the output gradient

@@ -8,10 +8,11 @@
 // output columns of one row per accumulator quad, which the epilogue stores
 // as one 8-byte write after bias, GELU and residual.
 //
-// Two kernels: gemm_dma_kernel (K % 64 == 0; 256 x 256 tiles, 8 waves,
-// global->LDS streaming) for every GEMM of the block and the rollout, plain or
-// with a fused epilogue, and gemm_bias_act_kernel (128 x 128 tiles,
-// register-staged loads) for any other K.
+// Two kernels: gemm_dma_kernel (256 x 256 tiles, 8 waves, global->LDS
+// streaming; the last K step masked when K is not a multiple of 64) for every
+// GEMM of the block and the rollout, plain or with a fused epilogue, and
+// gemm_bias_act_kernel (128 x 128 tiles, register-staged loads) for row
+// strides too long for the former's 32-bit lane offsets.
 #include "gemm.h"
 
 namespace strata {
@@ -292,7 +293,7 @@ __device__ __forceinline__ int gswz(int chunk, int row) {
   else return chunk ^ ((row >> 2) & 3);
 }
 
-// Large-tile GEMM for K % BK == 0: a BM x BN output tile per workgroup of
+// Large-tile GEMM (K a multiple of 8): a BM x BN output tile per workgroup of
 // WGM x WGN waves (128 x 64 each, v_mfma_f32_32x32x16_bf16).  A/B tiles of BK
 // columns stream from global memory straight into a double-buffered LDS ring
 // (buffer_load ... lds) one stage ahead of the MFMAs, one barrier per stage.
@@ -301,7 +302,8 @@ __device__ __forceinline__ int gswz(int chunk, int row) {
 // the epilogue runs in the other slot.
 // SAVE: also write act'(pre-activation) (GELU(tanh) only) to p.out2, for a
 // backward that then needs no recomputed GEMM.
-template <int BM, int BN, int WGM, int WGN, int BK, int NST, int ACT, int RES, bool SAVE = false>
+template <int BM, int BN, int WGM, int WGN, int BK, int NST, int ACT, int RES, bool SAVE = false,
+          bool KTAIL = false>
 __device__ __forceinline__ void gemm_dma_body(const GemmParams& p) {
   constexpr int NW = WGM * WGN;
   constexpr int WTM = BM / WGM;  // 128
@@ -360,12 +362,32 @@ __device__ __forceinline__ void gemm_dma_body(const GemmParams& p) {
     const bool ok = (isw ? n0 : m0) + row < (isw ? p.N : p.M);
     return ok ? (uint32_t)(row * (isw ? p.ldw : p.ldx) * 2 + lc * 16) : OOB;
   };
+  // KTAIL (K % BK != 0; separate instances, so that the others keep their
+  // registers): the last stage holds KT = K % BK columns (a multiple of 8); a
+  // lane's chunk of copy j past them takes the out-of-range offset and reads
+  // as zero (beyond K lies the row's padding or, on the last row, past the
+  // end of the tensor).  The chunk depends on the lane and the row inside the
+  // tile only; it is recomputed at that stage from an opaque copy of the lane
+  // id (a mask held across the tile walk costs more registers).
+  const int nk = (int)(KTAIL ? (p.K + BK - 1) / BK : p.K / BK);
   auto issue_at = [&](int64_t m0, int64_t n0, const uint32_t* vo, int kt, int buf) {
     const u32x4 rx = make_rsrc((const char*)(p.x + m0 * p.ldx) + (int64_t)kt * BK * 2, OOB);
     const u32x4 rw = make_rsrc((const char*)(p.w + n0 * p.ldw) + (int64_t)kt * BK * 2, OOB);
     const uint32_t dst = lds_base + buf * STAGE + wave * 1024;
+    if (KTAIL && kt == nk - 1) {  // uniform: the ragged last stage
+      int ln = lane;
+      asm volatile("" : "+v"(ln));
 #pragma unroll
-    for (int j = 0; j < LPW; ++j) dma_row16(j * NW + wave >= XCH ? rw : rx, dst + j * NW * 1024, vo[j]);
+      for (int j = 0; j < LPW; ++j) {
+        const int c = j * NW + wave;
+        const int row = RPC * (c >= XCH ? c - XCH : c) + ln / CH;
+        const bool ok = gswz<CH>(ln % CH, row) * 8 < (int)(p.K % BK);
+        dma_row16(c >= XCH ? rw : rx, dst + j * NW * 1024, ok ? vo[j] : OOB);
+      }
+    } else {
+#pragma unroll
+      for (int j = 0; j < LPW; ++j) dma_row16(j * NW + wave >= XCH ? rw : rx, dst + j * NW * 1024, vo[j]);
+    }
   };
   // A tile's first stage, with offsets computed on the spot.
   auto issue_first = [&](int64_t m0, int64_t n0, int buf) {
@@ -389,7 +411,6 @@ __device__ __forceinline__ void gemm_dma_body(const GemmParams& p) {
     for (int kk = 0; kk < 2; ++kk) boff[j][kk] = row * ROWB + gswz<CH>(2 * kk + hi, row) * 16;
   }
 
-  const int nk = (int)(p.K / BK);
   // Ring slots: `rd` holds the next stage to read, `wr` takes the next issue
   // (and, after a tile's last K step, that tile's epilogue slabs).
   int rd = 0, wr = 1;
@@ -616,19 +637,24 @@ __device__ __forceinline__ void gemm_dma_body(const GemmParams& p) {
 // 128 KiB ring.  (Measured alternatives at the block's shapes, all slower:
 // 256 x 128 tiles at two workgroups per CU; K step 32 with 3-5 stages; four
 // waves of 128 x 128 with the accumulators in AGPRs.)
-template <int ACT, int RES, bool SAVE = false>
+template <int ACT, int RES, bool SAVE = false, bool KTAIL = false>
 __global__ __launch_bounds__(512, 1) void gemm_dma_kernel(GemmParams p) {
-  gemm_dma_body<256, 256, 2, 4, 64, 2, ACT, RES, SAVE>(p);
+  gemm_dma_body<256, 256, 2, 4, 64, 2, ACT, RES, SAVE, KTAIL>(p);
 }
 
 template <int ACT>
 static void launch_dma_act(const GemmParams& p, dim3 grid, hipStream_t st) {
-  if (!p.res)
-    hipLaunchKernelGGL((gemm_dma_kernel<ACT, RES_NONE_T>), grid, dim3(512), 0, st, p);
-  else if (p.res_op == STRATA_HIP_RES_MUL)
-    hipLaunchKernelGGL((gemm_dma_kernel<ACT, RES_MUL_T>), grid, dim3(512), 0, st, p);
-  else
-    hipLaunchKernelGGL((gemm_dma_kernel<ACT, RES_ADD_T>), grid, dim3(512), 0, st, p);
+  auto go = [&](auto ktail) {
+    constexpr bool KT = decltype(ktail)::value;
+    if (!p.res)
+      hipLaunchKernelGGL((gemm_dma_kernel<ACT, RES_NONE_T, false, KT>), grid, dim3(512), 0, st, p);
+    else if (p.res_op == STRATA_HIP_RES_MUL)
+      hipLaunchKernelGGL((gemm_dma_kernel<ACT, RES_MUL_T, false, KT>), grid, dim3(512), 0, st, p);
+    else
+      hipLaunchKernelGGL((gemm_dma_kernel<ACT, RES_ADD_T, false, KT>), grid, dim3(512), 0, st, p);
+  };
+  if (p.K % 64) go(std::true_type{});
+  else go(std::false_type{});
 }
 
 // Compute units of the current device (cached per device).
@@ -695,12 +721,13 @@ static int gemm_params(const strata_hip_gemm_args* a, GemmParams& p) {
   return STRATA_HIP_OK;
 }
 
-// The large-tile kernels stream 64-wide K steps with 32-bit lane offsets
-// inside a 256-row block: K a multiple of 64, row strides small enough.
+// The large-tile kernel streams 64-wide K steps (the last one masked when K
+// is not a multiple of 64) with 32-bit lane offsets inside a 256-row block:
+// row strides small enough.
 // Sets the tile counts; the persistent grid is one workgroup per CU (the
 // 128 KiB ring admits one).
 static bool gemm_big(GemmParams& p, dim3& grid) {
-  if (!(p.K % 64 == 0 && 256 * p.ldx * 2 + 4096 < (int64_t)OOB && 256 * p.ldw * 2 + 4096 < (int64_t)OOB)) return false;
+  if (!(256 * p.ldx * 2 + 4096 < (int64_t)OOB && 256 * p.ldw * 2 + 4096 < (int64_t)OOB)) return false;
   p.mt = (int)((p.M + 255) / 256);
   p.nt = (int)((p.N + 255) / 256);
   const int64_t total = (int64_t)p.mt * p.nt;
@@ -741,9 +768,13 @@ extern "C" int strata_hip_gemm_gelu_save(const strata_hip_gemm_args* a, void* da
   p.out2 = (bf16*)dact;
   dim3 grid;
   if (!gemm_big(p, grid))
-    return fail(STRATA_HIP_EUNSUPPORTED, "gemm_gelu_save: needs K a multiple of 64 (the large-tile kernel)");
-  hipLaunchKernelGGL((gemm_dma_kernel<STRATA_HIP_ACT_GELU_TANH, RES_NONE_T, true>), grid, dim3(512), 0,
-                     (hipStream_t)stream, p);
+    return fail(STRATA_HIP_EUNSUPPORTED, "gemm_gelu_save: row strides too long for the large-tile kernel");
+  if (p.K % 64)
+    hipLaunchKernelGGL((gemm_dma_kernel<STRATA_HIP_ACT_GELU_TANH, RES_NONE_T, true, true>), grid, dim3(512), 0,
+                       (hipStream_t)stream, p);
+  else
+    hipLaunchKernelGGL((gemm_dma_kernel<STRATA_HIP_ACT_GELU_TANH, RES_NONE_T, true>), grid, dim3(512), 0,
+                       (hipStream_t)stream, p);
   return check_launch("gemm_dma_kernel (gelu save)");
 }
 

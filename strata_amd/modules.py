@@ -35,8 +35,8 @@ class GemmGeluMlp(nn.Module):
     Drop-in for physicsnemo's ``Mlp`` (layer indices 0/2 per
     screamcast/checkpoint_compat.py:243-249; GELU(tanh) per
     screamcast/strata_wrappers.py:76-100): fc1 + bias + GELU is one launch,
-    fc2 + bias (+ the block's residual) another.  Under autograd (tanh GELU,
-    in_features a multiple of 64) fc1's launch also writes gelu'(pre-activation),
+    fc2 + bias (+ the block's residual) another.  Under autograd (tanh GELU)
+    fc1's launch also writes gelu'(pre-activation),
     which the backward multiplies by the upstream gradient.
     """
 
@@ -64,7 +64,7 @@ class GemmGeluMlp(nn.Module):
     def forward(self, x: Tensor, residual: Optional[Tensor] = None) -> Tensor:
         fc1, act, fc2 = self.layers
         train = torch.is_grad_enabled() and (x.requires_grad or fc1.weight.requires_grad)
-        if train and act.approximate == "tanh" and x.shape[-1] % 64 == 0:
+        if train and act.approximate == "tanh":
             # fc1's launch also writes gelu'(pre-activation) for the backward (no recomputed GEMM)
             h, _ = ops.gemm_gelu_train(x, fc1.weight, fc1.bias)
         else:

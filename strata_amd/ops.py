@@ -624,7 +624,7 @@ def gemm_gelu_train(x: Tensor, w: Tensor, bias: Optional[Tensor]) -> tuple[Tenso
     """``gelu_tanh(x @ w.T + bias)`` and, from the same launch, its derivative at the
     pre-activation ``gelu_tanh'(x @ w.T + bias)`` (bf16): the MLP's fc1 under autograd,
     whose backward then multiplies the upstream gradient by the saved derivative
-    instead of recomputing the GEMM.  K must be a multiple of 64."""
+    instead of recomputing the GEMM.  K must be a multiple of 8."""
     name = "gemm_gelu_train"
     _require_gpu(name, x, w, bias)
     for t, nm in ((x, "x"), (w, "w"), (bias, "bias")):

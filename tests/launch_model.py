@@ -113,9 +113,11 @@ def _gswz8(chunk, row):
     return chunk ^ ((row & 7) ^ ((row >> 3) & 1))
 
 
-def _gemm_dma_offsets(m0, n0, M, N, ldx, ldw):
+def _gemm_dma_offsets(m0, n0, M, N, ldx, ldw, kt_cols=0):
     """Lane offsets voff[j] of a stage's x / w copies (gemm.hip dma_off), broadcast
-    over [tile, wave, lane]; and whether each copy reads w."""
+    over [tile, wave, lane]; and whether each copy reads w.  kt_cols > 0: the
+    ragged last K stage of issue_at, whose chunks at or past kt_cols columns take
+    the out-of-range offset (tail_ok)."""
     wave = np.arange(8)[None, :, None]
     lane = np.arange(64)[None, None, :]
     out = []
@@ -125,6 +127,8 @@ def _gemm_dma_offsets(m0, n0, M, N, ldx, ldw):
         row = 8 * np.where(isw, c - 32, c) + lane // 8
         lc = _gswz8(lane % 8, row)
         ok = np.where(isw, n0 + row < N, m0 + row < M)
+        if kt_cols:
+            ok = ok & (lc * 8 < kt_cols)
         ld = np.where(isw, ldw, ldx)
         out.append((np.where(ok, row * ld * 2 + lc * 16, OOB), np.broadcast_to(isw, ok.shape)))
     return out
@@ -151,21 +155,25 @@ def gemm_dma_launch(M: int, N: int, K: int, ldx: int, ldw: int, ldo: int, ldr: i
     separable sum tile base + lane offset; the ragged tiles of the last row and
     column panels lane by lane."""
     acc = Access()
-    assert K % 64 == 0 and 256 * ldx * 2 + 4096 < OOB and 256 * ldw * 2 + 4096 < OOB  # gemm_big
+    assert K % 8 == 0 and 256 * ldx * 2 + 4096 < OOB and 256 * ldw * 2 + 4096 < OOB  # gemm_params, gemm_big
     mt, nt = -(-M // 256), -(-N // 256)
     acc.u32("tiles", [mt * nt], 1 << 31)
     m0, n0 = gemm_tile_origins(M, N)
-    nk = K // 64
+    nk, kt_cols = -(-K // 64), K % 64
+    # the first and last K stages bound every stage's addresses; the last one
+    # masked past K when K is not a multiple of 64
+    stages = [(kt, kt_cols if kt == nk - 1 else 0) for kt in sorted({0, nk - 1})]
     full = (m0 + 256 <= M) & (n0 + 256 <= N)
     outs = [("out", ldo)] + ([("res", ldr)] if ldr is not None else []) + ([("out2", ldo)] if save else [])
     # ---- full tiles: offsets inside a full tile do not depend on which tile it is
     if full.any():
         fm, fn = m0[full], n0[full]
-        for voff, isw in _gemm_dma_offsets(np.int64(0), np.int64(0), 1 << 62, 1 << 62, ldx, ldw):
-            acc.lane_offsets("gemm dma", voff)
-            for kt in (0, nk - 1):
-                acc.add_sum("x", 2 * (fm * ldx + kt * 64), voff[~isw], 16)
-                acc.add_sum("w", 2 * (fn * ldw + kt * 64), voff[isw], 16)
+        for kt, kc in stages:
+            for voff, isw in _gemm_dma_offsets(np.int64(0), np.int64(0), 1 << 62, 1 << 62, ldx, ldw, kc):
+                acc.lane_offsets("gemm dma", voff)
+                live = voff + 16 <= OOB
+                acc.add_sum("x", 2 * (fm * ldx + kt * 64), voff[~isw & live], 16)
+                acc.add_sum("w", 2 * (fn * ldw + kt * 64), voff[isw & live], 16)
         rows, cols = _gemm_epilogue_lanes()
         for name, ld in outs:
             acc.add_sum(name, 2 * (fm * ld + fn), 2 * (rows * ld + cols), 16)
@@ -175,10 +183,10 @@ def gemm_dma_launch(M: int, N: int, K: int, ldx: int, ldw: int, ldo: int, ldr: i
     rg = ~full
     if rg.any():
         m0r, n0r = m0[rg][:, None, None], n0[rg][:, None, None]
-        for voff, isw in _gemm_dma_offsets(m0r, n0r, M, N, ldx, ldw):
-            acc.lane_offsets("gemm dma", voff)
-            live = voff + 16 <= OOB
-            for kt in (0, nk - 1):
+        for kt, kc in stages:
+            for voff, isw in _gemm_dma_offsets(m0r, n0r, M, N, ldx, ldw, kc):
+                acc.lane_offsets("gemm dma", voff)
+                live = voff + 16 <= OOB
                 base = np.where(isw, 2 * (n0r * ldw + kt * 64), 2 * (m0r * ldx + kt * 64))
                 acc.add("x", base + voff, 16, live & ~isw)
                 acc.add("w", base + voff, 16, live & isw)

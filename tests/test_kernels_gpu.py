@@ -123,6 +123,42 @@ def test_plain_gemm(gpu, case):
     assert torch.equal(torch.ops.strata_hip.gemm_bias_act(*args), out)
 
 
+@pytest.mark.parametrize("M, N, K", [(393216, 768, 80), (300, 136, 80), (257, 520, 16), (64, 640, 200),
+                                     (1000, 96, 1032), (77, 256, 8)])
+def test_gemm_ragged_k_masks_the_last_stage(gpu, M, N, K):
+    """K not a multiple of 64 (the rollout's patch embedding: K = 80) on the large-tile
+    kernel: the last K stage's chunks past K read as zero.  x and w are views into
+    wider rows whose padding holds NaN, so a chunk read past K would reach the output;
+    also x and w at row stride K (the tail of the last row is the allocation's end)."""
+    print(f"ragged K gemm {(M, N, K)}", flush=True)
+    g = torch.Generator().manual_seed(M + 3 * N + K)
+    x, w, b = _randn((M, K), g), _randn((N, K), g, K**-0.5), _randn((N,), g)
+    ref = x.double() @ w.double().T + b.double()
+    pad = 48
+    xp = torch.full((M, K + pad), float("nan"), dtype=torch.bfloat16, device=gpu)
+    wp = torch.full((N, K + pad), float("nan"), dtype=torch.bfloat16, device=gpu)
+    xp[:, :K], wp[:, :K] = x.to(gpu), w.to(gpu)
+    out = torch.ops.strata_hip.gemm_bias_act(xp[:, :K], wp[:, :K], b.to(gpu), None, _lib.ACT_NONE)
+    assert torch.isfinite(out.float()).all()
+    assert rel_l2(out.float(), ref) <= 1e-2
+    tight = torch.ops.strata_hip.gemm_bias_act(x.to(gpu), w.to(gpu), b.to(gpu), None, _lib.ACT_NONE)
+    assert torch.equal(tight, out)
+
+
+@pytest.mark.parametrize("K", [80, 200])
+def test_gemm_gelu_save_ragged_k(gpu, K):
+    """The GELU-saving fc1 launch at K not a multiple of 64: both outputs against fp64."""
+    M, N = 1000, 768
+    g = torch.Generator().manual_seed(K)
+    x, w, b = _randn((M, K), g), _randn((N, K), g, K**-0.5), _randn((N,), g)
+    pre = x.double() @ w.double().T + b.double()
+    out, dact = torch.ops.strata_hip.gemm_gelu_train(x.to(gpu), w.to(gpu), b.to(gpu))
+    pr = pre.clone().requires_grad_(True)
+    F.gelu(pr, approximate="tanh").sum().backward()
+    assert rel_l2(out.float(), F.gelu(pre, approximate="tanh")) <= 1e-2
+    assert rel_l2(dact.float(), pr.grad) <= 1e-2
+
+
 def test_plain_gemm_residual_in_place(gpu):
     """out may alias the residual (the C ABI's contract): out = x @ w.T + b + out."""
     M, N, K = 512, 768, 256

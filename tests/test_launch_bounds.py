@@ -72,6 +72,27 @@ def test_gemm_ragged_shapes_touch_exactly_their_tensors(M, N, K):
     assert acc.hi["x"] == sizes["x"] and acc.hi["w"] == sizes["w"] and acc.hi["bias"] == 2 * N
 
 
+@pytest.mark.parametrize("M, N, K", [(300, 136, 80), (393216, 768, 80), (257, 520, 16), (64, 640, 200),
+                                     (1000, 96, 1032)])
+def test_gemm_ragged_k_touches_exactly_its_tensors(M, N, K):
+    """K not a multiple of 64 (the rollout's patch embedding: K = 80): with row strides
+    equal to K the masked last stage reads up to the last element of x and w and no
+    further."""
+    acc = LM.gemm_dma_launch(M, N, K, K, K, N, bias=True)
+    sizes = LM.gemm_sizes(M, N, K, K, K, N, bias=True)
+    assert acc.check(sizes) == []
+    assert acc.hi["x"] == sizes["x"] and acc.hi["w"] == sizes["w"]
+
+
+def test_planted_unmasked_k_tail_is_caught(monkeypatch):
+    """The same launch with the last stage's K mask dropped reads past the end of x."""
+    orig = LM._gemm_dma_offsets
+    monkeypatch.setattr(LM, "_gemm_dma_offsets", lambda *a, **k: orig(*a[:6]))
+    M, N, K = 300, 136, 80
+    acc = LM.gemm_dma_launch(M, N, K, K, K, N, bias=True)
+    assert acc.check(LM.gemm_sizes(M, N, K, K, K, N, bias=True)) != []
+
+
 def test_planted_32bit_descriptor_is_caught():
     """A GEMM whose x stage used ONE descriptor for the whole matrix with the row
     offset folded into the 32-bit lane offset (the kernel instead moves the
