@@ -599,6 +599,35 @@ def na3d_region_launch(B, L, H, ker, dil, qs, ks, vs, os_, org=(0, 0, 0), ext=No
     return acc
 
 
+def na3d_column_launch(B, L, H, qs, ks, vs, os_) -> Access:
+    """Every global access of one na3d_column_kernel launch (na3d.hip: window (Z, 1, 1),
+    head_dim 64; launch_column's grid of four waves per workgroup, the item decode
+    (h, x, y, b) of each wave, its loads of the column's Q, K and V rows (lane l: row
+    l / 8 + 8 c for c < 4 when below Z, 16-byte chunk l % 8) and the output stores).
+    Offsets are 64-bit element offsets from each view's base."""
+    Z, Y, X = L
+    acc = Access()
+    items = B * Y * X * H
+    wgs = -(-items // 4)
+    acc.u32("column grid", [wgs], 1 << 31)
+    item = np.arange(wgs * 4, dtype=np.int64)
+    item = item[item < items]  # the wave returns before any access
+    h = item % H
+    t = item // H
+    x = t % X
+    t //= X
+    y = t % Y
+    b = t // Y
+    lane = np.arange(64, dtype=np.int64)
+    r = (lane // 8)[:, None] + 8 * np.arange(4, dtype=np.int64)[None, :]
+    live = r < Z
+    for name, st in (("q", qs), ("k", ks), ("v", vs), ("out", os_)):
+        base = b * st[0] + y * st[2] + x * st[3] + h * st[4]
+        inner = (r * st[1] + 8 * (lane % 8)[:, None])[live]
+        acc.add_sum(name, 2 * base, 2 * inner, 16)
+    return acc
+
+
 def tensor_bytes(shape, strides, esize=2) -> int:
     """Bytes from a view's first element to one past its last (non-negative strides)."""
     if any(s == 0 for s in shape):
@@ -614,11 +643,13 @@ def contiguous_strides(shape):
     return list(reversed(st))
 
 
-def production_block_launches(B, Z, Y, X, C, H, kernel, mlp_ratio=4, gated=True, cus=256):
+def production_block_launches(B, Z, Y, X, C, H, kernel, mlp_ratio=4, gated=True, cus=256, depthwise=False):
     """(name, Access, sizes) of every hand-written launch of one StrataBlock forward
     at inference with qk-norm (strata_amd/modules.py StrataBlock.forward,
     FusedNA3DAttention.attention): LN, qkv GEMM, pack (q and k, v read from qkv),
-    general NA3D, the gate GEMM, proj + residual, LN, fc1 + GELU, fc2 + residual."""
+    NA3D (the region or general kernel; with depthwise, the alternate block's
+    column kernel over window (Z, 1, 1)), the gate GEMM, proj + residual, LN,
+    fc1 + GELU, fc2 + residual."""
     D = C // H
     M = B * Z * Y * X
     F = int(C * mlp_ratio)
@@ -630,7 +661,9 @@ def production_block_launches(B, Z, Y, X, C, H, kernel, mlp_ratio=4, gated=True,
                 {"qkv": span(M, 3 * C, 3 * C), "q": 2 * M * C, "k": 2 * M * C, "tables": 4 * B * Y * X * D // 2}))
     tok = [Z * Y * X * H * D, Y * X * H * D, X * H * D, H * D, D]
     vst = [Z * Y * X * 3 * C, Y * X * 3 * C, X * 3 * C, 3 * C, D]
-    if kernel[0] == 3 and kernel[1] == 3 and kernel[2] <= 3 and region_fits_z(Z, 1, 0, Z):
+    if depthwise:
+        acc, kname = na3d_column_launch(B, (Z, Y, X), H, tok, tok, vst, tok), "na3d (column kernel)"
+    elif kernel[0] == 3 and kernel[1] == 3 and kernel[2] <= 3 and region_fits_z(Z, 1, 0, Z):
         acc, kname = na3d_region_launch(B, (Z, Y, X), H, kernel, (1, 1, 1), tok, tok, vst, tok), "na3d (region kernel)"
     else:
         acc, kname = na3d_general_launch(B, (Z, Y, X), H, kernel, (1, 1, 1), tok, tok, vst, tok), "na3d (general kernel)"
@@ -655,5 +688,5 @@ def cdiv(a, b):
 
 
 __all__ = ["Access", "OOB", "gemm_dma_launch", "gemm_sizes", "gemm_tile_origins", "layer_norm_launch",
-           "rope_pack_half_launch", "na3d_general_launch", "production_block_launches", "span", "tensor_bytes",
+           "rope_pack_half_launch", "na3d_general_launch", "na3d_column_launch", "production_block_launches", "span", "tensor_bytes",
            "contiguous_strides", "cdiv", "math"]

@@ -40,6 +40,29 @@ def test_block_launches_stay_inside_their_tensors(shape):
         assert set(acc.lo) <= set(sizes), name
 
 
+def test_production_depthwise_block_stays_inside_its_tensors():
+    """The production tile's alternate block (depth-wise attention, window (24, 1, 1) on
+    the column kernel, v strided through the 3.06 GB qkv buffer): every launch inside its
+    tensors, the column kernel's reads and writes reaching the views' last bytes."""
+    B, Z, Y, X, C, H = 1, 24, 144, 144, 1024, 16
+    launches = LM.production_block_launches(B, Z, Y, X, C, H, (Z, 1, 1), depthwise=True)
+    assert _problems(launches) == []
+    acc, sizes = {n: (a, s) for n, a, s in launches}["na3d (column kernel)"]
+    assert acc.lo["q"] == 0 and acc.hi["q"] == sizes["q"]
+    assert acc.hi["v"] == sizes["v"] and acc.hi["out"] == sizes["out"]
+
+
+def test_column_kernel_small_grid_touches_exactly_its_tensors():
+    """A ragged grid (Z = 5 of the 32 rows a wave loads; items not a multiple of 4): the
+    modelled accesses cover each tensor exactly."""
+    B, L, H = 2, (5, 3, 7), 3
+    st = LM.contiguous_strides([B, *L, H, 64])[:5]
+    acc = LM.na3d_column_launch(B, L, H, st, st, st, st)
+    n = 2 * B * L[0] * L[1] * L[2] * H * 64
+    assert acc.check({"q": n, "k": n, "v": n, "out": n}) == []
+    assert all(acc.lo[t] == 0 and acc.hi[t] == n for t in ("q", "k", "v", "out"))
+
+
 def test_production_tile_reaches_past_2gib():
     """The replay does reach the large offsets: qkv's last row lies beyond 2^31 bytes,
     fc1's output beyond 4 * 10^9."""
