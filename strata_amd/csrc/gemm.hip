@@ -370,23 +370,32 @@ __device__ __forceinline__ void gemm_dma_body(const GemmParams& p) {
   // tile only; it is recomputed at that stage from an opaque copy of the lane
   // id (a mask held across the tile walk costs more registers).
   const int nk = (int)(KTAIL ? (p.K + BK - 1) / BK : p.K / BK);
-  auto issue_at = [&](int64_t m0, int64_t n0, const uint32_t* vo, int kt, int buf) {
+  // The copies of stage kt into slot buf; PART: both tiles (ALL), or only the
+  // x tile's (XS) or the w tile's (WS) copies.  Copy j reads w exactly when
+  // j * NW >= XCH (XCH is a multiple of NW), so the split is compile-time.
+  enum { ALL = 0, XS = 1, WS = 2 };
+  static_assert(XCH % NW == 0, "a copy index reads x or w for every wave");
+  auto issue_at = [&](int64_t m0, int64_t n0, const uint32_t* vo, int kt, int buf, auto part) {
+    constexpr int PART = decltype(part)::value;
     const u32x4 rx = make_rsrc((const char*)(p.x + m0 * p.ldx) + (int64_t)kt * BK * 2, OOB);
     const u32x4 rw = make_rsrc((const char*)(p.w + n0 * p.ldw) + (int64_t)kt * BK * 2, OOB);
     const uint32_t dst = lds_base + buf * STAGE + wave * 1024;
+    auto mine = [](int j) { return PART == ALL || (PART == WS) == (j * NW >= XCH); };
     if (KTAIL && kt == nk - 1) {  // uniform: the ragged last stage
       int ln = lane;
       asm volatile("" : "+v"(ln));
 #pragma unroll
       for (int j = 0; j < LPW; ++j) {
-        const int c = j * NW + wave;
-        const int row = RPC * (c >= XCH ? c - XCH : c) + ln / CH;
+        if (!mine(j)) continue;
+        const bool isw = j * NW >= XCH;
+        const int row = RPC * (isw ? j * NW + wave - XCH : j * NW + wave) + ln / CH;
         const bool ok = gswz<CH>(ln % CH, row) * 8 < (int)(p.K % BK);
-        dma_row16(c >= XCH ? rw : rx, dst + j * NW * 1024, ok ? vo[j] : OOB);
+        dma_row16(isw ? rw : rx, dst + j * NW * 1024, ok ? vo[j] : OOB);
       }
     } else {
 #pragma unroll
-      for (int j = 0; j < LPW; ++j) dma_row16(j * NW + wave >= XCH ? rw : rx, dst + j * NW * 1024, vo[j]);
+      for (int j = 0; j < LPW; ++j)
+        if (mine(j)) dma_row16(j * NW >= XCH ? rw : rx, dst + j * NW * 1024, vo[j]);
     }
   };
   // A tile's first stage, with offsets computed on the spot.
@@ -394,7 +403,7 @@ __device__ __forceinline__ void gemm_dma_body(const GemmParams& p) {
     uint32_t vo[LPW];
 #pragma unroll
     for (int j = 0; j < LPW; ++j) vo[j] = dma_off(j, m0, n0);
-    issue_at(m0, n0, vo, 0, buf);
+    issue_at(m0, n0, vo, 0, buf, std::integral_constant<int, ALL>{});
   };
 
   // LDS read offsets of the MFMA operands for K sub-steps kk = 0, 1; kk = 2, 3
@@ -426,7 +435,7 @@ __device__ __forceinline__ void gemm_dma_body(const GemmParams& p) {
 #pragma unroll
   for (int j = 0; j < LPW; ++j) voff[j] = dma_off(j, m0, n0);
   // Slot rd was last read two K steps ago (or never): no barrier needed.
-  if (!first_in_flight) issue_at(m0, n0, voff, 0, rd);
+  if (!first_in_flight) issue_at(m0, n0, voff, 0, rd, std::integral_constant<int, ALL>{});
 
   // The bias enters as the C operand of each accumulator's first MFMA (no
   // zero fill, no add in the epilogue): acc[i][j][4q + e] holds column
@@ -466,8 +475,15 @@ __device__ __forceinline__ void gemm_dma_body(const GemmParams& p) {
     // output stores.
     wait_vmcnt(0);
     lds_barrier();  // the stage has landed for every wave; slot wr is free
+    // The next stage's copies in two bursts, x here and w after the first
+    // sub-step's MFMAs: all eight of a wave's copies at once right after the
+    // barrier stall every wave on the address path while the MFMA pipe idles
+    // (A/B at the block's shapes, bit-identical: 1.5-5% faster; copies
+    // placed later in the step or spread further, and all of them after the
+    // first sub-step: no faster or slower).
+    const int wr_now = wr;
     if (kt + 1 < nk) {
-      issue_at(m0, n0, voff, kt + 1, wr);
+      issue_at(m0, n0, voff, kt + 1, wr, std::integral_constant<int, XS>{});
     } else if (tn < ntiles) {
       // The next tile's first stage.  Its origin passes through an empty asm
       // so that its lane offsets are computed here, not hoisted out of the K
@@ -501,6 +517,11 @@ __device__ __forceinline__ void gemm_dma_body(const GemmParams& p) {
         for (int j = 0; j < FM; ++j)
           acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(af[cb][i], bfr[cb][j],
                                                              FIRST && kk == 0 ? binit[i] : acc[i][j], 0, 0, 0);
+      if (kk == 0 && kt + 1 < nk) {
+        __builtin_amdgcn_sched_barrier(0);
+        issue_at(m0, n0, voff, kt + 1, wr_now, std::integral_constant<int, WS>{});
+        __builtin_amdgcn_sched_barrier(0);
+      }
     }
     // Let the scheduler interleave the LDS reads of the next sub-step with
     // the MFMAs of the current one (measured 1-3% faster than the default
