@@ -1572,10 +1572,14 @@ __device__ __forceinline__ void na3d_strip_fast_body(const Na3dParams p, const N
       const bool starting = zc == 0 && gr > 0 && gr < NT;
       // The stage read now was issued NBUF - 1 issues ago.  At a tile's start its Q
       // copy (issued after the issue of the group's second slice) must have landed
-      // too: only the kz - 2 later issues may still be in flight.
-      if (starting)
-        wait_vmcnt((NBUF - 2 < kz - 2 ? NBUF - 2 : kz - 2) * LPT);
-      else
+      // too: only the kz - 2 later issues may still be in flight (none with a
+      // two-stage ring: a compile-time wait, no run-time switch at every start).
+      if (starting) {
+        if constexpr (NBUF == 2)
+          wait_vmcnt(0);
+        else
+          wait_vmcnt((NBUF - 2 < kz - 2 ? NBUF - 2 : kz - 2) * LPT);
+      } else
         wait_vmcnt((NBUF - 2) * LPT);
       lds_barrier();
       issue();
