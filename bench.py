@@ -714,6 +714,8 @@ def main():
     ap.add_argument("--no-halo", action="store_true")
     ap.add_argument("--no-backward", action="store_true")
     ap.add_argument("--no-cfg1", action="store_true")
+    ap.add_argument("--no-production", action="store_true", help="skip the production-tile block (profiling passes)")
+    ap.add_argument("--no-pixel", action="store_true", help="skip the pixel-stage block (profiling passes)")
     ap.add_argument("--cpu-full", action="store_true",
                     help="CPU baseline in full: configs[3] over its whole batch, warm-up + median of 5 everywhere")
     ap.add_argument(
@@ -802,9 +804,10 @@ def main():
     if not args.no_block:
         log("bench: timing the configs[3] block")
         result["block"] = bench_block(dev, max(3, args.steps // 2), 2)
-    if not args.no_block:
+    if not args.no_block and not args.no_production:
         log("bench: timing the production block (one (24,144,144) x 1024 rollout tile)")
         result["production"] = bench_production(dev, 3, 1)
+    if not args.no_block and not args.no_pixel:
         log("bench: timing the pixel-stage block")
         result["pixel"] = bench_pixel(dev, 5, 2)
     if not args.no_rollout:
