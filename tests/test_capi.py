@@ -175,6 +175,43 @@ def test_empty_problem_is_a_no_op(lib):
     assert lib.strata_hip_na3d_fwd(ctypes.byref(a), None) == _lib.OK
 
 
+def test_empty_problems_return_before_any_launch(lib):
+    """Zero rows (or batch 0) is a valid call for every compute entry point: it returns OK
+    without touching the device (this container has none, so a launch would fail)."""
+    g = _lib.GemmArgs()
+    g.k, g.ldx, g.ldw, g.ldo, g.n = 64, 64, 64, 128, 128  # m = 0
+    assert lib.strata_hip_gemm_bias_act(ctypes.byref(g), None) == _lib.OK, lib.strata_hip_last_error()
+    ln = _lib.LayerNormArgs()
+    ln.x = ln.out = 0x1000
+    ln.c, ln.ldx, ln.ldo, ln.eps = 1024, 1024, 1024, 1e-6  # m = 0
+    assert lib.strata_hip_layer_norm(ctypes.byref(ln), None) == _lib.OK, lib.strata_hip_last_error()
+    lm = _lib.LayerNormModulateArgs()
+    lm.x = lm.out = lm.shift = lm.scale = 0x1000
+    lm.c = lm.ldx = lm.ldo = lm.ld_shift = lm.ld_scale = 128
+    lm.eps = 1e-6
+    assert lib.strata_hip_layer_norm_modulate(ctypes.byref(lm), None) == _lib.OK, lib.strata_hip_last_error()
+    ga = _lib.GatedAddArgs()
+    ga.res = ga.gate = ga.y = ga.out = 0x1000
+    ga.c = ga.ld_res = ga.ld_gate = ga.ld_y = ga.ld_out = 128
+    assert lib.strata_hip_gated_add(ctypes.byref(ga), None) == _lib.OK, lib.strata_hip_last_error()
+    up = _lib.UpsampleDwGeluArgs()
+    up.cond = up.out = up.weight = 0x1000
+    up.batch, up.depth, up.height, up.width, up.channels, up.factor = 0, 4, 4, 4, 64, 4
+    up.cond_stride[:] = [4 * 4 * 4 * 64, 4 * 4 * 64, 4 * 64, 64]
+    up.out_stride[:] = [4 * 16 * 16 * 64, 16 * 16 * 64, 16 * 64, 64]
+    assert lib.strata_hip_upsample_dw_gelu(ctypes.byref(up), None) == _lib.OK, lib.strata_hip_last_error()
+    b = _lib.Na3dBwdArgs()
+    b.q = b.k = b.v = b.out = b.dout = b.dq = b.dk = b.dv = b.workspace = 0x1000
+    b.dtype, b.batch, b.heads, b.head_dim, b.scale = _lib.BF16, 0, 2, 64, 0.125
+    b.grid[:], b.kernel[:], b.dilation[:] = [4, 8, 8], [3, 3, 3], [1, 1, 1]
+    assert lib.strata_hip_na3d_bwd(ctypes.byref(b), None) == _lib.OK, lib.strata_hip_last_error()
+    r = _lib.RopePackArgs()
+    r.qkv = r.cos = r.sin = r.q = r.k = r.v = 0x1000
+    r.batch, r.table_z, r.heads, r.head_dim, r.layout, r.qkv_row_stride = 0, 1, 2, 64, _lib.ROPE_HALF, 384
+    r.grid[:] = [4, 8, 8]
+    assert lib.strata_hip_rope_qkv_pack(ctypes.byref(r), None) == _lib.OK, lib.strata_hip_last_error()
+
+
 def test_cube_validation(lib):
     a = _lib.CubePadArgs()
     a.src, a.dst, a.dtype, a.face_size, a.pad, a.lead = 0x1000, 0x2000, _lib.F32, 8, 9, 1
