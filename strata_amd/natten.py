@@ -9,12 +9,15 @@ name ``natten`` (see :func:`install_as_natten`) routes that call to
 so that the backward reuses the forward's log-sum-exp) without touching the caller.
 
 Supported: odd kernel sizes, any dilation with kernel*dilation <= size,
-non-causal, stride 1, default or explicit scale.  Everything else raises
-``NotImplementedError``; invalid sizes raise ``ValueError`` as NATTEN does.
+non-causal, stride 1, default or explicit scale, ``return_lse`` (the
+logsumexp, natural log, fp32 ``[B, Z, Y, X, H]``; no gradient through it).
+Everything else raises ``NotImplementedError``; invalid sizes raise
+``ValueError`` as NATTEN does.
 """
 
 from __future__ import annotations
 
+import math
 import sys
 import types
 from typing import Optional, Sequence
@@ -60,14 +63,12 @@ def na3d(
     backend: Optional[str] = None,
     return_lse: bool = False,
     **tile_kwargs,
-) -> Tensor:
+) -> Tensor | tuple[Tensor, Tensor]:
     """3D neighbourhood attention, NATTEN ``na3d`` signature, heads-last tensors."""
     _check_flag("stride", stride, 1)
     _check_flag("is_causal", is_causal, False)
     if additional_keys is not None or additional_values is not None:
         raise NotImplementedError("na3d: additional_keys/values are not supported by the HIP backend")
-    if return_lse:
-        raise NotImplementedError("na3d: return_lse is not supported by the HIP backend")
     if query.dim() != 6:
         raise ValueError(f"na3d expects heads-last [B, Z, Y, X, H, D] tensors, got {tuple(query.shape)}")
     if query.shape != key.shape or query.shape != value.shape:
@@ -84,6 +85,12 @@ def na3d(
             raise ValueError(
                 f"na3d: kernel_size * dilation ({k}*{d}) exceeds the input size {L} along axis {ax}"
             )
+    if return_lse:
+        # NATTEN's logsumexp: natural log of the sum of exp(scale * q.k) over each query's
+        # window, fp32 [B, Z, Y, X, H]; the kernels keep it in log2 units.  It carries no
+        # gradient (the output does, through the backward that consumes it).
+        out, lse2 = ops.na3d_fwd_lse(query, key, value, list(ks), list(dil), scale)
+        return out, lse2 * math.log(2.0)
     # with gradients wanted, the forward keeps its log-sum-exp for the backward
     return ops.na3d(query, key, value, list(ks), list(dil), scale)
 

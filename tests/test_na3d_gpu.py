@@ -124,6 +124,21 @@ def test_natten_shim(gpu):
         natten_na3d(q, k, v, kernel_size=(5, 3, 3))
 
 
+@pytest.mark.parametrize("dtype, tol", [(torch.float32, 1e-4), (torch.bfloat16, 3e-2)])
+def test_natten_shim_return_lse(gpu, dtype, tol):
+    """``return_lse=True`` (NATTEN's functional API): the output as without it, and the
+    natural-log logsumexp of each query's window against the float64 oracle (whose lse is
+    in log2 units), with dilation and clamped edges on every axis."""
+    import math
+
+    q, k, v = _rand((1, 5, 9, 11, 2, 32 if dtype == torch.float32 else 64), 8, dtype, gpu)
+    out, lse = natten_na3d(q, k, v, kernel_size=(3, 5, 5), dilation=(1, 1, 2), return_lse=True)
+    assert lse.dtype == torch.float32 and tuple(lse.shape) == tuple(q.shape[:5])
+    assert torch.equal(out, natten_na3d(q, k, v, kernel_size=(3, 5, 5), dilation=(1, 1, 2)))
+    _, ref = O.na3d(q.cpu(), k.cpu(), v.cpu(), (3, 5, 5), (1, 1, 2), compute_dtype=torch.float64, return_lse=True)
+    assert (lse.double().cpu() / math.log(2.0) - ref).abs().max().item() <= tol
+
+
 def test_cfg1_shape_subboxes(gpu):
     """configs[1] shape [2,8,64,64,8,64], W=(3,7,7): full launch, oracle on boxes
     at the grid corners and the middle (a few seconds of CPU)."""
