@@ -476,11 +476,11 @@ __device__ __forceinline__ void gemm_dma_body(const GemmParams& p) {
     wait_vmcnt(0);
     lds_barrier();  // the stage has landed for every wave; slot wr is free
     // The next stage's copies in two bursts, x here and w after the first
-    // sub-step's MFMAs: all eight of a wave's copies at once right after the
-    // barrier stall every wave on the address path while the MFMA pipe idles
-    // (A/B at the block's shapes, bit-identical: 1.5-5% faster; copies
-    // placed later in the step or spread further, and all of them after the
-    // first sub-step: no faster or slower).
+    // sub-step's MFMAs (A/B at the block's shapes, bit-identical: 1.5-5%
+    // faster than all eight of a wave's copies here; later in the step,
+    // spread further, all after the first sub-step, or the two waves of a
+    // SIMD out of step: no faster or slower).  The copies cost the K loop
+    // 25-35% with a whole stage in flight and 3-10% with half of one.
     const int wr_now = wr;
     if (kt + 1 < nk) {
       issue_at(m0, n0, voff, kt + 1, wr, std::integral_constant<int, XS>{});
