@@ -145,6 +145,41 @@ def test_gemm_ragged_k_masks_the_last_stage(gpu, M, N, K):
     assert torch.equal(tight, out)
 
 
+def _act_ref(act, y):
+    if act == _lib.ACT_GELU_TANH:
+        return F.gelu(y, approximate="tanh")
+    if act == _lib.ACT_GELU_ERF:
+        return F.gelu(y)
+    if act == _lib.ACT_SIGMOID:
+        return torch.sigmoid(y)
+    if act in (_lib.ACT_GELU_TANH_GRAD, _lib.ACT_SIGMOID_GRAD):
+        yr = y.clone().requires_grad_(True)
+        f = F.gelu(yr, approximate="tanh") if act == _lib.ACT_GELU_TANH_GRAD else torch.sigmoid(yr)
+        f.sum().backward()
+        return yr.grad
+    return y
+
+
+@pytest.mark.parametrize("act", [_lib.ACT_NONE, _lib.ACT_GELU_TANH, _lib.ACT_GELU_ERF, _lib.ACT_SIGMOID,
+                                 _lib.ACT_GELU_TANH_GRAD, _lib.ACT_SIGMOID_GRAD])
+@pytest.mark.parametrize("res", [None, _lib.RES_ADD, _lib.RES_MUL])
+def test_gemm_ragged_k_every_epilogue(gpu, act, res):
+    """Every activation x residual instance of the ragged-K kernel (K = 80: one full and one
+    16-column stage; ragged M and N) against float64."""
+    M, N, K = 300, 136, 80
+    g = torch.Generator().manual_seed(act * 3 + (0 if res is None else res + 1))
+    x, w, b = _randn((M, K), g), _randn((N, K), g, 2 * K**-0.5), _randn((N,), g)
+    r = _randn((M, N), g) if res is not None else None
+    args = [x.to(gpu), w.to(gpu), b.to(gpu), None if r is None else r.to(gpu), act]
+    out = torch.ops.strata_hip.gemm_bias_act(*args, _lib.RES_ADD if res is None else res)
+    ref = _act_ref(act, x.double() @ w.double().T + b.double())
+    if res == _lib.RES_ADD:
+        ref = ref + r.double()
+    elif res == _lib.RES_MUL:
+        ref = ref * r.double()
+    assert rel_l2(out.float(), ref) <= 1e-2
+
+
 @pytest.mark.parametrize("K", [80, 200])
 def test_gemm_gelu_save_ragged_k(gpu, K):
     """The GELU-saving fc1 launch at K not a multiple of 64: both outputs against fp64."""
