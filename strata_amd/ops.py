@@ -528,7 +528,10 @@ def gemm_bias_act(x: Tensor, w: Tensor, bias: Optional[Tensor], residual: Option
     fp32 accumulation, bf16 in/out.
 
     x ``[..., K]``, w ``[N, K]`` (nn.Linear layout), bias ``[N]``, residual
-    ``[..., N]``.  act: 0 none, 1 GELU(tanh), 2 GELU(erf), 3 sigmoid.  Replaces
+    ``[..., N]``.  act: 0 none, 1 GELU(tanh), 2 GELU(erf), 3 sigmoid, 4 / 5 the
+    derivatives of GELU(tanh) / sigmoid (the backward's epilogues).  K is any
+    multiple of 8 (a K not a multiple of 64 runs on the large-tile kernel's
+    ragged-K instances).  Replaces
     nn.Linear (+ nn.GELU) in the block's attn.qkv / attn.proj / Mlp
     (screamcast/checkpoint_compat.py:243-249, screamcast/strata_wrappers.py:76-100)
     and, with act 3 / res_op 1, the attention gate ``a * sigmoid(gate_proj(x))``.
