@@ -272,8 +272,9 @@ int strata_hip_rope_qkv_pack_bwd(const strata_hip_rope_pack_bwd_args* args, void
  * stride ldw), bias: [N] bf16 or NULL, residual: [M, N] bf16 (row stride ldr)
  * or NULL, out: [M, N] bf16 (row stride ldo).  fp32 accumulation.  The
  * residual is added (res_op ADD) or multiplied (res_op MUL) after the
- * activation.  K must be a multiple of 8 and every row stride a multiple of
- * 8 elements.  `out` may alias `residual`.
+ * activation.  K must be a multiple of 8, every row stride a multiple of 8
+ * elements, x, w, out and residual 16-byte aligned and bias 8-byte aligned
+ * (STRATA_HIP_EINVAL otherwise).  `out` may alias `residual`.
  * ------------------------------------------------------------------------- */
 typedef struct strata_hip_gemm_args {
   const void* x;

@@ -716,11 +716,12 @@ static int gemm_params(const strata_hip_gemm_args* a, GemmParams& p) {
     if (a->k % 8 != 0) return fail(STRATA_HIP_EINVAL, "gemm: k must be a multiple of 8");
     if (a->ldx < a->k || a->ldw < a->k || a->ldo < a->n || (a->residual && a->ldr < a->n))
       return fail(STRATA_HIP_EINVAL, "gemm: row stride smaller than the row length");
-    if (a->ldx % 8 || a->ldw % 8 || a->ldo % 4 || (a->residual && a->ldr % 4))
-      return fail(STRATA_HIP_EINVAL, "gemm: x/w row strides must be multiples of 8, out/residual of 4");
-    if (((uintptr_t)a->x & 15) || ((uintptr_t)a->w & 15) || ((uintptr_t)a->out & 7) ||
-        (a->residual && ((uintptr_t)a->residual & 7)) || (a->bias && ((uintptr_t)a->bias & 7)))
-      return fail(STRATA_HIP_EINVAL, "gemm: x/w must be 16-byte aligned, out/residual/bias 8-byte aligned");
+    // The epilogue stores and the residual loads move 16 bytes of a row at a time.
+    if (a->ldx % 8 || a->ldw % 8 || a->ldo % 8 || (a->residual && a->ldr % 8))
+      return fail(STRATA_HIP_EINVAL, "gemm: row strides must be multiples of 8 elements");
+    if (((uintptr_t)a->x & 15) || ((uintptr_t)a->w & 15) || ((uintptr_t)a->out & 15) ||
+        (a->residual && ((uintptr_t)a->residual & 15)) || (a->bias && ((uintptr_t)a->bias & 7)))
+      return fail(STRATA_HIP_EINVAL, "gemm: x, w, out and residual must be 16-byte aligned, bias 8-byte aligned");
   }
   if (a->act < STRATA_HIP_ACT_NONE || a->act > STRATA_HIP_ACT_SIGMOID_GRAD) return fail(STRATA_HIP_EINVAL, "gemm: bad act");
   if (a->res_op != STRATA_HIP_RES_ADD && a->res_op != STRATA_HIP_RES_MUL) return fail(STRATA_HIP_EINVAL, "gemm: bad res_op");

@@ -521,6 +521,22 @@ def _rows(name: str, t: Tensor, what: str) -> Tensor:
     return t2
 
 
+def _pad_n(w: Tensor, bias: Optional[Tensor], residual: Optional[Tensor]):
+    """N not a multiple of 8: w (and bias, residual) padded with zeros to the next
+    multiple, so that the output and residual rows are whole 16-byte chunks (the
+    C ABI's contract); the caller keeps the first N columns of the result."""
+    N = w.shape[0]
+    n8 = -(-N // 8) * 8
+    if n8 == N:
+        return w, bias, residual, N
+    w = torch.cat([w, w.new_zeros((n8 - N, w.shape[1]))])
+    if bias is not None:
+        bias = torch.cat([bias, bias.new_zeros(n8 - N)])
+    if residual is not None:
+        residual = torch.nn.functional.pad(residual, (0, n8 - N))
+    return w, bias, residual, N
+
+
 @torch.library.custom_op("strata_hip::gemm_bias_act", mutates_args=())
 def gemm_bias_act(x: Tensor, w: Tensor, bias: Optional[Tensor], residual: Optional[Tensor], act: int,
                   res_op: int = 0) -> Tensor:
@@ -550,6 +566,18 @@ def gemm_bias_act(x: Tensor, w: Tensor, bias: Optional[Tensor], residual: Option
     out_shape = (*x.shape[:-1], N)
     if residual is not None and tuple(residual.shape) != out_shape:
         raise ValueError(f"{name}: residual must have shape {out_shape}, got {tuple(residual.shape)}")
+    if N % 8:
+        w, bias, residual, _ = _pad_n(w, bias, residual)
+        return _gemm_launch(x, w, bias, residual, act, res_op)[..., :N].contiguous()
+    return _gemm_launch(x, w, bias, residual, act, res_op)
+
+
+def _gemm_launch(x: Tensor, w: Tensor, bias: Optional[Tensor], residual: Optional[Tensor], act: int,
+                 res_op: int) -> Tensor:
+    """strata_hip_gemm_bias_act on validated operands whose N is a multiple of 8."""
+    name = "gemm_bias_act"
+    K, N = x.shape[-1], w.shape[0]
+    out_shape = (*x.shape[:-1], N)
     x2 = _rows(name, x, "x")
     w2 = _rows(name, w, "w")
     b2 = bias.contiguous() if bias is not None else None
@@ -639,6 +667,17 @@ def gemm_gelu_train(x: Tensor, w: Tensor, bias: Optional[Tensor]) -> tuple[Tenso
     N = w.shape[0]
     if bias is not None and tuple(bias.shape) != (N,):
         raise ValueError(f"{name}: bias must be [{N}]")
+    if N % 8:
+        wp, bp, _, _ = _pad_n(w, bias, None)
+        out, dact = _gemm_gelu_train_launch(x, wp, bp)
+        return out[..., :N].contiguous(), dact[..., :N].contiguous()
+    return _gemm_gelu_train_launch(x, w, bias)
+
+
+def _gemm_gelu_train_launch(x: Tensor, w: Tensor, bias: Optional[Tensor]) -> tuple[Tensor, Tensor]:
+    """strata_hip_gemm_gelu_save on validated operands whose N is a multiple of 8."""
+    name = "gemm_gelu_train"
+    K, N = x.shape[-1], w.shape[0]
     x2, w2 = _rows(name, x, "x"), _rows(name, w, "w")
     b2 = bias.contiguous() if bias is not None else None
     out = torch.empty((*x.shape[:-1], N), dtype=torch.bfloat16, device=x.device)

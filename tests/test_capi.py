@@ -168,6 +168,14 @@ def test_gemm_and_layernorm_validation(lib):
     g.res_op, g.act = 0, 6
     assert lib.strata_hip_gemm_bias_act(ctypes.byref(g), None) == _lib.EINVAL
     assert "act" in lib.strata_hip_last_error().decode()
+    # output rows are written 16 bytes at a time: a row stride of 4 mod 8 elements, or an
+    # output 8 but not 16-byte aligned, is refused before any launch
+    g.act, g.ldo = 0, 20
+    assert lib.strata_hip_gemm_bias_act(ctypes.byref(g), None) == _lib.EINVAL
+    assert "multiples of 8" in lib.strata_hip_last_error().decode()
+    g.ldo, g.out = 16, 0x1008
+    assert lib.strata_hip_gemm_bias_act(ctypes.byref(g), None) == _lib.EINVAL
+    assert "16-byte aligned" in lib.strata_hip_last_error().decode()
 
 
 def test_empty_problem_is_a_no_op(lib):

@@ -180,6 +180,25 @@ def test_gemm_ragged_k_every_epilogue(gpu, act, res):
     assert rel_l2(out.float(), ref) <= 1e-2
 
 
+@pytest.mark.parametrize("N", [100, 36, 7])
+def test_gemm_odd_n_through_the_op(gpu, N):
+    """N not a multiple of 8: the op pads the weight (and bias, residual) to whole 16-byte
+    output rows for the C ABI and returns the first N columns; also the GELU-saving launch."""
+    M, K = 333, 128
+    g = torch.Generator().manual_seed(N)
+    x, w, b, r = _randn((M, K), g), _randn((N, K), g, K**-0.5), _randn((N,), g), _randn((M, N), g)
+    out = torch.ops.strata_hip.gemm_bias_act(x.to(gpu), w.to(gpu), b.to(gpu), r.to(gpu), _lib.ACT_GELU_TANH)
+    pre = x.double() @ w.double().T + b.double()
+    assert out.shape == (M, N) and out.is_contiguous()
+    assert rel_l2(out.float(), F.gelu(pre, approximate="tanh") + r.double()) <= 1e-2
+    h, dact = torch.ops.strata_hip.gemm_gelu_train(x.to(gpu), w.to(gpu), b.to(gpu))
+    pr = pre.clone().requires_grad_(True)
+    F.gelu(pr, approximate="tanh").sum().backward()
+    assert h.shape == dact.shape == (M, N)
+    assert rel_l2(h.float(), F.gelu(pre, approximate="tanh")) <= 1e-2
+    assert rel_l2(dact.float(), pr.grad) <= 1e-2
+
+
 @pytest.mark.parametrize("K", [80, 200])
 def test_gemm_gelu_save_ragged_k(gpu, K):
     """The GELU-saving fc1 launch at K not a multiple of 64: both outputs against fp64."""
