@@ -616,7 +616,7 @@ def cpu_baselines(full: bool):
 
     Headline (``cpu_baseline``): a bounded sample of configs[2] (tile 0, head 0,
     z 0-3 of the interior: 4.25 GFLOP), warm-up + median of 5.  ``cpu_configs``:
-    configs[0] and configs[1] in full (median of 5 / of 3), configs[3] on batch entry
+    configs[0] and configs[1] in full (median of 5 each), configs[3] on batch entry
     0 (x4, labelled extrapolated; in full with ``full``), configs[2] from the
     sample (x FLOP ratio) and configs[4] from one block per stage at batch 1
     (x tokens x blocks x tiles x steps), both labelled extrapolated."""
