@@ -420,6 +420,70 @@ __device__ __forceinline__ void gemm_dma_body(const GemmParams& p) {
     for (int kk = 0; kk < 2; ++kk) boff[j][kk] = row * ROWB + gswz<CH>(2 * kk + hi, row) * 16;
   }
 
+  // The bias as the first K step's C operand: binit[i][4q + e] holds column
+  // 32i + 8q + 4hi + e of the wave tile.  EARLY_BIAS: the next tile's bias is
+  // loaded at the start of the epilogue (all eight loads in flight together) and
+  // converted at its end, so that the loads' latency hides behind the epilogue.
+  // The instances with the saved derivative, GELU(erf), or the GELU derivative
+  // beside a residual spill with it: they load at the tile's start.
+  constexpr bool EARLY_BIAS = !SAVE && ACT != STRATA_HIP_ACT_GELU_ERF &&
+                              !(RES != RES_NONE_T && ACT == STRATA_HIP_ACT_GELU_TANH_GRAD);
+  f32x16 binit[FN];
+  // bb[i][q]: the bf16 pairs of columns n0x + wn * WTN + 32i + 8q + 4hi + (0..3).
+  // Uniform branches; a column panel inside the matrix loads with no per-lane
+  // condition (a divergent if / else writing the same registers makes the
+  // compiler wait for each load before issuing the next).
+  auto load_bias = [&](int64_t n0x, u32x2 (&bb)[FN][4]) {
+    const int64_t gb = n0x + wn * WTN + 4 * hi;
+    if (!p.bias) {
+#pragma unroll
+      for (int i = 0; i < FN; ++i)
+#pragma unroll
+        for (int q = 0; q < 4; ++q) bb[i][q] = (u32x2){0u, 0u};
+    } else if (n0x + BN <= p.N) {
+#pragma unroll
+      for (int i = 0; i < FN; ++i)
+#pragma unroll
+        for (int q = 0; q < 4; ++q) bb[i][q] = *(const u32x2*)(p.bias + gb + 32 * i + 8 * q);
+    } else {  // the ragged last column panel
+      const uint16_t* b16 = (const uint16_t*)p.bias;
+#pragma unroll
+      for (int i = 0; i < FN; ++i)
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+          u32x2 w2 = {0u, 0u};
+          for (int e = 0; e < 4; ++e) {
+            const int64_t gn = gb + 32 * i + 8 * q + e;
+            if (gn < p.N) w2[e >> 1] |= (uint32_t)b16[gn] << (16 * (e & 1));
+          }
+          bb[i][q] = w2;
+        }
+    }
+  };
+  // bb -> binit.  The empty asm takes the loaded registers as its output, so the
+  // compiler waits for the loads here, once, and the walk carries only computed
+  // registers (with the loads' registers carried to the next tile, it waited for
+  // them, and so for every store issued before, at the head of the next K loop).
+  auto settle_bias = [&](u32x2 (&bb)[FN][4]) {
+#pragma unroll
+    for (int i = 0; i < FN; ++i)
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        asm volatile("" : "+v"(bb[i][q]));
+        binit[i][4 * q + 0] = bf16_lo(bb[i][q][0]);
+        binit[i][4 * q + 1] = bf16_hi(bb[i][q][0]);
+        binit[i][4 * q + 2] = bf16_lo(bb[i][q][1]);
+        binit[i][4 * q + 3] = bf16_hi(bb[i][q][1]);
+      }
+  };
+  if (EARLY_BIAS && wg_id < ntiles) {
+    int64_t m0f, n0f;
+    tile_origin(wg_id, m0f, n0f);
+    u32x2 bb[FN][4];
+    load_bias(n0f, bb);
+    settle_bias(bb);
+  }
+
   // Ring slots: `rd` holds the next stage to read, `wr` takes the next issue
   // (and, after a tile's last K step, that tile's epilogue slabs).
   int rd = 0, wr = 1;
@@ -438,41 +502,42 @@ __device__ __forceinline__ void gemm_dma_body(const GemmParams& p) {
   if (!first_in_flight) issue_at(m0, n0, voff, 0, rd, std::integral_constant<int, ALL>{});
 
   // The bias enters as the C operand of each accumulator's first MFMA (no
-  // zero fill, no add in the epilogue): acc[i][j][4q + e] holds column
-  // 32i + 8q + 4hi + e of the wave tile.
+  // zero fill, no add in the epilogue).
   const int64_t gn0 = n0 + wn * WTN, gm0 = m0 + wm * WTM;
   const bool full = m0 + BM <= p.M && n0 + BN <= p.N;  // uniform
-  f32x16 binit[FN];
+  if constexpr (!EARLY_BIAS) {
 #pragma unroll
-  for (int i = 0; i < FN; ++i)
+    for (int i = 0; i < FN; ++i)
 #pragma unroll
-    for (int q = 0; q < 4; ++q) {
-      const int64_t gn = gn0 + 32 * i + 8 * q + 4 * hi;
-      float bv[4] = {0.f, 0.f, 0.f, 0.f};
-      if (p.bias) {
-        if (full || gn + 4 <= p.N) {
-          const u32x2 w2 = *(const u32x2*)(p.bias + gn);
-          bv[0] = bf16_lo(w2[0]);
-          bv[1] = bf16_hi(w2[0]);
-          bv[2] = bf16_lo(w2[1]);
-          bv[3] = bf16_hi(w2[1]);
-        } else {
-          for (int e = 0; e < 4; ++e) bv[e] = gn + e < p.N ? (float)p.bias[gn + e] : 0.f;  // ragged last columns
+      for (int q = 0; q < 4; ++q) {
+        const int64_t gn = gn0 + 32 * i + 8 * q + 4 * hi;
+        float bv[4] = {0.f, 0.f, 0.f, 0.f};
+        if (p.bias) {
+          if (full || gn + 4 <= p.N) {
+            const u32x2 w2 = *(const u32x2*)(p.bias + gn);
+            bv[0] = bf16_lo(w2[0]);
+            bv[1] = bf16_hi(w2[0]);
+            bv[2] = bf16_lo(w2[1]);
+            bv[3] = bf16_hi(w2[1]);
+          } else {
+            for (int e = 0; e < 4; ++e) bv[e] = gn + e < p.N ? (float)p.bias[gn + e] : 0.f;  // ragged last columns
+          }
         }
-      }
 #pragma unroll
-      for (int e = 0; e < 4; ++e) binit[i][4 * q + e] = bv[e];
-    }
+        for (int e = 0; e < 4; ++e) binit[i][4 * q + e] = bv[e];
+      }
+  }
 
   f32x16 acc[FN][FM];
   first_in_flight = false;
   // One K step; FIRST: the step that starts every accumulator from the bias.
   auto kstep = [&](int kt, auto first) {
     constexpr bool FIRST = decltype(first)::value;
-    // Loads and stores share vmcnt and may complete out of order with respect
-    // to each other, so the wait is for everything issued: the stage read now
-    // (issued one step ago) and, at a tile's first step, the previous tile's
-    // output stores.
+    // The wait is for everything issued: the stage read now (issued one step
+    // ago) and, at a tile's first step, the previous tile's output stores (the
+    // compiler holds the registers of their data until they complete, so a
+    // wait that left them in flight would stall on the first LDS reads
+    // instead).
     wait_vmcnt(0);
     lds_barrier();  // the stage has landed for every wave; slot wr is free
     // The next stage's copies in two bursts, x here and w after the first
@@ -547,6 +612,8 @@ __device__ __forceinline__ void gemm_dma_body(const GemmParams& p) {
   // slab is rewritten by the second half only after the first half's reads
   // (one wave, in order).
   constexpr int SRB = WTN * 2, CPR = WTN / 8, RPI = 64 / CPR, NIT = WTM / RPI, NH = NIT / 2;
+  u32x2 nb[FN][4];  // the next tile's bias (after the last tile: column panel 0's, unused)
+  if constexpr (EARLY_BIAS) load_bias(n0n, nb);
   lds_barrier();  // every wave is done reading the last stage
   char* slab = lds + wr * STAGE + wave * SLAB;
   const int c = lane % CPR;  // logical 16-byte chunk = 8 output columns
@@ -651,6 +718,7 @@ __device__ __forceinline__ void gemm_dma_body(const GemmParams& p) {
       from_slab(half, p.out2, std::false_type{});
     }
   }
+  if constexpr (EARLY_BIAS) settle_bias(nb);
   }  // tiles
 }
 
