@@ -22,10 +22,12 @@
 
 namespace strata {
 
-// GELU(tanh) = x * sigmoid(2u), u = sqrt(2/pi) (x + 0.044715 x^3) (the MLP's form).
+// GELU(tanh) = x * sigmoid(2u), u = sqrt(2/pi) (x + 0.044715 x^3), with 2u log2(e) folded
+// into one polynomial (the MLP GEMM's form): one exp2 and one reciprocal.
 __device__ __forceinline__ float px_gelu_tanh(float x) {
-  const float u = 0.7978845608028654f * (x + 0.044715f * x * x * x);
-  return x * __builtin_amdgcn_rcpf(1.f + __expf(-2.f * u));
+  constexpr float k1 = 2.f * 1.4426950408889634f * 0.7978845608028654f;
+  const float t = x * fmaf(k1 * 0.044715f, x * x, k1);
+  return x * __builtin_amdgcn_rcpf(1.f + __builtin_amdgcn_exp2f(-t));
 }
 
 // Source index pair and weight of one output coordinate of the bilinear upsampling
@@ -46,39 +48,61 @@ struct UpDwParams {
   const bf16* w;  // [9, C]: tap-major
   const bf16* b;  // [C] or null
   int B, Z, Yc, Xc, C, f;
+  int cgw, np, nxb;  // a workgroup's channel groups and output columns; workgroups per output row
   int64_t cs[4], os[4];
 };
 
-// One thread per output column (b, y, x) and 8 channels, walking every z (the taps and
-// the bilinear weights are the same at every z).  The 3x3 upsampled neighbourhood of
-// output (y, x) draws on at most 3 x 3 coarse tokens (rows r0 .. r0 + 2, columns
-// c0 .. c0 + 2): with by[dy][r] the weight of coarse row r0 + r in upsampled row
-// y + dy - 1 (zero outside the map: the convolution's padding) and bx likewise, the
-// output is sum_rc K[r][c] cond[r][c] with K = by^T (w bx) per channel, formed once per
-// thread; per z the thread loads the 9 coarse 16-byte runs and does 9 FMAs per channel.
-// The taps come in tap-major order [9, C], 16 bytes per tap.
-__global__ __launch_bounds__(256) void upsample_dw_gelu_kernel(UpDwParams p, int total) {
-  const int t = (int)(blockIdx.x * 256 + threadIdx.x);
-  if (t >= total) return;
-  const int cg = p.C / 8;
-  const int ch = 8 * (t % cg);
-  int r = t / cg;
+constexpr int UPDW_STAGE = 1024;  // staged 16-byte runs per z slice (4 per thread)
+
+// A workgroup owns cgw groups of 8 channels x np consecutive output columns of one
+// output row (b, y), every z; one thread per (column, channel group).  The 3 x 3
+// upsampled neighbourhood of output (y, x) draws on at most 3 x 3 coarse tokens (rows
+// r0 .. r0 + 2, columns c0 .. c0 + 2): with by[dy][r] the weight of coarse row r0 + r in
+// upsampled row y + dy - 1 (zero outside the map: the convolution's padding) and bx
+// likewise, the output is sum_rc K[r][c] cond[r][c] with K = by^T (w bx) per channel,
+// formed once per thread.  Per z the workgroup stages the coarse runs its windows touch
+// (3 rows x the columns from its first column's c0 to its last's c0 + 2, cgw channel
+// groups: at f = 4, 16 columns take 7 coarse columns) in LDS, STG loads per thread,
+// the next slice's loads issued before the current slice's arithmetic; each thread then
+// reads its 9 runs from LDS and does 9 FMAs per channel.  (One thread loading its own 9
+// runs from L2 took 9 vector-memory instructions per 16-byte output.)
+template <int STG>
+__global__ __launch_bounds__(256) void upsample_dw_gelu_kernel(UpDwParams p) {
+  __shared__ u32x4 stage[2][UPDW_STAGE];
+  const int tid = (int)threadIdx.x;
+  int blk = (int)blockIdx.x;
+  const int ncgb = (p.C / 8) / p.cgw;
+  const int cgb = blk % ncgb;
+  blk /= ncgb;
+  const int xb = blk % p.nxb;
+  blk /= p.nxb;
   const int Y = p.Yc * p.f, X = p.Xc * p.f;
-  const int x = r % X;
-  r /= X;
-  const int y = r % Y;
-  const int b = r / Y;
+  const int y = blk % Y;
+  const int b = blk / Y;
+  const int ci = tid % p.cgw, pi = tid / p.cgw;
+  const int x0 = xb * p.np;
+  const int xl = min(x0 + p.np, X) - 1;  // the workgroup's last column
+  const bool live = pi < p.np && x0 + pi <= xl;
+  const int x = live ? x0 + pi : xl;
+  const int ch = 8 * (cgb * p.cgw + ci);
   const float inv_f = 1.f / (float)p.f;
-  float by[3][3], bx[3][3];
-  int r0, c0;
+  auto c0_of = [&](int xx) {
+    int i0, i1;
+    float w1;
+    bilinear_src(max(xx - 1, 0), inv_f, p.Xc, i0, i1, w1);
+    return min(i0, max(p.Xc - 3, 0));
+  };
+  int r0;
   {
     int i0, i1;
     float w1;
     bilinear_src(max(y - 1, 0), inv_f, p.Yc, i0, i1, w1);
     r0 = min(i0, max(p.Yc - 3, 0));
-    bilinear_src(max(x - 1, 0), inv_f, p.Xc, i0, i1, w1);
-    c0 = min(i0, max(p.Xc - 3, 0));
   }
+  const int cfirst = c0_of(x0), c0 = c0_of(x);
+  const int ncol = c0_of(xl) - cfirst + 3;
+  const int nrun = 3 * ncol * p.cgw;  // <= STG * 256 (the host's bound)
+  float by[3][3], bx[3][3];
 #pragma unroll
   for (int d = 0; d < 3; ++d) {
 #pragma unroll
@@ -126,33 +150,52 @@ __global__ __launch_bounds__(256) void upsample_dw_gelu_kernel(UpDwParams p, int
 #pragma unroll
     for (int e = 0; e < 8; ++e) bias[e] = (e & 1) ? bf16_hi(bv[e >> 1]) : bf16_lo(bv[e >> 1]);
   }
-  // coarse runs (rows / columns past a grid of fewer than 3 repeat the last; their weights are 0)
-  int64_t off[9];
+  // Staged run s = (row i, column j, group g) at (i * ncol + j) * cgw + g; coarse rows and
+  // columns past a grid of fewer than 3 repeat the last (their weights are 0).
+  int64_t soff[STG];
 #pragma unroll
-  for (int i = 0; i < 3; ++i)
-#pragma unroll
-    for (int j = 0; j < 3; ++j)
-      off[3 * i + j] = (int64_t)min(r0 + i, p.Yc - 1) * p.cs[2] + (int64_t)min(c0 + j, p.Xc - 1) * p.cs[3];
-  const bf16* cb = p.cond + (int64_t)b * p.cs[0] + ch;
+  for (int u = 0; u < STG; ++u) {
+    const int s = min(tid + 256 * u, nrun - 1);
+    const int i = s / (ncol * p.cgw), rem = s % (ncol * p.cgw);
+    soff[u] = (int64_t)min(r0 + i, p.Yc - 1) * p.cs[2] + (int64_t)min(cfirst + rem / p.cgw, p.Xc - 1) * p.cs[3] +
+              8 * (cgb * p.cgw + rem % p.cgw);
+  }
+  const int tbase = (c0 - cfirst) * p.cgw + ci;  // tap (i, j) at tbase + (i * ncol + j) * cgw
+  const bf16* cb = p.cond + (int64_t)b * p.cs[0];
   bf16* ob = p.out + (int64_t)b * p.os[0] + (int64_t)y * p.os[2] + (int64_t)x * p.os[3] + ch;
-  for (int z = 0; z < p.Z; ++z) {
-    const bf16* cz = cb + (int64_t)z * p.cs[1];
-    u32x4 v[9];
+  u32x4 g[STG];
+  auto gload = [&](int z) {
 #pragma unroll
-    for (int k = 0; k < 9; ++k) v[k] = *(const u32x4*)(cz + off[k]);
-    float gl[8];
+    for (int u = 0; u < STG; ++u) g[u] = *(const u32x4*)(cb + (int64_t)z * p.cs[1] + soff[u]);
+  };
+  auto sput = [&](int buf) {
 #pragma unroll
-    for (int e = 0; e < 8; ++e) {
-      const int w2 = e >> 1;
-      float acc = bias[e];
+    for (int u = 0; u < STG; ++u)
+      if (tid + 256 * u < nrun) stage[buf][tid + 256 * u] = g[u];
+  };
+  gload(0);
+  sput(0);
+  __syncthreads();
+  for (int z = 0; z < p.Z; ++z) {  // every thread runs every slice (the barriers)
+    if (z + 1 < p.Z) gload(z + 1);
+    if (live) {
+      // tap-major: one staged run live at a time (each channel's sum in the same order)
+      float acc[8];
 #pragma unroll
-      for (int k = 0; k < 9; ++k) acc = fmaf(K[e][k], (e & 1) ? bf16_hi(v[k][w2]) : bf16_lo(v[k][w2]), acc);
-      gl[e] = px_gelu_tanh(acc);
+      for (int e = 0; e < 8; ++e) acc[e] = bias[e];
+#pragma unroll
+      for (int k = 0; k < 9; ++k) {
+        const u32x4 v = stage[z & 1][tbase + ((k / 3) * ncol + k % 3) * p.cgw];
+#pragma unroll
+        for (int e = 0; e < 8; ++e) acc[e] = fmaf(K[e][k], (e & 1) ? bf16_hi(v[e >> 1]) : bf16_lo(v[e >> 1]), acc[e]);
+      }
+      u32x4 o;
+#pragma unroll
+      for (int w2 = 0; w2 < 4; ++w2) o[w2] = pack_bf16x2(px_gelu_tanh(acc[2 * w2]), px_gelu_tanh(acc[2 * w2 + 1]));
+      *(u32x4*)(ob + (int64_t)z * p.os[1]) = o;
     }
-    u32x4 o;
-#pragma unroll
-    for (int w2 = 0; w2 < 4; ++w2) o[w2] = pack_bf16x2(gl[2 * w2], gl[2 * w2 + 1]);
-    *(u32x4*)(ob + (int64_t)z * p.os[1]) = o;
+    if (z + 1 < p.Z) sput((z + 1) & 1);  // the slot read one slice ago (the barrier below orders it)
+    __syncthreads();
   }
 }
 
@@ -266,11 +309,29 @@ extern "C" int strata_hip_upsample_dw_gelu(const strata_hip_upsample_dw_gelu_arg
     p.cs[i] = a->cond_stride[i];
     p.os[i] = a->out_stride[i];
   }
-  const int64_t total = (int64_t)p.B * p.Yc * p.f * p.Xc * p.f * (p.C / 8);  // threads: one per (b, y, x, 8 channels)
-  if (total == 0 || p.Z == 0) return STRATA_HIP_OK;
-  if (total > 0x7fffffff) return fail(STRATA_HIP_EUNSUPPORTED, "upsample_dw_gelu: too large");
-  hipLaunchKernelGGL(upsample_dw_gelu_kernel, dim3((unsigned)((total + 255) / 256)), dim3(256), 0, (hipStream_t)stream,
-                     p, (int)total);
+  if (p.B == 0 || p.Z == 0) return STRATA_HIP_OK;
+  // Channel groups per workgroup: the largest divisor of C / 8 up to 16; the rest of the
+  // 256 threads take consecutive output columns.
+  const int cg = p.C / 8;
+  p.cgw = 1;
+  for (int d = 16; d >= 1; --d)
+    if (cg % d == 0) {
+      p.cgw = d;
+      break;
+    }
+  p.np = 256 / p.cgw;
+  const int64_t X = (int64_t)p.Xc * p.f, Y = (int64_t)p.Yc * p.f;
+  p.nxb = (int)((X + p.np - 1) / p.np);
+  // Staged runs per slice: 3 rows x at most (np - 1) / f + 4 coarse columns (the span of
+  // the columns' c0, plus 3) x cgw; with np * cgw <= 256 and cgw <= 16, at most 912.
+  const int64_t nrun_max = 3 * ((int64_t)(p.np - 1) / p.f + 4) * p.cgw;
+  if (nrun_max > UPDW_STAGE) return fail(STRATA_HIP_EUNSUPPORTED, "upsample_dw_gelu: staging bound");
+  const int64_t blocks = (int64_t)p.B * Y * p.nxb * (cg / p.cgw);
+  if (blocks > 0x7fffffff || X > 0x7fffffff / 4) return fail(STRATA_HIP_EUNSUPPORTED, "upsample_dw_gelu: too large");
+  if (nrun_max <= 512)
+    hipLaunchKernelGGL(upsample_dw_gelu_kernel<2>, dim3((unsigned)blocks), dim3(256), 0, (hipStream_t)stream, p);
+  else
+    hipLaunchKernelGGL(upsample_dw_gelu_kernel<4>, dim3((unsigned)blocks), dim3(256), 0, (hipStream_t)stream, p);
   return check_launch("upsample_dw_gelu_kernel");
 }
 

@@ -628,6 +628,75 @@ def na3d_column_launch(B, L, H, qs, ks, vs, os_) -> Access:
     return acc
 
 
+def _bilinear_i0(o, inv_f, n):
+    """pixel.hip bilinear_src: the first source index of output coordinate o (fp32 as the
+    kernel: src = (o + 0.5) * (1 / f) - 0.5, clamped at 0, truncated, capped at n - 1)."""
+    src = (np.asarray(o, dtype=np.float32) + np.float32(0.5)) * inv_f - np.float32(0.5)
+    src = np.maximum(src, np.float32(0.0))
+    return np.minimum(src.astype(np.int64), n - 1)
+
+
+def upsample_dw_gelu_launch(B, Z, Yc, Xc, C, f, cs, os_) -> tuple[Access, list]:
+    """Every global access of one upsample_dw_gelu_kernel launch (pixel.hip), and its LDS
+    stage indices: the host's workgroup shape (cgw channel groups, np columns, nxb
+    workgroups per row), each thread's decode (cgb, xb, y, b; ci, pi), the staged runs
+    (3 rows x ncol columns x cgw groups, STG per thread, the index clamped to nrun - 1)
+    and the 9 stage indices a live thread reads.  Offsets are element offsets from each
+    view's base.  Returns (Access, problems with the LDS indices)."""
+    cg = C // 8
+    cgw = next(d for d in range(16, 0, -1) if cg % d == 0)
+    npx = 256 // cgw
+    Y, X = Yc * f, Xc * f
+    nxb = -(-X // npx)
+    nrun_max = 3 * ((npx - 1) // f + 4) * cgw
+    stg = 2 if nrun_max <= 512 else 4
+    lds = []
+    if nrun_max > 1024:
+        lds.append(f"nrun bound {nrun_max} > 1024")
+    inv_f = np.float32(1.0) / np.float32(f)
+    blocks = B * Y * nxb * (cg // cgw)
+    acc = Access()
+    acc.u32("upsample grid", [blocks], 1 << 31)
+    blk = np.arange(blocks, dtype=np.int64)
+    cgb = blk % (cg // cgw)
+    t = blk // (cg // cgw)
+    xb = t % nxb
+    t //= nxb
+    y = t % Y
+    b = t // Y
+    tid = np.arange(256, dtype=np.int64)
+    ci, pi = tid % cgw, tid // cgw
+    x0 = (xb * npx)[:, None]
+    xl = np.minimum(x0 + npx, X) - 1
+    live = (pi[None, :] < npx) & (x0 + pi[None, :] <= xl)
+    x = np.where(live, x0 + pi[None, :], xl)
+    c0_of = lambda xx: np.minimum(_bilinear_i0(np.maximum(xx - 1, 0), inv_f, Xc), max(Xc - 3, 0))
+    r0 = np.minimum(_bilinear_i0(np.maximum(y - 1, 0), inv_f, Yc), max(Yc - 3, 0))[:, None]
+    cfirst, c0 = c0_of(x0), c0_of(x)
+    ncol = c0_of(xl) - cfirst + 3
+    nrun = 3 * ncol * cgw
+    if (nrun > stg * 256).any():
+        lds.append(f"nrun {int(nrun.max())} > {stg} x 256")
+    for u in range(stg):
+        s = np.minimum(tid[None, :] + 256 * u, nrun - 1)
+        i, rem = s // (ncol * cgw), s % (ncol * cgw)
+        soff = (np.minimum(r0 + i, Yc - 1) * cs[2] + np.minimum(cfirst + rem // cgw, Xc - 1) * cs[3] +
+                8 * (cgb[:, None] * cgw + rem % cgw))
+        for z in (0, Z - 1):
+            acc.add("cond", 2 * (b[:, None] * cs[0] + z * cs[1] + soff), 16)
+    for i in range(3):
+        for j in range(3):
+            tix = (i * ncol + c0 - cfirst + j) * cgw + ci[None, :]
+            if ((tix < 0) | (tix >= nrun))[live].any():
+                lds.append(f"tap ({i}, {j}) outside the staged runs")
+    ch = 8 * (cgb[:, None] * cgw + ci[None, :])
+    acc.add("weight", 2 * (8 * C + ch), 16)
+    acc.add("weight", 2 * ch, 16)
+    for z in (0, Z - 1):
+        acc.add("out", 2 * (b[:, None] * os_[0] + z * os_[1] + y[:, None] * os_[2] + x * os_[3] + ch), 16, live)
+    return acc, lds
+
+
 def tensor_bytes(shape, strides, esize=2) -> int:
     """Bytes from a view's first element to one past its last (non-negative strides)."""
     if any(s == 0 for s in shape):

@@ -191,3 +191,26 @@ def test_region_kernel_launches_stay_inside_their_tensors(case):
     assert acc.check(sizes) == []
     assert acc.lo["out"] == 0 and acc.hi["out"] == no  # every output reached, nothing past it
 
+
+
+@pytest.mark.parametrize("B, Z, Yc, Xc, C, f", [
+    (6, 24, 16, 16, 1024, 4),   # the production pixel stage (cond at patch 4, upsampled x4)
+    (1, 24, 16, 16, 64, 4),
+    (2, 3, 5, 7, 32, 4),
+    (1, 2, 9, 6, 16, 2),
+    (1, 2, 6, 5, 8, 1),
+    (1, 2, 1, 2, 8, 4),
+    (1, 1, 2, 1, 16, 3),
+    (1, 2, 70, 3, 24, 1),       # 3 channel groups: 85 columns per workgroup, rows wider than one
+])
+def test_upsample_dw_gelu_stays_inside_its_tensors(B, Z, Yc, Xc, C, f):
+    """The upsampling kernel's staged coarse runs, LDS taps and stores, for the GPU test
+    shapes, the production shape and a ragged channel count: every read inside the
+    coarse tensor, every store covering exactly the output, every tap inside the stage."""
+    cs = LM.contiguous_strides([B, Z, Yc, Xc, C])[:4]
+    os_ = LM.contiguous_strides([B, Z, Yc * f, Xc * f, C])[:4]
+    acc, lds = LM.upsample_dw_gelu_launch(B, Z, Yc, Xc, C, f, cs, os_)
+    ncond, nout = 2 * B * Z * Yc * Xc * C, 2 * B * Z * Yc * f * Xc * f * C
+    assert lds == []
+    assert acc.check({"cond": ncond, "out": nout, "weight": 2 * 9 * C}) == []
+    assert acc.lo["out"] == 0 and acc.hi["out"] == nout
