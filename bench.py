@@ -582,14 +582,18 @@ def _cpu_model() -> str:
     return "unknown"
 
 
-def _median_time(fn, reps: int, warmup: int = 1) -> tuple[float, list[float]]:
+def _median_time(fn, reps: int, warmup: int = 1, what: str = "") -> tuple[float, list[float]]:
+    """Median wall time of reps calls after warmup calls; one progress line per call on
+    stderr (a full-size CPU case runs for minutes)."""
     for _ in range(warmup):
         fn()
     times = []
-    for _ in range(reps):
+    for i in range(reps):
         t0 = time.perf_counter()
         fn()
         times.append(time.perf_counter() - t0)
+        if what:
+            print(f"bench: cpu {what} run {i + 1}/{reps}: {times[-1]:.2f} s", file=sys.stderr, flush=True)
     return statistics.median(times), times
 
 
@@ -636,7 +640,7 @@ def cpu_baselines(full: bool):
     q, k, v = (torch.randn(shape, generator=g) for _ in range(3))
     box_o, box_e = (0, 8, 8), (4, 128, 128)
     f_sample = O.na3d_flops(1, 1, 64, box_e[0] * box_e[1] * box_e[2], (3, 13, 13))
-    t2, _ = _median_time(lambda: O.na3d(q, k, v, (3, 13, 13), q_origin=box_o, q_extent=box_e), 5)
+    t2, _ = _median_time(lambda: O.na3d(q, k, v, (3, 13, 13), q_origin=box_o, q_extent=box_e), 5, what="configs[2] sample")
     f2 = 4.0 * 6 * 16 * (16 * 128 * 128) * 507 * 64
     headline = {
         "value": f_sample / t2 / 1e12,
@@ -655,7 +659,7 @@ def cpu_baselines(full: bool):
     g = torch.Generator().manual_seed(0)
     s0 = (1, 4, 16, 16, 4, 32)
     q0, k0, v0 = (torch.randn(s0, generator=g) for _ in range(3))
-    t0, _ = _median_time(lambda: O.na3d(q0, k0, v0, (3, 5, 5)), 5)
+    t0, _ = _median_time(lambda: O.na3d(q0, k0, v0, (3, 5, 5)), 5, what="configs[0]")
     out["configs[0]"] = {"seconds": round(t0, 5), "gflops": round(O.na3d_flops(1, 4, 32, 4 * 16 * 16, (3, 5, 5)) / t0 / 1e9, 2)}
     # RoPE (level tables) + NA3D in full
     q1, k1, v1, _, c1, s1, _, _ = cfg1_inputs(torch.device("cpu"))
@@ -664,13 +668,14 @@ def cpu_baselines(full: bool):
     def run1():
         return O.na3d(R.apply_rope(q1, c1, s1), R.apply_rope(k1, c1, s1), v1, (3, 7, 7))
 
-    t1, _ = _median_time(run1, 5, 1)  # one warm-up, then the median of 5
+    t1, _ = _median_time(run1, 5, 1, what="configs[1]")  # one warm-up, then the median of 5
     out["configs[1]"] = {"seconds": round(t1, 3), "gflops": round(4.0 * 2 * 8 * 64 * 64 * 8 * 147 * 64 / t1 / 1e9, 2)}
     # the block
     B3 = 4 if full else 1
     x, prm, c, s = _cpu_block_case(4, (8, 64, 64), 1024, 16, (3, 7, 7))
     x, c, s = x[:B3], c[:B3], s[:B3]
-    t3, _ = _median_time(lambda: OB.block_forward(x, prm, 16, (3, 7, 7), c, s), reps if full else 1, 1 if full else 0)
+    t3, _ = _median_time(lambda: OB.block_forward(x, prm, 16, (3, 7, 7), c, s), reps if full else 1, 1 if full else 0,
+                         what="configs[3]")
     out["configs[3]"] = {"seconds": round(t3 * 4 / B3, 2), "extrapolated": not full,
                          "tokens_per_s": round(4 * 8 * 64 * 64 / (t3 * 4 / B3), 1),
                          "from": "in full" if full else "batch entry 0 (one run) x4"}
@@ -679,8 +684,8 @@ def cpu_baselines(full: bool):
     za = 16 if full else 4
     xa, pa, ca, sa = _cpu_block_case(1, (za, 64, 64), 768, 12, (3, 7, 7))
     xb, pb, cb, sb = _cpu_block_case(1, (8, 32, 32), 1024, 16, (3, 9, 9), ls_patch=2)
-    ta, _ = _median_time(lambda: OB.block_forward(xa, pa, 12, (3, 7, 7), ca, sa), 1, 0)
-    tb, _ = _median_time(lambda: OB.block_forward(xb, pb, 16, (3, 9, 9), cb, sb), 1, 0)
+    ta, _ = _median_time(lambda: OB.block_forward(xa, pa, 12, (3, 7, 7), ca, sa), 1, 0, what="configs[4] stage-1 block")
+    tb, _ = _median_time(lambda: OB.block_forward(xb, pb, 16, (3, 9, 9), cb, sb), 1, 0, what="configs[4] stage-2 block")
     ta *= 16 / za
     t4 = (ta * 12 + tb * 12) * 6 * 4
     out["configs[4]"] = {"seconds": round(t4, 1), "extrapolated": True,
