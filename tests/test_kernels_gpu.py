@@ -180,6 +180,39 @@ def test_gemm_ragged_k_every_epilogue(gpu, act, res):
     assert rel_l2(out.float(), ref) <= 1e-2
 
 
+@pytest.mark.parametrize("act, res, has_b", [
+    (_lib.ACT_NONE, None, True),                # early bias, the epilogue split by tile kind
+    (_lib.ACT_GELU_TANH, None, True),
+    (_lib.ACT_NONE, _lib.RES_ADD, True),        # early bias, one epilogue for both tile kinds
+    (_lib.ACT_GELU_TANH_GRAD, _lib.RES_MUL, True),  # the bias loaded at the tile's start
+    (_lib.ACT_NONE, None, False),
+])
+def test_gemm_walk_with_ragged_column_panels(gpu, act, res, has_b):
+    """More tiles than workgroups (M = 40000, N = 1000: 628 tiles, 232 columns in the last
+    panel), so workgroups load a later tile's bias, ragged panels included, while they
+    finish the tile before it; every column's bias is distinct.  Against float64."""
+    M, N, K = 40000, 1000, 128
+    print(f"gemm walk ragged N act {act} res {res} bias {has_b}", flush=True)
+    g = torch.Generator().manual_seed(act * 5 + (0 if res is None else res + 1) + has_b)
+    x, w = _randn((M, K), g), _randn((N, K), g, 2 * K**-0.5)
+    b = _randn((N,), g) if has_b else None
+    r = _randn((M, N), g) if res is not None else None
+    out = torch.ops.strata_hip.gemm_bias_act(x.to(gpu), w.to(gpu), None if b is None else b.to(gpu),
+                                             None if r is None else r.to(gpu), act,
+                                             _lib.RES_ADD if res is None else res)
+    pre = x.double() @ w.double().T
+    if b is not None:
+        pre = pre + b.double()
+    ref = _act_ref(act, pre)
+    if res == _lib.RES_ADD:
+        ref = ref + r.double()
+    elif res == _lib.RES_MUL:
+        ref = ref * r.double()
+    assert rel_l2(out.float(), ref) <= 1e-2
+    cols = (out.float().cpu().double() - ref).norm(dim=0) / ref.norm(dim=0).clamp_min(1e-30)
+    assert cols.max().item() <= 3e-2  # no column panel with a wrong bias hides in the total
+
+
 @pytest.mark.parametrize("N", [100, 36, 7])
 def test_gemm_odd_n_through_the_op(gpu, N):
     """N not a multiple of 8: the op pads the weight (and bias, residual) to whole 16-byte
