@@ -23,6 +23,7 @@ pytestmark = pytest.mark.gpu
     ((1, 2, 6, 5, 8), 1),          # factor 1: the depth-wise convolution alone
     ((1, 2, 1, 2, 8), 4),          # coarse grids narrower than the 3 x 3 block a thread loads
     ((1, 1, 2, 1, 16), 3),
+    ((1, 4, 8, 9, 256), 4),        # 16 channel groups, 16 columns per workgroup (the production layout)
     ((2, 3, 11, 17, 48), 3),       # 6 channel groups: 42 output columns per workgroup, ragged rows
     ((1, 2, 70, 3, 24), 1),        # 3 channel groups: 85 columns per workgroup, 256 % 3 threads idle
 ])
